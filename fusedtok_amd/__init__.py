@@ -1,0 +1,851 @@
+"""fusedtok_amd: the fusedtok decode hot path, native to AMD MI355X (gfx950).
+
+The public functions keep fusedtok 2.5.0's names, signatures and error
+contract for the decode hot path (reference python/fusedtok/__init__.py):
+
+- ``attention_decode`` / ``attention_decode_paged``: flash-decoding GQA
+  attention over contiguous / paged KV caches (f32, bf16, fp16 storage);
+- ``kv_append`` / ``kv_append_paged``: one fresh token's K/V rows per
+  sequence written in place at position ``lens[b]``;
+- ``quantize_int8``: symmetric per-tensor INT8 quantize;
+- ``qgemm`` / ``qgemm_perchannel``: W8A8 GEMM with exact int32 accumulation;
+- ``rmsnorm`` (+ residual), ``rope`` (interleaved / NeoX, ``pos_offset``),
+  ``swiglu``.
+
+Execution paths:
+
+- torch tensors on the GPU -> zero-copy: the HIP kernels read and write the
+  tensors' memory through ``data_ptr()`` on the current torch stream, with no
+  host synchronisation (``quantize_int8`` syncs once to return its Python
+  float scale, as the reference does).
+- host inputs (numpy arrays, CPU torch tensors) -> staged: uploaded, run on
+  the GPU, downloaded. This replaces both of the reference's host paths; the
+  ``cuda=`` keyword is accepted for compatibility. There is no CPU fallback:
+  without a HIP device, host inputs raise RuntimeError.
+
+Validation happens before any device work, with the reference's contract:
+TypeError for dtype / device-family problems, ValueError for shapes and
+values, RuntimeError for HIP failures. Device-resident ``lens`` and block
+tables are trusted (never read back); host-origin ones are range-checked.
+
+Build additions (not in the reference): fp16 storage for ``rmsnorm``,
+``rope`` and ``swiglu``; bf16 / fp16 input to ``quantize_int8`` and a
+device-resident scale (``device_scale=True``); bf16 / fp16 GEMM outputs
+(``out_dtype=``) and a device scale operand; ``qgemm_i32`` (raw int32
+accumulators); per-row RoPE positions (``positions=``).
+"""
+
+import numpy as np
+
+try:
+    from . import _fusedtok
+except ImportError as exc:  # pragma: no cover - exercised by packaging
+    raise ImportError(
+        "fusedtok_amd: the native extension is not built. Run "
+        "`python -c 'import __graft_entry__ as g; g.build()'` from the "
+        "repository root (needs hipcc for gfx950)."
+    ) from exc
+
+import torch
+
+__version__ = "0.1.0"
+
+__all__ = [
+    "cuda_available",
+    "rmsnorm",
+    "rope",
+    "swiglu",
+    "quantize_int8",
+    "qgemm",
+    "qgemm_perchannel",
+    "qgemm_i32",
+    "attention_decode",
+    "attention_decode_paged",
+    "kv_append",
+    "kv_append_paged",
+]
+
+# C-ABI dtype codes (include/fusedtok_amd.h)
+_DT_F32, _DT_BF16, _DT_F16 = 0, 1, 2
+_DT_CODE = {torch.float32: _DT_F32, torch.bfloat16: _DT_BF16,
+            torch.float16: _DT_F16}
+_HALF = (torch.bfloat16, torch.float16)
+
+
+def cuda_available():
+    """True if a usable HIP device is present (reference fusedtok.cu:34-37)."""
+    return _fusedtok.cuda_available()
+
+
+# ---------------------------------------------------------------------------
+# dispatch helpers
+# ---------------------------------------------------------------------------
+
+
+def _is_torch(x):
+    return torch.is_tensor(x)
+
+
+def _on_gpu(x):
+    return torch.is_tensor(x) and x.is_cuda
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _require_gpu(t, name):
+    if not _on_gpu(t):
+        raise TypeError(f"{name} must be a GPU tensor when the primary input "
+                        "is on the GPU")
+
+
+def _check_contiguous(t, name):
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _check_dtype(t, name, allowed):
+    if not t.is_cuda:
+        raise TypeError(f"{name} must be a GPU tensor (got a CPU tensor on "
+                        "the zero-copy path)")
+    if t.dtype not in allowed:
+        names = ", ".join(str(d).replace("torch.", "") for d in allowed)
+        raise TypeError(f"{name} must be one of ({names}), got {t.dtype}")
+    _check_contiguous(t, name)
+
+
+_FLOAT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _launcher(base, dtype):
+    if dtype is torch.bfloat16:
+        return getattr(_fusedtok, base + "_bf16")
+    if dtype is torch.float16:
+        return getattr(_fusedtok, base + "_fp16")
+    return getattr(_fusedtok, base)
+
+
+def _need_device():
+    if not _fusedtok.cuda_available():
+        raise RuntimeError(
+            "fusedtok_amd runs on the GPU only: no HIP device is available "
+            "for these host inputs (there is no CPU fallback)")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _host_f32(x, name):
+    """Host-origin input -> float32 C-contiguous numpy array."""
+    if _is_torch(x):
+        if x.is_cuda:
+            raise TypeError(f"{name} is a GPU tensor while another input is "
+                            "host-side; move all inputs to the same device")
+        x = x.detach()
+        if x.dtype is not torch.float32:
+            x = x.to(torch.float32)
+        return np.ascontiguousarray(x.numpy())
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+
+
+def _upload(arr, device):
+    return torch.from_numpy(np.ascontiguousarray(arr)).to(device)
+
+
+def _result(res_t, like):
+    """Staged result back to the caller's family (torch CPU or numpy)."""
+    out = res_t.cpu()
+    return out if _is_torch(like) else out.numpy()
+
+
+def _host_int_array(t, name):
+    """Host-origin integer values as numpy, or None for a GPU tensor."""
+    if _is_torch(t):
+        if t.is_cuda:
+            return None
+        host = t.detach().cpu().numpy()
+    else:
+        host = np.asarray(t)
+    if host.size and not np.issubdtype(host.dtype, np.integer):
+        raise TypeError(f"{name} must hold integer values (got dtype {host.dtype})")
+    return host
+
+
+def _host_lens_checked(lens, batch, limit, upper_inclusive=True):
+    host = _host_int_array(lens, "lens")
+    if host is None:
+        return None
+    host = np.ascontiguousarray(host, dtype=np.int32)
+    if host.ndim != 1 or host.shape[0] != batch:
+        raise ValueError("lens must be 1-D with batch entries")
+    bracket = "]" if upper_inclusive else ")"
+    if host.size and (host.min() < 0 or host.max() > limit
+                      or (not upper_inclusive and host.max() == limit)):
+        raise ValueError(f"lens entries must be in [0, {limit}{bracket}")
+    return host
+
+
+def _lens_tensor(lens, batch, limit, device, upper_inclusive=True):
+    host = _host_lens_checked(lens, batch, limit, upper_inclusive)
+    if host is not None:
+        return torch.from_numpy(host).to(device)
+    lt = lens
+    if lt.dtype is not torch.int32:
+        lt = lt.to(torch.int32)
+    if not lt.is_contiguous():
+        lt = lt.contiguous()
+    if lt.ndim != 1 or lt.numel() != batch:
+        raise ValueError("lens must be 1-D with batch entries")
+    return lt
+
+
+def _host_table_checked(table, batch, nblocks):
+    host = _host_int_array(table, "block_table")
+    if host is None:
+        return None
+    host = np.ascontiguousarray(host, dtype=np.int32)
+    if host.ndim != 2 or host.shape[0] != batch:
+        raise ValueError("block_table must be [B, S] with batch rows")
+    if host.size and (host.min() < 0 or host.max() >= nblocks):
+        raise ValueError(f"block_table entries must be in [0, {nblocks})")
+    return host
+
+
+def _table_tensor(table, batch, nblocks, device):
+    host = _host_table_checked(table, batch, nblocks)
+    if host is not None:
+        return torch.from_numpy(host).to(device)
+    bt = table
+    if bt.dtype is not torch.int32:
+        bt = bt.to(torch.int32)
+    if not bt.is_contiguous():
+        bt = bt.contiguous()
+    if bt.ndim != 2 or bt.shape[0] != batch:
+        raise ValueError("block_table must be [B, S] with batch rows")
+    return bt
+
+
+def _rows_cols(shape):
+    if len(shape) == 1:
+        return 1, shape[0]
+    if len(shape) == 2:
+        return shape[0], shape[1]
+    raise ValueError("expected a 1-D or 2-D tensor")
+
+
+# ---------------------------------------------------------------------------
+# swiglu (reference __init__.py:498-539)
+# ---------------------------------------------------------------------------
+
+
+def swiglu(gate, up, *, cuda=False):
+    """SwiGLU activation: ``silu(gate) * up`` = ``gate / (1 + exp(-gate)) * up``."""
+    if _on_gpu(gate):
+        _require_gpu(up, "up")
+        _check_dtype(gate, "gate", _FLOAT_DTYPES)
+        _check_dtype(up, "up", _FLOAT_DTYPES)
+        if gate.dtype is not up.dtype:
+            raise TypeError("inputs must have the same dtype")
+        if gate.shape != up.shape:
+            raise ValueError("inputs must have the same shape")
+        out = torch.empty_like(gate)
+        _launcher("swiglu_launch", gate.dtype)(
+            gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(),
+            _stream())
+        return out
+    g = _host_f32(gate, "gate")
+    u = _host_f32(up, "up")
+    if g.shape != u.shape:
+        raise ValueError("inputs must have the same shape")
+    dev = _need_device()
+    res = swiglu(_upload(g, dev), _upload(u, dev))
+    return _result(res, gate)
+
+
+# ---------------------------------------------------------------------------
+# rmsnorm (reference __init__.py:547-590)
+# ---------------------------------------------------------------------------
+
+
+def rmsnorm(x, weight, *, residual=None, eps=1e-6, cuda=False):
+    """RMSNorm, optionally fused with a residual add:
+
+    ``y = (x + r) * rsqrt(mean((x + r)^2) + eps) * weight``
+
+    x: [rows, cols] or [cols]; weight: [cols] (float32; bf16/fp16 weights
+    are upcast); residual: same shape and dtype as x.
+    """
+    if _on_gpu(x):
+        _check_dtype(x, "x", _FLOAT_DTYPES)
+        _require_gpu(weight, "weight")
+        if weight.dtype is not torch.float32:
+            weight = weight.to(torch.float32)
+        if not weight.is_contiguous():
+            weight = weight.contiguous()
+        rows, cols = _rows_cols(x.shape)
+        if weight.ndim != 1 or weight.numel() != cols:
+            raise ValueError("weight must be 1-D with cols entries")
+        r_ptr = None
+        if residual is not None:
+            _require_gpu(residual, "residual")
+            _check_dtype(residual, "residual", _FLOAT_DTYPES)
+            if residual.dtype is not x.dtype:
+                raise TypeError("residual must have the same dtype as x")
+            if residual.shape != x.shape:
+                raise ValueError("residual must have the same shape as x")
+            r_ptr = residual.data_ptr()
+        out = torch.empty_like(x)
+        _launcher("rmsnorm_launch", x.dtype)(
+            x.data_ptr(), weight.data_ptr(), r_ptr, out.data_ptr(), rows, cols,
+            float(eps), _stream())
+        return out
+    arr_x = _host_f32(x, "x")
+    arr_w = _host_f32(weight, "weight")
+    rows, cols = _rows_cols(arr_x.shape)
+    if arr_w.ndim != 1 or arr_w.shape[0] != cols:
+        raise ValueError("weight.size() must equal cols")
+    arr_r = None
+    if residual is not None:
+        arr_r = _host_f32(residual, "residual")
+        if arr_r.shape != arr_x.shape:
+            raise ValueError("x.size() must equal rows * cols (residual shape)")
+    if cols == 0:
+        raise ValueError("rows must be >= 0 and cols must be > 0")
+    dev = _need_device()
+    res = rmsnorm(_upload(arr_x, dev), _upload(arr_w, dev),
+                  residual=None if arr_r is None else _upload(arr_r, dev),
+                  eps=eps)
+    return _result(res, x)
+
+
+# ---------------------------------------------------------------------------
+# rope (reference __init__.py:645-702)
+# ---------------------------------------------------------------------------
+
+
+def rope(q, k=None, *, theta=10000.0, pos_offset=0, neox=False, cuda=False,
+         positions=None, rows_per_position=1):
+    """Rotary position embedding on (q, k).
+
+    q, k: [seq, dim] with even dim. ``neox=False`` rotates interleaved pairs
+    (2j, 2j+1); ``neox=True`` rotates the row halves (j, j + dim/2). Row r
+    sits at position ``r + pos_offset``; pair j turns by
+    ``position * theta^(-2j/dim)``. Returns ``(q_rot, k_rot)`` (None if k is).
+
+    Build addition: ``positions`` (a GPU int32 vector) with
+    ``rows_per_position`` places row r at ``positions[r // rows_per_position]
+    + pos_offset`` - e.g. q viewed as [B*Hq, D] with ``rows_per_position=Hq``
+    and per-sequence positions.
+    """
+    if _on_gpu(q):
+        _check_dtype(q, "q", _FLOAT_DTYPES)
+        if q.ndim != 2:
+            raise ValueError("q must be 2-D [seq, dim]")
+        seq, dim = q.shape
+        if dim % 2:
+            raise ValueError("dim must be even (RoPE pairs elements)")
+        if pos_offset < 0:
+            raise ValueError("pos_offset must be >= 0")
+        k_out = None
+        if k is not None:
+            _require_gpu(k, "k")
+            _check_dtype(k, "k", _FLOAT_DTYPES)
+            if k.dtype is not q.dtype:
+                raise TypeError("k must have the same dtype as q")
+            if k.shape != q.shape:
+                raise ValueError("k must have the same shape as q")
+        pos_ptr = None
+        if positions is not None:
+            _require_gpu(positions, "positions")
+            if positions.dtype is not torch.int32:
+                raise TypeError("positions must be int32")
+            _check_contiguous(positions, "positions")
+            if rows_per_position < 1:
+                raise ValueError("rows_per_position must be >= 1")
+            if positions.numel() * rows_per_position < seq:
+                raise ValueError("positions must cover every row")
+            pos_ptr = positions.data_ptr()
+        q_out = torch.empty_like(q)
+        if k is not None:
+            k_out = torch.empty_like(k)
+        code = _DT_CODE[q.dtype]
+        for src, dst in ((q, q_out), (k, k_out)):
+            if src is None:
+                continue
+            if pos_ptr is None and rows_per_position == 1:
+                if q.dtype is torch.float32:
+                    _fusedtok.rope_launch(bool(neox), src.data_ptr(), dst.data_ptr(),
+                                          seq, dim, float(theta), int(pos_offset),
+                                          _stream())
+                else:
+                    base = "rope_neox_launch" if neox else "rope_launch"
+                    _launcher(base, q.dtype)(src.data_ptr(), dst.data_ptr(), seq,
+                                             dim, float(theta), int(pos_offset),
+                                             _stream())
+            else:
+                _fusedtok.rope_launch_ex(src.data_ptr(), dst.data_ptr(), code, seq,
+                                         dim, float(theta), int(pos_offset),
+                                         pos_ptr, int(rows_per_position),
+                                         bool(neox), _stream())
+        return q_out, k_out
+    arr_q = _host_f32(q, "q")
+    arr_k = None if k is None else _host_f32(k, "k")
+    if arr_q.ndim != 2:
+        raise ValueError("q must be 2-D [seq, dim]")
+    if arr_q.shape[1] % 2:
+        raise ValueError("dim must be even (RoPE pairs elements)")
+    if pos_offset < 0:
+        raise ValueError("pos_offset must be >= 0")
+    if arr_k is not None and arr_k.shape != arr_q.shape:
+        raise ValueError("k.size() must equal q.size()")
+    dev = _need_device()
+    qr, kr = rope(_upload(arr_q, dev),
+                  None if arr_k is None else _upload(arr_k, dev),
+                  theta=theta, pos_offset=pos_offset, neox=neox)
+    return _result(qr, q), (None if kr is None else _result(kr, q))
+
+
+# ---------------------------------------------------------------------------
+# attention (reference __init__.py:710-788, 849-940)
+# ---------------------------------------------------------------------------
+
+
+def attention_decode(q, k_cache, v_cache, lens=None, *, cuda=False):
+    """Single-token causal attention with GQA over a contiguous KV cache:
+
+    ``out[b, h] = softmax(q[b,h] . K[b,kv(h)]^T / sqrt(D)) . V[b,kv(h)]``
+
+    q: [B, Hq, D]; k_cache / v_cache: [B, Hkv, T, D]; lens: [B] valid lengths
+    (<= T; None = all rows). q head h reads kv head ``h // (Hq // Hkv)``.
+    Length-0 sequences give zero rows. Storage f32 / bf16 / fp16; softmax and
+    accumulators are float32; the output matches the input dtype.
+    """
+    if _on_gpu(q):
+        for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+            _check_dtype(t, name, _FLOAT_DTYPES)
+        for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+            if t.dtype is not q.dtype:
+                raise TypeError(f"{name} must have the same dtype as q")
+        if q.ndim != 3 or k_cache.ndim != 4 or v_cache.ndim != 4:
+            raise ValueError("q must be [B, Hq, D]; k/v caches [B, Hkv, T, D]")
+        b, hq, d = q.shape
+        b2, hkv, t_rows, d2 = k_cache.shape
+        if (b2, d2) != (b, d) or v_cache.shape != k_cache.shape:
+            raise ValueError("k_cache/v_cache must match q's batch and dim")
+        if hq < 1 or hkv < 1:
+            raise ValueError("head counts must be >= 1")
+        if hq % hkv:
+            raise ValueError("q heads must be a multiple of kv heads")
+        lens_ptr = None
+        if lens is not None:
+            lens_ptr = _lens_tensor(lens, b, t_rows, q.device)
+        out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
+        if b * hq > 0:
+            _launcher("attention_decode_launch", q.dtype)(
+                q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                None if lens_ptr is None else lens_ptr.data_ptr(), out.data_ptr(),
+                b, hq, hkv, t_rows, d, _stream())
+        return out
+    arr_q = _host_f32(q, "q")
+    arr_k = _host_f32(k_cache, "k_cache")
+    arr_v = _host_f32(v_cache, "v_cache")
+    if arr_q.ndim != 3 or arr_k.ndim != 4 or arr_v.ndim != 4:
+        raise ValueError("q must be [B, Hq, D]; k/v caches [B, Hkv, T, D]")
+    b, hq, d = arr_q.shape
+    b2, hkv, t_rows, d2 = arr_k.shape
+    if (b2, d2) != (b, d) or arr_v.shape != arr_k.shape:
+        raise ValueError("k_cache/v_cache must match q's batch and dim")
+    if hkv < 1 or hq < 1:
+        raise ValueError("head counts must be >= 1")
+    if hq % hkv:
+        raise ValueError("q heads must be a multiple of kv heads")
+    if d % 4 or d > 512:
+        raise ValueError("dim must be a multiple of 4 and at most 512")
+    arr_l = None
+    if lens is not None:
+        arr_l = _host_lens_checked(lens, b, t_rows)
+        if arr_l is None:
+            raise TypeError("lens must be a host array on this path")
+    dev = _need_device()
+    res = attention_decode(_upload(arr_q, dev), _upload(arr_k, dev),
+                           _upload(arr_v, dev),
+                           None if arr_l is None else _upload(arr_l, dev))
+    return _result(res, q)
+
+
+def attention_decode_paged(q, k_pool, v_pool, block_table, lens=None, *,
+                           cuda=False):
+    """Single-token GQA attention over a PAGED KV cache.
+
+    k_pool / v_pool: [Nb, Hkv, P, D]; block_table: [B, S] int; token t of
+    sequence b is ``pool[block_table[b, t // P], kv, t % P]``; lens: [B]
+    (None = S * P rows each). GQA group sizes 1/2/4/8/16. Host-origin table
+    and lens values are validated; GPU-resident ones are trusted.
+    """
+    if _on_gpu(q):
+        for name, t in (("q", q), ("k_pool", k_pool), ("v_pool", v_pool)):
+            _check_dtype(t, name, _FLOAT_DTYPES)
+        for name, t in (("k_pool", k_pool), ("v_pool", v_pool)):
+            if t.dtype is not q.dtype:
+                raise TypeError(f"{name} must have the same dtype as q")
+        if q.ndim != 3 or k_pool.ndim != 4 or v_pool.ndim != 4:
+            raise ValueError("q must be [B, Hq, D]; pools [Nb, Hkv, P, D]")
+        b, hq, d = q.shape
+        nb, hkv, page, d2 = k_pool.shape
+        if d2 != d or v_pool.shape != k_pool.shape:
+            raise ValueError("pools must match q's dim and each other")
+        if hq < 1 or hkv < 1:
+            raise ValueError("head counts must be >= 1")
+        if hq % hkv:
+            raise ValueError("q heads must be a multiple of kv heads")
+        if hq // hkv not in (1, 2, 4, 8, 16):
+            raise ValueError("paged decode supports GQA group sizes "
+                             "1/2/4/8/16 (use attention_decode otherwise)")
+        bt = _table_tensor(block_table, b, nb, q.device)
+        s_width = bt.shape[1]
+        lt = None
+        if lens is not None:
+            lt = _lens_tensor(lens, b, s_width * page, q.device)
+        out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
+        if b * hq > 0:
+            _launcher("attention_decode_paged_launch", q.dtype)(
+                q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), bt.data_ptr(),
+                None if lt is None else lt.data_ptr(), out.data_ptr(),
+                b, hq, hkv, page, s_width, d, _stream())
+        return out
+    arr_q = _host_f32(q, "q")
+    arr_k = _host_f32(k_pool, "k_pool")
+    arr_v = _host_f32(v_pool, "v_pool")
+    if arr_q.ndim != 3 or arr_k.ndim != 4 or arr_v.ndim != 4:
+        raise ValueError("q must be [B, Hq, D]; pools [Nb, Hkv, P, D]; "
+                         "block_table [B, S]")
+    b, hq, d = arr_q.shape
+    nb, hkv, page, d2 = arr_k.shape
+    arr_t = _host_table_checked(block_table, b, nb)
+    if arr_t is None:
+        raise TypeError("block_table must be a host array on this path")
+    if d2 != d or arr_v.shape != arr_k.shape:
+        raise ValueError("pools must match q's dim and each other")
+    if hkv < 1 or hq < 1:
+        raise ValueError("head counts must be >= 1")
+    if hq % hkv:
+        raise ValueError("q heads must be a multiple of kv heads")
+    if hq // hkv not in (1, 2, 4, 8, 16):
+        raise ValueError("paged decode supports GQA group sizes "
+                         "1/2/4/8/16 (use attention_decode otherwise)")
+    if d % 4 or d > 512:
+        raise ValueError("dim must be a multiple of 4 and at most 512")
+    arr_l = None
+    if lens is not None:
+        arr_l = _host_lens_checked(lens, b, arr_t.shape[1] * page)
+        if arr_l is None:
+            raise TypeError("lens must be a host array on this path")
+    dev = _need_device()
+    res = attention_decode_paged(
+        _upload(arr_q, dev), _upload(arr_k, dev), _upload(arr_v, dev),
+        _upload(arr_t, dev), None if arr_l is None else _upload(arr_l, dev))
+    return _result(res, q)
+
+
+# ---------------------------------------------------------------------------
+# kv append (reference __init__.py:943-1112)
+# ---------------------------------------------------------------------------
+
+
+def _host_inplace_f32(arr, name):
+    raw = arr.numpy() if _is_torch(arr) else arr
+    if not isinstance(raw, np.ndarray) or raw.dtype != np.float32 \
+            or not raw.flags["C_CONTIGUOUS"]:
+        raise TypeError(f"{name} must be a float32 C-contiguous array "
+                        "(in-place op; conversion would drop writes)")
+    return raw
+
+
+def kv_append_paged(k_pool, v_pool, block_table, k_new, v_new, lens, *,
+                    cuda=False):
+    """Write one fresh token's K/V rows per sequence into the paged pools,
+    in place: ``k_new[b]`` lands at block ``block_table[b, lens[b] // P]``,
+    offset ``lens[b] % P``. lens is required (values in [0, S*P)). Returns
+    None."""
+    if _on_gpu(k_pool):
+        for name, t in (("k_pool", k_pool), ("v_pool", v_pool),
+                        ("k_new", k_new), ("v_new", v_new)):
+            _check_dtype(t, name, _FLOAT_DTYPES)
+        for name, t in (("v_pool", v_pool), ("k_new", k_new), ("v_new", v_new)):
+            if t.dtype is not k_pool.dtype:
+                raise TypeError(f"{name} must have the pool dtype")
+        if k_pool.ndim != 4 or v_pool.ndim != 4:
+            raise ValueError("pools must be [Nb, Hkv, P, D]")
+        if k_new.ndim != 3 or v_new.ndim != 3:
+            raise ValueError("k_new/v_new must be [B, Hkv, D]")
+        nb, hkv, page, d = k_pool.shape
+        b, hkv2, d2 = k_new.shape
+        if (hkv2, d2) != (hkv, d) or v_pool.shape != k_pool.shape \
+                or v_new.shape != k_new.shape:
+            raise ValueError("k/v operands must match the pool layout")
+        if b == 0:
+            return None
+        bt = _table_tensor(block_table, b, nb, k_pool.device)
+        lt = _lens_tensor(lens, b, bt.shape[1] * page, k_pool.device,
+                          upper_inclusive=False)
+        _launcher("kv_append_paged_launch", k_pool.dtype)(
+            k_new.data_ptr(), v_new.data_ptr(), bt.data_ptr(), lt.data_ptr(),
+            k_pool.data_ptr(), v_pool.data_ptr(), b, hkv, d, page, bt.shape[1],
+            _stream())
+        return None
+    kp = _host_inplace_f32(k_pool, "k_pool")
+    vp = _host_inplace_f32(v_pool, "v_pool")
+    kn = _host_f32(k_new, "k_new")
+    vn = _host_f32(v_new, "v_new")
+    if kp.ndim != 4 or kn.ndim != 3:
+        raise ValueError("pools [Nb,Hkv,P,D]; k_new [B,Hkv,D]")
+    nb, hkv, page, d = kp.shape
+    b = kn.shape[0]
+    if kn.shape != (b, hkv, d) or vp.shape != kp.shape or vn.shape != kn.shape:
+        raise ValueError("k/v operands must match the pool layout")
+    arr_t = _host_table_checked(block_table, b, nb)
+    if arr_t is None:
+        raise TypeError("block_table must be a host array on this path")
+    arr_l = _host_lens_checked(lens, b, arr_t.shape[1] * page,
+                               upper_inclusive=False)
+    if arr_l is None:
+        raise TypeError("lens must be a host array on this path")
+    if d % 4:
+        raise ValueError("dim must be a multiple of 4")
+    if b == 0:
+        return None
+    dev = _need_device()
+    kp_d, vp_d = _upload(kp, dev), _upload(vp, dev)
+    kv_append_paged(kp_d, vp_d, _upload(arr_t, dev), _upload(kn, dev),
+                    _upload(vn, dev), _upload(arr_l, dev))
+    np.copyto(kp, kp_d.cpu().numpy())
+    np.copyto(vp, vp_d.cpu().numpy())
+    return None
+
+
+def kv_append(k_cache, v_cache, k_new, v_new, lens, *, cuda=False):
+    """Write one fresh token's K/V rows per sequence into the contiguous
+    caches [B, Hkv, T, D] at row ``lens[b]`` (in place; lens in [0, T)).
+    Returns None."""
+    if _on_gpu(k_cache):
+        for name, t in (("k_cache", k_cache), ("v_cache", v_cache),
+                        ("k_new", k_new), ("v_new", v_new)):
+            _check_dtype(t, name, _FLOAT_DTYPES)
+        for name, t in (("v_cache", v_cache), ("k_new", k_new),
+                        ("v_new", v_new)):
+            if t.dtype is not k_cache.dtype:
+                raise TypeError(f"{name} must have the cache dtype")
+        if k_cache.ndim != 4 or v_cache.ndim != 4:
+            raise ValueError("caches must be [B, Hkv, T, D]")
+        if k_new.ndim != 3 or v_new.ndim != 3:
+            raise ValueError("k_new/v_new must be [B, Hkv, D]")
+        b, hkv, t_rows, d = k_cache.shape
+        if tuple(k_new.shape) != (b, hkv, d) or v_cache.shape != k_cache.shape \
+                or v_new.shape != k_new.shape:
+            raise ValueError("k/v operands must match the cache layout")
+        if b == 0:
+            return None
+        lt = _lens_tensor(lens, b, t_rows, k_cache.device, upper_inclusive=False)
+        _launcher("kv_append_launch", k_cache.dtype)(
+            k_new.data_ptr(), v_new.data_ptr(), lt.data_ptr(), k_cache.data_ptr(),
+            v_cache.data_ptr(), b, hkv, d, t_rows, _stream())
+        return None
+    kc = _host_inplace_f32(k_cache, "k_cache")
+    vc = _host_inplace_f32(v_cache, "v_cache")
+    kn = _host_f32(k_new, "k_new")
+    vn = _host_f32(v_new, "v_new")
+    if kc.ndim != 4 or kn.ndim != 3:
+        raise ValueError("caches [B,Hkv,T,D]; k_new [B,Hkv,D]")
+    b, hkv, t_rows, d = kc.shape
+    if kn.shape != (b, hkv, d) or vc.shape != kc.shape or vn.shape != kn.shape:
+        raise ValueError("k/v operands must match the cache layout")
+    arr_l = _host_lens_checked(lens, b, t_rows, upper_inclusive=False)
+    if arr_l is None:
+        raise TypeError("lens must be a host array on this path")
+    if d % 4:
+        raise ValueError("dim must be a multiple of 4")
+    if b == 0:
+        return None
+    dev = _need_device()
+    kc_d, vc_d = _upload(kc, dev), _upload(vc, dev)
+    kv_append(kc_d, vc_d, _upload(kn, dev), _upload(vn, dev), _upload(arr_l, dev))
+    np.copyto(kc, kc_d.cpu().numpy())
+    np.copyto(vc, vc_d.cpu().numpy())
+    return None
+
+
+# ---------------------------------------------------------------------------
+# INT8 (reference __init__.py:1402-1425, 1476-1599)
+# ---------------------------------------------------------------------------
+
+
+def quantize_int8(x, *, device_scale=False):
+    """Symmetric per-tensor INT8 quantization.
+
+    ``scale = max(|x|) / 127`` (1.0 for all-zero input);
+    ``q = clamp(rint(x * (1 / scale)), -127, 127)``. Returns ``(q, scale)``
+    with scale a Python float. Build additions: bf16 / fp16 GPU input, and
+    ``device_scale=True`` returns the scale as a 1-element GPU float32 tensor
+    without synchronising the stream.
+    """
+    if _on_gpu(x):
+        _check_dtype(x, "x", _FLOAT_DTYPES)
+        q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+        scale = torch.empty(1, dtype=torch.float32, device=x.device)
+        if x.dtype is torch.float32:
+            _fusedtok.quantize_launch(x.data_ptr(), q.data_ptr(), scale.data_ptr(),
+                                      x.numel(), _stream())
+        else:
+            _fusedtok.quantize_launch_ex(x.data_ptr(), _DT_CODE[x.dtype],
+                                         q.data_ptr(), scale.data_ptr(),
+                                         x.numel(), _stream())
+        if device_scale:
+            return q, scale
+        return q, float(scale)
+    arr = _host_f32(x, "x")
+    dev = _need_device()
+    q, s = quantize_int8(_upload(arr, dev))
+    return (q.cpu() if _is_torch(x) else q.cpu().numpy()), s
+
+
+def _qgemm_gpu_operands(a_q, b_q):
+    if not _on_gpu(b_q):
+        raise TypeError("both operands must be GPU int8 tensors")
+    if a_q.dtype is not torch.int8 or b_q.dtype is not torch.int8:
+        raise TypeError("operands must be int8")
+    _check_contiguous(a_q, "a_q")
+    _check_contiguous(b_q, "b_q")
+    if a_q.ndim != 2 or b_q.ndim != 2:
+        raise ValueError("operands must be 2-D [rows, K]")
+    m, k = a_q.shape
+    n, k2 = b_q.shape
+    if k != k2:
+        raise ValueError("inner dimensions must match")
+    return m, n, k
+
+
+def _int8_host(arr, name):
+    if _is_torch(arr):
+        if arr.is_cuda:
+            raise TypeError(f"{name} must be a host tensor on this path")
+        arr = arr.detach().numpy()
+    a = np.asarray(arr)
+    if a.size and not np.issubdtype(a.dtype, np.integer):
+        raise TypeError(f"{name} must be an integer array, got {a.dtype}")
+    return np.ascontiguousarray(a, dtype=np.int8)
+
+
+_OUT_CODES = {torch.float32: _DT_F32, torch.bfloat16: _DT_BF16,
+              torch.float16: _DT_F16}
+
+
+def _scale_arg(a_scale, device):
+    """Host float -> (float, None); GPU tensor -> (0.0, device pointer)."""
+    if _on_gpu(a_scale):
+        t = a_scale
+        if t.dtype is not torch.float32 or t.numel() != 1:
+            raise TypeError("a device a_scale must be a 1-element float32 tensor")
+        return 0.0, t
+    return float(a_scale), None
+
+
+def qgemm(a_q, a_scale, b_q, b_scale, *, cuda=False, out_dtype=None):
+    """INT8 matmul, exact int32 accumulation:
+    ``y[M, N] = (A_q[M, K] @ B_q[N, K]^T) * f32(a_scale * b_scale)``.
+
+    Output float32 (build addition: ``out_dtype`` bf16 / fp16 on the GPU
+    path, the float32 value rounded to nearest-even; ``a_scale`` may be a
+    1-element GPU tensor, e.g. from ``quantize_int8(..., device_scale=True)``).
+    """
+    if _on_gpu(a_q):
+        m, n, k = _qgemm_gpu_operands(a_q, b_q)
+        odt = torch.float32 if out_dtype is None else out_dtype
+        if odt not in _OUT_CODES:
+            raise TypeError("out_dtype must be float32, bfloat16 or float16")
+        y = torch.empty((m, n), dtype=odt, device=a_q.device)
+        sa, sa_t = _scale_arg(a_scale, a_q.device)
+        if m > 0 and n > 0:
+            if odt is torch.float32 and sa_t is None:
+                _fusedtok.qgemm_launch(a_q.data_ptr(), b_q.data_ptr(), y.data_ptr(),
+                                       m, n, k, sa, float(b_scale), _stream())
+            else:
+                _fusedtok.qgemm_launch_ex(
+                    a_q.data_ptr(), b_q.data_ptr(), None, float(b_scale), sa,
+                    None if sa_t is None else sa_t.data_ptr(), y.data_ptr(),
+                    _OUT_CODES[odt], m, n, k, _stream())
+        return y
+    a = _int8_host(a_q, "a_q")
+    b = _int8_host(b_q, "b_q")
+    if a.ndim != 2 or b.ndim != 2:
+        raise ValueError("operands must be 2-D [rows, K]")
+    if a.shape[1] != b.shape[1]:
+        raise ValueError("inner dimensions must match")
+    dev = _need_device()
+    y = qgemm(_upload(a, dev), float(a_scale), _upload(b, dev), float(b_scale))
+    return _result(y, a_q)
+
+
+def qgemm_perchannel(a_q, a_scale, b_q, b_scales, *, cuda=False, out_dtype=None):
+    """INT8 matmul with per-output-channel weight scales (W8A8):
+    ``y[M, N] = (A_q @ B_q^T) * f32(a_scale * b_scales[j])``; bit-identical to
+    the reference CPU path in float32. Build additions as in :func:`qgemm`.
+    """
+    if _on_gpu(a_q):
+        m, n, k = _qgemm_gpu_operands(a_q, b_q)
+        if not _is_torch(b_scales):
+            b_scales = torch.as_tensor(np.asarray(b_scales, dtype=np.float32),
+                                       device=a_q.device)
+        if b_scales.ndim != 1 or b_scales.numel() != n:
+            raise ValueError("b_scales must be 1-D with n entries")
+        if b_scales.dtype is not torch.float32:
+            b_scales = b_scales.to(torch.float32)
+        if not b_scales.is_contiguous():
+            b_scales = b_scales.contiguous()
+        if not b_scales.is_cuda:
+            b_scales = b_scales.to(a_q.device)
+        odt = torch.float32 if out_dtype is None else out_dtype
+        if odt not in _OUT_CODES:
+            raise TypeError("out_dtype must be float32, bfloat16 or float16")
+        y = torch.empty((m, n), dtype=odt, device=a_q.device)
+        sa, sa_t = _scale_arg(a_scale, a_q.device)
+        if m > 0 and n > 0:
+            if odt is torch.float32 and sa_t is None:
+                _fusedtok.qgemm_perchannel_launch(
+                    a_q.data_ptr(), b_q.data_ptr(), b_scales.data_ptr(),
+                    y.data_ptr(), m, n, k, sa, _stream())
+            else:
+                _fusedtok.qgemm_launch_ex(
+                    a_q.data_ptr(), b_q.data_ptr(), b_scales.data_ptr(), 0.0, sa,
+                    None if sa_t is None else sa_t.data_ptr(), y.data_ptr(),
+                    _OUT_CODES[odt], m, n, k, _stream())
+        return y
+    a = _int8_host(a_q, "a_q")
+    b = _int8_host(b_q, "b_q")
+    sb = np.ascontiguousarray(np.asarray(b_scales, dtype=np.float32))
+    if a.ndim != 2 or b.ndim != 2:
+        raise ValueError("operands must be 2-D [rows, K]")
+    if a.shape[1] != b.shape[1]:
+        raise ValueError("inner dimensions must match")
+    if sb.ndim != 1 or sb.shape[0] != b.shape[0]:
+        raise ValueError("b_scales must be 1-D with n entries")
+    dev = _need_device()
+    y = qgemm_perchannel(_upload(a, dev), float(a_scale), _upload(b, dev),
+                         _upload(sb, dev))
+    return _result(y, a_q)
+
+
+def qgemm_i32(a_q, b_q):
+    """Build addition (test hook): the exact int32 accumulators
+    ``A_q @ B_q^T`` through the same kernels as the float paths."""
+    if _on_gpu(a_q):
+        m, n, k = _qgemm_gpu_operands(a_q, b_q)
+        acc = torch.empty((m, n), dtype=torch.int32, device=a_q.device)
+        if m > 0 and n > 0:
+            _fusedtok.qgemm_i32_launch(a_q.data_ptr(), b_q.data_ptr(),
+                                       acc.data_ptr(), m, n, k, _stream())
+        return acc
+    a = _int8_host(a_q, "a_q")
+    b = _int8_host(b_q, "b_q")
+    if a.ndim != 2 or b.ndim != 2 or a.shape[1] != b.shape[1]:
+        raise ValueError("operands must be 2-D [rows, K] with matching K")
+    dev = _need_device()
+    return _result(qgemm_i32(_upload(a, dev), _upload(b, dev)), a_q)

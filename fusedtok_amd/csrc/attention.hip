@@ -1,0 +1,809 @@
+// Flash-decoding attention (contiguous and paged KV) and KV append for
+// gfx950.
+//
+//   out[b,h] = softmax(q[b,h] . K[b,h/G]^T / sqrt(D)) . V[b,h/G]
+//
+// Work decomposition (both cache layouts): a work unit is one
+// (sequence b, kv head, token chunk of `chunk` rows). The grid is
+// (Hkv * cmax, B) with cmax = ceil(span / chunk), span being the cache
+// capacity (T, or table width * page). A unit whose chunk starts at or past
+// lens[b] exits at once, so the work follows the REAL lengths rather than
+// the capacity (the reference slices the capacity: attention.cu:1816-1821).
+// Every live unit writes, for each of the G q heads of its kv group, the
+// float32 partial (m = max score, l = sum exp(s - m), acc[D] = sum
+// exp(s - m) v) into a library-owned workspace; a combine kernel folds a
+// row's partials with the log-sum-exp rule and divides by l. len == 0 rows
+// produce zeros (reference attention.cu:1349-1350).
+//
+// Two stage-1 kernels:
+//   attn_chunk_mfma    bf16/fp16 storage, D == 128, G <= 16: QK^T and PV on
+//                      the matrix cores (v_mfma_f32_16x16x32_{bf16,f16});
+//                      every K/V byte is read once, straight into the MFMA
+//                      operand layout with 16-byte loads.
+//   attn_chunk_generic any storage type, D % 4 == 0 <= 512, any G: VALU
+//                      dot products, chunk scores staged in LDS.
+#include "ft_common.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+#include <type_traits>
+
+namespace ft {
+namespace {
+
+constexpr int kMaxDim = 512;
+constexpr int kGenNT = 256;      // generic stage-1 workgroup
+constexpr int kGenHeads = 8;     // q heads per generic pass
+constexpr int kGenMaxChunk = 512;
+
+// reference attention.cu:184-193
+void attention_check(int batch, int hq, int hkv, long long t_seq, int dim) {
+    if (batch < 0 || hq < 1 || hkv < 1 || t_seq < 0 || dim < 1)
+        inval("attention shapes must satisfy batch>=0, heads>=1, rows>=0, dim>=1");
+    if (hq % hkv != 0)
+        inval("q heads must be a multiple of kv heads (contiguous GQA groups)");
+    if (dim % 4 != 0 || dim > kMaxDim)
+        inval("dim must be a multiple of 4 and at most 512");
+}
+
+inline int pow2_ceil(int x) {
+    int p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+
+__device__ __forceinline__ int pow2_ceil_dev(int x) {
+    int p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Chunk length: a power of two in [lo, hi] so that the capacity grid holds
+// about `target` units.
+int choose_chunk(int batch, int hkv, long long span, int lo, int hi,
+                 long long target) {
+    long long rows = (long long)batch * hkv * span;
+    int c = lo;
+    while (c < hi && rows / c > target) c <<= 1;
+    return c;
+}
+
+struct RowMap {
+    // contiguous: element offset (((b*hkv + kv) * t_rows) + t) * dim
+    // paged:      element offset ((table[b*S + t/P] * hkv + kv) * P + t%P) * dim
+    const int* table;
+    int hkv, dim, rows_or_page, tbl_width, page_shift;  // page_shift >= 0 if P is 2^k
+    __device__ __forceinline__ size_t operator()(int b, int kv, int t) const {
+        if (!table)
+            return (((size_t)b * hkv + kv) * rows_or_page + t) * dim;
+        int pg, off;
+        if (page_shift >= 0) {
+            pg = t >> page_shift;
+            off = t & (rows_or_page - 1);
+        } else {
+            pg = t / rows_or_page;
+            off = t - pg * rows_or_page;
+        }
+        const int blk = table[(size_t)b * tbl_width + pg];
+        return (((size_t)blk * hkv + kv) * rows_or_page + off) * dim;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// generic stage 1
+// ---------------------------------------------------------------------------
+template <typename T, int CPL>
+__global__ __launch_bounds__(kGenNT) void attn_chunk_generic(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int* __restrict__ lens, RowMap rm, float* __restrict__ ws_ml,
+    float* __restrict__ ws_acc, int hq, int group, int span, int chunk,
+    int cmax, float scale_log2) {
+    __shared__ float sc[kGenHeads][kGenMaxChunk];
+    __shared__ float ms[kGenHeads], ls[kGenHeads];
+    __shared__ float4 red[kGenNT];
+
+    const int per_b = rm.hkv * cmax;
+    const int b = blockIdx.x / per_b;
+    const int kv = (blockIdx.x - b * per_b) / cmax;
+    const int c = blockIdx.x - b * per_b - kv * cmax;
+    const int len = lens ? lens[b] : span;
+    const int t0 = c * chunk;
+    if (t0 >= len) return;
+    const int n = min(chunk, len - t0);
+    const int dim = rm.dim;
+    const int dc = dim >> 2;                     // 4-element chunks per row
+    const int lpt = min(64, pow2_ceil_dev(dc));  // lanes per token (phase 1)
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int sub = lane / lpt, li = lane % lpt;
+    const int tpw = 64 / lpt;
+
+    for (int g0 = 0; g0 < group; g0 += kGenHeads) {
+        const int gc = min(kGenHeads, group - g0);
+        // ---- phase 1: scores s[g][t] = scale * q_g . k_t ------------------
+        float4 qr[kGenHeads][CPL];
+#pragma unroll
+        for (int g = 0; g < kGenHeads; ++g)
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const int ch = li + i * lpt;
+                qr[g][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (g < gc && ch < dc)
+                    qr[g][i] = St<T>::ld4(
+                        q + ((size_t)b * hq + (size_t)kv * group + g0 + g) * dim +
+                        4 * ch);
+            }
+        for (int t = wave * tpw + sub; t < n; t += 4 * tpw) {
+            const T* kr = k + rm(b, kv, t0 + t);
+            float part[kGenHeads];
+#pragma unroll
+            for (int g = 0; g < kGenHeads; ++g) part[g] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const int ch = li + i * lpt;
+                if (ch < dc) {
+                    const float4 kk = St<T>::ld4(kr + 4 * ch);
+#pragma unroll
+                    for (int g = 0; g < kGenHeads; ++g)
+                        part[g] += qr[g][i].x * kk.x + qr[g][i].y * kk.y +
+                                   qr[g][i].z * kk.z + qr[g][i].w * kk.w;
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < kGenHeads; ++g)
+                for (int o = lpt >> 1; o > 0; o >>= 1)
+                    part[g] += __shfl_xor(part[g], o, 64);
+            if (li == 0) {
+#pragma unroll
+                for (int g = 0; g < kGenHeads; ++g)
+                    if (g < gc) sc[g][t] = part[g] * scale_log2;
+            }
+        }
+        __syncthreads();
+        // ---- phase 2: chunk softmax statistics -----------------------------
+        for (int g = wave; g < gc; g += kGenNT / 64) {
+            float m = -INFINITY;
+            for (int t = lane; t < n; t += 64) m = fmaxf(m, sc[g][t]);
+            m = wave_max(m);
+            float l = 0.0f;
+            for (int t = lane; t < n; t += 64) {
+                const float p = exp2f(sc[g][t] - m);
+                sc[g][t] = p;
+                l += p;
+            }
+            l = wave_sum(l);
+            if (lane == 0) {
+                ms[g] = m;
+                ls[g] = l;
+            }
+        }
+        __syncthreads();
+        // ---- phase 3: acc[g][d] = sum_t p[g][t] v[t][d] --------------------
+        const int dcp = pow2_ceil_dev(dc);
+        const int tg_n = kGenNT / dcp;
+        const int my_dc = tid % dcp, my_tg = tid / dcp;
+        float4 acc[kGenHeads];
+#pragma unroll
+        for (int g = 0; g < kGenHeads; ++g) acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (my_dc < dc) {
+            for (int t = my_tg; t < n; t += tg_n) {
+                const float4 vv = St<T>::ld4(v + rm(b, kv, t0 + t) + 4 * my_dc);
+#pragma unroll
+                for (int g = 0; g < kGenHeads; ++g) {
+                    if (g < gc) {
+                        const float p = sc[g][t];
+                        acc[g].x += p * vv.x;
+                        acc[g].y += p * vv.y;
+                        acc[g].z += p * vv.z;
+                        acc[g].w += p * vv.w;
+                    }
+                }
+            }
+        }
+        const size_t slot0 = (((size_t)b * rm.hkv + kv) * cmax + c) * group + g0;
+#pragma unroll
+        for (int g = 0; g < kGenHeads; ++g) {
+            if (g >= gc) break;
+            red[tid] = acc[g];
+            __syncthreads();
+            if (my_tg == 0 && my_dc < dc) {
+                float4 s = red[my_dc];
+                for (int j = 1; j < tg_n; ++j) {
+                    const float4 o = red[j * dcp + my_dc];
+                    s.x += o.x; s.y += o.y; s.z += o.z; s.w += o.w;
+                }
+                *reinterpret_cast<float4*>(ws_acc + (slot0 + g) * dim + 4 * my_dc) = s;
+            }
+            __syncthreads();
+        }
+        if (tid < gc) {
+            ws_ml[(slot0 + tid) * 2] = ms[tid];
+            ws_ml[(slot0 + tid) * 2 + 1] = ls[tid];
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA stage 1 (bf16 / fp16 storage, D == 128, G <= 16)
+//
+// Each of the 4 waves walks 32-token steps st = wave, wave+4, ... of the
+// unit's chunk with its own online-softmax state, then the waves merge in
+// LDS. With r = lane % 16 and g = lane / 16 (lane layout of
+// v_mfma_f32_16x16x32: A[r][8g+i], B[8g+i][r], C[4g+i][r]):
+//
+//  scores   S^T[tok][head] = K[tok][:] . Q[head][:]  (4 MFMAs per 16 tokens)
+//           A = K rows: lane loads K[tok r][32j+8g .. +7], one 16-byte load
+//           B = Q^T   : lane holds Q[head r][32j+8g .. +7] (preloaded)
+//           C         : lane gets S for tokens 4g+i (tile 0) and 16+4g+i
+//                       (tile 1) of head r, i.e. tau(g,i) for i = 0..7 with
+//                       tau(g,i) = i < 4 ? 4g+i : 16+4g+(i-4).
+//  softmax  per lane for head r over its 8 tokens; the step max is folded
+//           across the 4 lanes {r, r+16, r+32, r+48} (2 xor shuffles).
+//  V^T      C' = V_tile . Sel_e, Sel_e[k][c] = (k == c + 16e), gives lane
+//           (r,g) the values V[16h+4g+i][16n+r], n = 2j+e: the A operand of
+//           the PV product below, in the same tau order. Selecting with 1.0
+//           and adding zeros is exact, so the transpose is lossless.
+//  PV       O^T[dim][head] += V^T[dim][tau] . P^T[tau][head]
+//           A = V^T (above), B = P (the 8 probabilities the lane already
+//           holds), C: lane holds O[head r][16n+4g+i]: every accumulator of a
+//           lane belongs to head r, so the online rescale is per lane.
+//           bf16 P is split into hi + lo parts (two MFMAs) so the weights
+//           carry ~16 mantissa bits; fp16 P carries 11.
+// ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct Mfma;
+template <> struct Mfma<bf16> {
+    typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+    static constexpr bool kSplitP = true;
+    __device__ __forceinline__ static f32x4 mma(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct Mfma<f16> {
+    typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+    static constexpr bool kSplitP = false;
+    __device__ __forceinline__ static f32x4 mma(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+constexpr int kMfmaDim = 128;
+constexpr int kMfmaAccPitch = kMfmaDim + 4;   // LDS row pitch (bank spread)
+
+template <typename T>
+__global__ __launch_bounds__(256) void attn_chunk_mfma(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int* __restrict__ lens, RowMap rm, float* __restrict__ ws_ml,
+    float* __restrict__ ws_acc, int hq, int group, int span, int chunk,
+    int cmax, float scale_log2) {
+    using M = Mfma<T>;
+    using V8 = typename M::v8;
+    constexpr int D = kMfmaDim;
+    __shared__ float s_acc[4][16][kMfmaAccPitch];
+    __shared__ float s_m[4][16], s_l[4][16];
+
+    const int per_b = rm.hkv * cmax;
+    const int b = blockIdx.x / per_b;
+    const int kv = (blockIdx.x - b * per_b) / cmax;
+    const int c = blockIdx.x - b * per_b - kv * cmax;
+    const int len = lens ? lens[b] : span;
+    const int t0 = c * chunk;
+    if (t0 >= len) return;
+    const int n = min(chunk, len - t0);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+
+    // B operand of the score MFMAs: Q[head r][32j + 8g .. +7]
+    V8 qb[4];
+    {
+        const bool ok = r < group;
+        const T* qrow = q + ((size_t)b * hq + (size_t)kv * group + (ok ? r : 0)) * D;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            V8 z = {};
+            qb[j] = ok ? *reinterpret_cast<const V8*>(qrow + 32 * j + 8 * g) : z;
+        }
+    }
+    // selection operands of the transposing MFMAs
+    V8 sel0, sel1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        sel0[i] = (T)((8 * g + i == r) ? 1.0f : 0.0f);
+        sel1[i] = (T)((8 * g + i == r + 16) ? 1.0f : 0.0f);
+    }
+
+    f32x4 acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    const int nsteps = (n + 31) >> 5;
+    for (int st = wave; st < nsteps; st += 4) {
+        const int tb = st << 5;
+        V8 kt[2][4], vt[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int tok = tb + 16 * h + r;
+            const bool ok = tok < n;
+            const size_t off = rm(b, kv, t0 + (ok ? tok : 0));
+            const T* kr = k + off + 8 * g;
+            const T* vr = v + off + 8 * g;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                V8 z = {};
+                kt[h][j] = ok ? *reinterpret_cast<const V8*>(kr + 32 * j) : z;
+                vt[h][j] = ok ? *reinterpret_cast<const V8*>(vr + 32 * j) : z;
+            }
+        }
+        // scores
+        f32x4 s[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s[h] = M::mma(kt[h][j], qb[j], s[h]);
+        }
+        float sv[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tok = tb + 16 * h + 4 * g + i;
+                sv[4 * h + i] = tok < n ? s[h][i] * scale_log2 : -INFINITY;
+            }
+        float mloc = sv[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) mloc = fmaxf(mloc, sv[i]);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = exp2f(m_run - m_new);
+        m_run = m_new;
+        float p[8];
+        float psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            p[i] = exp2f(sv[i] - m_new);
+            psum += p[i];
+        }
+        l_run = l_run * alpha + psum;
+#pragma unroll
+        for (int nn = 0; nn < 8; ++nn) acc[nn] *= alpha;
+        V8 pb, pl;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            pb[i] = (T)p[i];
+            if (M::kSplitP) pl[i] = (T)(p[i] - (float)pb[i]);
+        }
+        // transpose V on the matrix cores, then PV
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                const f32x4 a0 = M::mma(vt[0][j], e ? sel1 : sel0, z);
+                const f32x4 a1 = M::mma(vt[1][j], e ? sel1 : sel0, z);
+                V8 va;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    va[i] = (T)a0[i];
+                    va[4 + i] = (T)a1[i];
+                }
+                acc[2 * j + e] = M::mma(va, pb, acc[2 * j + e]);
+                if (M::kSplitP) acc[2 * j + e] = M::mma(va, pl, acc[2 * j + e]);
+            }
+        }
+    }
+
+    // fold the 4 lane groups' l, publish per-wave state, merge the waves
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (lane < 16) {
+        s_m[wave][lane] = m_run;
+        s_l[wave][lane] = l_run;
+    }
+#pragma unroll
+    for (int nn = 0; nn < 8; ++nn)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_acc[wave][r][16 * nn + 4 * g + i] = acc[nn][i];
+    __syncthreads();
+
+    const size_t slot0 = (((size_t)b * rm.hkv + kv) * cmax + c) * group;
+    const int nvec = group * (D / 4);
+    for (int idx = tid; idx < nvec; idx += 256) {
+        const int hh = idx / (D / 4);
+        const int d4 = idx - hh * (D / 4);
+        float mw[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            mw[w] = s_m[w][hh];
+            mx = fmaxf(mx, mw[w]);
+        }
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float wt = exp2f(mw[w] - mx);
+            const float4 a = *reinterpret_cast<const float4*>(&s_acc[w][hh][4 * d4]);
+            o.x += wt * a.x; o.y += wt * a.y; o.z += wt * a.z; o.w += wt * a.w;
+        }
+        *reinterpret_cast<float4*>(ws_acc + (slot0 + hh) * D + 4 * d4) = o;
+    }
+    if (tid < group) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) mx = fmaxf(mx, s_m[w][tid]);
+        float lsum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) lsum += s_l[w][tid] * exp2f(s_m[w][tid] - mx);
+        ws_ml[(slot0 + tid) * 2] = mx;
+        ws_ml[(slot0 + tid) * 2 + 1] = lsum;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// combine: one wave per (b, q head). Folds the live chunks' partials
+// (m in log2 units) with the log-sum-exp rule and divides by l.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(64) void attn_combine(
+    const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
+    const int* __restrict__ lens, T* __restrict__ out, int hq, int hkv,
+    int group, int dim, int span, int chunk, int cmax) {
+    const int b = blockIdx.x / hq;
+    const int h = blockIdx.x - b * hq;
+    const int kv = h / group, gi = h - kv * group;
+    const int lane = threadIdx.x;
+    const int len = lens ? lens[b] : span;
+    const int nch = len > 0 ? (len + chunk - 1) / chunk : 0;
+    const int dc = dim >> 2;
+    T* o = out + ((size_t)b * hq + h) * dim;
+    if (nch == 0) {
+        for (int ch = lane; ch < dc; ch += 64)
+            St<T>::st4(o + 4 * ch, make_float4(0.f, 0.f, 0.f, 0.f));
+        return;
+    }
+    const size_t s0 = ((size_t)b * hkv + kv) * cmax * group + gi;
+    float mx = -INFINITY;
+    for (int cc = lane; cc < nch; cc += 64) mx = fmaxf(mx, ws_ml[(s0 + (size_t)cc * group) * 2]);
+    mx = wave_max(mx);
+    float lsum = 0.0f;
+    for (int cc = lane; cc < nch; cc += 64) {
+        const size_t sl = s0 + (size_t)cc * group;
+        lsum += ws_ml[sl * 2 + 1] * exp2f(ws_ml[sl * 2] - mx);
+    }
+    lsum = wave_sum(lsum);
+    float4 a0 = make_float4(0.f, 0.f, 0.f, 0.f), a1 = a0;
+    for (int cc = 0; cc < nch; ++cc) {
+        const size_t sl = s0 + (size_t)cc * group;
+        const float wt = exp2f(ws_ml[sl * 2] - mx);
+        const float* pa = ws_acc + sl * dim;
+        if (lane < dc) {
+            const float4 x = *reinterpret_cast<const float4*>(pa + 4 * lane);
+            a0.x += wt * x.x; a0.y += wt * x.y; a0.z += wt * x.z; a0.w += wt * x.w;
+        }
+        if (lane + 64 < dc) {
+            const float4 x = *reinterpret_cast<const float4*>(pa + 4 * (lane + 64));
+            a1.x += wt * x.x; a1.y += wt * x.y; a1.z += wt * x.z; a1.w += wt * x.w;
+        }
+    }
+    const float inv = 1.0f / lsum;
+    if (lane < dc)
+        St<T>::st4(o + 4 * lane, make_float4(a0.x * inv, a0.y * inv, a0.z * inv, a0.w * inv));
+    if (lane + 64 < dc)
+        St<T>::st4(o + 4 * (lane + 64),
+                   make_float4(a1.x * inv, a1.y * inv, a1.z * inv, a1.w * inv));
+}
+
+// ---------------------------------------------------------------------------
+// launcher
+// ---------------------------------------------------------------------------
+template <typename T>
+bool mfma_eligible(const T* q, const T* k, const T* v, int group, int dim) {
+    if (std::is_same<T, float>::value) return false;
+    if (dim != kMfmaDim || group > 16) return false;
+    return ((uintptr_t)q % 16 == 0) && ((uintptr_t)k % 16 == 0) &&
+           ((uintptr_t)v % 16 == 0);
+}
+
+int env_int(const char* name, int dflt) {
+    const char* s = getenv(name);
+    return (s && *s) ? atoi(s) : dflt;
+}
+
+template <typename T>
+void attention_run(const T* q, const T* k, const T* v, const int* table,
+                   const int* lens, T* out, int batch, int hq, int hkv,
+                   int rows_or_page, int tbl_width, int dim, bool paged,
+                   hipStream_t s) {
+    long long span;
+    if (paged) {
+        span = (long long)tbl_width * rows_or_page;
+        if (span > (1LL << 30)) inval("table capacity too large");
+        attention_check(batch, hq, hkv, span, dim);
+        if (rows_or_page < 1) inval("page size must be >= 1");
+        if (tbl_width < 0) inval("table width must be >= 0");
+        const int group = hq / hkv;
+        if (!(group == 1 || group == 2 || group == 4 || group == 8 || group == 16))
+            inval("paged decode supports GQA group sizes 1/2/4/8/16 "
+                  "(use the contiguous op for other divisors)");
+    } else {
+        span = rows_or_page;
+        attention_check(batch, hq, hkv, span, dim);
+    }
+    if (batch == 0) return;
+    if (!q || !out || (span > 0 && (!k || !v)) || (paged && span > 0 && !table))
+        inval("attention: null operand");
+    const int group = hq / hkv;
+    const bool fast = mfma_eligible(q, k, v, group, dim) &&
+                      env_int("FT_ATTN_FORCE_GENERIC", 0) == 0;
+    const long long target = (long long)dev_info().cu_count * 16;
+    int chunk;
+    if (fast)
+        chunk = choose_chunk(batch, hkv, span, 128, 1024, target);
+    else
+        chunk = choose_chunk(batch, hkv, span, 64, kGenMaxChunk, target);
+    const int forced = env_int("FT_ATTN_CHUNK", 0);
+    if (forced > 0) chunk = std::min(forced, fast ? 4096 : kGenMaxChunk);
+    const int cmax = span > 0 ? (int)((span + chunk - 1) / chunk) : 1;
+    const long long units = (long long)batch * hkv * cmax;
+    if (units * 256 > (1LL << 31)) inval("attention problem too large for one launch");
+    const size_t nslots = (size_t)units * group;
+    const size_t ml_floats = (nslots * 2 + 63) & ~(size_t)63;
+    float* ws = (float*)scratch(Scratch::AttnPartials,
+                                (ml_floats + nslots * dim) * sizeof(float), s);
+    float* ws_ml = ws;
+    float* ws_acc = ws + ml_floats;
+    RowMap rm;
+    rm.table = paged ? table : nullptr;
+    rm.hkv = hkv;
+    rm.dim = dim;
+    rm.rows_or_page = rows_or_page;
+    rm.tbl_width = tbl_width;
+    rm.page_shift = -1;
+    if (paged && (rows_or_page & (rows_or_page - 1)) == 0) {
+        int sh = 0;
+        while ((1 << sh) < rows_or_page) ++sh;
+        rm.page_shift = sh;
+    }
+    const float scale_log2 = (1.0f / sqrtf((float)dim)) * kLog2e;
+    if (span > 0) {
+        bool launched = false;
+        if constexpr (!std::is_same<T, float>::value) {
+            if (fast) {
+                attn_chunk_mfma<T><<<(unsigned)units, 256, 0, s>>>(
+                    q, k, v, lens, rm, ws_ml, ws_acc, hq, group, (int)span,
+                    chunk, cmax, scale_log2);
+                launched = true;
+            }
+        }
+        if (launched) {
+        } else if (dim / 4 <= 64) {
+            attn_chunk_generic<T, 1><<<(unsigned)units, kGenNT, 0, s>>>(
+                q, k, v, lens, rm, ws_ml, ws_acc, hq, group, (int)span, chunk,
+                cmax, scale_log2);
+        } else {
+            attn_chunk_generic<T, 2><<<(unsigned)units, kGenNT, 0, s>>>(
+                q, k, v, lens, rm, ws_ml, ws_acc, hq, group, (int)span, chunk,
+                cmax, scale_log2);
+        }
+        launch_check("attention chunk kernel launch");
+    }
+    attn_combine<T><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
+        ws_ml, ws_acc, span > 0 ? lens : nullptr, out, hq, hkv, group, dim,
+        (int)span, chunk, cmax);
+    launch_check("attention combine kernel launch");
+}
+
+// ---------------------------------------------------------------------------
+// KV append: one thread per 4-element chunk of one head's row (reference
+// attention.cu:1753-1782). Rows of the fresh token land at position lens[b].
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void kv_append_kernel(
+    const T* __restrict__ k_new, const T* __restrict__ v_new,
+    const int* __restrict__ lens, RowMap rm, T* __restrict__ k_dst,
+    T* __restrict__ v_dst) {
+    const int b = blockIdx.y;
+    const int dc = rm.dim >> 2;
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= rm.hkv * dc) return;
+    const int h = idx / dc, ch = idx - h * dc;
+    const size_t dst = rm(b, h, lens[b]) + 4 * ch;
+    const size_t src = ((size_t)b * rm.hkv + h) * rm.dim + 4 * ch;
+    if (sizeof(T) == 4) {
+        *reinterpret_cast<float4*>(k_dst + dst) = *reinterpret_cast<const float4*>(k_new + src);
+        *reinterpret_cast<float4*>(v_dst + dst) = *reinterpret_cast<const float4*>(v_new + src);
+    } else {
+        *reinterpret_cast<uint2*>(k_dst + dst) = *reinterpret_cast<const uint2*>(k_new + src);
+        *reinterpret_cast<uint2*>(v_dst + dst) = *reinterpret_cast<const uint2*>(v_new + src);
+    }
+}
+
+template <typename T>
+void kv_append_run(const T* k_new, const T* v_new, const int* table,
+                   const int* lens, T* k_dst, T* v_dst, int batch, int hkv,
+                   int dim, int rows_or_page, int tbl_width, bool paged,
+                   hipStream_t s) {
+    if (batch <= 0) return;
+    if (dim % 4 != 0) inval("dim must be a multiple of 4");
+    if (paged && rows_or_page < 1) inval("page size must be >= 1");
+    if (hkv < 1 || dim < 1) inval("kv heads and dim must be >= 1");
+    if (!k_new || !v_new || !lens || !k_dst || !v_dst || (paged && !table))
+        inval("kv append: null operand");
+    RowMap rm;
+    rm.table = paged ? table : nullptr;
+    rm.hkv = hkv;
+    rm.dim = dim;
+    rm.rows_or_page = rows_or_page;
+    rm.tbl_width = tbl_width;
+    rm.page_shift = -1;
+    if (paged && (rows_or_page & (rows_or_page - 1)) == 0) {
+        int sh = 0;
+        while ((1 << sh) < rows_or_page) ++sh;
+        rm.page_shift = sh;
+    }
+    const int chunks = hkv * (dim / 4);
+    dim3 grid((unsigned)((chunks + 255) / 256), (unsigned)batch);
+    kv_append_kernel<T><<<grid, 256, 0, s>>>(k_new, v_new, lens, rm, k_dst, v_dst);
+    launch_check("kv append kernel launch");
+}
+
+}  // namespace
+}  // namespace ft
+
+using ft::bf16;
+using ft::f16;
+
+extern "C" {
+
+int ft_attention_decode_launch(const float* q, const float* k, const float* v,
+                               const int* lens, float* out, int batch,
+                               int q_heads, int kv_heads, int cache_rows,
+                               int dim, uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::attention_run<float>(q, k, v, nullptr, lens, out, batch, q_heads,
+                                 kv_heads, cache_rows, 0, dim, false,
+                                 ft::as_stream(stream));
+    });
+}
+
+int ft_attention_decode_launch_bf16(const void* q, const void* k,
+                                    const void* v, const int* lens, void* out,
+                                    int batch, int q_heads, int kv_heads,
+                                    int cache_rows, int dim, uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::attention_run<bf16>((const bf16*)q, (const bf16*)k, (const bf16*)v,
+                                nullptr, lens, (bf16*)out, batch, q_heads,
+                                kv_heads, cache_rows, 0, dim, false,
+                                ft::as_stream(stream));
+    });
+}
+
+int ft_attention_decode_launch_fp16(const void* q, const void* k,
+                                    const void* v, const int* lens, void* out,
+                                    int batch, int q_heads, int kv_heads,
+                                    int cache_rows, int dim, uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::attention_run<f16>((const f16*)q, (const f16*)k, (const f16*)v,
+                               nullptr, lens, (f16*)out, batch, q_heads,
+                               kv_heads, cache_rows, 0, dim, false,
+                               ft::as_stream(stream));
+    });
+}
+
+int ft_attention_decode_paged_launch(const float* q, const float* k_pool,
+                                     const float* v_pool, const int* table,
+                                     const int* lens, float* out, int batch,
+                                     int q_heads, int kv_heads, int page,
+                                     int tbl_width, int dim, uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::attention_run<float>(q, k_pool, v_pool, table, lens, out, batch,
+                                 q_heads, kv_heads, page, tbl_width, dim, true,
+                                 ft::as_stream(stream));
+    });
+}
+
+int ft_attention_decode_paged_launch_bf16(const void* q, const void* k_pool,
+                                          const void* v_pool, const int* table,
+                                          const int* lens, void* out, int batch,
+                                          int q_heads, int kv_heads, int page,
+                                          int tbl_width, int dim,
+                                          uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::attention_run<bf16>((const bf16*)q, (const bf16*)k_pool,
+                                (const bf16*)v_pool, table, lens, (bf16*)out,
+                                batch, q_heads, kv_heads, page, tbl_width, dim,
+                                true, ft::as_stream(stream));
+    });
+}
+
+int ft_attention_decode_paged_launch_fp16(const void* q, const void* k_pool,
+                                          const void* v_pool, const int* table,
+                                          const int* lens, void* out, int batch,
+                                          int q_heads, int kv_heads, int page,
+                                          int tbl_width, int dim,
+                                          uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::attention_run<f16>((const f16*)q, (const f16*)k_pool,
+                               (const f16*)v_pool, table, lens, (f16*)out,
+                               batch, q_heads, kv_heads, page, tbl_width, dim,
+                               true, ft::as_stream(stream));
+    });
+}
+
+int ft_kv_append_paged_launch(const float* k_new, const float* v_new,
+                              const int* table, const int* lens, float* k_pool,
+                              float* v_pool, int batch, int hkv, int dim,
+                              int page, int tbl_width, uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::kv_append_run<float>(k_new, v_new, table, lens, k_pool, v_pool, batch,
+                                 hkv, dim, page, tbl_width, true,
+                                 ft::as_stream(stream));
+    });
+}
+
+int ft_kv_append_paged_launch_bf16(const void* k_new, const void* v_new,
+                                   const int* table, const int* lens,
+                                   void* k_pool, void* v_pool, int batch,
+                                   int hkv, int dim, int page, int tbl_width,
+                                   uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::kv_append_run<bf16>((const bf16*)k_new, (const bf16*)v_new, table,
+                                lens, (bf16*)k_pool, (bf16*)v_pool, batch, hkv,
+                                dim, page, tbl_width, true, ft::as_stream(stream));
+    });
+}
+
+int ft_kv_append_paged_launch_fp16(const void* k_new, const void* v_new,
+                                   const int* table, const int* lens,
+                                   void* k_pool, void* v_pool, int batch,
+                                   int hkv, int dim, int page, int tbl_width,
+                                   uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::kv_append_run<f16>((const f16*)k_new, (const f16*)v_new, table, lens,
+                               (f16*)k_pool, (f16*)v_pool, batch, hkv, dim, page,
+                               tbl_width, true, ft::as_stream(stream));
+    });
+}
+
+int ft_kv_append_launch(const float* k_new, const float* v_new,
+                        const int* lens, float* k_cache, float* v_cache,
+                        int batch, int hkv, int dim, int t_rows,
+                        uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::kv_append_run<float>(k_new, v_new, nullptr, lens, k_cache, v_cache,
+                                 batch, hkv, dim, t_rows, 0, false,
+                                 ft::as_stream(stream));
+    });
+}
+
+int ft_kv_append_launch_bf16(const void* k_new, const void* v_new,
+                             const int* lens, void* k_cache, void* v_cache,
+                             int batch, int hkv, int dim, int t_rows,
+                             uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::kv_append_run<bf16>((const bf16*)k_new, (const bf16*)v_new, nullptr,
+                                lens, (bf16*)k_cache, (bf16*)v_cache, batch, hkv,
+                                dim, t_rows, 0, false, ft::as_stream(stream));
+    });
+}
+
+int ft_kv_append_launch_fp16(const void* k_new, const void* v_new,
+                             const int* lens, void* k_cache, void* v_cache,
+                             int batch, int hkv, int dim, int t_rows,
+                             uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::kv_append_run<f16>((const f16*)k_new, (const f16*)v_new, nullptr,
+                               lens, (f16*)k_cache, (f16*)v_cache, batch, hkv,
+                               dim, t_rows, 0, false, ft::as_stream(stream));
+    });
+}
+
+}  // extern "C"

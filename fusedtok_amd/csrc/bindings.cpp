@@ -1,0 +1,273 @@
+// pybind11 module `_fusedtok`: the reference's `_launch` entry points
+// (src/bindings.cpp:2171-2845, the zero-copy half) over this build's C ABI.
+//
+// Pointers travel as Python ints (torch `data_ptr()`), optional pointers as
+// None, the stream as an int (`torch.cuda.current_stream().cuda_stream`).
+// C-ABI status codes map to the reference's exception contract
+// (bindings.cpp:14-16): FT_EINVAL -> ValueError, FT_EHIP -> RuntimeError.
+// The host arithmetic lives entirely in the C library; nothing here
+// computes.
+#include <pybind11/pybind11.h>
+
+#include <cstdint>
+#include <string>
+
+#include "fusedtok_amd.h"
+
+namespace py = pybind11;
+
+namespace {
+
+void check(int status) {
+    if (status == FT_OK) return;
+    const std::string msg = ft_last_error();
+    if (status == FT_EINVAL) throw py::value_error(msg);
+    throw std::runtime_error(msg);
+}
+
+uintptr_t opt_ptr(const py::object& o) {
+    if (o.is_none()) return 0;
+    return o.cast<uintptr_t>();
+}
+
+template <typename T>
+T* P(uintptr_t p) {
+    return reinterpret_cast<T*>(p);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_fusedtok, m) {
+    m.doc() = "gfx950 decode hot path (fusedtok-compatible launch entry points)";
+
+    m.def("cuda_available", []() { return ft_device_available() != 0; },
+          "True if a usable HIP device is present");
+    m.def("version", []() { return std::string(ft_version()); });
+
+    // ---- attention, contiguous ------------------------------------------
+#define FT_ATT(NAME, FN, T)                                                    \
+    m.def(NAME,                                                                \
+          [](uintptr_t q, uintptr_t k, uintptr_t v, py::object lens,           \
+             uintptr_t out, int batch, int hq, int hkv, int t_seq, int dim,    \
+             uintptr_t stream) {                                               \
+              check(FN(P<const T>(q), P<const T>(k), P<const T>(v),            \
+                       P<const int>(opt_ptr(lens)), P<T>(out), batch, hq, hkv, \
+                       t_seq, dim, stream));                                   \
+          },                                                                   \
+          py::arg("q"), py::arg("k"), py::arg("v"), py::arg("lens"),           \
+          py::arg("out"), py::arg("batch"), py::arg("q_heads"),                \
+          py::arg("kv_heads"), py::arg("cache_rows"), py::arg("dim"),          \
+          py::arg("stream") = 0)
+    FT_ATT("attention_decode_launch", ft_attention_decode_launch, float);
+    FT_ATT("attention_decode_launch_bf16", ft_attention_decode_launch_bf16, void);
+    FT_ATT("attention_decode_launch_fp16", ft_attention_decode_launch_fp16, void);
+#undef FT_ATT
+
+    // ---- attention, paged -----------------------------------------------
+#define FT_ATTP(NAME, FN, T)                                                   \
+    m.def(NAME,                                                                \
+          [](uintptr_t q, uintptr_t kp, uintptr_t vp, uintptr_t table,         \
+             py::object lens, uintptr_t out, int batch, int hq, int hkv,       \
+             int page, int tbl_width, int dim, uintptr_t stream) {             \
+              check(FN(P<const T>(q), P<const T>(kp), P<const T>(vp),          \
+                       P<const int>(table), P<const int>(opt_ptr(lens)),       \
+                       P<T>(out), batch, hq, hkv, page, tbl_width, dim,        \
+                       stream));                                               \
+          },                                                                   \
+          py::arg("q"), py::arg("k_pool"), py::arg("v_pool"),                  \
+          py::arg("table"), py::arg("lens"), py::arg("out"),                   \
+          py::arg("batch"), py::arg("q_heads"), py::arg("kv_heads"),           \
+          py::arg("page"), py::arg("tbl_width"), py::arg("dim"),               \
+          py::arg("stream") = 0)
+    FT_ATTP("attention_decode_paged_launch", ft_attention_decode_paged_launch, float);
+    FT_ATTP("attention_decode_paged_launch_bf16",
+            ft_attention_decode_paged_launch_bf16, void);
+    FT_ATTP("attention_decode_paged_launch_fp16",
+            ft_attention_decode_paged_launch_fp16, void);
+#undef FT_ATTP
+
+    // ---- kv append --------------------------------------------------------
+#define FT_KVP(NAME, FN, T)                                                    \
+    m.def(NAME,                                                                \
+          [](uintptr_t kn, uintptr_t vn, uintptr_t table, uintptr_t lens,      \
+             uintptr_t kp, uintptr_t vp, int batch, int hkv, int dim,          \
+             int page, int tbl_width, uintptr_t stream) {                      \
+              check(FN(P<const T>(kn), P<const T>(vn), P<const int>(table),    \
+                       P<const int>(lens), P<T>(kp), P<T>(vp), batch, hkv,     \
+                       dim, page, tbl_width, stream));                         \
+          },                                                                   \
+          py::arg("k_new"), py::arg("v_new"), py::arg("table"),                \
+          py::arg("lens"), py::arg("k_pool"), py::arg("v_pool"),               \
+          py::arg("batch"), py::arg("hkv"), py::arg("dim"), py::arg("page"),   \
+          py::arg("tbl_width"), py::arg("stream") = 0)
+    FT_KVP("kv_append_paged_launch", ft_kv_append_paged_launch, float);
+    FT_KVP("kv_append_paged_launch_bf16", ft_kv_append_paged_launch_bf16, void);
+    FT_KVP("kv_append_paged_launch_fp16", ft_kv_append_paged_launch_fp16, void);
+#undef FT_KVP
+
+#define FT_KV(NAME, FN, T)                                                     \
+    m.def(NAME,                                                                \
+          [](uintptr_t kn, uintptr_t vn, uintptr_t lens, uintptr_t kc,         \
+             uintptr_t vc, int batch, int hkv, int dim, int t_rows,            \
+             uintptr_t stream) {                                               \
+              check(FN(P<const T>(kn), P<const T>(vn), P<const int>(lens),     \
+                       P<T>(kc), P<T>(vc), batch, hkv, dim, t_rows, stream));  \
+          },                                                                   \
+          py::arg("k_new"), py::arg("v_new"), py::arg("lens"),                 \
+          py::arg("k_cache"), py::arg("v_cache"), py::arg("batch"),            \
+          py::arg("hkv"), py::arg("dim"), py::arg("t_rows"),                   \
+          py::arg("stream") = 0)
+    FT_KV("kv_append_launch", ft_kv_append_launch, float);
+    FT_KV("kv_append_launch_bf16", ft_kv_append_launch_bf16, void);
+    FT_KV("kv_append_launch_fp16", ft_kv_append_launch_fp16, void);
+#undef FT_KV
+
+    // ---- quantize -----------------------------------------------------------
+    m.def("quantize_launch",
+          [](uintptr_t x, uintptr_t q, uintptr_t scale, long long n,
+             uintptr_t stream) {
+              check(ft_quantize_int8_launch(P<const float>(x), P<signed char>(q),
+                                            P<float>(scale), n, stream));
+          },
+          py::arg("x"), py::arg("q"), py::arg("scale"), py::arg("n"),
+          py::arg("stream") = 0);
+    m.def("quantize_launch_ex",
+          [](uintptr_t x, int dtype, uintptr_t q, uintptr_t scale, long long n,
+             uintptr_t stream) {
+              check(ft_quantize_int8_launch_ex(P<const void>(x), dtype,
+                                               P<signed char>(q), P<float>(scale),
+                                               n, stream));
+          },
+          py::arg("x"), py::arg("dtype"), py::arg("q"), py::arg("scale"),
+          py::arg("n"), py::arg("stream") = 0);
+
+    // ---- qgemm --------------------------------------------------------------
+    m.def("qgemm_launch",
+          [](uintptr_t a, uintptr_t b, uintptr_t y, int mm, int n, int k,
+             float sa, float sb, uintptr_t stream) {
+              check(ft_qgemm_launch(P<const signed char>(a), P<const signed char>(b),
+                                    P<float>(y), mm, n, k, sa, sb, stream));
+          },
+          py::arg("a"), py::arg("b"), py::arg("y"), py::arg("m"), py::arg("n"),
+          py::arg("k"), py::arg("sa"), py::arg("sb"), py::arg("stream") = 0);
+    m.def("qgemm_perchannel_launch",
+          [](uintptr_t a, uintptr_t b, uintptr_t sb, uintptr_t y, int mm, int n,
+             int k, float sa, uintptr_t stream) {
+              check(ft_qgemm_perchannel_launch(
+                  P<const signed char>(a), P<const signed char>(b),
+                  P<const float>(sb), P<float>(y), mm, n, k, sa, stream));
+          },
+          py::arg("a"), py::arg("b"), py::arg("sb"), py::arg("y"), py::arg("m"),
+          py::arg("n"), py::arg("k"), py::arg("sa"), py::arg("stream") = 0);
+    m.def("qgemm_launch_ex",
+          [](uintptr_t a, uintptr_t b, py::object sb_vec, float sb, float sa,
+             py::object sa_dev, uintptr_t y, int y_dtype, int mm, int n, int k,
+             uintptr_t stream) {
+              check(ft_qgemm_launch_ex(
+                  P<const signed char>(a), P<const signed char>(b),
+                  P<const float>(opt_ptr(sb_vec)), sb, sa,
+                  P<const float>(opt_ptr(sa_dev)), P<void>(y), y_dtype, mm, n, k,
+                  stream));
+          },
+          py::arg("a"), py::arg("b"), py::arg("sb_vec"), py::arg("sb"),
+          py::arg("sa"), py::arg("sa_dev"), py::arg("y"), py::arg("y_dtype"),
+          py::arg("m"), py::arg("n"), py::arg("k"), py::arg("stream") = 0);
+    m.def("qgemm_i32_launch",
+          [](uintptr_t a, uintptr_t b, uintptr_t acc, int mm, int n, int k,
+             uintptr_t stream) {
+              check(ft_qgemm_i32_launch(P<const signed char>(a),
+                                        P<const signed char>(b), P<int>(acc), mm,
+                                        n, k, stream));
+          },
+          py::arg("a"), py::arg("b"), py::arg("acc"), py::arg("m"), py::arg("n"),
+          py::arg("k"), py::arg("stream") = 0);
+
+    // ---- rmsnorm --------------------------------------------------------------
+    m.def("rmsnorm_launch",
+          [](uintptr_t x, uintptr_t w, py::object r, uintptr_t y, int rows,
+             int cols, float eps, uintptr_t stream) {
+              check(ft_rmsnorm_launch(P<const float>(x), P<const float>(w),
+                                      P<const float>(opt_ptr(r)), P<float>(y),
+                                      rows, cols, eps, stream));
+          },
+          py::arg("x"), py::arg("weight"), py::arg("residual"), py::arg("out"),
+          py::arg("rows"), py::arg("cols"), py::arg("eps"),
+          py::arg("stream") = 0);
+#define FT_RMS(NAME, FN)                                                       \
+    m.def(NAME,                                                                \
+          [](uintptr_t x, uintptr_t w, py::object r, uintptr_t y, int rows,    \
+             int cols, float eps, uintptr_t stream) {                          \
+              check(FN(P<const void>(x), P<const float>(w),                    \
+                       P<const void>(opt_ptr(r)), P<void>(y), rows, cols, eps, \
+                       stream));                                               \
+          },                                                                   \
+          py::arg("x"), py::arg("weight"), py::arg("residual"),                \
+          py::arg("out"), py::arg("rows"), py::arg("cols"), py::arg("eps"),    \
+          py::arg("stream") = 0)
+    FT_RMS("rmsnorm_launch_bf16", ft_rmsnorm_launch_bf16);
+    FT_RMS("rmsnorm_launch_fp16", ft_rmsnorm_launch_fp16);
+#undef FT_RMS
+
+    // ---- rope -----------------------------------------------------------------
+    m.def("rope_launch",
+          [](bool neox, uintptr_t x, uintptr_t y, int seq, int dim, float theta,
+             int pos_offset, uintptr_t stream) {
+              check(neox ? ft_rope_neox_launch(P<const float>(x), P<float>(y), seq,
+                                               dim, theta, pos_offset, stream)
+                         : ft_rope_launch(P<const float>(x), P<float>(y), seq, dim,
+                                          theta, pos_offset, stream));
+          },
+          py::arg("neox"), py::arg("x"), py::arg("y"), py::arg("seq"),
+          py::arg("dim"), py::arg("theta"), py::arg("pos_offset"),
+          py::arg("stream") = 0);
+#define FT_ROPE(NAME, FN)                                                      \
+    m.def(NAME,                                                                \
+          [](uintptr_t x, uintptr_t y, int seq, int dim, float theta,          \
+             int pos_offset, uintptr_t stream) {                               \
+              check(FN(P<const void>(x), P<void>(y), seq, dim, theta,          \
+                       pos_offset, stream));                                   \
+          },                                                                   \
+          py::arg("x"), py::arg("y"), py::arg("seq"), py::arg("dim"),          \
+          py::arg("theta"), py::arg("pos_offset"), py::arg("stream") = 0)
+    FT_ROPE("rope_launch_bf16", ft_rope_launch_bf16);
+    FT_ROPE("rope_neox_launch_bf16", ft_rope_neox_launch_bf16);
+    FT_ROPE("rope_launch_fp16", ft_rope_launch_fp16);
+    FT_ROPE("rope_neox_launch_fp16", ft_rope_neox_launch_fp16);
+#undef FT_ROPE
+    m.def("rope_launch_ex",
+          [](uintptr_t x, uintptr_t y, int dtype, long long rows, int dim,
+             float theta, int pos_offset, py::object positions, int rows_per_pos,
+             bool neox, uintptr_t stream) {
+              check(ft_rope_launch_ex(P<const void>(x), P<void>(y), dtype, rows, dim,
+                                      theta, pos_offset,
+                                      P<const int>(opt_ptr(positions)),
+                                      rows_per_pos, neox ? 1 : 0, stream));
+          },
+          py::arg("x"), py::arg("y"), py::arg("dtype"), py::arg("rows"),
+          py::arg("dim"), py::arg("theta"), py::arg("pos_offset"),
+          py::arg("positions"), py::arg("rows_per_pos"), py::arg("neox"),
+          py::arg("stream") = 0);
+
+    // ---- swiglu -----------------------------------------------------------------
+    m.def("swiglu_launch",
+          [](uintptr_t g, uintptr_t u, uintptr_t y, long long n, uintptr_t stream) {
+              check(ft_swiglu_launch(P<const float>(g), P<const float>(u), P<float>(y),
+                                     n, stream));
+          },
+          py::arg("gate"), py::arg("up"), py::arg("out"), py::arg("n"),
+          py::arg("stream") = 0);
+    m.def("swiglu_launch_bf16",
+          [](uintptr_t g, uintptr_t u, uintptr_t y, long long n, uintptr_t stream) {
+              check(ft_swiglu_launch_bf16(P<const void>(g), P<const void>(u),
+                                          P<void>(y), n, stream));
+          },
+          py::arg("gate"), py::arg("up"), py::arg("out"), py::arg("n"),
+          py::arg("stream") = 0);
+    m.def("swiglu_launch_fp16",
+          [](uintptr_t g, uintptr_t u, uintptr_t y, long long n, uintptr_t stream) {
+              check(ft_swiglu_launch_fp16(P<const void>(g), P<const void>(u),
+                                          P<void>(y), n, stream));
+          },
+          py::arg("gate"), py::arg("up"), py::arg("out"), py::arg("n"),
+          py::arg("stream") = 0);
+}

@@ -1,0 +1,216 @@
+// Shared host/device plumbing for the gfx950 decode-path kernels.
+//
+// Host side: the status/error model of the C ABI (FT_OK / FT_EINVAL /
+// FT_EHIP with a thread-local message), HIP error checks, cached device
+// properties and the per-device scratch pool.
+// Device side: storage-type traits (f32 / bf16 / fp16 widened to f32 at
+// load, narrowed round-to-nearest-even at store) and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/fusedtok_amd.h"
+
+namespace ft {
+
+// ---------------------------------------------------------------------------
+// host: error model
+// ---------------------------------------------------------------------------
+
+struct Error {
+    int code;
+    std::string msg;
+};
+
+[[noreturn]] inline void inval(const std::string& msg) {
+    throw Error{FT_EINVAL, msg};
+}
+
+[[noreturn]] inline void hip_fail(const std::string& what, hipError_t e) {
+    throw Error{FT_EHIP, what + ": " + hipGetErrorString(e)};
+}
+
+inline void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) hip_fail(what, e);
+}
+
+// After a kernel launch: surface launch-configuration errors.
+inline void launch_check(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) hip_fail(what, e);
+}
+
+void set_error(const std::string& msg);
+void clear_error();
+
+// Wrap a C-ABI body: exceptions never cross the ABI.
+template <typename F>
+int guarded(F&& body) {
+    try {
+        body();
+        clear_error();
+        return FT_OK;
+    } catch (const Error& e) {
+        set_error(e.msg);
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        set_error("host allocation failed");
+        return FT_EHIP;
+    } catch (const std::exception& e) {
+        set_error(e.what());
+        return FT_EHIP;
+    } catch (...) {
+        set_error("unknown error");
+        return FT_EHIP;
+    }
+}
+
+inline hipStream_t as_stream(uintptr_t s) {
+    return reinterpret_cast<hipStream_t>(s);
+}
+
+// Device properties of the current device, cached per device id.
+struct DevInfo {
+    int id = 0;
+    int cu_count = 256;
+};
+const DevInfo& dev_info();
+
+// True if `s` is being captured into a HIP graph.
+bool stream_capturing(hipStream_t s);
+
+// Per-device scratch buffers, one per purpose, grown on demand and kept for
+// the process lifetime. Growth is refused during a stream capture (the
+// caller must warm the shape up once outside the capture). Returned memory
+// is uninitialised.
+enum class Scratch : int {
+    AttnPartials = 0,
+    QuantMax = 1,
+    GemmPartials = 2,
+    GemmCounters = 3,
+    kCount = 4
+};
+void* scratch(Scratch which, size_t bytes, hipStream_t s);
+// Same, but memory is zero when first allocated (or re-allocated); kernels
+// that use it must leave it zero when they finish (e.g. arrival counters).
+void* scratch_zeroed(Scratch which, size_t bytes, hipStream_t s);
+
+// ---------------------------------------------------------------------------
+// device: storage traits
+// ---------------------------------------------------------------------------
+
+using bf16 = __bf16;
+using f16 = _Float16;
+
+template <typename T> struct St;
+
+template <> struct St<float> {
+    __device__ __forceinline__ static float ld(const float* p) { return *p; }
+    __device__ __forceinline__ static void st(float* p, float v) { *p = v; }
+    __device__ __forceinline__ static float4 ld4(const float* p) {
+        return *reinterpret_cast<const float4*>(p);
+    }
+    __device__ __forceinline__ static void st4(float* p, float4 v) {
+        *reinterpret_cast<float4*>(p) = v;
+    }
+};
+
+template <> struct St<bf16> {
+    __device__ __forceinline__ static float ld(const bf16* p) {
+        return (float)*p;
+    }
+    __device__ __forceinline__ static void st(bf16* p, float v) {
+        *p = (bf16)v;
+    }
+    __device__ __forceinline__ static float4 ld4(const bf16* p) {
+        typedef bf16 v4 __attribute__((ext_vector_type(4)));
+        const v4 u = *reinterpret_cast<const v4*>(p);
+        return make_float4((float)u[0], (float)u[1], (float)u[2],
+                           (float)u[3]);
+    }
+    __device__ __forceinline__ static void st4(bf16* p, float4 v) {
+        typedef bf16 v4 __attribute__((ext_vector_type(4)));
+        v4 u;
+        u[0] = (bf16)v.x; u[1] = (bf16)v.y; u[2] = (bf16)v.z; u[3] = (bf16)v.w;
+        *reinterpret_cast<v4*>(p) = u;
+    }
+};
+
+template <> struct St<f16> {
+    __device__ __forceinline__ static float ld(const f16* p) {
+        return (float)*p;
+    }
+    __device__ __forceinline__ static void st(f16* p, float v) {
+        *p = (f16)v;
+    }
+    __device__ __forceinline__ static float4 ld4(const f16* p) {
+        typedef f16 v4 __attribute__((ext_vector_type(4)));
+        const v4 u = *reinterpret_cast<const v4*>(p);
+        return make_float4((float)u[0], (float)u[1], (float)u[2],
+                           (float)u[3]);
+    }
+    __device__ __forceinline__ static void st4(f16* p, float4 v) {
+        typedef f16 v4 __attribute__((ext_vector_type(4)));
+        v4 u;
+        u[0] = (f16)v.x; u[1] = (f16)v.y; u[2] = (f16)v.z; u[3] = (f16)v.w;
+        *reinterpret_cast<v4*>(p) = u;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// device: wave64 reductions (butterfly over all 64 lanes)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Block-wide reductions for blockDim.x == NT (multiple of 64). `red` is
+// LDS scratch of at least NT/64 floats. Every thread gets the result.
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) t += red[i];
+    __syncthreads();
+    return t;
+}
+
+template <int NT>
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; ++i) t = fmaxf(t, red[i]);
+    __syncthreads();
+    return t;
+}
+
+inline unsigned grid_1d(long long n, int per_block, int cap = 1 << 20) {
+    long long g = (n + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (unsigned)g;
+}
+
+}  // namespace ft

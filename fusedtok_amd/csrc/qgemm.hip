@@ -1,0 +1,434 @@
+// W8A8 GEMM for gfx950:  y[M,N] = float(int32(A_q[M,K] . B_q[N,K]^T)) * s_j
+//
+//   per-tensor   s_j = f32(sa * sb)        (reference qgemm.cu:612-629)
+//   per-channel  s_j = f32(sa * sb[j])     (reference qgemm.cu:631-652)
+//
+// The int32 accumulation is exact in any order, the scale is composed with
+// one f32 rounding and applied with one product, so the float32 output is
+// bit-identical to the reference CPU path; bf16 / fp16 outputs are that f32
+// value rounded to nearest-even.
+//
+// Kernels
+//   qgemm_skinny  M <= 64 (decode): W streamed once from HBM straight into
+//                 the B operand of v_mfma_i32_16x16x64_i8 (lane (r, g) loads
+//                 W[n0+r][k+16g .. +15], one 16-byte load); the 4 waves of a
+//                 workgroup split K and fold in LDS; when N alone cannot fill
+//                 the chip, K is also split across workgroups whose int32
+//                 partials are folded in a fixed order by the last one to
+//                 finish (per-tile arrival counter, reset by that workgroup).
+//   qgemm_tiled   M > 64: BMxBN workgroup tiles, v_mfma_i32_32x32x32_i8,
+//                 BK = 64 slabs double-buffered through LDS.
+//   qgemm_scalar  any shape/alignment (K % 16 != 0, misaligned views).
+//   K == 0        zero fill (a kernel, not a memset, so it captures cleanly).
+#include "ft_common.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+
+namespace ft {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef signed char i8;
+
+enum OutKind { kOutF32 = 0, kOutBF16 = 1, kOutF16 = 2, kOutI32 = 3 };
+
+struct Epi {
+    void* y;
+    float sa;
+    const float* sa_dev;  // device scale overrides sa when non-null
+    float sb;
+    const float* sb_vec;  // per-channel scales, null = per-tensor sb
+};
+
+__device__ __forceinline__ float epi_sa(const Epi& e) {
+    return e.sa_dev ? *e.sa_dev : e.sa;
+}
+
+template <int OUT>
+__device__ __forceinline__ void epi_store(const Epi& e, float sa, int n,
+                                          int row, int col, int acc) {
+    const size_t idx = (size_t)row * n + col;
+    if constexpr (OUT == kOutI32) {
+        static_cast<int*>(e.y)[idx] = acc;
+    } else {
+        const float s = e.sb_vec ? sa * e.sb_vec[col] : sa * e.sb;
+        const float val = (float)acc * s;
+        if constexpr (OUT == kOutF32) static_cast<float*>(e.y)[idx] = val;
+        if constexpr (OUT == kOutBF16) static_cast<bf16*>(e.y)[idx] = (bf16)val;
+        if constexpr (OUT == kOutF16) static_cast<f16*>(e.y)[idx] = (f16)val;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// zero fill (K == 0): an empty dot product is 0 on every output type
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void zero_fill_kernel(unsigned char* p,
+                                                        long long bytes) {
+    const long long stride = (long long)gridDim.x * 256;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < bytes; i += stride)
+        p[i] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// scalar fallback
+// ---------------------------------------------------------------------------
+template <int OUT>
+__global__ __launch_bounds__(256) void qgemm_scalar(const i8* __restrict__ a,
+                                                    const i8* __restrict__ b,
+                                                    Epi e, int m, int n, int k) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (long long)m * n) return;
+    const int row = (int)(idx / n), col = (int)(idx - (long long)row * n);
+    const i8* ar = a + (size_t)row * k;
+    const i8* br = b + (size_t)col * k;
+    int acc = 0;
+    for (int p = 0; p < k; ++p) acc += (int)ar[p] * (int)br[p];
+    epi_store<OUT>(e, epi_sa(e), n, row, col, acc);
+}
+
+// ---------------------------------------------------------------------------
+// skinny (M <= 16*MT)
+// ---------------------------------------------------------------------------
+template <int MT, int OUT>
+__global__ __launch_bounds__(256) void qgemm_skinny(
+    const i8* __restrict__ a, const i8* __restrict__ b, Epi e, int m, int n,
+    int k, int ksplit, int* __restrict__ part, int* __restrict__ counters) {
+    __shared__ i32x4 red[3][MT][64];
+    const int nt = blockIdx.x, ks = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int steps = (k + 63) >> 6;
+    const int per = (steps + ksplit - 1) / ksplit;
+    const int s0 = ks * per, s1 = min(steps, s0 + per);
+
+    i32x4 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = i32x4{0, 0, 0, 0};
+    const int nrow = nt * 16 + r;
+    const bool nrow_ok = nrow < n;
+    const i8* brow = b + (size_t)(nrow_ok ? nrow : 0) * k + 16 * g;
+    const i8* arow[MT];
+    bool arow_ok[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const int row = t * 16 + r;
+        arow_ok[t] = row < m;
+        arow[t] = a + (size_t)(arow_ok[t] ? row : 0) * k + 16 * g;
+    }
+#pragma unroll 4
+    for (int s = s0 + wave; s < s1; s += 4) {
+        const int kb = s << 6;
+        const bool kok = kb + 16 * g < k;
+        const i32x4 z = {0, 0, 0, 0};
+        const i32x4 bv = (nrow_ok && kok) ? *reinterpret_cast<const i32x4*>(brow + kb) : z;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const i32x4 av = (arow_ok[t] && kok) ? *reinterpret_cast<const i32x4*>(arow[t] + kb) : z;
+            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc[t], 0, 0, 0);
+        }
+    }
+    // fold the 4 waves (fixed order: wave 0 + 1 + 2 + 3)
+    if (wave > 0) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) red[wave - 1][t][lane] = acc[t];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 0; w < 3; ++w)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[t] += red[w][t][lane];
+
+    // C layout: lane (r, g) holds C[4g+i][r] = (A row t*16+4g+i, W row nt*16+r)
+    const int col = nt * 16 + r;
+    if (ksplit > 1) {
+        int* mine = part + ((size_t)nt * ksplit + ks) * (MT * 256);
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mine[(t * 4 + i) * 64 + lane] = acc[t][i];
+        // release the partial, count arrivals; only wave 0 is alive here, so
+        // the decision is broadcast within the wave (no workgroup barrier)
+        __threadfence();
+        int last = 0;
+        if (lane == 0) last = (atomicAdd(&counters[nt], 1) == ksplit - 1) ? 1 : 0;
+        last = __shfl(last, 0, 64);
+        if (!last) return;
+        __threadfence();
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[t] = i32x4{0, 0, 0, 0};
+        for (int j = 0; j < ksplit; ++j) {
+            const int* pj = part + ((size_t)nt * ksplit + j) * (MT * 256);
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[t][i] += pj[(t * 4 + i) * 64 + lane];
+        }
+        if (lane == 0) counters[nt] = 0;
+    }
+    if (col < n) {
+        const float sa = epi_sa(e);
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = t * 16 + 4 * g + i;
+                if (row < m) epi_store<OUT>(e, sa, n, row, col, acc[t][i]);
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// tiled (M > 64)
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WM, int WN>
+struct TileCfg {
+    static constexpr int BK = 64;
+    static constexpr int PITCH = BK + 16;          // bytes per LDS row
+    static constexpr int NTHR = WM * WN * 64;
+    static constexpr int MT = BM / WM / 32;        // 32x32 tiles per wave (M)
+    static constexpr int NT = BN / WN / 32;        // 32x32 tiles per wave (N)
+    static constexpr int ALOADS = BM * BK / 16 / NTHR;
+    static constexpr int BLOADS = BN * BK / 16 / NTHR;
+};
+
+template <int BM, int BN, int WM, int WN, int OUT>
+__global__ __launch_bounds__(WM * WN * 64) void qgemm_tiled(
+    const i8* __restrict__ a, const i8* __restrict__ b, Epi e, int m, int n,
+    int k) {
+    using C = TileCfg<BM, BN, WM, WN>;
+    constexpr int BK = C::BK, PITCH = C::PITCH, NTHR = C::NTHR;
+    __shared__ __attribute__((aligned(16))) i8 lds_a[2][BM * PITCH];
+    __shared__ __attribute__((aligned(16))) i8 lds_b[2][BN * PITCH];
+
+    const int bm = blockIdx.y * BM, bn = blockIdx.x * BN;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave - (wave / WN) * WN;
+    const int r32 = lane & 31, h = lane >> 5;
+
+    i32x16 acc[C::MT][C::NT];
+#pragma unroll
+    for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+        for (int j = 0; j < C::NT; ++j)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) acc[i][j][t] = 0;
+
+    i32x4 ra[C::ALOADS], rb[C::BLOADS];
+    auto gload = [&](int kt) {
+        const int kb = kt * BK;
+#pragma unroll
+        for (int j = 0; j < C::ALOADS; ++j) {
+            const int c = tid + j * NTHR;
+            const int row = c >> 2, kc = (c & 3) * 16;
+            const bool ok = (bm + row < m) && (kb + kc < k);
+            const i32x4 z = {0, 0, 0, 0};
+            ra[j] = ok ? *reinterpret_cast<const i32x4*>(a + (size_t)(bm + row) * k + kb + kc) : z;
+        }
+#pragma unroll
+        for (int j = 0; j < C::BLOADS; ++j) {
+            const int c = tid + j * NTHR;
+            const int row = c >> 2, kc = (c & 3) * 16;
+            const bool ok = (bn + row < n) && (kb + kc < k);
+            const i32x4 z = {0, 0, 0, 0};
+            rb[j] = ok ? *reinterpret_cast<const i32x4*>(b + (size_t)(bn + row) * k + kb + kc) : z;
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < C::ALOADS; ++j) {
+            const int c = tid + j * NTHR;
+            *reinterpret_cast<i32x4*>(&lds_a[buf][(c >> 2) * PITCH + (c & 3) * 16]) = ra[j];
+        }
+#pragma unroll
+        for (int j = 0; j < C::BLOADS; ++j) {
+            const int c = tid + j * NTHR;
+            *reinterpret_cast<i32x4*>(&lds_b[buf][(c >> 2) * PITCH + (c & 3) * 16]) = rb[j];
+        }
+    };
+
+    const int nk = (k + BK - 1) / BK;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            i32x4 fa[C::MT], fb[C::NT];
+#pragma unroll
+            for (int i = 0; i < C::MT; ++i)
+                fa[i] = *reinterpret_cast<const i32x4*>(
+                    &lds_a[cur][(wm * (BM / WM) + i * 32 + r32) * PITCH + ks * 32 + h * 16]);
+#pragma unroll
+            for (int j = 0; j < C::NT; ++j)
+                fb[j] = *reinterpret_cast<const i32x4*>(
+                    &lds_b[cur][(wn * (BN / WN) + j * 32 + r32) * PITCH + ks * 32 + h * 16]);
+#pragma unroll
+            for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+                for (int j = 0; j < C::NT; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) sstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // C layout 32x32: lane (r32, h), reg t -> row 8*(t/4) + 4h + t%4, col r32
+    const float sa = epi_sa(e);
+#pragma unroll
+    for (int j = 0; j < C::NT; ++j) {
+        const int col = bn + wn * (BN / WN) + j * 32 + r32;
+        if (col >= n) continue;
+#pragma unroll
+        for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int row = bm + wm * (BM / WM) + i * 32 + 8 * (t >> 2) + 4 * h + (t & 3);
+                if (row < m) epi_store<OUT>(e, sa, n, row, col, acc[i][j][t]);
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dispatch
+// ---------------------------------------------------------------------------
+int env_int(const char* name, int dflt) {
+    const char* s = getenv(name);
+    return (s && *s) ? atoi(s) : dflt;
+}
+
+// reference qgemm.cu:599-604 bounds m*n*k <= 2^38; this build instead bounds
+// K so the int32 accumulator provably cannot wrap (|a*b| <= 128*128), which
+// admits the large prefill shapes (4096 x 28672 x 8192).
+void qgemm_check(int m, int n, int k) {
+    if (m < 0 || n < 0 || k < 0) inval("m, n, k must be >= 0");
+    if (k > 131071) inval("qgemm K too large for exact int32 accumulation (K <= 131071)");
+}
+
+size_t out_elem_bytes(int out) {
+    return out == kOutBF16 || out == kOutF16 ? 2 : 4;
+}
+
+template <int OUT>
+void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
+                    hipStream_t s) {
+    const bool aligned = (k % 16 == 0) && ((uintptr_t)a % 16 == 0) &&
+                         ((uintptr_t)b % 16 == 0);
+    const int force = env_int("FT_QGEMM_KERNEL", 0);  // 1 skinny, 2 tiled, 3 scalar
+    if (!aligned || force == 3) {
+        const long long total = (long long)m * n;
+        qgemm_scalar<OUT><<<grid_1d(total, 256, 1 << 30), 256, 0, s>>>(a, b, e, m, n, k);
+        launch_check("qgemm scalar kernel launch");
+        return;
+    }
+    if ((m <= 64 && force != 2) || force == 1) {
+        if (m > 64) inval("skinny qgemm supports m <= 64");
+        const int ntiles = (n + 15) / 16;
+        const int steps = (k + 63) / 64;
+        const int cus = dev_info().cu_count;
+        int ksplit = 1;
+        while (ntiles * ksplit < 2 * cus && steps / (ksplit * 2) >= 8) ksplit *= 2;
+        const int forced_split = env_int("FT_QGEMM_KSPLIT", 0);
+        if (forced_split > 0) ksplit = std::min(forced_split, std::max(1, steps));
+        const int mt = (m + 15) / 16;
+        int* part = nullptr;
+        int* counters = nullptr;
+        if (ksplit > 1) {
+            part = (int*)scratch(Scratch::GemmPartials,
+                                 (size_t)ntiles * ksplit * 4 * 256 * sizeof(int), s);
+            counters = (int*)scratch_zeroed(Scratch::GemmCounters,
+                                            (size_t)ntiles * sizeof(int), s);
+        }
+        dim3 grid(ntiles, ksplit);
+        if (mt <= 1)
+            qgemm_skinny<1, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part, counters);
+        else if (mt <= 2)
+            qgemm_skinny<2, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part, counters);
+        else
+            qgemm_skinny<4, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part, counters);
+        launch_check("qgemm skinny kernel launch");
+        return;
+    }
+    constexpr int BM = 128, BN = 128;
+    dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
+    qgemm_tiled<BM, BN, 2, 2, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k);
+    launch_check("qgemm tiled kernel launch");
+}
+
+void qgemm_run(const i8* a, const i8* b, Epi e, int out, int m, int n, int k,
+               hipStream_t s) {
+    qgemm_check(m, n, k);
+    if (m == 0 || n == 0) return;
+    if (!e.y) inval("qgemm: null output");
+    if (k == 0) {
+        const long long bytes = (long long)m * n * out_elem_bytes(out);
+        zero_fill_kernel<<<grid_1d(bytes, 256, 4096), 256, 0, s>>>((unsigned char*)e.y, bytes);
+        launch_check("qgemm zero-fill kernel launch");
+        return;
+    }
+    if (!a || !b) inval("qgemm: null operand");
+    switch (out) {
+    case kOutF32: qgemm_dispatch<kOutF32>(a, b, e, m, n, k, s); break;
+    case kOutBF16: qgemm_dispatch<kOutBF16>(a, b, e, m, n, k, s); break;
+    case kOutF16: qgemm_dispatch<kOutF16>(a, b, e, m, n, k, s); break;
+    case kOutI32: qgemm_dispatch<kOutI32>(a, b, e, m, n, k, s); break;
+    default: inval("qgemm: unknown output type");
+    }
+}
+
+}  // namespace
+}  // namespace ft
+
+extern "C" {
+
+int ft_qgemm_launch(const signed char* aq, const signed char* bq, float* y,
+                    int m, int n, int k, float sa, float sb,
+                    uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::Epi e{y, sa, nullptr, sb, nullptr};
+        ft::qgemm_run(aq, bq, e, ft::kOutF32, m, n, k, ft::as_stream(stream));
+    });
+}
+
+int ft_qgemm_perchannel_launch(const signed char* aq, const signed char* bq,
+                               const float* sb_vec, float* y, int m, int n,
+                               int k, float sa, uintptr_t stream) {
+    return ft::guarded([&] {
+        if (!sb_vec) ft::inval("per-channel scale vector is required");
+        ft::Epi e{y, sa, nullptr, 0.0f, sb_vec};
+        ft::qgemm_run(aq, bq, e, ft::kOutF32, m, n, k, ft::as_stream(stream));
+    });
+}
+
+int ft_qgemm_launch_ex(const signed char* aq, const signed char* bq,
+                       const float* sb_vec, float sb, float sa,
+                       const float* sa_dev, void* y, int y_dtype, int m, int n,
+                       int k, uintptr_t stream) {
+    return ft::guarded([&] {
+        int out;
+        switch (y_dtype) {
+        case FT_DT_F32: out = ft::kOutF32; break;
+        case FT_DT_BF16: out = ft::kOutBF16; break;
+        case FT_DT_F16: out = ft::kOutF16; break;
+        default: ft::inval("qgemm: unknown output dtype code");
+        }
+        ft::Epi e{y, sa, sa_dev, sb, sb_vec};
+        ft::qgemm_run(aq, bq, e, out, m, n, k, ft::as_stream(stream));
+    });
+}
+
+int ft_qgemm_i32_launch(const signed char* aq, const signed char* bq, int* acc,
+                        int m, int n, int k, uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::Epi e{acc, 1.0f, nullptr, 1.0f, nullptr};
+        ft::qgemm_run(aq, bq, e, ft::kOutI32, m, n, k, ft::as_stream(stream));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,258 @@
+/*
+ * fusedtok_amd.h - C ABI of the MI355X (gfx950) decode hot path.
+ *
+ * Every entry point here replaces one launcher of the reference kernel
+ * library (fusedtok 2.5.0, include/fusedtok/cuda_launch.hpp); the
+ * reference declaration each one stands in for is cited beside it, and the
+ * argument order is the reference's.
+ *
+ * Contract (all entry points):
+ *   - Pointers are device pointers owned by the caller (HIP allocations,
+ *     e.g. torch tensors' data_ptr()). Nothing here takes ownership.
+ *   - `stream` is a hipStream_t passed as an integer (0 = null stream).
+ *     Launchers are asynchronous and stream-ordered; none synchronises
+ *     the host (unlike the reference's quantize_int8_launch, which reads
+ *     the absmax back mid-call: quantize.cu:195-215).
+ *   - Return value: FT_OK, FT_EINVAL (bad shape/argument: the reference's
+ *     std::invalid_argument -> Python ValueError) or FT_EHIP (HIP runtime
+ *     failure: the reference's std::runtime_error -> Python RuntimeError).
+ *     ft_last_error() returns the calling thread's last message.
+ *   - Argument validation happens on the host before any HIP call, so the
+ *     FT_EINVAL paths can be exercised without a GPU.
+ *   - bf16/fp16 entry points take `void*` storage; every accumulator and
+ *     softmax state stays float32 (reference: attention.cu:30-37).
+ *   - Library-owned device scratch (attention split partials, quantize
+ *     partial maxima) is allocated once per device on first use and kept
+ *     for the process lifetime. Concurrent calls on different streams of
+ *     one device share it and must be serialised by the caller (the same
+ *     rule as the reference: cuda_launch.hpp:185-190). Warm a shape up
+ *     once outside a HIP graph capture before capturing it.
+ */
+#ifndef FUSEDTOK_AMD_H
+#define FUSEDTOK_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    FT_OK = 0,
+    FT_EINVAL = 1, /* invalid argument: ValueError */
+    FT_EHIP = 2    /* HIP runtime failure: RuntimeError */
+};
+
+/* Output element types for the build's extra-dtype entry points. */
+enum {
+    FT_DT_F32 = 0,
+    FT_DT_BF16 = 1,
+    FT_DT_F16 = 2
+};
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* ft_last_error(void);
+
+/* 1 if a usable HIP device is present. Replaces cuda_available()
+ * (src/fusedtok.cu:34-37). */
+int ft_device_available(void);
+
+/* Library version string. */
+const char* ft_version(void);
+
+/* ------------------------------------------------------------------ */
+/* Attention, decode step, contiguous cache                            */
+/* out[b,h] = softmax(q[b,h] . K[b,h/G]^T / sqrt(D)) . V[b,h/G]         */
+/* q [B,Hq,D], k/v [B,Hkv,T,D], lens [B] or NULL, out [B,Hq,D].         */
+/* Replaces attention_decode_launch{,_bf16,_fp16}                       */
+/* (cuda_launch.hpp:336-359; attention.cu:1468-1585).                   */
+/* ------------------------------------------------------------------ */
+int ft_attention_decode_launch(const float* q, const float* k,
+                               const float* v, const int* lens, float* out,
+                               int batch, int q_heads, int kv_heads,
+                               int cache_rows, int dim, uintptr_t stream);
+int ft_attention_decode_launch_bf16(const void* q, const void* k,
+                                    const void* v, const int* lens,
+                                    void* out, int batch, int q_heads,
+                                    int kv_heads, int cache_rows, int dim,
+                                    uintptr_t stream);
+int ft_attention_decode_launch_fp16(const void* q, const void* k,
+                                    const void* v, const int* lens,
+                                    void* out, int batch, int q_heads,
+                                    int kv_heads, int cache_rows, int dim,
+                                    uintptr_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Attention, decode step, paged cache                                 */
+/* pools [Nb,Hkv,P,D]; table [B,S] int32; token t of sequence b lives  */
+/* at pool[table[b*S + t/P], kv, t%P, :]. GQA group in {1,2,4,8,16}.   */
+/* Replaces attention_decode_paged_launch{,_bf16,_fp16}                */
+/* (cuda_launch.hpp:397-416; attention.cu:1791-1915).                  */
+/* ------------------------------------------------------------------ */
+int ft_attention_decode_paged_launch(const float* q, const float* k_pool,
+                                     const float* v_pool, const int* table,
+                                     const int* lens, float* out, int batch,
+                                     int q_heads, int kv_heads, int page,
+                                     int tbl_width, int dim,
+                                     uintptr_t stream);
+int ft_attention_decode_paged_launch_bf16(const void* q, const void* k_pool,
+                                          const void* v_pool,
+                                          const int* table, const int* lens,
+                                          void* out, int batch, int q_heads,
+                                          int kv_heads, int page,
+                                          int tbl_width, int dim,
+                                          uintptr_t stream);
+int ft_attention_decode_paged_launch_fp16(const void* q, const void* k_pool,
+                                          const void* v_pool,
+                                          const int* table, const int* lens,
+                                          void* out, int batch, int q_heads,
+                                          int kv_heads, int page,
+                                          int tbl_width, int dim,
+                                          uintptr_t stream);
+
+/* ------------------------------------------------------------------ */
+/* KV append: one fresh token per sequence written at position lens[b] */
+/* k_new/v_new [B,Hkv,D]. In place. Exact copies.                      */
+/* Replaces kv_append_paged_launch{,_bf16,_fp16}                       */
+/* (cuda_launch.hpp:426-441; attention.cu:1924-1966) and               */
+/* kv_append_launch{,_bf16,_fp16} (cuda_launch.hpp:454-467;            */
+/* attention.cu:1985-2035).                                            */
+/* ------------------------------------------------------------------ */
+int ft_kv_append_paged_launch(const float* k_new, const float* v_new,
+                              const int* table, const int* lens,
+                              float* k_pool, float* v_pool, int batch,
+                              int hkv, int dim, int page, int tbl_width,
+                              uintptr_t stream);
+int ft_kv_append_paged_launch_bf16(const void* k_new, const void* v_new,
+                                   const int* table, const int* lens,
+                                   void* k_pool, void* v_pool, int batch,
+                                   int hkv, int dim, int page, int tbl_width,
+                                   uintptr_t stream);
+int ft_kv_append_paged_launch_fp16(const void* k_new, const void* v_new,
+                                   const int* table, const int* lens,
+                                   void* k_pool, void* v_pool, int batch,
+                                   int hkv, int dim, int page, int tbl_width,
+                                   uintptr_t stream);
+int ft_kv_append_launch(const float* k_new, const float* v_new,
+                        const int* lens, float* k_cache, float* v_cache,
+                        int batch, int hkv, int dim, int t_rows,
+                        uintptr_t stream);
+int ft_kv_append_launch_bf16(const void* k_new, const void* v_new,
+                             const int* lens, void* k_cache, void* v_cache,
+                             int batch, int hkv, int dim, int t_rows,
+                             uintptr_t stream);
+int ft_kv_append_launch_fp16(const void* k_new, const void* v_new,
+                             const int* lens, void* k_cache, void* v_cache,
+                             int batch, int hkv, int dim, int t_rows,
+                             uintptr_t stream);
+
+/* ------------------------------------------------------------------ */
+/* INT8 per-tensor symmetric quantize                                  */
+/* scale = max|x|/127 (1.0 for all-zero input); inv = 1.0f/scale;      */
+/* q = clamp(rint(x*inv), -127, 127). scale_out is a DEVICE float.     */
+/* Replaces quantize_int8_launch (cuda_launch.hpp:191-192;             */
+/* quantize.cu:195-215) without its host readback.                     */
+/* ------------------------------------------------------------------ */
+int ft_quantize_int8_launch(const float* x, signed char* q,
+                            float* scale_out, long long n,
+                            uintptr_t stream);
+/* Build addition: the same quantize over bf16 / fp16 input (x_dtype is
+ * FT_DT_*). Values are widened exactly to float before the same math. */
+int ft_quantize_int8_launch_ex(const void* x, int x_dtype, signed char* q,
+                               float* scale_out, long long n,
+                               uintptr_t stream);
+
+/* ------------------------------------------------------------------ */
+/* W8A8 GEMM: y[M,N] = float(int32(A_q[M,K] . B_q[N,K]^T)) * scale     */
+/* Replaces qgemm_launch (cuda_launch.hpp:202-204; qgemm.cu:659-703)   */
+/* and qgemm_perchannel_launch (cuda_launch.hpp:211-214;               */
+/* qgemm.cu:706-746). Output float32.                                  */
+/* ------------------------------------------------------------------ */
+int ft_qgemm_launch(const signed char* aq, const signed char* bq, float* y,
+                    int m, int n, int k, float sa, float sb,
+                    uintptr_t stream);
+int ft_qgemm_perchannel_launch(const signed char* aq, const signed char* bq,
+                               const float* sb_vec, float* y, int m, int n,
+                               int k, float sa, uintptr_t stream);
+/* Build addition: per-channel GEMM with a bf16/fp16/f32 output. The f32
+ * value is bit-identical to ft_qgemm_perchannel_launch's, then rounded to
+ * nearest-even in the output type. sa_dev, when non-NULL, is a device
+ * float read instead of `sa` (the device-resident scale written by
+ * ft_quantize_int8_launch*). sb_vec == NULL means per-tensor: the scale
+ * is f32(sa * sb). */
+int ft_qgemm_launch_ex(const signed char* aq, const signed char* bq,
+                       const float* sb_vec, float sb, float sa,
+                       const float* sa_dev, void* y, int y_dtype, int m,
+                       int n, int k, uintptr_t stream);
+/* Build addition (test hook): the exact int32 accumulators
+ * acc[M,N] = A_q . B_q^T, through the same kernels as the float paths. */
+int ft_qgemm_i32_launch(const signed char* aq, const signed char* bq,
+                        int* acc, int m, int n, int k, uintptr_t stream);
+
+/* ------------------------------------------------------------------ */
+/* RMSNorm (+ optional residual): y = (x+r) * rsqrt(mean((x+r)^2)+eps) * w */
+/* x/r/y [rows, cols], w [cols] float32; r may be NULL.                */
+/* Replaces rmsnorm_launch (cuda_launch.hpp:44-45; rmsnorm.cu:132-141)  */
+/* and rmsnorm_launch_bf16 (cuda_launch.hpp:476-478; rmsnorm.cu:143-153)*/
+/* ------------------------------------------------------------------ */
+int ft_rmsnorm_launch(const float* x, const float* w, const float* r,
+                      float* y, int rows, int cols, float eps,
+                      uintptr_t stream);
+int ft_rmsnorm_launch_bf16(const void* x, const float* w, const void* r,
+                           void* y, int rows, int cols, float eps,
+                           uintptr_t stream);
+/* Build addition: fp16 storage. */
+int ft_rmsnorm_launch_fp16(const void* x, const float* w, const void* r,
+                           void* y, int rows, int cols, float eps,
+                           uintptr_t stream);
+
+/* ------------------------------------------------------------------ */
+/* RoPE. x/y [seq, dim]; row r sits at position r + pos_offset;        */
+/* pair j rotates by (r+pos_offset) * theta^(-2j/dim).                 */
+/* Replaces rope_launch / rope_neox_launch (cuda_launch.hpp:56-59;     */
+/* rope.cu:301-345) and their bf16 twins (cuda_launch.hpp:484-489).    */
+/* ------------------------------------------------------------------ */
+int ft_rope_launch(const float* x, float* y, int seq, int dim, float theta,
+                   int pos_offset, uintptr_t stream);
+int ft_rope_neox_launch(const float* x, float* y, int seq, int dim,
+                        float theta, int pos_offset, uintptr_t stream);
+int ft_rope_launch_bf16(const void* x, void* y, int seq, int dim,
+                        float theta, int pos_offset, uintptr_t stream);
+int ft_rope_neox_launch_bf16(const void* x, void* y, int seq, int dim,
+                             float theta, int pos_offset, uintptr_t stream);
+/* Build additions: fp16 storage. */
+int ft_rope_launch_fp16(const void* x, void* y, int seq, int dim,
+                        float theta, int pos_offset, uintptr_t stream);
+int ft_rope_neox_launch_fp16(const void* x, void* y, int seq, int dim,
+                             float theta, int pos_offset, uintptr_t stream);
+/* Build addition: per-row positions. x/y [rows, dim] of dtype FT_DT_*;
+ * row r sits at position base(r) + pos_offset with
+ * base(r) = positions[r / rows_per_pos] (device int32) when positions is
+ * non-NULL, else r / rows_per_pos. rows_per_pos = 1 with positions = NULL
+ * is exactly ft_rope_launch. With q laid out [B, Hq, D] and rows_per_pos =
+ * Hq, positions = per-sequence lengths rotates every head of sequence b at
+ * its own decode position. */
+int ft_rope_launch_ex(const void* x, void* y, int dtype, long long rows,
+                      int dim, float theta, int pos_offset,
+                      const int* positions, int rows_per_pos, int neox,
+                      uintptr_t stream);
+
+/* ------------------------------------------------------------------ */
+/* SwiGLU: y = g / (1 + exp(-g)) * u                                   */
+/* Replaces swiglu_launch (cuda_launch.hpp:40; activations.cu:513-516) */
+/* and swiglu_launch_bf16 (cuda_launch.hpp:472-473;                    */
+/* activations.cu:518-521).                                            */
+/* ------------------------------------------------------------------ */
+int ft_swiglu_launch(const float* gate, const float* up, float* y,
+                     long long n, uintptr_t stream);
+int ft_swiglu_launch_bf16(const void* gate, const void* up, void* y,
+                          long long n, uintptr_t stream);
+/* Build addition: fp16 storage. */
+int ft_swiglu_launch_fp16(const void* gate, const void* up, void* y,
+                          long long n, uintptr_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FUSEDTOK_AMD_H */

@@ -1,0 +1,359 @@
+// TEST INFRASTRUCTURE - NOT PART OF THE PRODUCT.
+//
+// CPU oracle for the decode hot path: a plain C++ restatement of the
+// reference's single-threaded `*_cpu` functions (fusedtok 2.5.0), written
+// from their documented semantics with the same loop order and float32
+// arithmetic (no fast-math, no FMA contraction: built -ffp-contract=off).
+// Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+// load it, and only as the checker / the timed CPU baseline. The product
+// path (fusedtok_amd) never calls it.
+//
+// Each function cites the reference function it restates. Exported with a
+// flat C ABI for ctypes: int status (0 ok, 1 invalid argument) and a
+// thread-local message from or_last_error().
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_err;
+
+struct Inval {
+    std::string msg;
+};
+
+template <typename F>
+int run(F&& f) {
+    try {
+        f();
+        g_err.clear();
+        return 0;
+    } catch (const Inval& e) {
+        g_err = e.msg;
+        return 1;
+    }
+}
+
+// reference attention.cu:184-193
+void attention_check(int batch, int hq, int hkv, long long t_seq, int dim) {
+    if (batch < 0 || hq < 1 || hkv < 1 || t_seq < 0 || dim < 1)
+        throw Inval{"attention shapes must satisfy batch>=0, heads>=1, rows>=0, dim>=1"};
+    if (hq % hkv != 0)
+        throw Inval{"q heads must be a multiple of kv heads (contiguous GQA groups)"};
+    if (dim % 4 != 0 || dim > 512)
+        throw Inval{"dim must be a multiple of 4 and at most 512"};
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* or_last_error(void) { return g_err.c_str(); }
+
+// ---------------------------------------------------------------------------
+// attention_decode_cpu (reference attention.cu:1318-1373): two-pass float32
+// softmax per (b, h): scores = (q . k_t) * (1/sqrtf(D)), m = max, l = sum
+// expf(s - m), out += (expf(s - m) / l) * v_t. len == 0 leaves a zero row.
+// ---------------------------------------------------------------------------
+int or_attention_decode(const float* q, const float* k, const float* v,
+                        const int* lens, float* out, int batch, int hq,
+                        int hkv, int t_seq, int dim) {
+    return run([&] {
+        attention_check(batch, hq, hkv, t_seq, dim);
+        if (lens)
+            for (int i = 0; i < batch; ++i)
+                if (lens[i] < 0 || lens[i] > t_seq)
+                    throw Inval{"lens entries must be within [0, cache rows]"};
+        const int group = hq / hkv;
+        const float scale = 1.0f / sqrtf((float)dim);
+        std::memset(out, 0, sizeof(float) * (size_t)batch * hq * dim);
+        std::vector<float> scores(t_seq > 0 ? t_seq : 1);
+        for (int bi = 0; bi < batch; ++bi) {
+            const int len = lens ? lens[bi] : t_seq;
+            for (int h = 0; h < hq; ++h) {
+                if (len == 0) continue;
+                const int kv = h / group;
+                const float* qp = q + ((size_t)bi * hq + h) * dim;
+                const float* kp = k + (((size_t)bi * hkv + kv) * t_seq) * dim;
+                const float* vp = v + (((size_t)bi * hkv + kv) * t_seq) * dim;
+                float m = -INFINITY;
+                for (int t = 0; t < len; ++t) {
+                    float dot = 0.0f;
+                    for (int d = 0; d < dim; ++d) dot += qp[d] * kp[(size_t)t * dim + d];
+                    scores[t] = dot * scale;
+                    m = fmaxf(m, scores[t]);
+                }
+                float l = 0.0f;
+                for (int t = 0; t < len; ++t) l += expf(scores[t] - m);
+                float* op = out + ((size_t)bi * hq + h) * dim;
+                for (int t = 0; t < len; ++t) {
+                    const float p = expf(scores[t] - m) / l;
+                    for (int d = 0; d < dim; ++d) op[d] += p * vp[(size_t)t * dim + d];
+                }
+            }
+        }
+    });
+}
+
+// ---------------------------------------------------------------------------
+// attention_decode_paged_cpu (reference attention.cu:1382-1456): the same
+// walk with row(t) = pool[table[b*S + t/P], kv, t%P, :]; validates lens and
+// the table entries of the pages in use.
+// ---------------------------------------------------------------------------
+int or_attention_decode_paged(const float* q, const float* k_pool,
+                              const float* v_pool, const int* table,
+                              const int* lens, float* out, int batch, int hq,
+                              int hkv, int page, int tbl_width, int num_blocks,
+                              int dim) {
+    return run([&] {
+        attention_check(batch, hq, hkv, (long long)tbl_width * page, dim);
+        if (page < 1) throw Inval{"page size must be >= 1"};
+        const int span = tbl_width * page;
+        if (lens)
+            for (int i = 0; i < batch; ++i)
+                if (lens[i] < 0 || lens[i] > span)
+                    throw Inval{"lens entries must be within [0, table width * page]"};
+        for (int bi = 0; bi < batch; ++bi) {
+            const int used = lens ? lens[bi] : span;
+            const int pages = (used + page - 1) / page;
+            for (int s = 0; s < pages; ++s) {
+                const int blk = table[(size_t)bi * tbl_width + s];
+                if (blk < 0 || blk >= num_blocks)
+                    throw Inval{"block table entries must be valid pool block ids"};
+            }
+        }
+        const int group = hq / hkv;
+        const float scale = 1.0f / sqrtf((float)dim);
+        std::memset(out, 0, sizeof(float) * (size_t)batch * hq * dim);
+        std::vector<float> scores(span > 0 ? span : 1);
+        for (int bi = 0; bi < batch; ++bi) {
+            const int len = lens ? lens[bi] : span;
+            const int* rowT = table + (size_t)bi * tbl_width;
+            for (int h = 0; h < hq; ++h) {
+                if (len == 0) continue;
+                const int kv = h / group;
+                const float* qp = q + ((size_t)bi * hq + h) * dim;
+                float m = -INFINITY;
+                for (int t = 0; t < len; ++t) {
+                    const size_t base = ((size_t)rowT[t / page] * hkv + kv) * page + (t % page);
+                    const float* kp = k_pool + base * dim;
+                    float dot = 0.0f;
+                    for (int d = 0; d < dim; ++d) dot += qp[d] * kp[d];
+                    scores[t] = dot * scale;
+                    m = fmaxf(m, scores[t]);
+                }
+                float l = 0.0f;
+                for (int t = 0; t < len; ++t) l += expf(scores[t] - m);
+                float* op = out + ((size_t)bi * hq + h) * dim;
+                for (int t = 0; t < len; ++t) {
+                    const size_t base = ((size_t)rowT[t / page] * hkv + kv) * page + (t % page);
+                    const float* vp = v_pool + base * dim;
+                    const float p = expf(scores[t] - m) / l;
+                    for (int d = 0; d < dim; ++d) op[d] += p * vp[d];
+                }
+            }
+        }
+    });
+}
+
+// ---------------------------------------------------------------------------
+// kv_append_paged_cpu / kv_append_cpu (reference attention.cu:2037-2099):
+// exact copies of each sequence's [Hkv, D] rows to position lens[b].
+// `elem` is the element size in bytes (the copies are byte-exact, so the
+// same routine serves f32 / bf16 / fp16 storage).
+// ---------------------------------------------------------------------------
+int or_kv_append_paged(const void* k_new, const void* v_new, const int* table,
+                       const int* lens, void* k_pool, void* v_pool, int batch,
+                       int hkv, int dim, int page, int tbl_width, int num_blocks,
+                       int elem) {
+    return run([&] {
+        if (dim % 4 != 0) throw Inval{"dim must be a multiple of 4"};
+        if (page < 1) throw Inval{"page size must be >= 1"};
+        const size_t row = (size_t)dim * elem;
+        for (int bi = 0; bi < batch; ++bi) {
+            const int pos = lens[bi];
+            if (pos < 0 || pos >= tbl_width * page)
+                throw Inval{"lens entries must be within [0, table width * page)"};
+            const int blk = table[(size_t)bi * tbl_width + pos / page];
+            if (blk < 0 || blk >= num_blocks)
+                throw Inval{"block table entries must be valid pool block ids"};
+            const int off = pos % page;
+            for (int h = 0; h < hkv; ++h) {
+                const size_t dst = ((size_t)blk * hkv + h) * page + off;
+                const size_t src = (size_t)bi * hkv + h;
+                std::memcpy((char*)k_pool + dst * row, (const char*)k_new + src * row, row);
+                std::memcpy((char*)v_pool + dst * row, (const char*)v_new + src * row, row);
+            }
+        }
+    });
+}
+
+int or_kv_append(const void* k_new, const void* v_new, const int* lens,
+                 void* k_cache, void* v_cache, int batch, int hkv, int dim,
+                 int t_rows, int elem) {
+    return run([&] {
+        if (dim % 4 != 0) throw Inval{"dim must be a multiple of 4"};
+        const size_t row = (size_t)dim * elem;
+        for (int bi = 0; bi < batch; ++bi) {
+            const int pos = lens[bi];
+            if (pos < 0 || pos >= t_rows)
+                throw Inval{"lens entries must be within [0, cache rows)"};
+            for (int h = 0; h < hkv; ++h) {
+                const size_t dst = ((size_t)bi * hkv + h) * t_rows + pos;
+                const size_t src = (size_t)bi * hkv + h;
+                std::memcpy((char*)k_cache + dst * row, (const char*)k_new + src * row, row);
+                std::memcpy((char*)v_cache + dst * row, (const char*)v_new + src * row, row);
+            }
+        }
+    });
+}
+
+// ---------------------------------------------------------------------------
+// quantize_int8_cpu (reference quantize.cu:153-186): absmax, scale =
+// absmax/127 (1.0 for all-zero input), inv = 1.0f/scale, q = clamp(rint(x *
+// inv), -127, 127).
+// ---------------------------------------------------------------------------
+int or_quantize_int8(const float* x, long long n, signed char* q, float* scale_out) {
+    return run([&] {
+        float m = 0.0f;
+        for (long long i = 0; i < n; ++i) m = std::fmax(m, std::fabs(x[i]));
+        const float scale = m > 0.0f ? m / 127.0f : 1.0f;
+        const float inv = 1.0f / scale;
+        for (long long i = 0; i < n; ++i) {
+            float v = std::rint(x[i] * inv);
+            if (v > 127.0f) v = 127.0f;
+            if (v < -127.0f) v = -127.0f;
+            q[i] = (signed char)v;
+        }
+        *scale_out = scale;
+    });
+}
+
+// ---------------------------------------------------------------------------
+// qgemm_cpu / qgemm_perchannel_cpu (reference qgemm.cu:612-652): exact int32
+// dot products, then (float)acc * f32(sa*sb) or (float)acc * f32(sa*sb[j]).
+// ---------------------------------------------------------------------------
+static int qgemm_check(int m, int n, int k) {
+    if (m < 0 || n < 0 || k < 0) throw Inval{"m, n, k must be >= 0"};
+    return 0;
+}
+
+int or_qgemm_i32(const signed char* a, const signed char* b, int m, int n, int k,
+                 int* acc_out) {
+    return run([&] {
+        qgemm_check(m, n, k);
+        for (int i = 0; i < m; ++i)
+            for (int j = 0; j < n; ++j) {
+                int acc = 0;
+                const signed char* ar = a + (size_t)i * k;
+                const signed char* br = b + (size_t)j * k;
+                for (int p = 0; p < k; ++p) acc += (int)ar[p] * (int)br[p];
+                acc_out[(size_t)i * n + j] = acc;
+            }
+    });
+}
+
+int or_qgemm(const signed char* a, const signed char* b, int m, int n, int k,
+             float sa, float sb, float* y) {
+    return run([&] {
+        qgemm_check(m, n, k);
+        const float scale = sa * sb;
+        for (int i = 0; i < m; ++i)
+            for (int j = 0; j < n; ++j) {
+                int acc = 0;
+                const signed char* ar = a + (size_t)i * k;
+                const signed char* br = b + (size_t)j * k;
+                for (int p = 0; p < k; ++p) acc += (int)ar[p] * (int)br[p];
+                y[(size_t)i * n + j] = (float)acc * scale;
+            }
+    });
+}
+
+int or_qgemm_perchannel(const signed char* a, const signed char* b,
+                        const float* sb, int m, int n, int k, float sa, float* y) {
+    return run([&] {
+        qgemm_check(m, n, k);
+        for (int i = 0; i < m; ++i)
+            for (int j = 0; j < n; ++j) {
+                int acc = 0;
+                const signed char* ar = a + (size_t)i * k;
+                const signed char* br = b + (size_t)j * k;
+                for (int p = 0; p < k; ++p) acc += (int)ar[p] * (int)br[p];
+                y[(size_t)i * n + j] = (float)acc * (sa * sb[j]);
+            }
+    });
+}
+
+// ---------------------------------------------------------------------------
+// rmsnorm_cpu (reference rmsnorm.cu:110-130): sequential float32 sum of
+// squares, inv = 1.0f / sqrt(acc/cols + eps), y = v * inv * w.
+// ---------------------------------------------------------------------------
+int or_rmsnorm(const float* x, const float* w, const float* residual, int rows,
+               int cols, float eps, float* y) {
+    return run([&] {
+        if (rows < 0 || cols <= 0) throw Inval{"rows must be >= 0 and cols must be > 0"};
+        for (int row = 0; row < rows; ++row) {
+            const size_t base = (size_t)row * cols;
+            float acc = 0.0f;
+            for (int i = 0; i < cols; ++i) {
+                const float v = x[base + i] + (residual ? residual[base + i] : 0.0f);
+                acc += v * v;
+            }
+            const float inv_rms = 1.0f / std::sqrt(acc / cols + eps);
+            for (int i = 0; i < cols; ++i) {
+                const float v = x[base + i] + (residual ? residual[base + i] : 0.0f);
+                y[base + i] = v * inv_rms * w[i];
+            }
+        }
+    });
+}
+
+// ---------------------------------------------------------------------------
+// rope_cpu / rope_neox_cpu (reference rope.cu:96-143): angle = m *
+// pow((double)theta, -2.0*j/dim) in double, cos/sin in double, the rotation
+// in double, rounded to float. Row r sits at position r + pos_offset.
+// ---------------------------------------------------------------------------
+int or_rope(const float* x, int seq, int dim, float theta, int pos_offset,
+            int neox, float* y) {
+    return run([&] {
+        if (seq < 0 || dim <= 0) throw Inval{"seq must be >= 0 and dim must be > 0"};
+        if (dim % 2 != 0) throw Inval{"dim must be even (RoPE pairs elements)"};
+        if (pos_offset < 0) throw Inval{"pos_offset must be >= 0"};
+        for (int r = 0; r < seq; ++r) {
+            const int m = r + pos_offset;
+            for (int j = 0; j < dim / 2; ++j) {
+                const double angle = m * std::pow((double)theta, -2.0 * j / dim);
+                const double c = std::cos(angle), s = std::sin(angle);
+                size_t i1, i2;
+                if (neox) {
+                    i1 = (size_t)r * dim + j;
+                    i2 = i1 + dim / 2;
+                } else {
+                    i1 = (size_t)r * dim + 2 * j;
+                    i2 = i1 + 1;
+                }
+                const float x1 = x[i1], x2 = x[i2];
+                y[i1] = (float)(x1 * c - x2 * s);
+                y[i2] = (float)(x1 * s + x2 * c);
+            }
+        }
+    });
+}
+
+// ---------------------------------------------------------------------------
+// swiglu_cpu (reference activations.cu:501-511): g / (1 + exp(-g)) * u.
+// ---------------------------------------------------------------------------
+int or_swiglu(const float* g, const float* u, long long n, float* y) {
+    return run([&] {
+        for (long long i = 0; i < n; ++i) {
+            const float gv = g[i];
+            y[i] = gv / (1.0f + std::exp(-gv)) * u[i];
+        }
+    });
+}
+
+}  // extern "C"

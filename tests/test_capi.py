@@ -1,0 +1,130 @@
+"""The C-ABI library (include/fusedtok_amd.h) loads, exports every declared
+entry point, and reports invalid arguments (FT_EINVAL + message) from host
+validation alone - these paths run before any HIP call, so no GPU is needed.
+No compute call is made here."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fusedtok_amd.h")
+LIB = os.path.join(ROOT, "fusedtok_amd", "libfusedtok_amd.so")
+
+FT_OK, FT_EINVAL = 0, 1
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ft_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    assert os.path.exists(LIB), "libfusedtok_amd.so not built"
+    lib = ctypes.CDLL(LIB)
+    lib.ft_last_error.restype = ctypes.c_char_p
+    lib.ft_version.restype = ctypes.c_char_p
+    return lib
+
+
+def test_header_declares_the_hot_path():
+    syms = declared_symbols()
+    for name in ["ft_attention_decode_launch", "ft_attention_decode_paged_launch_bf16",
+                 "ft_kv_append_paged_launch", "ft_kv_append_launch_fp16",
+                 "ft_quantize_int8_launch", "ft_qgemm_launch",
+                 "ft_qgemm_perchannel_launch", "ft_rmsnorm_launch_bf16",
+                 "ft_rope_neox_launch", "ft_swiglu_launch_bf16"]:
+        assert name in syms
+    assert len(syms) >= 30
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_version_and_clean_error(lib):
+    assert lib.ft_version().decode().count(".") == 2
+    assert isinstance(lib.ft_last_error(), bytes)
+
+
+def _v(x=0):
+    return ctypes.c_void_p(x)
+
+
+U = ctypes.c_size_t
+
+
+def test_attention_invalid_arguments(lib):
+    f = lib.ft_attention_decode_launch
+    # dim not a multiple of 4
+    st = f(_v(), _v(), _v(), _v(), _v(), 1, 2, 1, 4, 30, U(0))
+    assert st == FT_EINVAL
+    assert b"multiple of 4" in lib.ft_last_error()
+    # Hq not a multiple of Hkv
+    assert f(_v(), _v(), _v(), _v(), _v(), 1, 5, 2, 4, 32, U(0)) == FT_EINVAL
+    # dim > 512
+    assert f(_v(), _v(), _v(), _v(), _v(), 1, 2, 1, 4, 516, U(0)) == FT_EINVAL
+    # batch 0 is a valid no-op (no device work at all)
+    assert f(_v(), _v(), _v(), _v(), _v(), 0, 2, 1, 4, 32, U(0)) == FT_OK
+    p = lib.ft_attention_decode_paged_launch
+    # unsupported GQA group on the paged path (reference attention.cu:1806-1811)
+    st = p(_v(), _v(), _v(), _v(), _v(), _v(), 1, 6, 2, 16, 4, 32, U(0))
+    assert st == FT_EINVAL and b"group" in lib.ft_last_error()
+    # page < 1
+    assert p(_v(), _v(), _v(), _v(), _v(), _v(), 1, 2, 2, 0, 4, 32, U(0)) == FT_EINVAL
+    # absurd table capacity
+    assert p(_v(), _v(), _v(), _v(), _v(), _v(), 1, 2, 2, 1 << 16, 1 << 16, 32,
+             U(0)) == FT_EINVAL
+
+
+def test_kv_append_invalid_arguments(lib):
+    f = lib.ft_kv_append_launch
+    assert f(_v(), _v(), _v(), _v(), _v(), 2, 2, 30, 8, U(0)) == FT_EINVAL
+    assert f(_v(), _v(), _v(), _v(), _v(), 0, 2, 30, 8, U(0)) == FT_OK   # batch 0
+    g = lib.ft_kv_append_paged_launch
+    assert g(_v(), _v(), _v(), _v(), _v(), _v(), 2, 2, 32, 0, 4, U(0)) == FT_EINVAL
+
+
+def test_qgemm_invalid_arguments(lib):
+    f = lib.ft_qgemm_launch
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                  ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float,
+                  ctypes.c_size_t]
+    assert f(None, None, None, -1, 4, 4, 1.0, 1.0, 0) == FT_EINVAL
+    assert f(None, None, None, 4, 4, 200000, 1.0, 1.0, 0) == FT_EINVAL
+    assert f(None, None, None, 0, 4, 4, 1.0, 1.0, 0) == FT_OK      # empty
+    g = lib.ft_qgemm_perchannel_launch
+    g.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 3 + [ctypes.c_float,
+                                                             ctypes.c_size_t]
+    st = g(None, None, None, None, 4, 4, 4, 1.0, 0)
+    assert st == FT_EINVAL and b"per-channel" in lib.ft_last_error()
+    h = lib.ft_qgemm_launch_ex
+    h.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float,
+                  ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                  ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_size_t]
+    assert h(None, None, None, 1.0, 1.0, None, None, 7, 4, 4, 4, 0) == FT_EINVAL
+
+
+def test_norm_rope_swiglu_invalid_arguments(lib):
+    r = lib.ft_rmsnorm_launch
+    r.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                          ctypes.c_size_t]
+    assert r(None, None, None, None, 2, 0, 1e-6, 0) == FT_EINVAL
+    assert r(None, None, None, None, 0, 8, 1e-6, 0) == FT_OK           # no rows
+    ro = lib.ft_rope_launch
+    ro.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_float, ctypes.c_int, ctypes.c_size_t]
+    assert ro(None, None, 2, 7, 10000.0, 0, 0) == FT_EINVAL            # odd dim
+    assert ro(None, None, 2, 8, 10000.0, -1, 0) == FT_EINVAL           # offset < 0
+    s = lib.ft_swiglu_launch
+    s.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_longlong, ctypes.c_size_t]
+    assert s(None, None, None, -1, 0) == FT_EINVAL
+    qz = lib.ft_quantize_int8_launch_ex
+    qz.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                   ctypes.c_longlong, ctypes.c_size_t]
+    assert qz(None, 9, None, None, 4, 0) == FT_EINVAL                  # bad dtype

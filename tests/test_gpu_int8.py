@@ -1,0 +1,199 @@
+"""GPU parity, bit-exact: INT8 quantize codes and scale, int32 GEMM
+accumulators and the float32 GEMM epilogue equal the CPU oracle exactly;
+bf16 / fp16 GEMM outputs equal the oracle's float32 value rounded to
+nearest-even. Every GEMM kernel is exercised: skinny (M <= 64, with and
+without the cross-workgroup K split), tiled (M > 64), scalar fallback
+(K % 16 != 0) and the K == 0 zero fill."""
+
+import numpy as np
+import pytest
+import torch
+
+import fusedtok_amd as ft
+import oracle
+from tests import refs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def t(a, dtype=None):
+    x = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    return x if dtype is None else x.to(dtype)
+
+
+def rand_q(rng, rows, k):
+    return rng.integers(-127, 128, size=(rows, k)).astype(np.int8)
+
+
+# ---------------------------------------------------------------------------
+# quantize
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("n", [1, 5, 777, 4096, 65536, 65537, 1 << 20, 3_000_001])
+def test_quantize_f32_bit_exact(n):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 2.5).astype(np.float32)
+    q, s = ft.quantize_int8(t(x))
+    rq, rs = oracle.quantize_int8(x)
+    assert q.dtype == torch.int8 and isinstance(s, float)
+    assert s == rs
+    np.testing.assert_array_equal(q.cpu().numpy(), rq)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n", [4096 * 16, 4096 * 64 + 3])
+def test_quantize_half_input_bit_exact(dt, n):
+    rng = np.random.default_rng(n + 1)
+    xt = torch.from_numpy((rng.standard_normal(n) * 3).astype(np.float32)).to(DEV, dt)
+    q, s = ft.quantize_int8(xt)
+    rq, rs = oracle.quantize_int8(xt.float().cpu().numpy())
+    assert s == rs
+    np.testing.assert_array_equal(q.cpu().numpy(), rq)
+
+
+def test_quantize_known_answers_and_device_scale():
+    q, s = ft.quantize_int8(t(np.array([-2.0, -1.0, 0.0, 1.0, 2.0], np.float32)))
+    assert s == pytest.approx(2.0 / 127.0)
+    assert q.cpu().tolist() == [-127, -64, 0, 64, 127]
+    q, s = ft.quantize_int8(t(np.zeros(8, np.float32)))
+    assert s == 1.0 and (q == 0).all()
+    q, s = ft.quantize_int8(t(np.array([1e30, -1e30], np.float32)))
+    assert q.cpu().tolist() == [127, -127]
+    x = np.random.default_rng(2).standard_normal((16, 4096)).astype(np.float32)
+    q, sd = ft.quantize_int8(t(x), device_scale=True)
+    assert sd.is_cuda and sd.dtype == torch.float32 and sd.numel() == 1
+    rq, rs = oracle.quantize_int8(x)
+    assert float(sd) == rs
+    np.testing.assert_array_equal(q.cpu().numpy(), rq)
+
+
+def test_quantize_misaligned_view_and_staged():
+    x = np.random.default_rng(3).standard_normal(1001).astype(np.float32)
+    xt = t(x)
+    q, s = ft.quantize_int8(xt[1:])          # 4-byte offset view: scalar path
+    rq, rs = oracle.quantize_int8(x[1:])
+    assert s == rs
+    np.testing.assert_array_equal(q.cpu().numpy(), rq)
+    q2, s2 = ft.quantize_int8(x)             # host input -> staged
+    rq2, rs2 = oracle.quantize_int8(x)
+    assert s2 == rs2 and isinstance(q2, np.ndarray)
+    np.testing.assert_array_equal(q2, rq2)
+
+
+# ---------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------
+
+GEMM_SHAPES = [
+    (1, 8, 16),            # skinny, tiny
+    (1, 1000, 4096),       # skinny, decode-like
+    (3, 5, 7),             # scalar fallback (odd K)
+    (8, 11008, 4096),      # BASELINE config 2, M = 8
+    (16, 11008, 4096),     # BASELINE config 2, M = 16
+    (1, 11008, 4096),      # BASELINE config 2, M = 1
+    (33, 300, 1024),       # skinny MT = 4, K split
+    (64, 4096, 4096),      # BASELINE config 4 o_proj shape
+    (64, 512, 14336),      # BASELINE config 4 down-proj K, fewer rows
+    (65, 63, 33),          # scalar fallback
+    (65, 130, 96),         # tiled, ragged edges
+    (128, 256, 512),       # tiled
+    (300, 500, 1024),      # tiled, ragged
+    (17, 4096, 129),       # scalar fallback, tall N
+    (100, 50, 16),         # tiled, single short slab
+    (1024, 1024, 1024),    # tiled, many tiles
+]
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
+def test_qgemm_bit_exact(m, n, k):
+    rng = np.random.default_rng(m * 1000 + n + k)
+    a, b = rand_q(rng, m, k), rand_q(rng, n, k)
+    sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    at, bt = t(a), t(b)
+    acc = ft.qgemm_i32(at, bt)
+    y_pt = ft.qgemm(at, 0.03, bt, 0.02)
+    y_pc = ft.qgemm_perchannel(at, 0.031, bt, t(sb))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(acc.cpu().numpy(), oracle.qgemm_i32(a, b))
+    np.testing.assert_array_equal(y_pt.cpu().numpy(), oracle.qgemm(a, 0.03, b, 0.02))
+    np.testing.assert_array_equal(y_pc.cpu().numpy(),
+                                  oracle.qgemm_perchannel(a, 0.031, b, sb))
+
+
+@pytest.mark.parametrize("kernel", ["1", "2", "3"])
+def test_every_gemm_kernel_bit_exact(kernel, monkeypatch):
+    monkeypatch.setenv("FT_QGEMM_KERNEL", kernel)
+    rng = np.random.default_rng(int(kernel))
+    m = 48 if kernel == "1" else 80
+    a, b = rand_q(rng, m, 640), rand_q(rng, 200, 640)
+    sb = rng.uniform(1e-3, 1e-2, 200).astype(np.float32)
+    y = ft.qgemm_perchannel(t(a), 0.5, t(b), t(sb))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), oracle.qgemm_perchannel(a, 0.5, b, sb))
+
+
+@pytest.mark.parametrize("ksplit", ["1", "2", "4", "7"])
+def test_skinny_k_split_bit_exact_and_counters_reset(ksplit, monkeypatch):
+    monkeypatch.setenv("FT_QGEMM_KSPLIT", ksplit)
+    rng = np.random.default_rng(int(ksplit) + 50)
+    a, b = rand_q(rng, 16, 4096), rand_q(rng, 700, 4096)
+    for rep in range(3):   # repeats reuse the arrival counters
+        acc = ft.qgemm_i32(t(a), t(b))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(acc.cpu().numpy(), oracle.qgemm_i32(a, b))
+
+
+@pytest.mark.parametrize("odt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [16, 256])
+def test_half_outputs_are_rounded_f32(odt, m):
+    rng = np.random.default_rng(m + 9)
+    a, b = rand_q(rng, m, 2048), rand_q(rng, 384, 2048)
+    sb = rng.uniform(1e-3, 1e-2, 384).astype(np.float32)
+    y = ft.qgemm_perchannel(t(a), 0.013, t(b), t(sb), out_dtype=odt)
+    torch.cuda.synchronize()
+    ref = torch.from_numpy(oracle.qgemm_perchannel(a, 0.013, b, sb)).to(odt)
+    assert y.dtype == odt
+    assert torch.equal(y.cpu(), ref)
+
+
+def test_device_scale_operand_matches_host_scale():
+    rng = np.random.default_rng(10)
+    x = rng.standard_normal((8, 1024)).astype(np.float32)
+    b = rand_q(rng, 256, 1024)
+    sb = rng.uniform(1e-3, 1e-2, 256).astype(np.float32)
+    qx, sd = ft.quantize_int8(t(x), device_scale=True)
+    y_dev = ft.qgemm_perchannel(qx, sd, t(b), t(sb))
+    y_host = ft.qgemm_perchannel(qx, float(sd), t(b), t(sb))
+    torch.cuda.synchronize()
+    assert torch.equal(y_dev, y_host)
+    rq, rs = oracle.quantize_int8(x)
+    np.testing.assert_array_equal(y_dev.cpu().numpy(),
+                                  oracle.qgemm_perchannel(rq, rs, b, sb))
+
+
+def test_k0_and_extremes_and_empty():
+    y = ft.qgemm(torch.zeros((4, 0), dtype=torch.int8, device=DEV), 0.5,
+                 torch.zeros((3, 0), dtype=torch.int8, device=DEV), 0.25)
+    y16 = ft.qgemm(torch.zeros((4, 0), dtype=torch.int8, device=DEV), 0.5,
+                   torch.zeros((3, 0), dtype=torch.int8, device=DEV), 0.25,
+                   out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert (y == 0).all() and (y16 == 0).all()
+    a = np.full((70, 4096), -128, np.int8)
+    b = np.full((33, 4096), -128, np.int8)
+    acc = ft.qgemm_i32(t(a), t(b))
+    torch.cuda.synchronize()
+    assert (acc.cpu().numpy() == 128 * 128 * 4096).all()
+    e = ft.qgemm(torch.zeros((0, 16), dtype=torch.int8, device=DEV), 1.0,
+                 torch.zeros((5, 16), dtype=torch.int8, device=DEV), 1.0)
+    assert e.shape == (0, 5)
+
+
+def test_staged_host_gemm():
+    rng = np.random.default_rng(12)
+    a, b = rand_q(rng, 20, 256), rand_q(rng, 30, 256)
+    sb = rng.uniform(1e-3, 1e-2, 30).astype(np.float32)
+    y = ft.qgemm_perchannel(a, 0.1, b, sb, cuda=True)
+    np.testing.assert_array_equal(y, refs.ref_qgemm_pc(a, 0.1, b, sb))
