@@ -1,0 +1,308 @@
+#!/usr/bin/env python3
+"""Benchmark of the decode hot path on one MI355X.
+
+Headline workload: paged flash-decoding with GQA, bf16,
+batch 32, 32 query heads, 8 KV heads, head_dim 128, page size 16, per-row
+context lengths uniform in [512, 32768], block table a seeded random
+permutation of a page pool four times larger than the pages in use. One
+"step" is what a decode loop does per token: kv_append_paged of one new
+token per row at position lens[b], then attention_decode_paged over
+lens[b] + 1 tokens.
+
+  value     = algorithmic bytes per step / measured step time   (GB/s)
+              bytes: K+V rows read (sum_b (lens_b+1) * Hkv * D * 2 * 2 B),
+              q, out, the block-table entries of the pages in use, and the
+              kv_append copy (read + write of the new K/V rows). This is the
+              reference's counting (benchmarks/bench.py:480,496) plus the
+              table and the append.
+  roofline  = attention only (stage-1 chunk kernel + combine kernel, timed
+              together with HIP events recorded on the stream they are
+              launched on): attention bytes / attention time, against
+              8 TB/s.
+  secondary = BASELINE config 5a: W8A8 GEMM M=4096 K=8192 N=28672, int8
+              uniform in [-127, 127], per-channel scales, bf16 output;
+              TOPS = 2*M*N*K / t (reference benchmarks/bench.py:451), against
+              the 5.0 POP/s dense int8 MFMA peak.
+  cpu_baseline = the C++ restatement of the reference's single-threaded
+              attention_decode_paged_cpu / kv_append_paged_cpu (oracle/),
+              on a bounded sample of the same rows, one core.
+
+`traffic` (HBM bytes per launch, from rocprofv3 FETCH_SIZE / WRITE_SIZE
+counters scaled by a copy-kernel calibration) is read from
+profiles/hbm_traffic.json when that file holds an entry for the kernel.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+
+C3 = dict(batch=32, hq=32, hkv=8, dim=128, page=16, len_lo=512, len_hi=32768,
+          pool_factor=4, seed=2026)
+C5A = dict(m=4096, k=8192, n=28672, seed=5)
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true",
+                   help="skip the CPU baseline leg")
+    p.add_argument("--no-gemm", action="store_true",
+                   help="skip the secondary W8A8 GEMM measurement")
+    p.add_argument("--only", choices=["decode", "gemm"], default=None,
+                   help="run one workload only (profiling runs)")
+    return p.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# config 3 workload
+# ---------------------------------------------------------------------------
+def make_c3(torch, np, dev):
+    c = C3
+    rng = np.random.default_rng(c["seed"])
+    b, hq, hkv, d, page = c["batch"], c["hq"], c["hkv"], c["dim"], c["page"]
+    lens = rng.integers(c["len_lo"], c["len_hi"] + 1, size=b).astype(np.int32)
+    npg = (lens + 1 + page - 1) // page           # pages after the append
+    width = int(npg.max())
+    used = int(npg.sum())
+    pool = used * c["pool_factor"]
+    perm = rng.permutation(pool).astype(np.int32)
+    table = np.zeros((b, width), np.int32)
+    off = 0
+    for i in range(b):
+        table[i, :npg[i]] = perm[off:off + npg[i]]
+        off += npg[i]
+    gen = torch.Generator(device=dev).manual_seed(c["seed"])
+    bf = torch.bfloat16
+    kp = torch.empty((pool, hkv, page, d), dtype=bf, device=dev)
+    vp = torch.empty((pool, hkv, page, d), dtype=bf, device=dev)
+    for t in (kp, vp):  # N(0,1), generated in slabs to bound the f32 temp
+        flat = t.view(pool, -1)
+        for s in range(0, pool, 8192):
+            e = min(pool, s + 8192)
+            flat[s:e].copy_(torch.randn((e - s, flat.shape[1]), device=dev,
+                                        generator=gen))
+    q = torch.randn((b, hq, d), device=dev, generator=gen).to(bf)
+    kn = torch.randn((b, hkv, d), device=dev, generator=gen).to(bf)
+    vn = torch.randn((b, hkv, d), device=dev, generator=gen).to(bf)
+    w = dict(lens=lens, table=table, kp=kp, vp=vp, q=q, kn=kn, vn=vn,
+             lens_t=torch.from_numpy(lens).to(dev),
+             lens1_t=torch.from_numpy(lens + 1).to(dev),
+             table_t=torch.from_numpy(table).to(dev),
+             pool_pages=pool, used_pages=used)
+    tokens = int((lens + 1).sum())
+    w["attn_bytes"] = (tokens * hkv * d * 2 * 2      # K + V rows
+                       + 2 * b * hq * d * 2          # q + out
+                       + used * 4 + b * 4)           # table entries + lens
+    w["append_bytes"] = 2 * (2 * b * hkv * d * 2) + b * 4 + b * 4
+    w["tokens"] = tokens
+    return w
+
+
+def c3_step(ft, w):
+    ft.kv_append_paged(w["kp"], w["vp"], w["table_t"], w["kn"], w["vn"],
+                       w["lens_t"])
+    ft.attention_decode_paged(w["q"], w["kp"], w["vp"], w["table_t"],
+                              w["lens1_t"])
+
+
+def bench_c3(torch, np, ft, dev, steps, warmup):
+    w = make_c3(torch, np, dev)
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        c3_step(ft, w)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()   # the stream ft launches on
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ft.kv_append_paged(w["kp"], w["vp"], w["table_t"], w["kn"], w["vn"],
+                           w["lens_t"])
+        ev[i][0].record(stream)
+        ft.attention_decode_paged(w["q"], w["kp"], w["vp"], w["table_t"],
+                                  w["lens1_t"])
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    attn_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
+    return w, wall, attn_ms
+
+
+# ---------------------------------------------------------------------------
+# config 5a workload (secondary)
+# ---------------------------------------------------------------------------
+def bench_c5a(torch, ft, dev, steps, warmup):
+    c = C5A
+    gen = torch.Generator(device=dev).manual_seed(c["seed"])
+    m, k, n = c["m"], c["k"], c["n"]
+    a = torch.randint(-127, 128, (m, k), device=dev, generator=gen,
+                      dtype=torch.int32).to(torch.int8)
+    bq = torch.randint(-127, 128, (n, k), device=dev, generator=gen,
+                       dtype=torch.int32).to(torch.int8)
+    sb = (torch.rand((n,), device=dev, generator=gen) * 9e-3 + 1e-3).float()
+    sa = 0.0123
+    for _ in range(warmup):
+        ft.qgemm_perchannel(a, sa, bq, sb, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        ft.qgemm_perchannel(a, sa, bq, sb, out_dtype=torch.bfloat16)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    ops = 2.0 * m * n * k
+    tops = ops / (ms * 1e-3) / 1e12
+    return dict(metric="W8A8 GEMM TOPS (BASELINE config 5a)", value=round(tops, 2),
+                unit="TOPS", ms_per_launch=round(ms, 4), dtype="int8",
+                config={"workload": "qgemm_perchannel M=4096 K=8192 N=28672, bf16 out",
+                        "seed": c["seed"]},
+                roofline={"bound": "mfma", "achieved": round(tops, 2),
+                          "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                          "frac": round(tops / INT8_PEAK_TOPS, 4),
+                          "traffic": traffic_for("qgemm_c5a")})
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle on a bounded sample of config 3's rows
+# ---------------------------------------------------------------------------
+def cpu_baseline_c3(torch, np, w, budget_s=12.0):
+    import oracle
+    c = C3
+    page, hkv, d = c["page"], c["hkv"], c["dim"]
+    lens, table = w["lens"], w["table"]
+    done_rows, done_bytes, spent = 0, 0, 0.0
+    for i in range(len(lens)):
+        npg = (int(lens[i]) + 1 + page - 1) // page
+        blocks = torch.from_numpy(table[i, :npg].astype(np.int64)).to(w["kp"].device)
+        # the row's pages as the oracle sees them (bf16 values widened to f32),
+        # taken BEFORE the append so the CPU leg does the same work
+        kp = w["kp"][blocks].float().cpu().numpy()
+        vp = w["vp"][blocks].float().cpu().numpy()
+        q = w["q"][i:i + 1].float().cpu().numpy()
+        kn = w["kn"][i:i + 1].float().cpu().numpy()
+        vn = w["vn"][i:i + 1].float().cpu().numpy()
+        sub = np.arange(npg, dtype=np.int32)[None, :]
+        ln = lens[i:i + 1].astype(np.int32)
+        t0 = time.perf_counter()
+        oracle.kv_append_paged(kp, vp, sub, kn, vn, ln)
+        oracle.attention_decode_paged(q, kp, vp, sub, ln + 1)
+        spent += time.perf_counter() - t0
+        done_rows += 1
+        done_bytes += ((int(lens[i]) + 1) * hkv * d * 2 * 2 + 2 * c["hq"] * d * 2
+                       + npg * 4 + 4 + 2 * 2 * hkv * d * 2)
+        if spent >= budget_s:
+            break
+    gbs = done_bytes / spent / 1e9
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{done_rows} of {len(lens)} config-3 rows "
+                      f"(kv_append_paged + attention_decode_paged, "
+                      f"{int(lens[:done_rows].sum()) + done_rows} tokens), "
+                      f"oracle/oracle.cpp restatement of the reference *_cpu "
+                      f"functions, g++ -O2, single thread, {spent:.2f} s"}
+
+
+def traffic_for(key):
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(key, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this "
+              "build's decode path is single-GPU; run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import fusedtok_amd as ft
+    if not ft.cuda_available():
+        print("no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    if args.only == "gemm":
+        log("gemm", json.dumps(bench_c5a(torch, ft, dev, args.steps, args.warmup)))
+        return
+
+    log(f"config 3: building workload (seed {C3['seed']})")
+    w, wall, attn_ms = bench_c3(torch, np, ft, dev, args.steps, args.warmup)
+    step_bytes = w["attn_bytes"] + w["append_bytes"]
+    ms_step = wall / args.steps * 1e3
+    value = step_bytes / (wall / args.steps) / 1e9
+    attn_gbs = w["attn_bytes"] / (attn_ms * 1e-3) / 1e9
+    log(f"config 3: {ms_step:.4f} ms/step, {value:.1f} GB/s; attention "
+        f"{attn_ms * 1e3:.1f} us, {attn_gbs:.1f} GB/s")
+
+    secondary = None
+    if not args.no_gemm and args.only is None:
+        del w["kp"], w["vp"]
+        torch.cuda.empty_cache()
+        secondary = bench_c5a(torch, ft, dev, max(5, args.steps // 2), 3)
+        log(f"config 5a: {secondary['value']} TOPS")
+
+    cpu = None
+    if not args.no_cpu and args.only is None:
+        w2 = make_c3(torch, np, dev)  # pools were released for the GEMM leg
+        cpu = cpu_baseline_c3(torch, np, w2)
+        log(f"cpu baseline: {cpu['value']} GB/s over {cpu['sample']}")
+
+    line = {
+        "metric": "flash-decode KV GB/s (% HBM peak); W8A8 GEMM TOPS (% int8 MFMA peak)",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V/q, lens ~ U[512,32768], permuted page pool)",
+        "config": {"workload": "BASELINE config 3: kv_append_paged + "
+                               "attention_decode_paged, bf16, B=32 Hq=32 Hkv=8 "
+                               "D=128 P=16",
+                   "seed": C3["seed"], "tokens": w["tokens"],
+                   "pool_pages": w["pool_pages"], "used_pages": w["used_pages"],
+                   "bytes_per_step": step_bytes, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_for("attention_c3"),
+                     "kernel": "attention_decode_paged (chunk + combine)",
+                     "avg_us": round(attn_ms * 1e3, 2),
+                     "bytes_per_launch": w["attn_bytes"]},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -37,6 +37,13 @@ accumulators); per-row RoPE positions (``positions=``).
 
 import numpy as np
 
+# torch first: its bundled HIP runtime (libamdhip64.so, soname
+# libamdhip64.so.7) must be the one loaded in this process, so that the
+# library's own libamdhip64.so.7 dependency binds to it by soname. Loading the
+# library first would pull in a second HIP runtime from /opt/rocm; two
+# runtimes in one process do not share devices or stream handles.
+import torch
+
 try:
     from . import _fusedtok
 except ImportError as exc:  # pragma: no cover - exercised by packaging
@@ -45,8 +52,6 @@ except ImportError as exc:  # pragma: no cover - exercised by packaging
         "`python -c 'import __graft_entry__ as g; g.build()'` from the "
         "repository root (needs hipcc for gfx950)."
     ) from exc
-
-import torch
 
 __version__ = "0.1.0"
 

@@ -60,6 +60,14 @@ __device__ __forceinline__ int pow2_ceil_dev(int x) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Device-resident lengths are not read back by the host. A length outside
+// [0, span] (span = the cache's row capacity) is clamped into it, so no
+// value can make a kernel index past the cache or the block table.
+__device__ __forceinline__ int clamp_len(const int* lens, int b, int span) {
+    if (!lens) return span;
+    return min(max(lens[b], 0), span);
+}
+
 // Chunk length: a power of two in [lo, hi] so that the capacity grid holds
 // about `target` units.
 int choose_chunk(int batch, int hkv, long long span, int lo, int hi,
@@ -108,7 +116,7 @@ __global__ __launch_bounds__(kGenNT) void attn_chunk_generic(
     const int b = blockIdx.x / per_b;
     const int kv = (blockIdx.x - b * per_b) / cmax;
     const int c = blockIdx.x - b * per_b - kv * cmax;
-    const int len = lens ? lens[b] : span;
+    const int len = clamp_len(lens, b, span);
     const int t0 = c * chunk;
     if (t0 >= len) return;
     const int n = min(chunk, len - t0);
@@ -290,7 +298,7 @@ __global__ __launch_bounds__(256) void attn_chunk_mfma(
     const int b = blockIdx.x / per_b;
     const int kv = (blockIdx.x - b * per_b) / cmax;
     const int c = blockIdx.x - b * per_b - kv * cmax;
-    const int len = lens ? lens[b] : span;
+    const int len = clamp_len(lens, b, span);
     const int t0 = c * chunk;
     if (t0 >= len) return;
     const int n = min(chunk, len - t0);
@@ -460,7 +468,7 @@ __global__ __launch_bounds__(64) void attn_combine(
     const int h = blockIdx.x - b * hq;
     const int kv = h / group, gi = h - kv * group;
     const int lane = threadIdx.x;
-    const int len = lens ? lens[b] : span;
+    const int len = clamp_len(lens, b, span);
     const int nch = len > 0 ? (len + chunk - 1) / chunk : 0;
     const int dc = dim >> 2;
     T* o = out + ((size_t)b * hq + h) * dim;
@@ -608,14 +616,18 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
 template <typename T>
 __global__ __launch_bounds__(256) void kv_append_kernel(
     const T* __restrict__ k_new, const T* __restrict__ v_new,
-    const int* __restrict__ lens, RowMap rm, T* __restrict__ k_dst,
-    T* __restrict__ v_dst) {
-    const int b = blockIdx.y;
+    const int* __restrict__ lens, RowMap rm, int capacity, int per_row,
+    T* __restrict__ k_dst, T* __restrict__ v_dst) {
+    const int b = blockIdx.x / per_row;
     const int dc = rm.dim >> 2;
-    const int idx = blockIdx.x * 256 + threadIdx.x;
+    const int idx = (blockIdx.x - b * per_row) * 256 + threadIdx.x;
     if (idx >= rm.hkv * dc) return;
     const int h = idx / dc, ch = idx - h * dc;
-    const size_t dst = rm(b, h, lens[b]) + 4 * ch;
+    const int pos = lens[b];
+    // device lengths are trusted by the API but never turned into an
+    // out-of-range address: a position outside [0, capacity) writes nothing
+    if (pos < 0 || pos >= capacity) return;
+    const size_t dst = rm(b, h, pos) + 4 * ch;
     const size_t src = ((size_t)b * rm.hkv + h) * rm.dim + 4 * ch;
     if (sizeof(T) == 4) {
         *reinterpret_cast<float4*>(k_dst + dst) = *reinterpret_cast<const float4*>(k_new + src);
@@ -631,10 +643,11 @@ void kv_append_run(const T* k_new, const T* v_new, const int* table,
                    const int* lens, T* k_dst, T* v_dst, int batch, int hkv,
                    int dim, int rows_or_page, int tbl_width, bool paged,
                    hipStream_t s) {
-    if (batch <= 0) return;
+    if (batch <= 0) return;  // nothing to append (reference attention.cu:1930-1931)
     if (dim % 4 != 0) inval("dim must be a multiple of 4");
     if (paged && rows_or_page < 1) inval("page size must be >= 1");
-    if (hkv < 1 || dim < 1) inval("kv heads and dim must be >= 1");
+    if (hkv < 1 || dim < 1 || dim > kMaxDim) inval("kv heads >= 1 and 1 <= dim <= 512 required");
+    if (rows_or_page < 0 || tbl_width < 0) inval("cache rows / table width must be >= 0");
     if (!k_new || !v_new || !lens || !k_dst || !v_dst || (paged && !table))
         inval("kv append: null operand");
     RowMap rm;
@@ -649,9 +662,15 @@ void kv_append_run(const T* k_new, const T* v_new, const int* table,
         while ((1 << sh) < rows_or_page) ++sh;
         rm.page_shift = sh;
     }
+    const long long cap = paged ? (long long)tbl_width * rows_or_page
+                                : (long long)rows_or_page;
+    if (cap > (1LL << 30)) inval("cache capacity too large");
+    if (cap == 0) return;  // no row can hold the token
     const int chunks = hkv * (dim / 4);
-    dim3 grid((unsigned)((chunks + 255) / 256), (unsigned)batch);
-    kv_append_kernel<T><<<grid, 256, 0, s>>>(k_new, v_new, lens, rm, k_dst, v_dst);
+    const int per_row = (chunks + 255) / 256;
+    if ((long long)batch * per_row > (1LL << 31) - 1) inval("kv append: batch too large");
+    kv_append_kernel<T><<<(unsigned)(batch * per_row), 256, 0, s>>>(
+        k_new, v_new, lens, rm, (int)cap, per_row, k_dst, v_dst);
     launch_check("kv append kernel launch");
 }
 

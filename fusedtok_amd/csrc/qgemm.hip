@@ -53,8 +53,14 @@ __device__ __forceinline__ void epi_store(const Epi& e, float sa, int n,
     if constexpr (OUT == kOutI32) {
         static_cast<int*>(e.y)[idx] = acc;
     } else {
+        // Two f32 roundings (scale, then product), then one to the output
+        // type - never fused: the backend would otherwise fold the product
+        // and an f16 narrowing into one single-rounding mixed-precision FMA
+        // (v_fma_mixlo_f16), which can land on the other side of an f16
+        // tie. The empty asm makes the rounded f32 product opaque to it.
         const float s = e.sb_vec ? sa * e.sb_vec[col] : sa * e.sb;
-        const float val = (float)acc * s;
+        float val = (float)acc * s;
+        asm("" : "+v"(val));
         if constexpr (OUT == kOutF32) static_cast<float*>(e.y)[idx] = val;
         if constexpr (OUT == kOutBF16) static_cast<bf16*>(e.y)[idx] = (bf16)val;
         if constexpr (OUT == kOutF16) static_cast<f16*>(e.y)[idx] = (f16)val;

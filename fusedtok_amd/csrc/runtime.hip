@@ -79,14 +79,11 @@ void* scratch_impl(Scratch which, size_t bytes, hipStream_t s, bool zero) {
         throw Error{FT_EHIP,
                     "device scratch must grow outside a HIP graph capture: "
                     "run the shape once before capturing it"};
-    if (slot.ptr) {
-        // in-flight kernels may still read the old buffer
-        hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize (scratch grow)");
-        hip_check(hipFree(slot.ptr), "hipFree (scratch grow)");
-        slot.ptr = nullptr;
-        slot.bytes = 0;
-    }
+    // A grown slot's old buffer is retired, never freed: in-flight kernels
+    // and HIP graphs captured earlier still hold its address. Growth is
+    // geometric, so a process retires at most a few dozen buffers.
     size_t want = bytes < 4096 ? 4096 : bytes;
+    if (slot.ptr && want < 2 * slot.bytes) want = 2 * slot.bytes;
     want = (want + 4095) & ~(size_t)4095;
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, want);

@@ -2,6 +2,9 @@ import os
 import sys
 
 import pytest
+# torch's HIP runtime must be loaded before libfusedtok_amd.so (which binds to
+# it by soname) in every test process, whichever test module loads first
+import torch  # noqa: F401
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:

@@ -8,6 +8,7 @@ import os
 import re
 
 import pytest
+import torch  # noqa: F401  (HIP runtime first: the library binds to it)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "fusedtok_amd.h")

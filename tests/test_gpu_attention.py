@@ -291,7 +291,11 @@ def test_paged_graph_capture_replay():
     232-267)."""
     rng = np.random.default_rng(77)
     dt = torch.bfloat16
-    q, kp, vp, tbl, ln = paged_case(rng, 4, 32, 8, 128, [500, 900, 33, 1200])
+    # the table covers lens + 1 rows: the appended token lands at lens[b]
+    # (1200 fills page 75 exactly, so the append needs a 76th page)
+    q, kp, vp, tbl, ln1 = paged_case(rng, 4, 32, 8, 128, [501, 901, 34, 1201])
+    ln = ln1 - 1
+    assert (ln < tbl.shape[1] * 16).all()
     qt, kpt, vpt, tblt, lnt = t(q, dt), t(kp, dt), t(vp, dt), t(tbl), t(ln)
     kn = t(rng.standard_normal((4, 8, 128)).astype(np.float32), dt)
     vn = t(rng.standard_normal((4, 8, 128)).astype(np.float32), dt)
