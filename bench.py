@@ -61,8 +61,10 @@ def parse():
                    help="skip the CPU baseline leg")
     p.add_argument("--no-gemm", action="store_true",
                    help="skip the secondary W8A8 GEMM measurement")
-    p.add_argument("--only", choices=["decode", "gemm"], default=None,
-                   help="run one workload only (profiling runs)")
+    p.add_argument("--only", choices=["decode", "gemm", "copy"], default=None,
+                   help="run one workload only (profiling runs); 'copy' is "
+                        "the HBM-counter calibration: a plain 1 GiB "
+                        "device-to-device tensor copy")
     return p.parse_args()
 
 
@@ -246,6 +248,14 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
 
+    if args.only == "copy":
+        src = torch.ones((1 << 29,), dtype=torch.bfloat16, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy: {args.warmup + args.steps} x 1 GiB read + 1 GiB written")
+        return
     if args.only == "gemm":
         log("gemm", json.dumps(bench_c5a(torch, ft, dev, args.steps, args.warmup)))
         return
@@ -258,6 +268,8 @@ def main():
     attn_gbs = w["attn_bytes"] / (attn_ms * 1e-3) / 1e9
     log(f"config 3: {ms_step:.4f} ms/step, {value:.1f} GB/s; attention "
         f"{attn_ms * 1e3:.1f} us, {attn_gbs:.1f} GB/s")
+    if args.only == "decode":
+        return
 
     secondary = None
     if not args.no_gemm and args.only is None:
