@@ -15,11 +15,12 @@
 // row's partials with the log-sum-exp rule and divides by l. len == 0 rows
 // produce zeros (reference attention.cu:1349-1350).
 //
-// Two stage-1 kernels:
-//   attn_chunk_mfma    bf16/fp16 storage, D == 128, G <= 16: QK^T and PV on
+// Two kernel families, each followed by attn_combine:
+//   attn_decode_mfma   bf16/fp16 storage, D == 128, G <= 16: QK^T and PV on
 //                      the matrix cores (v_mfma_f32_16x16x32_{bf16,f16});
 //                      every K/V byte is read once, straight into the MFMA
-//                      operand layout with 16-byte loads.
+//                      operand layout with 16-byte loads, double-buffered;
+//                      single-chunk rows are finished in the kernel.
 //   attn_chunk_generic any storage type, D % 4 == 0 <= 512, any G: VALU
 //                      dot products, chunk scores staged in LDS.
 #include "ft_common.hpp"
@@ -235,12 +236,12 @@ __global__ __launch_bounds__(kGenNT) void attn_chunk_generic(
 }
 
 // ---------------------------------------------------------------------------
-// MFMA stage 1 (bf16 / fp16 storage, D == 128, G <= 16)
+// MFMA decode kernel (bf16 / fp16 storage, D == 128, G <= 16)
 //
-// Each of the 4 waves walks 32-token steps st = wave, wave+4, ... of the
-// unit's chunk with its own online-softmax state, then the waves merge in
-// LDS. With r = lane % 16 and g = lane / 16 (lane layout of
-// v_mfma_f32_16x16x32: A[r][8g+i], B[8g+i][r], C[4g+i][r]):
+// One workgroup = one unit (sequence b, kv head, token chunk). Its 4 waves
+// walk 32-token steps st = wave, wave+4, ... with their own online-softmax
+// state, then merge in LDS. With r = lane % 16 and g = lane / 16 (lane layout
+// of v_mfma_f32_16x16x32: A[r][8g+i], B[8g+i][r], C[4g+i][r]):
 //
 //  scores   S^T[tok][head] = K[tok][:] . Q[head][:]  (4 MFMAs per 16 tokens)
 //           A = K rows: lane loads K[tok r][32j+8g .. +7], one 16-byte load
@@ -260,6 +261,20 @@ __global__ __launch_bounds__(kGenNT) void attn_chunk_generic(
 //           lane belongs to head r, so the online rescale is per lane.
 //           bf16 P is split into hi + lo parts (two MFMAs) so the weights
 //           carry ~16 mantissa bits; fp16 P carries 11.
+//
+// Memory pipeline: the unit's block-table slice is staged in LDS once, so a
+// step's 16 loads per lane depend on no other global load; each wave holds
+// two steps of K/V in registers and issues step st+4's loads before it
+// computes step st (the prefetch is unconditional - clamped to the last
+// step - so the compiler's wait counts stay exact). Token indices past the
+// chunk's end are clamped to its last row (a real row) and masked to -inf.
+//
+// Combine: a row that fits one chunk is normalised and stored here (the
+// combine kernel skips it). Otherwise every unit writes its f32
+// (m, l, acc[D]) partial per head and attn_combine folds them after the
+// kernel boundary. (Folding in the last-arriving unit instead needs a
+// device-scope release/acquire per unit - an L2 writeback + invalidate on
+// gfx950 - which costs far more than the second launch.)
 // ---------------------------------------------------------------------------
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -281,31 +296,74 @@ template <> struct Mfma<f16> {
 
 constexpr int kMfmaDim = 128;
 constexpr int kMfmaAccPitch = kMfmaDim + 4;   // LDS row pitch (bank spread)
+constexpr int kMfmaMaxChunk = 1024;
+constexpr int kMfmaTblSlots = kMfmaMaxChunk + 2;  // pages one chunk can touch
 
-template <typename T>
-__global__ __launch_bounds__(256) void attn_chunk_mfma(
+template <typename T, bool PAGED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_decode_mfma(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    const int* __restrict__ lens, RowMap rm, float* __restrict__ ws_ml,
-    float* __restrict__ ws_acc, int hq, int group, int span, int chunk,
-    int cmax, float scale_log2) {
+    const int* __restrict__ table, const int* __restrict__ lens,
+    float* __restrict__ ws_ml, float* __restrict__ ws_acc,
+    T* __restrict__ out, int hq, int hkv, int group, int rows_or_page,
+    int page_shift, int tbl_width, int span, int chunk, int cmax,
+    float scale_log2) {
     using M = Mfma<T>;
     using V8 = typename M::v8;
     constexpr int D = kMfmaDim;
     __shared__ float s_acc[4][16][kMfmaAccPitch];
     __shared__ float s_m[4][16], s_l[4][16];
+    __shared__ int s_tbl[PAGED ? kMfmaTblSlots : 1];
 
-    const int per_b = rm.hkv * cmax;
+    const int per_b = hkv * cmax;
     const int b = blockIdx.x / per_b;
     const int kv = (blockIdx.x - b * per_b) / cmax;
     const int c = blockIdx.x - b * per_b - kv * cmax;
     const int len = clamp_len(lens, b, span);
     const int t0 = c * chunk;
-    if (t0 >= len) return;
-    const int n = min(chunk, len - t0);
-
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    // wave-uniform in a scalar register, so the step loop branches on
+    // scalars
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15, g = lane >> 4;
+    T* const orow = out + ((size_t)b * hq + (size_t)kv * group) * D;  // G rows
+    if (t0 >= len) {
+        // an empty row is all zeros (reference attention.cu:1349-1350)
+        if (len == 0 && c == 0)
+            for (int i = tid; i < group * (D / 4); i += 256)
+                St<T>::st4(orow + 4 * i, make_float4(0.f, 0.f, 0.f, 0.f));
+        return;
+    }
+    const int n = min(chunk, len - t0);
+    const int nch = (len + chunk - 1) / chunk;
+
+    int p0 = 0;
+    if constexpr (PAGED) {
+        const int last = t0 + n - 1;
+        p0 = page_shift >= 0 ? (t0 >> page_shift) : t0 / rows_or_page;
+        const int p1 = page_shift >= 0 ? (last >> page_shift) : last / rows_or_page;
+        const int* trow = table + (size_t)b * tbl_width;
+        for (int i = tid; i <= p1 - p0; i += 256) s_tbl[i] = trow[p0 + i];
+        __syncthreads();
+    }
+    auto row_off = [&](int tok) -> size_t {
+        const int t = t0 + tok;
+        if constexpr (PAGED) {
+            int pg, off;
+            if (page_shift >= 0) {
+                pg = t >> page_shift;
+                off = t & (rows_or_page - 1);
+            } else {
+                pg = t / rows_or_page;
+                off = t - pg * rows_or_page;
+            }
+            const int blk = s_tbl[pg - p0];
+            return (((size_t)blk * hkv + kv) * rows_or_page + off) * D;
+        } else {
+            return (((size_t)b * hkv + kv) * rows_or_page + t) * D;
+        }
+    };
 
     // B operand of the score MFMAs: Q[head r][32j + 8g .. +7]
     V8 qb[4];
@@ -331,25 +389,20 @@ __global__ __launch_bounds__(256) void attn_chunk_mfma(
     for (int i = 0; i < 8; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    const int nsteps = (n + 31) >> 5;
-    for (int st = wave; st < nsteps; st += 4) {
-        const int tb = st << 5;
-        V8 kt[2][4], vt[2][4];
+    auto load_step = [&](int st, V8 (&kt)[2][4], V8 (&vt)[2][4]) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int tok = tb + 16 * h + r;
-            const bool ok = tok < n;
-            const size_t off = rm(b, kv, t0 + (ok ? tok : 0));
-            const T* kr = k + off + 8 * g;
-            const T* vr = v + off + 8 * g;
+            const int tok = min((st << 5) + 16 * h + r, n - 1);
+            const size_t off = row_off(tok) + 8 * g;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                V8 z = {};
-                kt[h][j] = ok ? *reinterpret_cast<const V8*>(kr + 32 * j) : z;
-                vt[h][j] = ok ? *reinterpret_cast<const V8*>(vr + 32 * j) : z;
+                kt[h][j] = *reinterpret_cast<const V8*>(k + off + 32 * j);
+                vt[h][j] = *reinterpret_cast<const V8*>(v + off + 32 * j);
             }
         }
-        // scores
+    };
+    auto compute_step = [&](int st, const V8 (&kt)[2][4], const V8 (&vt)[2][4]) {
+        const int tb = st << 5;
         f32x4 s[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -389,7 +442,6 @@ __global__ __launch_bounds__(256) void attn_chunk_mfma(
             pb[i] = (T)p[i];
             if (M::kSplitP) pl[i] = (T)(p[i] - (float)pb[i]);
         }
-        // transpose V on the matrix cores, then PV
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -407,6 +459,23 @@ __global__ __launch_bounds__(256) void attn_chunk_mfma(
                 if (M::kSplitP) acc[2 * j + e] = M::mma(va, pl, acc[2 * j + e]);
             }
         }
+    };
+
+    const int nsteps = (n + 31) >> 5;
+    int st = wave;
+    if (st < nsteps) {
+        V8 ka[2][4], va_[2][4], kb[2][4], vb[2][4];
+        load_step(st, ka, va_);
+        while (true) {
+            load_step(min(st + 4, nsteps - 1), kb, vb);
+            compute_step(st, ka, va_);
+            st += 4;
+            if (st >= nsteps) break;
+            load_step(min(st + 4, nsteps - 1), ka, va_);
+            compute_step(st, kb, vb);
+            st += 4;
+            if (st >= nsteps) break;
+        }
     }
 
     // fold the 4 lane groups' l, publish per-wave state, merge the waves
@@ -422,8 +491,31 @@ __global__ __launch_bounds__(256) void attn_chunk_mfma(
         for (int i = 0; i < 4; ++i) s_acc[wave][r][16 * nn + 4 * g + i] = acc[nn][i];
     __syncthreads();
 
-    const size_t slot0 = (((size_t)b * rm.hkv + kv) * cmax + c) * group;
     const int nvec = group * (D / 4);
+    if (nch == 1) {  // the whole row is this unit: normalise and store
+        for (int idx = tid; idx < nvec; idx += 256) {
+            const int hh = idx / (D / 4);
+            const int d4 = idx - hh * (D / 4);
+            float mx = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) mx = fmaxf(mx, s_m[w][hh]);
+            float lsum = 0.0f;
+            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float wt = exp2f(s_m[w][hh] - mx);
+                lsum += s_l[w][hh] * wt;
+                const float4 a = *reinterpret_cast<const float4*>(&s_acc[w][hh][4 * d4]);
+                o.x += wt * a.x; o.y += wt * a.y; o.z += wt * a.z; o.w += wt * a.w;
+            }
+            const float inv = 1.0f / lsum;
+            St<T>::st4(orow + (size_t)hh * D + 4 * d4,
+                       make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv));
+        }
+        return;
+    }
+
+    const size_t slot0 = (((size_t)b * hkv + kv) * cmax + c) * group;
     for (int idx = tid; idx < nvec; idx += 256) {
         const int hh = idx / (D / 4);
         const int d4 = idx - hh * (D / 4);
@@ -456,14 +548,19 @@ __global__ __launch_bounds__(256) void attn_chunk_mfma(
 }
 
 // ---------------------------------------------------------------------------
-// combine: one wave per (b, q head). Folds the live chunks' partials
-// (m in log2 units) with the log-sum-exp rule and divides by l.
+// combine: one wave per (b, q head). Folds the live chunks' partials (m in
+// log2 units) with the log-sum-exp rule and divides by l. The wave's lanes
+// are split into groups of L = min(64, pow2ceil(D/4)) lanes; each group
+// walks every (64/L)-th chunk over the row's D/4 float4 columns, and the
+// groups are summed with xor shuffles at the end (fixed order).
+// skip_single: rows of exactly one chunk were already normalised and stored
+// by the stage-1 kernel.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, int CPL>
 __global__ __launch_bounds__(64) void attn_combine(
     const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
     const int* __restrict__ lens, T* __restrict__ out, int hq, int hkv,
-    int group, int dim, int span, int chunk, int cmax) {
+    int group, int dim, int span, int chunk, int cmax, int skip_single) {
     const int b = blockIdx.x / hq;
     const int h = blockIdx.x - b * hq;
     const int kv = h / group, gi = h - kv * group;
@@ -477,9 +574,11 @@ __global__ __launch_bounds__(64) void attn_combine(
             St<T>::st4(o + 4 * ch, make_float4(0.f, 0.f, 0.f, 0.f));
         return;
     }
+    if (skip_single && nch == 1) return;
     const size_t s0 = ((size_t)b * hkv + kv) * cmax * group + gi;
     float mx = -INFINITY;
-    for (int cc = lane; cc < nch; cc += 64) mx = fmaxf(mx, ws_ml[(s0 + (size_t)cc * group) * 2]);
+    for (int cc = lane; cc < nch; cc += 64)
+        mx = fmaxf(mx, ws_ml[(s0 + (size_t)cc * group) * 2]);
     mx = wave_max(mx);
     float lsum = 0.0f;
     for (int cc = lane; cc < nch; cc += 64) {
@@ -487,26 +586,64 @@ __global__ __launch_bounds__(64) void attn_combine(
         lsum += ws_ml[sl * 2 + 1] * exp2f(ws_ml[sl * 2] - mx);
     }
     lsum = wave_sum(lsum);
-    float4 a0 = make_float4(0.f, 0.f, 0.f, 0.f), a1 = a0;
-    for (int cc = 0; cc < nch; ++cc) {
+
+    int L = 1;
+    while (L < dc && L < 64) L <<= 1;
+    const int groups = 64 / L;
+    const int grp = lane / L, li = lane - grp * L;
+    float4 a[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) a[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+    for (int cc = grp; cc < nch; cc += groups) {
         const size_t sl = s0 + (size_t)cc * group;
         const float wt = exp2f(ws_ml[sl * 2] - mx);
         const float* pa = ws_acc + sl * dim;
-        if (lane < dc) {
-            const float4 x = *reinterpret_cast<const float4*>(pa + 4 * lane);
-            a0.x += wt * x.x; a0.y += wt * x.y; a0.z += wt * x.z; a0.w += wt * x.w;
-        }
-        if (lane + 64 < dc) {
-            const float4 x = *reinterpret_cast<const float4*>(pa + 4 * (lane + 64));
-            a1.x += wt * x.x; a1.y += wt * x.y; a1.z += wt * x.z; a1.w += wt * x.w;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int d4 = li + i * L;
+            if (d4 < dc) {
+                const float4 x = *reinterpret_cast<const float4*>(pa + 4 * d4);
+                a[i].x += wt * x.x; a[i].y += wt * x.y;
+                a[i].z += wt * x.z; a[i].w += wt * x.w;
+            }
         }
     }
+    for (int off = L; off < 64; off <<= 1) {
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            a[i].x += __shfl_xor(a[i].x, off, 64);
+            a[i].y += __shfl_xor(a[i].y, off, 64);
+            a[i].z += __shfl_xor(a[i].z, off, 64);
+            a[i].w += __shfl_xor(a[i].w, off, 64);
+        }
+    }
+    if (grp != 0) return;
     const float inv = 1.0f / lsum;
-    if (lane < dc)
-        St<T>::st4(o + 4 * lane, make_float4(a0.x * inv, a0.y * inv, a0.z * inv, a0.w * inv));
-    if (lane + 64 < dc)
-        St<T>::st4(o + 4 * (lane + 64),
-                   make_float4(a1.x * inv, a1.y * inv, a1.z * inv, a1.w * inv));
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const int d4 = li + i * L;
+        if (d4 < dc)
+            St<T>::st4(o + 4 * d4, make_float4(a[i].x * inv, a[i].y * inv,
+                                               a[i].z * inv, a[i].w * inv));
+    }
+}
+
+template <typename T>
+void launch_combine(const float* ws_ml, const float* ws_acc, const int* lens,
+                    T* out, int batch, int hq, int hkv, int group, int dim,
+                    int span, int chunk, int cmax, bool skip_single,
+                    hipStream_t s) {
+    const unsigned grid = (unsigned)((long long)batch * hq);
+    if (dim / 4 <= 64)
+        attn_combine<T, 1><<<grid, 64, 0, s>>>(ws_ml, ws_acc, lens, out, hq, hkv,
+                                               group, dim, span, chunk, cmax,
+                                               skip_single ? 1 : 0);
+    else
+        attn_combine<T, 2><<<grid, 64, 0, s>>>(ws_ml, ws_acc, lens, out, hq, hkv,
+                                               group, dim, span, chunk, cmax,
+                                               skip_single ? 1 : 0);
+    launch_check("attention combine kernel launch");
 }
 
 // ---------------------------------------------------------------------------
@@ -554,11 +691,11 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
     const long long target = (long long)dev_info().cu_count * 16;
     int chunk;
     if (fast)
-        chunk = choose_chunk(batch, hkv, span, 128, 1024, target);
+        chunk = choose_chunk(batch, hkv, span, 128, kMfmaMaxChunk, target);
     else
         chunk = choose_chunk(batch, hkv, span, 64, kGenMaxChunk, target);
     const int forced = env_int("FT_ATTN_CHUNK", 0);
-    if (forced > 0) chunk = std::min(forced, fast ? 4096 : kGenMaxChunk);
+    if (forced > 0) chunk = std::min(forced, fast ? kMfmaMaxChunk : kGenMaxChunk);
     const int cmax = span > 0 ? (int)((span + chunk - 1) / chunk) : 1;
     const long long units = (long long)batch * hkv * cmax;
     if (units * 256 > (1LL << 31)) inval("attention problem too large for one launch");
@@ -568,45 +705,52 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
                                 (ml_floats + nslots * dim) * sizeof(float), s);
     float* ws_ml = ws;
     float* ws_acc = ws + ml_floats;
+    int page_shift = -1;
+    if (paged && (rows_or_page & (rows_or_page - 1)) == 0) {
+        int sh = 0;
+        while ((1 << sh) < rows_or_page) ++sh;
+        page_shift = sh;
+    }
+    const float scale_log2 = (1.0f / sqrtf((float)dim)) * kLog2e;
+    if constexpr (!std::is_same<T, float>::value) {
+        if (fast && span > 0) {
+            if (paged)
+                attn_decode_mfma<T, true><<<(unsigned)units, 256, 0, s>>>(
+                    q, k, v, table, lens, ws_ml, ws_acc, out, hq, hkv, group,
+                    rows_or_page, page_shift, tbl_width, (int)span, chunk, cmax,
+                    scale_log2);
+            else
+                attn_decode_mfma<T, false><<<(unsigned)units, 256, 0, s>>>(
+                    q, k, v, nullptr, lens, ws_ml, ws_acc, out, hq, hkv, group,
+                    rows_or_page, -1, 0, (int)span, chunk, cmax, scale_log2);
+            launch_check("attention decode kernel launch");
+            if (cmax > 1)  // some row may span several chunks
+                launch_combine<T>(ws_ml, ws_acc, lens, out, batch, hq, hkv,
+                                  group, dim, (int)span, chunk, cmax, true, s);
+            return;
+        }
+    }
     RowMap rm;
     rm.table = paged ? table : nullptr;
     rm.hkv = hkv;
     rm.dim = dim;
     rm.rows_or_page = rows_or_page;
     rm.tbl_width = tbl_width;
-    rm.page_shift = -1;
-    if (paged && (rows_or_page & (rows_or_page - 1)) == 0) {
-        int sh = 0;
-        while ((1 << sh) < rows_or_page) ++sh;
-        rm.page_shift = sh;
-    }
-    const float scale_log2 = (1.0f / sqrtf((float)dim)) * kLog2e;
+    rm.page_shift = page_shift;
     if (span > 0) {
-        bool launched = false;
-        if constexpr (!std::is_same<T, float>::value) {
-            if (fast) {
-                attn_chunk_mfma<T><<<(unsigned)units, 256, 0, s>>>(
-                    q, k, v, lens, rm, ws_ml, ws_acc, hq, group, (int)span,
-                    chunk, cmax, scale_log2);
-                launched = true;
-            }
-        }
-        if (launched) {
-        } else if (dim / 4 <= 64) {
+        if (dim / 4 <= 64)
             attn_chunk_generic<T, 1><<<(unsigned)units, kGenNT, 0, s>>>(
                 q, k, v, lens, rm, ws_ml, ws_acc, hq, group, (int)span, chunk,
                 cmax, scale_log2);
-        } else {
+        else
             attn_chunk_generic<T, 2><<<(unsigned)units, kGenNT, 0, s>>>(
                 q, k, v, lens, rm, ws_ml, ws_acc, hq, group, (int)span, chunk,
                 cmax, scale_log2);
-        }
         launch_check("attention chunk kernel launch");
     }
-    attn_combine<T><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
-        ws_ml, ws_acc, span > 0 ? lens : nullptr, out, hq, hkv, group, dim,
-        (int)span, chunk, cmax);
-    launch_check("attention combine kernel launch");
+    // (also the zero fill of every row when the cache holds no rows at all)
+    launch_combine<T>(ws_ml, ws_acc, span > 0 ? lens : nullptr, out, batch, hq,
+                      hkv, group, dim, (int)span, chunk, cmax, false, s);
 }
 
 // ---------------------------------------------------------------------------
