@@ -15,14 +15,15 @@
 // row's partials with the log-sum-exp rule and divides by l. len == 0 rows
 // produce zeros (reference attention.cu:1349-1350).
 //
-// Two kernel families, each followed by attn_combine:
-//   attn_decode_mfma   bf16/fp16 storage, D == 128, G <= 16: QK^T and PV on
-//                      the matrix cores (v_mfma_f32_16x16x32_{bf16,f16});
-//                      every K/V byte is read once, straight into the MFMA
+// Two kernel families:
+//   attn_decode_stream bf16/fp16 storage, D == 128, G <= 16: QK^T and PV on
+//     + attn_combine_  the matrix cores (v_mfma_f32_16x16x32_{bf16,f16});
+//       stream         every K/V byte is read once, straight into the MFMA
 //                      operand layout with 16-byte loads, double-buffered;
-//                      single-chunk rows are finished in the kernel.
+//                      equal token segments per workgroup (stream split).
 //   attn_chunk_generic any storage type, D % 4 == 0 <= 512, any G: VALU
-//                      dot products, chunk scores staged in LDS.
+//     + attn_combine   dot products, chunk scores staged in LDS; the grid
+//                      covers the cache capacity in fixed chunks.
 #include "ft_common.hpp"
 
 #include <algorithm>
@@ -238,10 +239,26 @@ __global__ __launch_bounds__(kGenNT) void attn_chunk_generic(
 // ---------------------------------------------------------------------------
 // MFMA decode kernel (bf16 / fp16 storage, D == 128, G <= 16)
 //
-// One workgroup = one unit (sequence b, kv head, token chunk). Its 4 waves
-// walk 32-token steps st = wave, wave+4, ... with their own online-softmax
-// state, then merge in LDS. With r = lane % 16 and g = lane / 16 (lane layout
-// of v_mfma_f32_16x16x32: A[r][8g+i], B[8g+i][r], C[4g+i][r]):
+// Work split ("stream" split-K). All (sequence b, kv head) token rows are
+// laid end to end, b-major then kv: row (b, kv) owns the flat positions
+// [Hkv*pref[b] + kv*len_b, + len_b) with pref the exclusive prefix of the
+// lengths. The G workgroups of the grid each take one equal contiguous
+// segment of that flat range (at least kStreamMinSeg tokens), so every
+// workgroup streams the same number of K/V bytes whatever the length mix,
+// and the per-workgroup set-up is paid once per segment, not per chunk. A
+// segment crossing row ends is processed as consecutive pieces, one per row
+// it touches. A piece that is a whole row is normalised and stored here;
+// any other piece writes its f32 (m, l, acc[D]) partial per head to slot
+// (segment + row) - unique, since pieces are ordered in both indices - and
+// attn_combine_stream folds a row's pieces after the kernel boundary.
+// (Folding in the last-arriving workgroup instead needs a device-scope
+// release/acquire per workgroup - an L2 writeback + invalidate on gfx950 -
+// which costs far more than the second launch.)
+//
+// Inside a piece, the 4 waves walk 32-token steps st = wave, wave+4, ...
+// with their own online-softmax state, merged in LDS at the piece end. With
+// r = lane % 16 and g = lane / 16 (lane layout of v_mfma_f32_16x16x32:
+// A[r][8g+i], B[8g+i][r], C[4g+i][r]):
 //
 //  scores   S^T[tok][head] = K[tok][:] . Q[head][:]  (4 MFMAs per 16 tokens)
 //           A = K rows: lane loads K[tok r][32j+8g .. +7], one 16-byte load
@@ -262,19 +279,14 @@ __global__ __launch_bounds__(kGenNT) void attn_chunk_generic(
 //           bf16 P is split into hi + lo parts (two MFMAs) so the weights
 //           carry ~16 mantissa bits; fp16 P carries 11.
 //
-// Memory pipeline: the unit's block-table slice is staged in LDS once, so a
-// step's 16 loads per lane depend on no other global load; each wave holds
-// two steps of K/V in registers and issues step st+4's loads before it
-// computes step st (the prefetch is unconditional - clamped to the last
-// step - so the compiler's wait counts stay exact). Token indices past the
-// chunk's end are clamped to its last row (a real row) and masked to -inf.
-//
-// Combine: a row that fits one chunk is normalised and stored here (the
-// combine kernel skips it). Otherwise every unit writes its f32
-// (m, l, acc[D]) partial per head and attn_combine folds them after the
-// kernel boundary. (Folding in the last-arriving unit instead needs a
-// device-scope release/acquire per unit - an L2 writeback + invalidate on
-// gfx950 - which costs far more than the second launch.)
+// Memory pipeline, per wave: K/V of two steps live in registers (buffers
+// A, B); step st+4's 16 loads are issued before step st is computed. The
+// block-table entries a step needs (one per lane per 16-token tile) are
+// loaded two steps ahead of its K/V loads, so with the in-order load
+// counter a K/V load never waits on a table entry issued after the K/V of
+// the step being computed. Prefetches past the piece end are clamped to its
+// last step (a real row), which keeps the load count per iteration fixed
+// and the compiler's wait counts exact; tokens past the end are masked.
 // ---------------------------------------------------------------------------
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -295,87 +307,85 @@ template <> struct Mfma<f16> {
 };
 
 constexpr int kMfmaDim = 128;
-constexpr int kMfmaAccPitch = kMfmaDim + 4;   // LDS row pitch (bank spread)
-constexpr int kMfmaMaxChunk = 1024;
-constexpr int kMfmaTblSlots = kMfmaMaxChunk + 2;  // pages one chunk can touch
+constexpr int kMfmaAccPitch = kMfmaDim + 4;  // LDS row pitch (bank spread)
+constexpr int kStreamScanRows = 2048;        // sequences per launch (LDS prefix)
+constexpr long long kStreamMinSeg = 1024;    // minimum tokens per segment
 
-template <typename T, bool PAGED>
+// Row addressing modes of attn_decode_stream.
+enum RowMode { kRowsContig = 0, kRowsPagedPow2 = 1, kRowsPagedDiv = 2 };
+
+// Exclusive prefix of the clamped lengths into s_pref[0..batch] (wave 0;
+// each lane takes a contiguous run of rows, then a wave scan of the runs).
+__device__ __forceinline__ void scan_lengths(const int* __restrict__ lens,
+                                             int batch, int span, int lane,
+                                             long long* s_pref) {
+    const int per = (batch + 63) / 64;
+    const int r0 = lane * per;
+    long long local = 0;
+    for (int i = 0; i < per; ++i)
+        if (r0 + i < batch) local += clamp_len(lens, r0 + i, span);
+    long long incl = local;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const long long y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    long long run = incl - local;
+    for (int i = 0; i < per; ++i)
+        if (r0 + i < batch) {
+            s_pref[r0 + i] = run;
+            run += clamp_len(lens, r0 + i, span);
+        }
+    if (lane == 63) s_pref[batch] = incl;
+}
+
+// A value every lane holds identically, moved to scalar registers (the
+// compiler cannot prove that values read from LDS are wave-uniform).
+__device__ __forceinline__ long long uniform64(long long x) {
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)x);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)((unsigned long long)x >> 32));
+    return (long long)(((unsigned long long)hi << 32) | lo);
+}
+
+__device__ __forceinline__ long long stream_seg_len(long long total, int nseg) {
+    const long long s = (total + nseg - 1) / nseg;
+    return s < kStreamMinSeg ? kStreamMinSeg : s;
+}
+
+template <typename T, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_decode_mfma(
+void attn_decode_stream(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int* __restrict__ table, const int* __restrict__ lens,
     float* __restrict__ ws_ml, float* __restrict__ ws_acc,
-    T* __restrict__ out, int hq, int hkv, int group, int rows_or_page,
-    int page_shift, int tbl_width, int span, int chunk, int cmax,
-    float scale_log2) {
+    long long* __restrict__ pref_out, T* __restrict__ out, int batch, int hq,
+    int hkv, int group, int rows_or_page, int page_shift, int tbl_width,
+    int span, float scale_log2) {
     using M = Mfma<T>;
     using V8 = typename M::v8;
     constexpr int D = kMfmaDim;
+    constexpr bool PAGED = MODE != kRowsContig;
     __shared__ float s_acc[4][16][kMfmaAccPitch];
     __shared__ float s_m[4][16], s_l[4][16];
-    __shared__ int s_tbl[PAGED ? kMfmaTblSlots : 1];
+    __shared__ long long s_pref[kStreamScanRows + 1];
 
-    const int per_b = hkv * cmax;
-    const int b = blockIdx.x / per_b;
-    const int kv = (blockIdx.x - b * per_b) / cmax;
-    const int c = blockIdx.x - b * per_b - kv * cmax;
-    const int len = clamp_len(lens, b, span);
-    const int t0 = c * chunk;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    // wave-uniform in a scalar register, so the step loop branches on
-    // scalars
+    // wave-uniform in a scalar register, so the step loops branch on scalars
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15, g = lane >> 4;
-    T* const orow = out + ((size_t)b * hq + (size_t)kv * group) * D;  // G rows
-    if (t0 >= len) {
-        // an empty row is all zeros (reference attention.cu:1349-1350)
-        if (len == 0 && c == 0)
-            for (int i = tid; i < group * (D / 4); i += 256)
-                St<T>::st4(orow + 4 * i, make_float4(0.f, 0.f, 0.f, 0.f));
-        return;
-    }
-    const int n = min(chunk, len - t0);
-    const int nch = (len + chunk - 1) / chunk;
 
-    int p0 = 0;
-    if constexpr (PAGED) {
-        const int last = t0 + n - 1;
-        p0 = page_shift >= 0 ? (t0 >> page_shift) : t0 / rows_or_page;
-        const int p1 = page_shift >= 0 ? (last >> page_shift) : last / rows_or_page;
-        const int* trow = table + (size_t)b * tbl_width;
-        for (int i = tid; i <= p1 - p0; i += 256) s_tbl[i] = trow[p0 + i];
-        __syncthreads();
-    }
-    auto row_off = [&](int tok) -> size_t {
-        const int t = t0 + tok;
-        if constexpr (PAGED) {
-            int pg, off;
-            if (page_shift >= 0) {
-                pg = t >> page_shift;
-                off = t & (rows_or_page - 1);
-            } else {
-                pg = t / rows_or_page;
-                off = t - pg * rows_or_page;
-            }
-            const int blk = s_tbl[pg - p0];
-            return (((size_t)blk * hkv + kv) * rows_or_page + off) * D;
-        } else {
-            return (((size_t)b * hkv + kv) * rows_or_page + t) * D;
-        }
-    };
+    if (wave == 0) scan_lengths(lens, batch, span, lane, s_pref);
+    __syncthreads();
+    if (blockIdx.x == 0)  // the combine kernel's copy of the prefix
+        for (int i = tid; i <= batch; i += 256) pref_out[i] = s_pref[i];
+    const long long total = uniform64(s_pref[batch]) * hkv;
+    const int nseg = gridDim.x;
+    const long long S = stream_seg_len(total, nseg);
+    const long long seg_lo = (long long)blockIdx.x * S;
+    if (seg_lo >= total) return;
+    const long long seg_hi = min(seg_lo + S, total);
 
-    // B operand of the score MFMAs: Q[head r][32j + 8g .. +7]
-    V8 qb[4];
-    {
-        const bool ok = r < group;
-        const T* qrow = q + ((size_t)b * hq + (size_t)kv * group + (ok ? r : 0)) * D;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            V8 z = {};
-            qb[j] = ok ? *reinterpret_cast<const V8*>(qrow + 32 * j + 8 * g) : z;
-        }
-    }
     // selection operands of the transposing MFMAs
     V8 sel0, sel1;
 #pragma unroll
@@ -384,115 +394,179 @@ void attn_decode_mfma(
         sel1[i] = (T)((8 * g + i == r + 16) ? 1.0f : 0.0f);
     }
 
-    f32x4 acc[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.0f;
+    long long pos = seg_lo;
+    while (pos < seg_hi) {
+        // ---- locate the piece: row (b, kv), tokens [t0, t0 + n) ------------
+        int lo = 0, hi = batch - 1;  // last sequence starting at or before pos
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (uniform64(s_pref[mid]) * hkv <= pos) lo = mid; else hi = mid - 1;
+        }
+        const int b = lo;
+        const long long pb = uniform64(s_pref[b]);
+        const long long base = pb * hkv;
+        const int len = (int)(uniform64(s_pref[b + 1]) - pb);
+        const int kv = (int)((pos - base) / len);
+        const int t0 = (int)(pos - base - (long long)kv * len);
+        const long long row_end = base + (long long)(kv + 1) * len;
+        const long long piece_hi = min(seg_hi, row_end);
+        const int n = (int)(piece_hi - pos);
+        const bool whole = (t0 == 0 && n == len);
+        const int row = b * hkv + kv;
+        const int* trow = PAGED ? table + (size_t)b * tbl_width : nullptr;
 
-    auto load_step = [&](int st, V8 (&kt)[2][4], V8 (&vt)[2][4]) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int tok = min((st << 5) + 16 * h + r, n - 1);
-            const size_t off = row_off(tok) + 8 * g;
+        // B operand of the score MFMAs: Q[head r][32j + 8g .. +7]
+        V8 qb[4];
+        {
+            const bool ok = r < group;
+            const T* qrow = q + ((size_t)b * hq + (size_t)kv * group + (ok ? r : 0)) * D;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                kt[h][j] = *reinterpret_cast<const V8*>(k + off + 32 * j);
-                vt[h][j] = *reinterpret_cast<const V8*>(v + off + 32 * j);
+                V8 z = {};
+                qb[j] = ok ? *reinterpret_cast<const V8*>(qrow + 32 * j + 8 * g) : z;
             }
         }
-    };
-    auto compute_step = [&](int st, const V8 (&kt)[2][4], const V8 (&vt)[2][4]) {
-        const int tb = st << 5;
-        f32x4 s[2];
+
+        f32x4 acc[8];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < 8; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        float m_run = -INFINITY, l_run = 0.0f;
+
+        // token (within the row) that lane row r of tile h of step st reads
+        auto tok_of = [&](int st, int h) {
+            return t0 + min((st << 5) + 16 * h + r, n - 1);
+        };
+        auto tbl_load = [&](int st, int (&e)[2]) {
+            if constexpr (PAGED) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) s[h] = M::mma(kt[h][j], qb[j], s[h]);
-        }
-        float sv[8];
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int tok = tb + 16 * h + 4 * g + i;
-                sv[4 * h + i] = tok < n ? s[h][i] * scale_log2 : -INFINITY;
+                for (int h = 0; h < 2; ++h) {
+                    const int t = tok_of(st, h);
+                    e[h] = trow[MODE == kRowsPagedPow2 ? (t >> page_shift)
+                                                        : (t / rows_or_page)];
+                }
             }
-        float mloc = sv[0];
+        };
+        auto kv_load = [&](int st, const int (&e)[2], V8 (&kt)[2][4], V8 (&vt)[2][4]) {
 #pragma unroll
-        for (int i = 1; i < 8; ++i) mloc = fmaxf(mloc, sv[i]);
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float m_new = fmaxf(m_run, mloc);
-        const float alpha = exp2f(m_run - m_new);
-        m_run = m_new;
-        float p[8];
-        float psum = 0.0f;
+            for (int h = 0; h < 2; ++h) {
+                const int t = tok_of(st, h);
+                size_t off;
+                if constexpr (MODE == kRowsContig) {
+                    off = ((size_t)row * rows_or_page + t) * D;
+                } else {
+                    const int in_pg = MODE == kRowsPagedPow2 ? (t & (rows_or_page - 1))
+                                                             : (t % rows_or_page);
+                    off = (((size_t)e[h] * hkv + kv) * rows_or_page + in_pg) * D;
+                }
+                off += 8 * g;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            p[i] = exp2f(sv[i] - m_new);
-            psum += p[i];
-        }
-        l_run = l_run * alpha + psum;
+                for (int j = 0; j < 4; ++j) {
+                    kt[h][j] = *reinterpret_cast<const V8*>(k + off + 32 * j);
+                    vt[h][j] = *reinterpret_cast<const V8*>(v + off + 32 * j);
+                }
+            }
+        };
+        auto compute_step = [&](int st, const V8 (&kt)[2][4], const V8 (&vt)[2][4]) {
+            const int tb = st << 5;
+            f32x4 s[2];
 #pragma unroll
-        for (int nn = 0; nn < 8; ++nn) acc[nn] *= alpha;
-        V8 pb, pl;
+            for (int h = 0; h < 2; ++h) {
+                s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            pb[i] = (T)p[i];
-            if (M::kSplitP) pl[i] = (T)(p[i] - (float)pb[i]);
-        }
+                for (int j = 0; j < 4; ++j) s[h] = M::mma(kt[h][j], qb[j], s[h]);
+            }
+            float sv[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                const f32x4 a0 = M::mma(vt[0][j], e ? sel1 : sel0, z);
-                const f32x4 a1 = M::mma(vt[1][j], e ? sel1 : sel0, z);
-                V8 va;
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    va[i] = (T)a0[i];
-                    va[4 + i] = (T)a1[i];
+                    const int tok = tb + 16 * h + 4 * g + i;
+                    sv[4 * h + i] = tok < n ? s[h][i] * scale_log2 : -INFINITY;
                 }
-                acc[2 * j + e] = M::mma(va, pb, acc[2 * j + e]);
-                if (M::kSplitP) acc[2 * j + e] = M::mma(va, pl, acc[2 * j + e]);
+            float mloc = sv[0];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) mloc = fmaxf(mloc, sv[i]);
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+            const float m_new = fmaxf(m_run, mloc);
+            const float alpha = exp2f(m_run - m_new);
+            m_run = m_new;
+            float p[8];
+            float psum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                p[i] = exp2f(sv[i] - m_new);
+                psum += p[i];
             }
-        }
-    };
-
-    const int nsteps = (n + 31) >> 5;
-    int st = wave;
-    if (st < nsteps) {
-        V8 ka[2][4], va_[2][4], kb[2][4], vb[2][4];
-        load_step(st, ka, va_);
-        while (true) {
-            load_step(min(st + 4, nsteps - 1), kb, vb);
-            compute_step(st, ka, va_);
-            st += 4;
-            if (st >= nsteps) break;
-            load_step(min(st + 4, nsteps - 1), ka, va_);
-            compute_step(st, kb, vb);
-            st += 4;
-            if (st >= nsteps) break;
-        }
-    }
-
-    // fold the 4 lane groups' l, publish per-wave state, merge the waves
-    l_run += __shfl_xor(l_run, 16, 64);
-    l_run += __shfl_xor(l_run, 32, 64);
-    if (lane < 16) {
-        s_m[wave][lane] = m_run;
-        s_l[wave][lane] = l_run;
-    }
+            l_run = l_run * alpha + psum;
 #pragma unroll
-    for (int nn = 0; nn < 8; ++nn)
+            for (int nn = 0; nn < 8; ++nn) acc[nn] *= alpha;
+            V8 pb, pl;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s_acc[wave][r][16 * nn + 4 * g + i] = acc[nn][i];
-    __syncthreads();
+            for (int i = 0; i < 8; ++i) {
+                pb[i] = (T)p[i];
+                if (M::kSplitP) pl[i] = (T)(p[i] - (float)pb[i]);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                    const f32x4 a0 = M::mma(vt[0][j], e ? sel1 : sel0, z);
+                    const f32x4 a1 = M::mma(vt[1][j], e ? sel1 : sel0, z);
+                    V8 va;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        va[i] = (T)a0[i];
+                        va[4 + i] = (T)a1[i];
+                    }
+                    acc[2 * j + e] = M::mma(va, pb, acc[2 * j + e]);
+                    if (M::kSplitP) acc[2 * j + e] = M::mma(va, pl, acc[2 * j + e]);
+                }
+            }
+        };
 
-    const int nvec = group * (D / 4);
-    if (nch == 1) {  // the whole row is this unit: normalise and store
+        // ---- stream the piece: two steps per iteration (buffers A, B) ------
+        const int nsteps = (n + 31) >> 5;
+        const int last = nsteps - 1;
+        int st = wave;
+        if (st < nsteps) {
+            V8 ka[2][4], va_[2][4], kb[2][4], vb[2][4];
+            int ea[2] = {0, 0}, eb[2] = {0, 0};
+            tbl_load(st, ea);
+            tbl_load(min(st + 4, last), eb);
+            kv_load(st, ea, ka, va_);
+            for (; st + 4 < nsteps; st += 8) {
+                tbl_load(min(st + 8, last), ea);
+                kv_load(st + 4, eb, kb, vb);
+                // keep the prefetch ahead of the compute that follows it (the
+                // scheduler would otherwise sink the loads below the waits)
+                __builtin_amdgcn_sched_barrier(0);
+                compute_step(st, ka, va_);
+                tbl_load(min(st + 12, last), eb);
+                kv_load(min(st + 8, last), ea, ka, va_);
+                __builtin_amdgcn_sched_barrier(0);
+                compute_step(st + 4, kb, vb);
+            }
+            if (st < nsteps) compute_step(st, ka, va_);
+        }
+
+        // ---- merge the 4 waves, then store the row or the piece's partial --
+        l_run += __shfl_xor(l_run, 16, 64);
+        l_run += __shfl_xor(l_run, 32, 64);
+        if (lane < 16) {
+            s_m[wave][lane] = m_run;
+            s_l[wave][lane] = l_run;
+        }
+#pragma unroll
+        for (int nn = 0; nn < 8; ++nn)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s_acc[wave][r][16 * nn + 4 * g + i] = acc[nn][i];
+        __syncthreads();
+
+        const int nvec = group * (D / 4);
+        const size_t slot0 = ((size_t)blockIdx.x + row) * group;
+        T* const orow = out + ((size_t)b * hq + (size_t)kv * group) * D;
         for (int idx = tid; idx < nvec; idx += 256) {
             const int hh = idx / (D / 4);
             const int d4 = idx - hh * (D / 4);
@@ -508,43 +582,77 @@ void attn_decode_mfma(
                 const float4 a = *reinterpret_cast<const float4*>(&s_acc[w][hh][4 * d4]);
                 o.x += wt * a.x; o.y += wt * a.y; o.z += wt * a.z; o.w += wt * a.w;
             }
-            const float inv = 1.0f / lsum;
-            St<T>::st4(orow + (size_t)hh * D + 4 * d4,
-                       make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv));
+            if (whole) {
+                const float inv = 1.0f / lsum;
+                St<T>::st4(orow + (size_t)hh * D + 4 * d4,
+                           make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv));
+            } else {
+                *reinterpret_cast<float4*>(ws_acc + (slot0 + hh) * D + 4 * d4) = o;
+                if (d4 == 0) {
+                    ws_ml[(slot0 + hh) * 2] = mx;
+                    ws_ml[(slot0 + hh) * 2 + 1] = lsum;
+                }
+            }
         }
+        __syncthreads();  // LDS is reused by the next piece
+        pos = piece_hi;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// combine for attn_decode_stream: one wave per (b, q head). Row (b, kv)
+// spans segments [s_lo, s_hi] of length S; its pieces' partials sit at
+// slots s + row. A row inside one segment was stored by the decode kernel;
+// a row of length 0 is zero-filled here (reference attention.cu:1349-1350).
+// Lanes split into 2 groups of 32 (one float4 column of D = 128 each) that
+// walk alternate pieces; the groups are summed with one xor shuffle.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(64) void attn_combine_stream(
+    const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
+    const long long* __restrict__ pref, T* __restrict__ out, int batch, int hq,
+    int hkv, int group, int nseg) {
+    constexpr int D = kMfmaDim;
+    const int b = blockIdx.x / hq;
+    const int h = blockIdx.x - b * hq;
+    const int kv = h / group, gi = h - kv * group;
+    const int lane = threadIdx.x;
+    T* o = out + ((size_t)b * hq + h) * D;
+    const int len = (int)(pref[b + 1] - pref[b]);
+    if (len == 0) {
+        if (lane < D / 4) St<T>::st4(o + 4 * lane, make_float4(0.f, 0.f, 0.f, 0.f));
         return;
     }
-
-    const size_t slot0 = (((size_t)b * hkv + kv) * cmax + c) * group;
-    for (int idx = tid; idx < nvec; idx += 256) {
-        const int hh = idx / (D / 4);
-        const int d4 = idx - hh * (D / 4);
-        float mw[4];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            mw[w] = s_m[w][hh];
-            mx = fmaxf(mx, mw[w]);
-        }
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float wt = exp2f(mw[w] - mx);
-            const float4 a = *reinterpret_cast<const float4*>(&s_acc[w][hh][4 * d4]);
-            o.x += wt * a.x; o.y += wt * a.y; o.z += wt * a.z; o.w += wt * a.w;
-        }
-        *reinterpret_cast<float4*>(ws_acc + (slot0 + hh) * D + 4 * d4) = o;
+    const long long S = stream_seg_len(pref[batch] * hkv, nseg);
+    const long long start = pref[b] * hkv + (long long)kv * len;
+    const int s_lo = (int)(start / S), s_hi = (int)((start + len - 1) / S);
+    if (s_lo == s_hi) return;  // stored whole by the decode kernel
+    const int row = b * hkv + kv;
+    const int np = s_hi - s_lo + 1;
+    auto slot = [&](int i) { return ((size_t)s_lo + i + row) * group + gi; };
+    float mx = -INFINITY;
+    for (int i = lane; i < np; i += 64) mx = fmaxf(mx, ws_ml[slot(i) * 2]);
+    mx = wave_max(mx);
+    float lsum = 0.0f;
+    for (int i = lane; i < np; i += 64)
+        lsum += ws_ml[slot(i) * 2 + 1] * exp2f(ws_ml[slot(i) * 2] - mx);
+    lsum = wave_sum(lsum);
+    const int grp = lane >> 5, d4 = lane & 31;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+    for (int i = grp; i < np; i += 2) {
+        const size_t sl = slot(i);
+        const float wt = exp2f(ws_ml[sl * 2] - mx);
+        const float4 x = *reinterpret_cast<const float4*>(ws_acc + sl * D + 4 * d4);
+        a.x += wt * x.x; a.y += wt * x.y; a.z += wt * x.z; a.w += wt * x.w;
     }
-    if (tid < group) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) mx = fmaxf(mx, s_m[w][tid]);
-        float lsum = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) lsum += s_l[w][tid] * exp2f(s_m[w][tid] - mx);
-        ws_ml[(slot0 + tid) * 2] = mx;
-        ws_ml[(slot0 + tid) * 2 + 1] = lsum;
-    }
+    a.x += __shfl_xor(a.x, 32, 64);
+    a.y += __shfl_xor(a.y, 32, 64);
+    a.z += __shfl_xor(a.z, 32, 64);
+    a.w += __shfl_xor(a.w, 32, 64);
+    if (grp != 0) return;
+    const float inv = 1.0f / lsum;
+    St<T>::st4(o + 4 * d4, make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv));
 }
 
 // ---------------------------------------------------------------------------
@@ -686,25 +794,8 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
     if (!q || !out || (span > 0 && (!k || !v)) || (paged && span > 0 && !table))
         inval("attention: null operand");
     const int group = hq / hkv;
-    const bool fast = mfma_eligible(q, k, v, group, dim) &&
+    const bool fast = mfma_eligible(q, k, v, group, dim) && batch <= kStreamScanRows &&
                       env_int("FT_ATTN_FORCE_GENERIC", 0) == 0;
-    const long long target = (long long)dev_info().cu_count * 16;
-    int chunk;
-    if (fast)
-        chunk = choose_chunk(batch, hkv, span, 128, kMfmaMaxChunk, target);
-    else
-        chunk = choose_chunk(batch, hkv, span, 64, kGenMaxChunk, target);
-    const int forced = env_int("FT_ATTN_CHUNK", 0);
-    if (forced > 0) chunk = std::min(forced, fast ? kMfmaMaxChunk : kGenMaxChunk);
-    const int cmax = span > 0 ? (int)((span + chunk - 1) / chunk) : 1;
-    const long long units = (long long)batch * hkv * cmax;
-    if (units * 256 > (1LL << 31)) inval("attention problem too large for one launch");
-    const size_t nslots = (size_t)units * group;
-    const size_t ml_floats = (nslots * 2 + 63) & ~(size_t)63;
-    float* ws = (float*)scratch(Scratch::AttnPartials,
-                                (ml_floats + nslots * dim) * sizeof(float), s);
-    float* ws_ml = ws;
-    float* ws_acc = ws + ml_floats;
     int page_shift = -1;
     if (paged && (rows_or_page & (rows_or_page - 1)) == 0) {
         int sh = 0;
@@ -714,22 +805,51 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
     const float scale_log2 = (1.0f / sqrtf((float)dim)) * kLog2e;
     if constexpr (!std::is_same<T, float>::value) {
         if (fast && span > 0) {
-            if (paged)
-                attn_decode_mfma<T, true><<<(unsigned)units, 256, 0, s>>>(
-                    q, k, v, table, lens, ws_ml, ws_acc, out, hq, hkv, group,
-                    rows_or_page, page_shift, tbl_width, (int)span, chunk, cmax,
-                    scale_log2);
+            // stream split: G equal token segments, G = 2 workgroups per CU
+            // (the kernel's register budget allows exactly two per CU)
+            int nseg = env_int("FT_ATTN_SEGS", 2 * dev_info().cu_count);
+            nseg = std::max(1, std::min(nseg, 1 << 20));
+            const size_t nslots = ((size_t)nseg + (size_t)batch * hkv) * group;
+            const size_t ml_floats = (nslots * 2 + 63) & ~(size_t)63;
+            const size_t acc_floats = nslots * dim;
+            char* ws = (char*)scratch(
+                Scratch::AttnPartials,
+                (ml_floats + acc_floats) * sizeof(float) + (batch + 1) * sizeof(long long), s);
+            float* ws_ml = (float*)ws;
+            float* ws_acc = ws_ml + ml_floats;
+            long long* pref = (long long*)(ws_acc + acc_floats);
+            if (paged && page_shift >= 0)
+                attn_decode_stream<T, kRowsPagedPow2><<<(unsigned)nseg, 256, 0, s>>>(
+                    q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv,
+                    group, rows_or_page, page_shift, tbl_width, (int)span, scale_log2);
+            else if (paged)
+                attn_decode_stream<T, kRowsPagedDiv><<<(unsigned)nseg, 256, 0, s>>>(
+                    q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv,
+                    group, rows_or_page, -1, tbl_width, (int)span, scale_log2);
             else
-                attn_decode_mfma<T, false><<<(unsigned)units, 256, 0, s>>>(
-                    q, k, v, nullptr, lens, ws_ml, ws_acc, out, hq, hkv, group,
-                    rows_or_page, -1, 0, (int)span, chunk, cmax, scale_log2);
+                attn_decode_stream<T, kRowsContig><<<(unsigned)nseg, 256, 0, s>>>(
+                    q, k, v, nullptr, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv,
+                    group, rows_or_page, -1, 0, (int)span, scale_log2);
             launch_check("attention decode kernel launch");
-            if (cmax > 1)  // some row may span several chunks
-                launch_combine<T>(ws_ml, ws_acc, lens, out, batch, hq, hkv,
-                                  group, dim, (int)span, chunk, cmax, true, s);
+            attn_combine_stream<T><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
+                ws_ml, ws_acc, pref, out, batch, hq, hkv, group, nseg);
+            launch_check("attention combine kernel launch");
             return;
         }
     }
+    const long long target = (long long)dev_info().cu_count * 16;
+    int chunk = choose_chunk(batch, hkv, span, 64, kGenMaxChunk, target);
+    const int forced = env_int("FT_ATTN_CHUNK", 0);
+    if (forced > 0) chunk = std::min(forced, kGenMaxChunk);
+    const int cmax = span > 0 ? (int)((span + chunk - 1) / chunk) : 1;
+    const long long units = (long long)batch * hkv * cmax;
+    if (units * 256 > (1LL << 31)) inval("attention problem too large for one launch");
+    const size_t nslots = (size_t)units * group;
+    const size_t ml_floats = (nslots * 2 + 63) & ~(size_t)63;
+    float* ws = (float*)scratch(Scratch::AttnPartials,
+                                (ml_floats + nslots * dim) * sizeof(float), s);
+    float* ws_ml = ws;
+    float* ws_acc = ws + ml_floats;
     RowMap rm;
     rm.table = paged ? table : nullptr;
     rm.hkv = hkv;
