@@ -24,6 +24,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 namespace ft {
 namespace {
@@ -302,6 +303,445 @@ __global__ __launch_bounds__(WM * WN * 64) void qgemm_tiled(
 }
 
 // ---------------------------------------------------------------------------
+// big (M >= 256, N >= 256): 256x256 workgroup tiles, K slabs of 64 bytes,
+// 4 waves each owning a 128x128 sub-tile = 4x4 blocks of
+// v_mfma_i32_32x32x32_i8 (256 int32 accumulators per lane, so one wave per
+// SIMD). A and B slabs are staged global -> registers -> LDS, double
+// buffered, one barrier per slab. LDS rows are 64 bytes = four 16-byte
+// chunks; chunk c of row r is stored at position c ^ big_swz(r) with
+// big_swz(r) = (r >> 2) & 3: the gfx950 LDS serves a ds_read_b128 16 lanes
+// (256 bytes, all 64 banks) per cycle, and the 16 consecutive rows of such a
+// group then hit 16 distinct 16-byte bank groups (rows r and r + 4k share the
+// same 64-byte slot of the 256, so they need different chunk positions). Tiles are numbered XCD-aware: the
+// tiles dispatched to one XCD are consecutive in a column-major walk of
+// 4-row tile bands, so the ~32 tiles an XCD runs at a time cover a 4 x 8
+// block of the output and share their A / B panels through its L2.
+// ---------------------------------------------------------------------------
+constexpr int kBigT = 256;    // tile edge (M and N)
+constexpr int kBigK = 64;     // K bytes per slab
+constexpr int kBigBand = 4;   // tile rows per band of the XCD-aware order
+
+__device__ __forceinline__ int big_swz(int row) { return (row >> 2) & 3; }
+
+__device__ __forceinline__ int big_lds_off(int row, int c) {
+    return row * kBigK + ((c ^ big_swz(row)) << 4);
+}
+
+template <int OUT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void qgemm_big(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
+               int m, int n, int k) {
+    __shared__ __attribute__((aligned(16))) i8 lds_a[2][kBigT * kBigK];
+    __shared__ __attribute__((aligned(16))) i8 lds_b[2][kBigT * kBigK];
+
+    // ---- tile id: XCD-contiguous, then banded column-major ---------------
+    const int tm = (m + kBigT - 1) / kBigT, tn = (n + kBigT - 1) / kBigT;
+    const int ntiles = tm * tn;
+    int pid = blockIdx.x;
+    if (ntiles % 8 == 0) pid = (pid % 8) * (ntiles / 8) + pid / 8;
+    const int band = pid / (kBigBand * tn);
+    const int first_m = band * kBigBand;
+    const int band_m = min(tm - first_m, kBigBand);
+    const int in_band = pid - band * kBigBand * tn;
+    const int tile_m = first_m + in_band % band_m;
+    const int tile_n = in_band / band_m;
+    const int bm = tile_m * kBigT, bn = tile_n * kBigT;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r32 = lane & 31, h = lane >> 5;
+
+    // staging: 4 chunks of A and 4 of B per thread per slab; chunk q = tid +
+    // 256 j lands at LDS position q (consecutive lanes, consecutive 16 B)
+    i32x4 ga[4], gb[4];
+    auto gload = [&](int kt) {
+        const int kb = kt * kBigK;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int q = tid + 256 * j;
+            const int row = q >> 2;
+            const int c = (q & 3) ^ big_swz(row);
+            const int kc = kb + 16 * c;
+            const i32x4 z = {0, 0, 0, 0};
+            ga[j] = (bm + row < m && kc < k)
+                        ? *reinterpret_cast<const i32x4*>(a + (size_t)(bm + row) * k + kc) : z;
+            gb[j] = (bn + row < n && kc < k)
+                        ? *reinterpret_cast<const i32x4*>(b + (size_t)(bn + row) * k + kc) : z;
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int q = tid + 256 * j;
+            *reinterpret_cast<i32x4*>(&lds_a[buf][q * 16]) = ga[j];
+            *reinterpret_cast<i32x4*>(&lds_b[buf][q * 16]) = gb[j];
+        }
+    };
+
+    i32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) acc[i][j][t] = 0;
+
+    const int nk = (k + kBigK - 1) / kBigK;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    if (nk > 1) gload(1);
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            i32x4 fa[4], fb[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                fa[i] = *reinterpret_cast<const i32x4*>(
+                    &lds_a[cur][big_lds_off(wm * 128 + i * 32 + r32, 2 * s + h)]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                fb[j] = *reinterpret_cast<const i32x4*>(
+                    &lds_b[cur][big_lds_off(wn * 128 + j * 32 + r32, 2 * s + h)]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) sstore(cur ^ 1);
+        __syncthreads();
+        if (kt + 2 < nk) gload(kt + 2);
+    }
+
+    // ---- epilogue: C layout 32x32, lane (r32, h), reg t -> row
+    // 8*(t/4) + 4h + t%4, col r32
+    const float sa = epi_sa(e);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int col = bn + wn * 128 + j * 32 + r32;
+        if (col >= n) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int row = bm + wm * 128 + i * 32 + 8 * (t >> 2) + 4 * h + (t & 3);
+                if (row < m) epi_store<OUT>(e, sa, n, row, col, acc[i][j][t]);
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// big, DMA-fed (K % 64 == 0): the same tiles, order and LDS layout as
+// qgemm_big, but
+//  - slabs go global -> LDS directly (global_load_lds_dwordx4: lane i of a
+//    wave's load lands at the wave's LDS base + 16 i), so no registers hold
+//    them; a ring of kDmaStages 32 KB stages keeps kDmaStages - 1 slabs in
+//    flight ahead of the MFMAs (the L2 / HBM latency under load spans
+//    several slabs of MFMA work);
+//  - operand fragments are read with inline-asm ds_read_b128 (invisible to
+//    the compiler's LDS-DMA alias tracking, which would otherwise wait for
+//    every in-flight slab before each read), interleaved with the MFMAs of
+//    the previous fragment set; a slab is waited for with an explicit vmcnt
+//    sized to the slabs issued after it, then a bare s_barrier;
+//  - the accumulators hold C^T blocks (operands swapped), so each lane owns
+//    4 consecutive output columns per register quad: 2-byte outputs are
+//    staged through LDS per wave and leave as 16-byte row-contiguous stores,
+//    4-byte outputs as 16-byte stores straight from registers.
+// Rows past M / N load a clamped (real) row; they only feed outputs that
+// are never stored.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void* lds_void_p;
+constexpr int kDmaStages = 5;
+constexpr int kSlabBytes = 2 * kBigT * kBigK;  // A + B slab, 32 KB
+constexpr int kSlabLoads = 8;  // DMA instructions per thread per slab (4 A + 4 B)
+constexpr int kEpiPitch = 272;  // LDS row pitch of the output staging (16-byte rows)
+
+// s_waitcnt with only the vector-memory count bounded (gfx9 encoding;
+// expcnt and lgkmcnt fields at their maxima = no wait).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+    return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// 16-byte LDS read issued as inline asm: invisible to the compiler's
+// memory model (see above). The result is valid only after lds_wait.
+__device__ __forceinline__ i32x4 lds_read16(unsigned addr) {
+    i32x4 v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+// Wait for every outstanding LDS read; the fragments are in/out operands, so
+// nothing that uses them can be scheduled above the wait.
+__device__ __forceinline__ void lds_wait(i32x4 (&f)[8]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]),
+                   "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]));
+}
+
+// The scaled f32 value of one accumulator (two f32 roundings, unfused: see
+// epi_store).
+__device__ __forceinline__ float epi_val(int acc, float s) {
+    float val = (float)acc * s;
+    asm("" : "+v"(val));
+    return val;
+}
+
+template <int OUT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void qgemm_big_dma(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
+                   int m, int n, int k) {
+    __shared__ __attribute__((aligned(16))) i8 lds[kDmaStages * kSlabBytes];
+
+    const int tm = (m + kBigT - 1) / kBigT, tn = (n + kBigT - 1) / kBigT;
+    const int ntiles = tm * tn;
+    int pid = blockIdx.x;
+    if (ntiles % 8 == 0) pid = (pid % 8) * (ntiles / 8) + pid / 8;
+    const int band = pid / (kBigBand * tn);
+    const int first_m = band * kBigBand;
+    const int band_m = min(tm - first_m, kBigBand);
+    const int in_band = pid - band * kBigBand * tn;
+    const int bm = (first_m + in_band % band_m) * kBigT;
+    const int bn = (in_band / band_m) * kBigT;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r32 = lane & 31, h = lane >> 5;
+
+    // this lane's sources: LDS chunk q = tid + 256 j holds tile row
+    // q/4 = tid/4 + 64 j, logical chunk (q%4) ^ big_swz(row), which is
+    // the same for all j. Addresses = wave-uniform tile base (scalar) + a
+    // 32-bit per-lane offset (rows past the edge clamp to the last row).
+    const int c16 = 16 * ((tid & 3) ^ big_swz(tid >> 2));
+    unsigned aoff[4], boff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = (tid >> 2) + 64 * j;
+        aoff[j] = (unsigned)(min(row, m - 1 - bm) * k + c16);
+        boff[j] = (unsigned)(min(row, n - 1 - bn) * k + c16);
+    }
+    const i8* const abase = a + (size_t)bm * k;
+    const i8* const bbase = b + (size_t)bn * k;
+    auto stage_a = [&](int st) { return lds + st * kSlabBytes; };
+    auto stage_b = [&](int st) { return lds + st * kSlabBytes + kBigT * kBigK; };
+    auto issue = [&](int kt, int st) {
+        const i8* ak = abase + (size_t)kt * kBigK;
+        const i8* bk = bbase + (size_t)kt * kBigK;
+        i8* la = stage_a(st);
+        i8* lb = stage_b(st);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int dst = (256 * j + 64 * wave) * 16;  // this wave's 1 KB
+            __builtin_amdgcn_global_load_lds(ak + aoff[j], (lds_void_p)(la + dst), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(bk + boff[j], (lds_void_p)(lb + dst), 16, 0, 0);
+        }
+    };
+
+    i32x16 acc[4][4];  // acc[i][j] = C^T block (n block j, m block i)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) acc[i][j][t] = 0;
+
+    // Operand fragments of one 32-byte K step: f[0..3] A row blocks,
+    // f[4..7] B column blocks; two sets (f0, f1) alternate. Row offsets of
+    // this lane's fragment rows within a stage, chunk 0; chunk c of a row
+    // sits at 16 * (c ^ big_swz(row)), i.e. XOR (c << 4) into the offset.
+    unsigned arow_off[4], brow_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        arow_off[i] = (unsigned)big_lds_off(wm * 128 + i * 32 + r32, 0);
+        brow_off[i] = (unsigned)big_lds_off(wn * 128 + i * 32 + r32, 0);
+    }
+    const unsigned lds0 = lds_addr(lds);
+    auto read_frags = [&](int st, int sub, i32x4 (&f)[8]) {
+        const unsigned la = lds0 + st * kSlabBytes, lb = la + kBigT * kBigK;
+        const unsigned cx = (unsigned)((2 * sub + h) << 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f[i] = lds_read16(la + (arow_off[i] ^ cx));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f[4 + j] = lds_read16(lb + (brow_off[j] ^ cx));
+    };
+    // 16 MFMAs on f; with rd, the next fragment set's 8 reads go out between
+    // them (one after every second MFMA)
+    auto mfma_and_read = [&](const i32x4 (&f)[8], bool rd, int st, int sub,
+                             i32x4 (&nf)[8]) {
+        const unsigned la = lds0 + st * kSlabBytes, lb = la + kBigT * kBigK;
+        const unsigned cx = (unsigned)((2 * sub + h) << 4);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int i = q >> 2, j = q & 3;
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[4 + j], f[i], acc[i][j], 0, 0, 0);
+            if (rd && (q & 1)) {
+                const int x = q >> 1;  // 0..7
+                __builtin_amdgcn_sched_barrier(0);
+                nf[x] = lds_read16(x < 4 ? la + (arow_off[x] ^ cx)
+                                         : lb + (brow_off[x - 4] ^ cx));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+
+    // Per slab kt (in stage st = kt % kDmaStages), with f0 = (kt, sub 0) in
+    // registers:
+    //   16 MFMAs on f0 while f1 = (kt, sub 1) is read; wait f1;
+    //   wait for slab kt+1's DMA, barrier (every wave is past its reads of
+    //   stage st, and slab kt+1 is visible); refill stage st with slab
+    //   kt + kDmaStages;
+    //   16 MFMAs on f1 while f0 = (kt+1, sub 0) is read; wait f0.
+    const int nk = k / kBigK;
+    const int pre = min(kDmaStages, nk);
+    for (int s = 0; s < pre; ++s) issue(s, s);
+    // slab 0 landed: at most pre - 1 slabs issued after it still in flight
+    switch (pre - 1) {
+    case 4: wait_vmcnt<4 * kSlabLoads>(); break;
+    case 3: wait_vmcnt<3 * kSlabLoads>(); break;
+    case 2: wait_vmcnt<2 * kSlabLoads>(); break;
+    case 1: wait_vmcnt<1 * kSlabLoads>(); break;
+    default: wait_vmcnt<0>(); break;
+    }
+    __builtin_amdgcn_s_barrier();
+    i32x4 f0[8], f1[8];
+    read_frags(0, 0, f0);
+    lds_wait(f0);
+    int st = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+        const int st_next = st + 1 == kDmaStages ? 0 : st + 1;
+        mfma_and_read(f0, true, st, 1, f1);
+        lds_wait(f1);
+        // slabs issued after kt+1: kt+2 .. min(nk, kt + kDmaStages) - 1
+        const int after = min(kDmaStages - 2, nk - 2 - kt);
+        switch (after) {
+        case 3: wait_vmcnt<3 * kSlabLoads>(); break;
+        case 2: wait_vmcnt<2 * kSlabLoads>(); break;
+        case 1: wait_vmcnt<1 * kSlabLoads>(); break;
+        default: wait_vmcnt<0>(); break;
+        }
+        // bare barrier: this wave's slab kt+1 DMAs and stage-st reads are
+        // already waited for; __syncthreads() would add a release fence that
+        // drains every in-flight DMA (the later slabs too)
+        __builtin_amdgcn_s_barrier();
+        if (kt + kDmaStages < nk) issue(kt + kDmaStages, st);
+        const bool more = kt + 1 < nk;
+        mfma_and_read(f1, more, st_next, 0, f0);
+        if (more) lds_wait(f0);
+        st = st_next;
+    }
+
+    // ---- epilogue. acc[i][j] holds C^T: lane (r32, h), register t ->
+    // C[row = i*32 + r32][col = j*32 + 8(t/4) + 4h + t%4] of this wave's
+    // 128 x 128 sub-tile, i.e. 4 consecutive columns per register quad.
+    __syncthreads();  // every wave is done with the stages: LDS is reused
+    const float sa = epi_sa(e);
+    const int row0 = bm + wm * 128, col0 = bn + wn * 128;
+    auto scales4 = [&](int col) {  // f32(sa * sb[col .. col+3]), clamped at n
+        float4 s4;
+        if (e.sb_vec) {
+            s4.x = sa * e.sb_vec[min(col, n - 1)];
+            s4.y = sa * e.sb_vec[min(col + 1, n - 1)];
+            s4.z = sa * e.sb_vec[min(col + 2, n - 1)];
+            s4.w = sa * e.sb_vec[min(col + 3, n - 1)];
+        } else {
+            const float s = sa * e.sb;
+            s4 = make_float4(s, s, s, s);
+        }
+        return s4;
+    };
+    if constexpr (OUT == kOutBF16 || OUT == kOutF16) {
+        typedef typename std::conditional<OUT == kOutBF16, bf16, f16>::type OT;
+        typedef OT ot4 __attribute__((ext_vector_type(4)));
+        i8* const stg = lds + wave * (64 * kEpiPitch);  // this wave's 64 rows
+        float4 sc[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) sc[j][g] = scales4(col0 + j * 32 + 8 * g + 4 * h);
+        OT* const y = static_cast<OT*>(e.y);
+#pragma unroll
+        for (int ih = 0; ih < 2; ++ih) {
+#pragma unroll
+            for (int i2 = 0; i2 < 2; ++i2) {
+                const int i = 2 * ih + i2;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        ot4 v;
+                        v[0] = (OT)epi_val(acc[i][j][4 * g + 0], sc[j][g].x);
+                        v[1] = (OT)epi_val(acc[i][j][4 * g + 1], sc[j][g].y);
+                        v[2] = (OT)epi_val(acc[i][j][4 * g + 2], sc[j][g].z);
+                        v[3] = (OT)epi_val(acc[i][j][4 * g + 3], sc[j][g].w);
+                        *reinterpret_cast<ot4*>(stg + (i2 * 32 + r32) * kEpiPitch +
+                                                (j * 32 + 8 * g + 4 * h) * 2) = v;
+                    }
+            }
+            // 64 rows x 256 bytes back out: 16 lanes per row, 16 bytes each
+#pragma unroll
+            for (int rr = 0; rr < 16; ++rr) {
+                const int lr = rr * 4 + (lane >> 4);
+                const int row = row0 + ih * 64 + lr;
+                const int cb = (lane & 15) * 8;  // first of 8 columns
+                const i8* src = stg + lr * kEpiPitch + cb * 2;
+                if (row >= m) continue;
+                OT* dst = y + (size_t)row * n + col0 + cb;
+                if ((n & 7) == 0) {
+                    if (col0 + cb < n)
+                        *reinterpret_cast<i32x4*>(dst) = *reinterpret_cast<const i32x4*>(src);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; ++c)
+                        if (col0 + cb + c < n) dst[c] = reinterpret_cast<const OT*>(src)[c];
+                }
+            }
+        }
+    } else {  // 4-byte outputs: 16-byte stores of 4 consecutive columns
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int col = col0 + j * 32 + 8 * g + 4 * h;
+                float4 s4;
+                if constexpr (OUT == kOutF32) s4 = scales4(col);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = row0 + i * 32 + r32;
+                    if (row >= m || col >= n) continue;
+                    i32x4 o;
+                    if constexpr (OUT == kOutI32) {
+                        o = i32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1],
+                                  acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                    } else {
+                        o = i32x4{__float_as_int(epi_val(acc[i][j][4 * g], s4.x)),
+                                  __float_as_int(epi_val(acc[i][j][4 * g + 1], s4.y)),
+                                  __float_as_int(epi_val(acc[i][j][4 * g + 2], s4.z)),
+                                  __float_as_int(epi_val(acc[i][j][4 * g + 3], s4.w))};
+                    }
+                    int* dst = static_cast<int*>(e.y) + (size_t)row * n + col;
+                    if ((n & 3) == 0) {
+                        *reinterpret_cast<i32x4*>(dst) = o;
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            if (col + c < n) dst[c] = o[c];
+                    }
+                }
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // dispatch
 // ---------------------------------------------------------------------------
 int env_int(const char* name, int dflt) {
@@ -326,7 +766,7 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
                     hipStream_t s) {
     const bool aligned = (k % 16 == 0) && ((uintptr_t)a % 16 == 0) &&
                          ((uintptr_t)b % 16 == 0);
-    const int force = env_int("FT_QGEMM_KERNEL", 0);  // 1 skinny, 2 tiled, 3 scalar
+    const int force = env_int("FT_QGEMM_KERNEL", 0);  // 1 skinny, 2 tiled, 3 scalar, 4 big
     if (!aligned || force == 3) {
         const long long total = (long long)m * n;
         qgemm_scalar<OUT><<<grid_1d(total, 256, 1 << 30), 256, 0, s>>>(a, b, e, m, n, k);
@@ -359,6 +799,16 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         else
             qgemm_skinny<4, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part, counters);
         launch_check("qgemm skinny kernel launch");
+        return;
+    }
+    if ((m >= kBigT && n >= kBigT && force != 2) || force == 4) {
+        const long long tiles = (long long)((m + kBigT - 1) / kBigT) * ((n + kBigT - 1) / kBigT);
+        if (tiles > (1LL << 30)) inval("qgemm problem too large for one launch");
+        if (k % kBigK == 0 && env_int("FT_QGEMM_NO_DMA", 0) == 0)
+            qgemm_big_dma<OUT><<<(unsigned)tiles, 256, 0, s>>>(a, b, e, m, n, k);
+        else
+            qgemm_big<OUT><<<(unsigned)tiles, 256, 0, s>>>(a, b, e, m, n, k);
+        launch_check("qgemm big kernel launch");
         return;
     }
     constexpr int BM = 128, BN = 128;

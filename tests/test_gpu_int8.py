@@ -102,7 +102,9 @@ GEMM_SHAPES = [
     (300, 500, 1024),      # tiled, ragged
     (17, 4096, 129),       # scalar fallback, tall N
     (100, 50, 16),         # tiled, single short slab
-    (1024, 1024, 1024),    # tiled, many tiles
+    (1024, 1024, 1024),    # big tiles (256 x 256)
+    (257, 300, 80),        # big tiles, ragged M/N, K not a multiple of 64
+    (512, 256, 1040),      # big tiles, K tail
 ]
 
 
@@ -122,7 +124,7 @@ def test_qgemm_bit_exact(m, n, k):
                                   oracle.qgemm_perchannel(a, 0.031, b, sb))
 
 
-@pytest.mark.parametrize("kernel", ["1", "2", "3"])
+@pytest.mark.parametrize("kernel", ["1", "2", "3", "4"])
 def test_every_gemm_kernel_bit_exact(kernel, monkeypatch):
     monkeypatch.setenv("FT_QGEMM_KERNEL", kernel)
     rng = np.random.default_rng(int(kernel))
@@ -146,11 +148,12 @@ def test_skinny_k_split_bit_exact_and_counters_reset(ksplit, monkeypatch):
 
 
 @pytest.mark.parametrize("odt", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m", [16, 256])
-def test_half_outputs_are_rounded_f32(odt, m):
-    rng = np.random.default_rng(m + 9)
-    a, b = rand_q(rng, m, 2048), rand_q(rng, 384, 2048)
-    sb = rng.uniform(1e-3, 1e-2, 384).astype(np.float32)
+@pytest.mark.parametrize("m,n", [(16, 384), (256, 384), (300, 384), (300, 260)])
+def test_half_outputs_are_rounded_f32(odt, m, n):
+    # (300, 260): ragged tile edges and N % 8 != 0 (element-wise stores)
+    rng = np.random.default_rng(m + n + 9)
+    a, b = rand_q(rng, m, 2048), rand_q(rng, n, 2048)
+    sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
     y = ft.qgemm_perchannel(t(a), 0.013, t(b), t(sb), out_dtype=odt)
     torch.cuda.synchronize()
     ref = torch.from_numpy(oracle.qgemm_perchannel(a, 0.013, b, sb)).to(odt)
