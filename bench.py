@@ -15,9 +15,9 @@ lens[b] + 1 tokens.
               kv_append copy (read + write of the new K/V rows). This is the
               reference's counting (benchmarks/bench.py:480,496) plus the
               table and the append.
-  roofline  = attention only (stage-1 chunk kernel + combine kernel, timed
-              together with HIP events recorded on the stream they are
-              launched on): attention bytes / attention time, against
+  roofline  = attention only (attn_decode_stream + attn_combine_stream,
+              timed together with HIP events recorded on the stream they
+              are launched on): attention bytes / attention time, against
               8 TB/s.
   secondary = BASELINE config 5a: W8A8 GEMM M=4096 K=8192 N=28672, int8
               uniform in [-127, 127], per-channel scales, bf16 output;
@@ -180,7 +180,8 @@ def bench_c5a(torch, ft, dev, steps, warmup):
                 roofline={"bound": "mfma", "achieved": round(tops, 2),
                           "peak": INT8_PEAK_TOPS, "unit": "TOPS",
                           "frac": round(tops / INT8_PEAK_TOPS, 4),
-                          "traffic": traffic_for("qgemm_c5a")})
+                          "traffic": traffic_for("qgemm_c5a"),
+                          "kernel": "qgemm_big_dma"})
 
 
 # ---------------------------------------------------------------------------
@@ -307,7 +308,7 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic_for("attention_c3"),
-                     "kernel": "attention_decode_paged (chunk + combine)",
+                     "kernel": "attention_decode_paged = attn_decode_stream + attn_combine_stream",
                      "avg_us": round(attn_ms * 1e3, 2),
                      "bytes_per_launch": w["attn_bytes"]},
         "cpu_baseline": cpu,
