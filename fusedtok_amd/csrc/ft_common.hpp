@@ -92,8 +92,7 @@ enum class Scratch : int {
     AttnPartials = 0,
     QuantMax = 1,
     GemmPartials = 2,
-    GemmCounters = 3,
-    kCount = 4
+    kCount = 3
 };
 void* scratch(Scratch which, size_t bytes, hipStream_t s);
 // Same, but memory is zero when first allocated (or re-allocated); kernels

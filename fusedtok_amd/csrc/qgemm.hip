@@ -9,17 +9,20 @@
 // value rounded to nearest-even.
 //
 // Kernels
-//   qgemm_skinny  M <= 64 (decode): W streamed once from HBM straight into
-//                 the B operand of v_mfma_i32_16x16x64_i8 (lane (r, g) loads
-//                 W[n0+r][k+16g .. +15], one 16-byte load); the 4 waves of a
-//                 workgroup split K and fold in LDS; when N alone cannot fill
-//                 the chip, K is also split across workgroups whose int32
-//                 partials are folded in a fixed order by the last one to
-//                 finish (per-tile arrival counter, reset by that workgroup).
-//   qgemm_tiled   M > 64: BMxBN workgroup tiles, v_mfma_i32_32x32x32_i8,
-//                 BK = 64 slabs double-buffered through LDS.
-//   qgemm_scalar  any shape/alignment (K % 16 != 0, misaligned views).
-//   K == 0        zero fill (a kernel, not a memset, so it captures cleanly).
+//   qgemv_dot4     M <= 8 (decode GEMV, no MFMA): v_dot4_i32_i8 over 16-byte
+//                  K pieces, several W rows in flight per wave, wave sums.
+//   qgemm_skinny   8 < M <= 64: W streamed once into the B operand of
+//                  v_mfma_i32_16x16x64_i8, 64 columns per workgroup (A shared
+//                  through L1), K split across workgroups when N alone cannot
+//                  fill the chip; int32 partials folded by qgemm_ksum.
+//   qgemm_big_dma  M, N >= 256, K % 64 == 0: 256x256 tiles on
+//                  v_mfma_i32_32x32x32_i8 fed by a 5-stage global->LDS DMA
+//                  ring; LDS-staged, coalesced epilogue.
+//   qgemm_big      M, N >= 256, other K: the same tiles, register-staged.
+//   qgemm_tiled    64 < M (< 256 or N < 256): 128x128 tiles, 64-byte slabs
+//                  double-buffered through LDS.
+//   qgemm_scalar   any shape/alignment (K % 16 != 0, misaligned views).
+//   K == 0         zero fill (a kernel, not a memset, so it captures cleanly).
 #include "ft_common.hpp"
 
 #include <algorithm>
@@ -34,6 +37,8 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef signed char i8;
 
 enum OutKind { kOutF32 = 0, kOutBF16 = 1, kOutF16 = 2, kOutI32 = 3 };
+
+typedef __attribute__((address_space(3))) void* lds_void_p;
 
 struct Epi {
     void* y;
@@ -96,96 +101,184 @@ __global__ __launch_bounds__(256) void qgemm_scalar(const i8* __restrict__ a,
 }
 
 // ---------------------------------------------------------------------------
-// skinny (M <= 16*MT)
+// decode GEMV (M <= 8, no MFMA): y[m][j] = sum_k A[m][k] * W[j][k] on
+// v_dot4_i32_i8. A wave owns kGemvRows consecutive W rows at a time; its
+// lanes span K in 16-byte pieces (lane l reads bytes 16 l + 1024 c of each
+// row, so one load instruction covers 1 KB of a row contiguously). K is
+// walked in passes of kGemvChunks KB: all weight and activation pieces of a
+// pass are loaded before any is consumed, so a 4096-byte row costs one
+// memory round trip. Every lane keeps the M x rows partial dot products,
+// summed across the wave at the end (integer sums: exact in any order).
 // ---------------------------------------------------------------------------
+constexpr int kGemvRows = 4;
+constexpr int kGemvChunks = 4;
+
+template <int M_, int OUT>
+__global__ __launch_bounds__(256) void qgemv_dot4(const i8* __restrict__ a,
+                                                  const i8* __restrict__ b,
+                                                  Epi e, int n, int k) {
+    const int lane = threadIdx.x & 63;
+    const int gwave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nwaves = gridDim.x * 4;
+    const float sa = epi_sa(e);
+    for (int j0 = gwave * kGemvRows; j0 < n; j0 += nwaves * kGemvRows) {
+        int acc[kGemvRows][M_];
+#pragma unroll
+        for (int r = 0; r < kGemvRows; ++r)
+#pragma unroll
+            for (int mm = 0; mm < M_; ++mm) acc[r][mm] = 0;
+        for (int kp = 0; kp < k; kp += 1024 * kGemvChunks) {
+            i32x4 w[kGemvChunks][kGemvRows], x[kGemvChunks][M_];
+#pragma unroll
+            for (int c = 0; c < kGemvChunks; ++c) {
+                const int kk = kp + 1024 * c + 16 * lane;
+                const bool kok = kk < k;  // k % 16 == 0: a piece is all in or out
+                const i32x4 z = {0, 0, 0, 0};
+#pragma unroll
+                for (int r = 0; r < kGemvRows; ++r) {
+                    const int row = min(j0 + r, n - 1);
+                    w[c][r] = kok ? *reinterpret_cast<const i32x4*>(b + (size_t)row * k + kk) : z;
+                }
+#pragma unroll
+                for (int mm = 0; mm < M_; ++mm)
+                    x[c][mm] = kok ? *reinterpret_cast<const i32x4*>(a + (size_t)mm * k + kk) : z;
+            }
+#pragma unroll
+            for (int c = 0; c < kGemvChunks; ++c)
+#pragma unroll
+                for (int mm = 0; mm < M_; ++mm)
+#pragma unroll
+                    for (int r = 0; r < kGemvRows; ++r) {
+                        int s = acc[r][mm];
+                        s = __builtin_amdgcn_sdot4(w[c][r][0], x[c][mm][0], s, false);
+                        s = __builtin_amdgcn_sdot4(w[c][r][1], x[c][mm][1], s, false);
+                        s = __builtin_amdgcn_sdot4(w[c][r][2], x[c][mm][2], s, false);
+                        s = __builtin_amdgcn_sdot4(w[c][r][3], x[c][mm][3], s, false);
+                        acc[r][mm] = s;
+                    }
+        }
+#pragma unroll
+        for (int r = 0; r < kGemvRows; ++r)
+#pragma unroll
+            for (int mm = 0; mm < M_; ++mm) {
+                int v = acc[r][mm];
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+                acc[r][mm] = v;
+            }
+        // lane r * M_ + mm stores (r, mm)
+#pragma unroll
+        for (int r = 0; r < kGemvRows; ++r)
+#pragma unroll
+            for (int mm = 0; mm < M_; ++mm)
+                if (lane == r * M_ + mm && j0 + r < n)
+                    epi_store<OUT>(e, sa, n, mm, j0 + r, acc[r][mm]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// skinny MFMA GEMM (M <= 16*MT <= 64): a workgroup covers 64 output columns,
+// wave w the 16 columns of W rows [64 bx + 16 w, +16), over the workgroup's
+// K range (K split across blockIdx.y when N alone cannot fill the chip).
+// K is walked in 1 KB chunks. Per chunk, the A rows are copied into LDS
+// once for the whole workgroup (global_load_lds_dwordx4: one instruction
+// per 1 KB row, rows padded to kSkPitch bytes so the 16 rows of a fragment
+// read fall in distinct banks), while each wave has all 16 of its W K-steps
+// (lane (r, g): W[n0 + r][k + 16 g .. +15], the B operand of
+// v_mfma_i32_16x16x64_i8) in flight. With a K split, int32 partials go to
+// scratch and qgemm_ksum folds them (fixed order, exact) and applies the
+// epilogue: a second launch instead of a device-scope fence per workgroup.
+// ---------------------------------------------------------------------------
+constexpr int kSkChunk = 1024;           // K bytes per chunk
+constexpr int kSkSteps = kSkChunk / 64;  // MFMA K steps per chunk
+constexpr int kSkPitch = kSkChunk + 16;  // LDS row pitch of staged A rows
+
 template <int MT, int OUT>
 __global__ __launch_bounds__(256) void qgemm_skinny(
     const i8* __restrict__ a, const i8* __restrict__ b, Epi e, int m, int n,
-    int k, int ksplit, int* __restrict__ part, int* __restrict__ counters) {
-    __shared__ i32x4 red[3][MT][64];
-    const int nt = blockIdx.x, ks = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int k, int ksplit, int* __restrict__ part) {
+    __shared__ __attribute__((aligned(16))) i8 sa_rows[16 * MT * kSkPitch];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
-    const int steps = (k + 63) >> 6;
-    const int per = (steps + ksplit - 1) / ksplit;
-    const int s0 = ks * per, s1 = min(steps, s0 + per);
+    const int n0 = (blockIdx.x * 4 + wave) * 16;
+    const bool live = n0 < n;  // this wave's column tile exists
+    const int ks = blockIdx.y;
+    const int chunks = (k + kSkChunk - 1) / kSkChunk;
+    const int per = (chunks + ksplit - 1) / ksplit;
+    const int c0 = ks * per, c1 = min(chunks, c0 + per);
 
     i32x4 acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = i32x4{0, 0, 0, 0};
-    const int nrow = nt * 16 + r;
-    const bool nrow_ok = nrow < n;
-    const i8* brow = b + (size_t)(nrow_ok ? nrow : 0) * k + 16 * g;
-    const i8* arow[MT];
-    bool arow_ok[MT];
+    const i8* brow = b + (size_t)min(n0 + r, n - 1) * k + 16 * g;
+    for (int c = c0; c < c1; ++c) {
+        const int kc = c * kSkChunk;
+        __syncthreads();  // every wave is done with the previous chunk's A
+        // stage A rows [0, 16 MT) x [kc, kc + 1 KB): wave w copies rows w, w+4, ..
+        // (rows past M repeat row M-1; K past the end reads zeros below)
+        for (int row = wave; row < 16 * MT; row += 4) {
+            const int src_row = min(row, m - 1);
+            const int kk = min(kc + 16 * lane, k - 16);
+            __builtin_amdgcn_global_load_lds(a + (size_t)src_row * k + kk,
+                                             (lds_void_p)(sa_rows + row * kSkPitch), 16, 0, 0);
+        }
+        i32x4 bv[kSkSteps];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-        const int row = t * 16 + r;
-        arow_ok[t] = row < m;
-        arow[t] = a + (size_t)(arow_ok[t] ? row : 0) * k + 16 * g;
-    }
-#pragma unroll 4
-    for (int s = s0 + wave; s < s1; s += 4) {
-        const int kb = s << 6;
-        const bool kok = kb + 16 * g < k;
-        const i32x4 z = {0, 0, 0, 0};
-        const i32x4 bv = (nrow_ok && kok) ? *reinterpret_cast<const i32x4*>(brow + kb) : z;
+        for (int u = 0; u < kSkSteps; ++u) {
+            const int kb = kc + 64 * u + 16 * g;
+            const i32x4 z = {0, 0, 0, 0};
+            bv[u] = (live && kb < k) ? *reinterpret_cast<const i32x4*>(brow + kc + 64 * u) : z;
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's A copies (and W loads) landed
+        __syncthreads();
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const i32x4 av = (arow_ok[t] && kok) ? *reinterpret_cast<const i32x4*>(arow[t] + kb) : z;
-            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc[t], 0, 0, 0);
+        for (int u = 0; u < kSkSteps; ++u) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                i32x4 av = *reinterpret_cast<const i32x4*>(
+                    sa_rows + (16 * t + r) * kSkPitch + 64 * u + 16 * g);
+                if (kc + 64 * u + 16 * g >= k) av = i32x4{0, 0, 0, 0};
+                acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[u], acc[t], 0, 0, 0);
+            }
         }
     }
-    // fold the 4 waves (fixed order: wave 0 + 1 + 2 + 3)
-    if (wave > 0) {
-#pragma unroll
-        for (int t = 0; t < MT; ++t) red[wave - 1][t][lane] = acc[t];
-    }
-    __syncthreads();
-    if (wave != 0) return;
-#pragma unroll
-    for (int w = 0; w < 3; ++w)
-#pragma unroll
-        for (int t = 0; t < MT; ++t) acc[t] += red[w][t][lane];
-
-    // C layout: lane (r, g) holds C[4g+i][r] = (A row t*16+4g+i, W row nt*16+r)
-    const int col = nt * 16 + r;
-    if (ksplit > 1) {
-        int* mine = part + ((size_t)nt * ksplit + ks) * (MT * 256);
-#pragma unroll
-        for (int t = 0; t < MT; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mine[(t * 4 + i) * 64 + lane] = acc[t][i];
-        // release the partial, count arrivals; only wave 0 is alive here, so
-        // the decision is broadcast within the wave (no workgroup barrier)
-        __threadfence();
-        int last = 0;
-        if (lane == 0) last = (atomicAdd(&counters[nt], 1) == ksplit - 1) ? 1 : 0;
-        last = __shfl(last, 0, 64);
-        if (!last) return;
-        __threadfence();
-#pragma unroll
-        for (int t = 0; t < MT; ++t) acc[t] = i32x4{0, 0, 0, 0};
-        for (int j = 0; j < ksplit; ++j) {
-            const int* pj = part + ((size_t)nt * ksplit + j) * (MT * 256);
-#pragma unroll
-            for (int t = 0; t < MT; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    acc[t][i] += pj[(t * 4 + i) * 64 + lane];
-        }
-        if (lane == 0) counters[nt] = 0;
-    }
-    if (col < n) {
+    if (!live) return;
+    // C layout: lane (r, g) holds C[4g + i][r] = (A row 16t + 4g + i, W row n0 + r)
+    const int col = n0 + r;
+    if (col >= n) return;
+    if (ksplit == 1) {
         const float sa = epi_sa(e);
 #pragma unroll
         for (int t = 0; t < MT; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int row = t * 16 + 4 * g + i;
+                const int row = 16 * t + 4 * g + i;
                 if (row < m) epi_store<OUT>(e, sa, n, row, col, acc[t][i]);
             }
+    } else {
+        int* mine = part + (size_t)ks * m * n;
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = 16 * t + 4 * g + i;
+                if (row < m) mine[(size_t)row * n + col] = acc[t][i];
+            }
     }
+}
+
+// K-split fold: out[row][col] = sum over ks (in order) of part[ks][row][col]
+template <int OUT>
+__global__ __launch_bounds__(256) void qgemm_ksum(const int* __restrict__ part,
+                                                  Epi e, int m, int n, int ksplit) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long mn = (long long)m * n;
+    if (idx >= mn) return;
+    int s = 0;
+    for (int j = 0; j < ksplit; ++j) s += part[(size_t)j * mn + idx];
+    const int row = (int)(idx / n), col = (int)(idx - (long long)row * n);
+    epi_store<OUT>(e, epi_sa(e), n, row, col, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -453,7 +546,6 @@ void qgemm_big(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
 // Rows past M / N load a clamped (real) row; they only feed outputs that
 // are never stored.
 // ---------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) void* lds_void_p;
 constexpr int kDmaStages = 5;
 constexpr int kSlabBytes = 2 * kBigT * kBigK;  // A + B slab, 32 KB
 constexpr int kSlabLoads = 8;  // DMA instructions per thread per slab (4 A + 4 B)
@@ -766,39 +858,60 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
                     hipStream_t s) {
     const bool aligned = (k % 16 == 0) && ((uintptr_t)a % 16 == 0) &&
                          ((uintptr_t)b % 16 == 0);
-    const int force = env_int("FT_QGEMM_KERNEL", 0);  // 1 skinny, 2 tiled, 3 scalar, 4 big
+    // FT_QGEMM_KERNEL: 1 skinny, 2 tiled, 3 scalar, 4 big, 5 gemv
+    const int force = env_int("FT_QGEMM_KERNEL", 0);
     if (!aligned || force == 3) {
         const long long total = (long long)m * n;
         qgemm_scalar<OUT><<<grid_1d(total, 256, 1 << 30), 256, 0, s>>>(a, b, e, m, n, k);
         launch_check("qgemm scalar kernel launch");
         return;
     }
-    if ((m <= 64 && force != 2) || force == 1) {
+    if ((m <= 8 && force == 0) || force == 5) {
+        if (m > 8) inval("gemv qgemm supports m <= 8");
+        const long long waves = std::min<long long>((n + kGemvRows - 1) / kGemvRows,
+                                                    (long long)dev_info().cu_count * 16);
+        const unsigned grid = (unsigned)((waves + 3) / 4);
+        switch (m) {
+        case 1: qgemv_dot4<1, OUT><<<grid, 256, 0, s>>>(a, b, e, n, k); break;
+        case 2: qgemv_dot4<2, OUT><<<grid, 256, 0, s>>>(a, b, e, n, k); break;
+        case 3: qgemv_dot4<3, OUT><<<grid, 256, 0, s>>>(a, b, e, n, k); break;
+        case 4: qgemv_dot4<4, OUT><<<grid, 256, 0, s>>>(a, b, e, n, k); break;
+        case 5: qgemv_dot4<5, OUT><<<grid, 256, 0, s>>>(a, b, e, n, k); break;
+        case 6: qgemv_dot4<6, OUT><<<grid, 256, 0, s>>>(a, b, e, n, k); break;
+        case 7: qgemv_dot4<7, OUT><<<grid, 256, 0, s>>>(a, b, e, n, k); break;
+        default: qgemv_dot4<8, OUT><<<grid, 256, 0, s>>>(a, b, e, n, k); break;
+        }
+        launch_check("qgemm gemv kernel launch");
+        return;
+    }
+    if ((m <= 64 && force != 2 && force != 4) || force == 1) {
         if (m > 64) inval("skinny qgemm supports m <= 64");
-        const int ntiles = (n + 15) / 16;
-        const int steps = (k + 63) / 64;
+        const int col_wgs = (n + 63) / 64;
+        const int chunks = (k + kSkChunk - 1) / kSkChunk;  // 1 KB K chunks
         const int cus = dev_info().cu_count;
-        int ksplit = 1;
-        while (ntiles * ksplit < 2 * cus && steps / (ksplit * 2) >= 8) ksplit *= 2;
+        // enough workgroups for 2 per CU
+        int ksplit = std::max(1, std::min((2 * cus + col_wgs - 1) / col_wgs, chunks));
         const int forced_split = env_int("FT_QGEMM_KSPLIT", 0);
-        if (forced_split > 0) ksplit = std::min(forced_split, std::max(1, steps));
+        if (forced_split > 0) ksplit = std::min(forced_split, chunks);
+        if (ksplit > 65535) ksplit = 65535;
         const int mt = (m + 15) / 16;
         int* part = nullptr;
-        int* counters = nullptr;
-        if (ksplit > 1) {
+        if (ksplit > 1)
             part = (int*)scratch(Scratch::GemmPartials,
-                                 (size_t)ntiles * ksplit * 4 * 256 * sizeof(int), s);
-            counters = (int*)scratch_zeroed(Scratch::GemmCounters,
-                                            (size_t)ntiles * sizeof(int), s);
-        }
-        dim3 grid(ntiles, ksplit);
+                                 (size_t)ksplit * m * n * sizeof(int), s);
+        dim3 grid(col_wgs, ksplit);
         if (mt <= 1)
-            qgemm_skinny<1, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part, counters);
+            qgemm_skinny<1, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part);
         else if (mt <= 2)
-            qgemm_skinny<2, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part, counters);
+            qgemm_skinny<2, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part);
         else
-            qgemm_skinny<4, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part, counters);
+            qgemm_skinny<4, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part);
         launch_check("qgemm skinny kernel launch");
+        if (ksplit > 1) {
+            const long long mn = (long long)m * n;
+            qgemm_ksum<OUT><<<grid_1d(mn, 256, 1 << 30), 256, 0, s>>>(part, e, m, n, ksplit);
+            launch_check("qgemm k-split fold launch");
+        }
         return;
     }
     if ((m >= kBigT && n >= kBigT && force != 2) || force == 4) {
