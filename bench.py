@@ -23,6 +23,13 @@ lens[b] + 1 tokens.
               uniform in [-127, 127], per-channel scales, bf16 output;
               TOPS = 2*M*N*K / t (reference benchmarks/bench.py:451), against
               the 5.0 POP/s dense int8 MFMA peak.
+  chains    = BASELINE config 2 (RMSNorm -> int8 quantize -> W8A8 GEMM,
+              M in {1, 8, 16}, K=4096, N=11008, fp16 in/out) and config 4
+              (one Llama-3-8B W8A8 decode layer at batch 64, context 8192),
+              each replayed as a captured HIP graph (the launch sequence of
+              a decode loop without per-call Python cost); weights are
+              cycled over enough copies to exceed the 256 MB last-level
+              cache, as a model's successive layers would.
   cpu_baseline = the C++ restatement of the reference's single-threaded
               attention_decode_paged_cpu / kv_append_paged_cpu (oracle/),
               on a bounded sample of the same rows, one core.
@@ -50,6 +57,9 @@ INT8_PEAK_TOPS = 5000.0
 C3 = dict(batch=32, hq=32, hkv=8, dim=128, page=16, len_lo=512, len_hi=32768,
           pool_factor=4, seed=2026)
 C5A = dict(m=4096, k=8192, n=28672, seed=5)
+C2 = dict(ms=(1, 8, 16), k=4096, n=11008, seed=2, copies=8, reps=20)
+C4 = dict(batch=64, ctx=8192, hidden=4096, hq=32, hkv=8, dim=128, inter=14336,
+          page=16, eps=1e-5, theta=500000.0, layers=2, seed=4, reps=10)
 
 
 def parse():
@@ -61,7 +71,10 @@ def parse():
                    help="skip the CPU baseline leg")
     p.add_argument("--no-gemm", action="store_true",
                    help="skip the secondary W8A8 GEMM measurement")
-    p.add_argument("--only", choices=["decode", "gemm", "copy"], default=None,
+    p.add_argument("--no-chains", action="store_true",
+                   help="skip the config 2 / config 4 chain measurements")
+    p.add_argument("--only", choices=["decode", "gemm", "copy", "c2", "c4"],
+                   default=None,
                    help="run one workload only (profiling runs); 'copy' is "
                         "the HBM-counter calibration: a plain 1 GiB "
                         "device-to-device tensor copy")
@@ -185,6 +198,125 @@ def bench_c5a(torch, ft, dev, steps, warmup):
 
 
 # ---------------------------------------------------------------------------
+# chains: config 2 and config 4, timed as HIP graph replays
+# ---------------------------------------------------------------------------
+def graph_time_us(torch, fn, per_graph, reps, warmup=2):
+    """Capture `per_graph` calls of fn() into one HIP graph; replay it `reps`
+    times; return microseconds per fn() call."""
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(per_graph):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+    del g
+    return us
+
+
+def bench_c2(torch, ft, dev):
+    c = C2
+    gen = torch.Generator(device=dev).manual_seed(c["seed"])
+    k, n = c["k"], c["n"]
+    ws = [torch.randint(-127, 128, (n, k), device=dev, generator=gen,
+                        dtype=torch.int32).to(torch.int8) for _ in range(c["copies"])]
+    sb = (torch.rand((n,), device=dev, generator=gen) * 9e-3 + 1e-3).float()
+    wn = (torch.rand((k,), device=dev, generator=gen) + 0.5).float()
+    out = []
+    for m in c["ms"]:
+        x = torch.randn((m, k), device=dev, generator=gen).to(torch.float16)
+
+        def chain(i):
+            q, s = ft.rmsnorm_quant(x, wn, eps=1e-5, device_scale=True)
+            return ft.qgemm_perchannel(q, s, ws[i % len(ws)], sb, out_dtype=torch.float16)
+        us = graph_time_us(torch, chain, 2 * len(ws), c["reps"])
+        nbytes = n * k + n * 4 + k * 4 + m * k * (2 + 1) + m * n * 2
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out.append({"m": m, "us_per_chain": round(us, 2), "GB/s": round(gbs, 1),
+                    "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)})
+    del ws
+    return {"metric": "fused RMSNorm -> quantize -> W8A8 GEMM (BASELINE config 2)",
+            "unit": "us per chain", "dtype": "int8 GEMM, fp16 in/out",
+            "config": {"workload": "rmsnorm_quant + qgemm_perchannel, K=4096 "
+                                   "N=11008, per-channel scales, fp16 out",
+                       "seed": c["seed"], "weight_copies": c["copies"]},
+            "bytes": "W (N*K) + scales + x, q, y", "results": out}
+
+
+def bench_c4(torch, np, ft, dev):
+    c = C4
+    gen = torch.Generator(device=dev).manual_seed(c["seed"])
+    b, hq, hkv, d, hid, inter = c["batch"], c["hq"], c["hkv"], c["dim"], c["hidden"], c["inter"]
+    page = c["page"]
+    bf = torch.bfloat16
+
+    def wq(rows, cols):
+        return (torch.randint(-127, 128, (rows, cols), device=dev, generator=gen,
+                              dtype=torch.int32).to(torch.int8),
+                (torch.rand((rows,), device=dev, generator=gen) * 9e-3 + 1e-3).float())
+    layers = []
+    for _ in range(c["layers"]):
+        layers.append(dict(wn1=(torch.rand((hid,), device=dev, generator=gen) + 0.5).float(),
+                           wn2=(torch.rand((hid,), device=dev, generator=gen) + 0.5).float(),
+                           qkv=wq((hq + 2 * hkv) * d, hid), o=wq(hid, hq * d),
+                           gu=wq(2 * inter, hid), down=wq(hid, inter)))
+    # paged KV: every row holds ctx tokens; the new token goes to slot ctx
+    npg = (c["ctx"] + 1 + page - 1) // page
+    pool = b * npg + 64
+    rng = np.random.default_rng(c["seed"])
+    table = torch.from_numpy(rng.permutation(pool)[: b * npg].reshape(b, npg)
+                             .astype(np.int32)).to(dev)
+    kp = torch.randn((pool, hkv, page, d), device=dev, generator=gen, dtype=bf)
+    vp = torch.randn((pool, hkv, page, d), device=dev, generator=gen, dtype=bf)
+    lens = torch.full((b,), c["ctx"], dtype=torch.int32, device=dev)
+    lens1 = lens + 1
+    x = torch.randn((b, hid), device=dev, generator=gen).to(bf)
+
+    def layer(i):
+        L = layers[i % len(layers)]
+        q1, s1 = ft.rmsnorm_quant(x, L["wn1"], eps=c["eps"], device_scale=True)
+        qkv = ft.qgemm_perchannel(q1, s1, *L["qkv"], out_dtype=bf)
+        # position ctx = lens[b] + pos_offset 0
+        qr = ft.rope_kv_append_paged(qkv, hq, hkv, kp, vp, table, lens,
+                                     theta=c["theta"], pos_offset=0, neox=True)
+        att = ft.attention_decode_paged(qr, kp, vp, table, lens1)
+        qa, sa = ft.quantize_int8(att.reshape(b, hq * d), device_scale=True)
+        o = ft.qgemm_perchannel(qa, sa, *L["o"], out_dtype=bf)
+        q2, s2 = ft.rmsnorm_quant(o, L["wn2"], residual=x, eps=c["eps"],
+                                  device_scale=True)
+        h = ft.qgemm_perchannel(q2, s2, *L["gu"], out_dtype=bf)
+        q3, s3 = ft.swiglu_quant(h[:, :inter], h[:, inter:], device_scale=True)
+        return ft.qgemm_perchannel(q3, s3, *L["down"], out_dtype=bf)
+    us = graph_time_us(torch, layer, 2 * len(layers), c["reps"])
+    wbytes = sum(int(w[0].numel()) + 4 * int(w[1].numel())
+                 for w in (layers[0]["qkv"], layers[0]["o"], layers[0]["gu"], layers[0]["down"]))
+    kvbytes = b * (c["ctx"] + 1) * hkv * d * 2 * 2
+    nbytes = wbytes + kvbytes
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del kp, vp, layers
+    return {"metric": "Llama-3-8B W8A8 decode layer (BASELINE config 4)",
+            "value": round(us, 2), "unit": "us per layer",
+            "tokens_per_s": round(b / (us * 1e-6), 1),
+            "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_layer": nbytes, "dtype": "bf16 activations / KV, int8 GEMMs",
+            "config": {"workload": "rmsnorm_quant -> QKV qgemm -> rope_kv_append_paged "
+                                   "(NeoX, position 8192) -> attention_decode_paged -> "
+                                   "quantize -> o_proj qgemm -> rmsnorm_quant(+residual) "
+                                   "-> gate/up qgemm -> swiglu_quant -> down qgemm",
+                       "batch": b, "context": c["ctx"], "layers_cycled": c["layers"],
+                       "seed": c["seed"]}}
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline: the oracle on a bounded sample of config 3's rows
 # ---------------------------------------------------------------------------
 def cpu_baseline_c3(torch, np, w, budget_s=12.0):
@@ -260,6 +392,12 @@ def main():
     if args.only == "gemm":
         log("gemm", json.dumps(bench_c5a(torch, ft, dev, args.steps, args.warmup)))
         return
+    if args.only == "c2":
+        log("c2", json.dumps(bench_c2(torch, ft, dev)))
+        return
+    if args.only == "c4":
+        log("c4", json.dumps(bench_c4(torch, np, ft, dev)))
+        return
 
     log(f"config 3: building workload (seed {C3['seed']})")
     w, wall, attn_ms = bench_c3(torch, np, ft, dev, args.steps, args.warmup)
@@ -278,6 +416,16 @@ def main():
         torch.cuda.empty_cache()
         secondary = bench_c5a(torch, ft, dev, max(5, args.steps // 2), 3)
         log(f"config 5a: {secondary['value']} TOPS")
+
+    chains = None
+    if not args.no_chains and args.only is None:
+        torch.cuda.empty_cache()
+        chains = [bench_c2(torch, ft, dev)]
+        log("config 2:", json.dumps(chains[0]["results"]))
+        torch.cuda.empty_cache()
+        chains.append(bench_c4(torch, np, ft, dev))
+        log(f"config 4: {chains[1]['value']} us per layer")
+        torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu and args.only is None:
@@ -313,6 +461,7 @@ def main():
                      "bytes_per_launch": w["attn_bytes"]},
         "cpu_baseline": cpu,
         "secondary": secondary,
+        "chains": chains,
     }
     print(json.dumps(line), flush=True)
 

@@ -32,7 +32,9 @@ Build additions (not in the reference): fp16 storage for ``rmsnorm``,
 ``rope`` and ``swiglu``; bf16 / fp16 input to ``quantize_int8`` and a
 device-resident scale (``device_scale=True``); bf16 / fp16 GEMM outputs
 (``out_dtype=``) and a device scale operand; ``qgemm_i32`` (raw int32
-accumulators); per-row RoPE positions (``positions=``).
+accumulators); per-row RoPE positions (``positions=``); the fused
+decode-chain steps ``rmsnorm_quant``, ``swiglu_quant`` and
+``rope_kv_append_paged`` (GPU tensors only).
 """
 
 import numpy as np
@@ -68,6 +70,9 @@ __all__ = [
     "attention_decode_paged",
     "kv_append",
     "kv_append_paged",
+    "rmsnorm_quant",
+    "swiglu_quant",
+    "rope_kv_append_paged",
 ]
 
 # C-ABI dtype codes (include/fusedtok_amd.h)
@@ -710,6 +715,139 @@ def quantize_int8(x, *, device_scale=False):
     dev = _need_device()
     q, s = quantize_int8(_upload(arr, dev))
     return (q.cpu() if _is_torch(x) else q.cpu().numpy()), s
+
+
+# ---------------------------------------------------------------------------
+# fused decode-chain steps (build additions; GPU tensors only). The
+# reference runs these as separate ops (rmsnorm -> quantize_int8,
+# swiglu -> quantize_int8, rope -> kv_append_paged); each fused op returns
+# exactly what this library's unfused chain returns.
+# ---------------------------------------------------------------------------
+
+
+def _gpu_only(t, name):
+    if not _on_gpu(t):
+        raise TypeError(f"{name} must be a GPU tensor (fused ops have no "
+                        "host path)")
+
+
+def rmsnorm_quant(x, weight, *, residual=None, eps=1e-6, device_scale=False):
+    """``quantize_int8(rmsnorm(x, weight, residual=residual, eps=eps))`` with
+    the RMSNorm output kept in float32 registers: returns ``(q, scale)``, q
+    int8 of x's shape, bit-identical to the unfused float32 chain. cols must
+    be a multiple of 4. ``device_scale=True`` returns the scale as a
+    1-element GPU float32 tensor without synchronising."""
+    _gpu_only(x, "x")
+    _check_dtype(x, "x", _FLOAT_DTYPES)
+    _require_gpu(weight, "weight")
+    if weight.dtype is not torch.float32:
+        weight = weight.to(torch.float32)
+    if not weight.is_contiguous():
+        weight = weight.contiguous()
+    rows, cols = _rows_cols(x.shape)
+    if weight.ndim != 1 or weight.numel() != cols:
+        raise ValueError("weight must be 1-D with cols entries")
+    r_ptr = None
+    if residual is not None:
+        _require_gpu(residual, "residual")
+        _check_dtype(residual, "residual", _FLOAT_DTYPES)
+        if residual.dtype is not x.dtype:
+            raise TypeError("residual must have the same dtype as x")
+        if residual.shape != x.shape:
+            raise ValueError("residual must have the same shape as x")
+        r_ptr = residual.data_ptr()
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    scale = torch.ones(1, dtype=torch.float32, device=x.device)
+    _fusedtok.rmsnorm_quant_launch(x.data_ptr(), _DT_CODE[x.dtype],
+                                   weight.data_ptr(), r_ptr, q.data_ptr(),
+                                   scale.data_ptr(), rows, cols, float(eps),
+                                   _stream())
+    return (q, scale) if device_scale else (q, float(scale))
+
+
+def swiglu_quant(gate, up, *, device_scale=False):
+    """``quantize_int8(swiglu(gate, up))`` without the float intermediate:
+    returns ``(q, scale)`` with q a dense int8 [rows, cols]. gate and up are
+    [rows, cols] (or 1-D) GPU tensors of one dtype whose rows may be strided
+    alike, e.g. ``h[:, :f]`` and ``h[:, f:]`` of one gate|up GEMM output."""
+    _gpu_only(gate, "gate")
+    _require_gpu(up, "up")
+    for name, t in (("gate", gate), ("up", up)):
+        if t.dtype not in _FLOAT_DTYPES:
+            raise TypeError(f"{name} must be float32, bfloat16 or float16")
+    if up.dtype is not gate.dtype:
+        raise TypeError("up must have the same dtype as gate")
+    if gate.shape != up.shape:
+        raise ValueError("gate and up must have the same shape")
+    if gate.ndim == 1:
+        gate, up = gate.reshape(1, -1), up.reshape(1, -1)
+    if gate.ndim != 2:
+        raise ValueError("gate and up must be 1-D or 2-D")
+    rows, cols = gate.shape
+    ld = gate.stride(0) if rows > 1 else cols
+    if rows > 0 and cols > 0:
+        if gate.stride(1) != 1 or up.stride(1) != 1 or \
+                (rows > 1 and up.stride(0) != ld):
+            raise ValueError("gate and up must have unit column stride and "
+                             "the same row stride")
+    q = torch.empty((rows, cols), dtype=torch.int8, device=gate.device)
+    scale = torch.ones(1, dtype=torch.float32, device=gate.device)
+    _fusedtok.swiglu_quant_launch(gate.data_ptr(), up.data_ptr(),
+                                  _DT_CODE[gate.dtype], q.data_ptr(),
+                                  scale.data_ptr(), rows, cols, ld, _stream())
+    return (q, scale) if device_scale else (q, float(scale))
+
+
+def rope_kv_append_paged(qkv, q_heads, kv_heads, k_pool, v_pool, block_table,
+                         lens, *, theta=10000.0, pos_offset=0, neox=False):
+    """The decode token's RoPE and paged KV append in one launch.
+
+    qkv: [B, (q_heads + 2 * kv_heads) * D] (rows may be strided), holding
+    each sequence's q heads, then its k heads, then its v heads. Sequence b's
+    token sits at position ``lens[b] + pos_offset``: returns the rotated q
+    [B, q_heads, D]; the rotated k heads and the v heads are written in place
+    into slot ``lens[b]`` of the pools [Nb, kv_heads, P, D]. Equal to
+    ``rope(q, positions=lens)`` plus ``kv_append_paged(..., rope(k), v, lens)``.
+    lens is not advanced."""
+    _gpu_only(qkv, "qkv")
+    for name, t in (("qkv", qkv), ("k_pool", k_pool), ("v_pool", v_pool)):
+        _require_gpu(t, name)
+        if t.dtype not in _FLOAT_DTYPES:
+            raise TypeError(f"{name} must be float32, bfloat16 or float16")
+    for name, t in (("k_pool", k_pool), ("v_pool", v_pool)):
+        if t.dtype is not qkv.dtype:
+            raise TypeError(f"{name} must have the qkv dtype")
+        _check_contiguous(t, name)
+    if int(q_heads) < 1 or int(kv_heads) < 1:
+        raise ValueError("q_heads and kv_heads must be >= 1")
+    if q_heads % kv_heads:
+        raise ValueError("q_heads must be a multiple of kv_heads")
+    if k_pool.ndim != 4 or v_pool.shape != k_pool.shape:
+        raise ValueError("pools must be [Nb, Hkv, P, D] of one shape")
+    nb, hkv, page, d = k_pool.shape
+    if hkv != kv_heads:
+        raise ValueError("kv_heads must equal the pools' head count")
+    if qkv.ndim != 2 or qkv.shape[1] != (q_heads + 2 * kv_heads) * d:
+        raise ValueError("qkv must be [B, (q_heads + 2 * kv_heads) * D]")
+    if d % 2:
+        raise ValueError("dim must be even (RoPE pairs elements)")
+    if int(pos_offset) < 0:
+        raise ValueError("pos_offset must be >= 0")
+    b = qkv.shape[0]
+    q_out = torch.empty((b, q_heads, d), dtype=qkv.dtype, device=qkv.device)
+    if b == 0:
+        return q_out
+    if qkv.stride(1) != 1:
+        raise ValueError("qkv rows must be contiguous")
+    bt = _table_tensor(block_table, b, nb, qkv.device)
+    lt = _lens_tensor(lens, b, bt.shape[1] * page, qkv.device,
+                      upper_inclusive=False)
+    _fusedtok.rope_kv_append_paged_launch(
+        qkv.data_ptr(), _DT_CODE[qkv.dtype], qkv.stride(0) if b > 1 else qkv.shape[1],
+        lt.data_ptr(), bt.data_ptr(), q_out.data_ptr(), k_pool.data_ptr(),
+        v_pool.data_ptr(), b, q_heads, kv_heads, d, page, bt.shape[1],
+        float(theta), int(pos_offset), bool(neox), _stream())
+    return q_out
 
 
 def _qgemm_gpu_operands(a_q, b_q):

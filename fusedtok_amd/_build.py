@@ -37,6 +37,7 @@ HIP_SOURCES = [
     "qgemm.hip",
     "quantize.hip",
     "norm_rope_act.hip",
+    "fused.hip",
 ]
 
 HIP_FLAGS = [

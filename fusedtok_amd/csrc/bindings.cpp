@@ -270,4 +270,43 @@ PYBIND11_MODULE(_fusedtok, m) {
           },
           py::arg("gate"), py::arg("up"), py::arg("out"), py::arg("n"),
           py::arg("stream") = 0);
+
+    // ---- fused decode-chain steps ----------------------------------------------
+    m.def("rmsnorm_quant_launch",
+          [](uintptr_t x, int dtype, uintptr_t w, py::object r, uintptr_t q,
+             uintptr_t scale, int rows, int cols, float eps, uintptr_t stream) {
+              check(ft_rmsnorm_quant_launch(P<const void>(x), dtype, P<const float>(w),
+                                            P<const void>(opt_ptr(r)),
+                                            P<signed char>(q), P<float>(scale), rows,
+                                            cols, eps, stream));
+          },
+          py::arg("x"), py::arg("dtype"), py::arg("weight"), py::arg("residual"),
+          py::arg("q"), py::arg("scale"), py::arg("rows"), py::arg("cols"),
+          py::arg("eps"), py::arg("stream") = 0);
+    m.def("swiglu_quant_launch",
+          [](uintptr_t g, uintptr_t u, int dtype, uintptr_t q, uintptr_t scale,
+             int rows, int cols, long long ld, uintptr_t stream) {
+              check(ft_swiglu_quant_launch(P<const void>(g), P<const void>(u), dtype,
+                                           P<signed char>(q), P<float>(scale), rows,
+                                           cols, ld, stream));
+          },
+          py::arg("gate"), py::arg("up"), py::arg("dtype"), py::arg("q"),
+          py::arg("scale"), py::arg("rows"), py::arg("cols"), py::arg("ld"),
+          py::arg("stream") = 0);
+    m.def("rope_kv_append_paged_launch",
+          [](uintptr_t qkv, int dtype, long long ld, uintptr_t lens, uintptr_t table,
+             uintptr_t q_out, uintptr_t k_pool, uintptr_t v_pool, int batch,
+             int q_heads, int kv_heads, int dim, int page, int tbl_width, float theta,
+             int pos_offset, bool neox, uintptr_t stream) {
+              check(ft_rope_kv_append_paged_launch(
+                  P<const void>(qkv), dtype, ld, P<const int>(lens),
+                  P<const int>(table), P<void>(q_out), P<void>(k_pool),
+                  P<void>(v_pool), batch, q_heads, kv_heads, dim, page, tbl_width,
+                  theta, pos_offset, neox ? 1 : 0, stream));
+          },
+          py::arg("qkv"), py::arg("dtype"), py::arg("ld"), py::arg("lens"),
+          py::arg("table"), py::arg("q_out"), py::arg("k_pool"), py::arg("v_pool"),
+          py::arg("batch"), py::arg("q_heads"), py::arg("kv_heads"), py::arg("dim"),
+          py::arg("page"), py::arg("tbl_width"), py::arg("theta"),
+          py::arg("pos_offset"), py::arg("neox"), py::arg("stream") = 0);
 }

@@ -1,0 +1,373 @@
+// Fused decode-chain kernels for gfx950. The reference composes these steps
+// from separate ops (rmsnorm -> quantize_int8, swiglu -> quantize_int8,
+// rope -> kv_append_paged); each fused op here computes exactly what the
+// unfused chain of this library computes on the same device, with fewer
+// launches and no float intermediate in HBM:
+//
+//   rmsnorm_quant   y = RMSNorm(x [+ r]) * w in f32 -> per-tensor int8 codes
+//                   + device scale (2 launches: per-row pass, fold+quantize)
+//   swiglu_quant    y = silu(g) * u in f32 -> per-tensor int8 codes + device
+//                   scale (2 launches); g / u may be strided row views (the
+//                   halves of one gate|up GEMM output)
+//   rope_kv_append  the QKV GEMM output row of each sequence -> RoPE(q) into
+//                   q_out, RoPE(k) and v written into the paged cache at
+//                   slot lens[b] (position lens[b] + pos_offset), one launch
+//
+// Arithmetic contracts:
+//   RMSNorm sum of squares: thread t of 256 accumulates fmaf(v, v, acc) over
+//   4-element chunks t, t + 256, ... in element order, then the wave
+//   butterfly (xor 32, 16, ..., 1) and the sum of the 4 wave totals in
+//   order; inv = 1 / sqrtf(total / cols + eps) (IEEE divide / sqrt);
+//   y = (v * inv) * w. The standalone rmsnorm kernel uses the same order, so
+//   rmsnorm_quant == quantize_int8(rmsnorm(x), f32 out) bit for bit.
+//   Quantize: scale = max|y| / 127 (1 if 0), inv = 1 / scale,
+//   q = clamp(rint(y * inv), -127, 127) (reference quantize.cu:169-186).
+//   SwiGLU: g / (1 + expf(-g)) * u (reference activations.cu:68-72, 501-511).
+//   RoPE: angle, cos/sin and rotation in float64 as the rope kernel.
+#include "ft_common.hpp"
+
+#include <cmath>
+
+namespace ft {
+namespace {
+
+constexpr int kFNT = 256;
+
+__device__ __forceinline__ signed char quant1(float y, float inv) {
+    return (signed char)fmaxf(-127.0f, fminf(127.0f, rintf(y * inv)));
+}
+
+__device__ __forceinline__ float make_scale(float absmax) {
+    return absmax > 0.0f ? absmax / 127.0f : 1.0f;
+}
+
+// ---------------------------------------------------------------------------
+// rmsnorm_quant
+// ---------------------------------------------------------------------------
+struct RowStat {
+    float absmax;
+    float inv;
+};
+
+template <typename T>
+__device__ __forceinline__ float4 rms_in4(const T* x, const T* r, size_t off) {
+    float4 v = St<T>::ld4(x + off);
+    if (r) {
+        const float4 b = St<T>::ld4(r + off);
+        v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
+    }
+    return v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kFNT) void rmsq_rows(
+    const T* __restrict__ x, const T* __restrict__ r, const float* __restrict__ w,
+    RowStat* __restrict__ stat, int cols, float eps) {
+    __shared__ float red[kFNT / 64];
+    const size_t base = (size_t)blockIdx.x * cols;
+    const int chunks = cols >> 2;
+    float acc = 0.0f;
+    for (int c = threadIdx.x; c < chunks; c += kFNT) {
+        const float4 v = rms_in4(x, r, base + 4 * c);
+        acc = fmaf(v.x, v.x, acc);
+        acc = fmaf(v.y, v.y, acc);
+        acc = fmaf(v.z, v.z, acc);
+        acc = fmaf(v.w, v.w, acc);
+    }
+    const float total = block_sum<kFNT>(acc, red);
+    const float inv = 1.0f / sqrtf(total / (float)cols + eps);
+    float m = 0.0f;
+    for (int c = threadIdx.x; c < chunks; c += kFNT) {
+        const float4 v = rms_in4(x, r, base + 4 * c);
+        const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c);
+        m = fmaxf(m, fabsf(v.x * inv * wv.x));
+        m = fmaxf(m, fabsf(v.y * inv * wv.y));
+        m = fmaxf(m, fabsf(v.z * inv * wv.z));
+        m = fmaxf(m, fabsf(v.w * inv * wv.w));
+    }
+    m = block_max<kFNT>(m, red);
+    if (threadIdx.x == 0) stat[blockIdx.x] = RowStat{m, inv};
+}
+
+template <typename T>
+__global__ __launch_bounds__(kFNT) void rmsq_quant(
+    const T* __restrict__ x, const T* __restrict__ r, const float* __restrict__ w,
+    const RowStat* __restrict__ stat, signed char* __restrict__ q,
+    float* __restrict__ scale_out, int rows, int cols) {
+    __shared__ float red[kFNT / 64];
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < rows; i += kFNT) m = fmaxf(m, stat[i].absmax);
+    m = block_max<kFNT>(m, red);
+    const float scale = make_scale(m);
+    const float inv_s = 1.0f / scale;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+    const long long n4 = (long long)rows * cols / 4;
+    const int cols4 = cols >> 2;
+    for (long long e = (long long)blockIdx.x * kFNT + threadIdx.x; e < n4;
+         e += (long long)gridDim.x * kFNT) {
+        const int row = (int)(e / cols4);
+        const int c = (int)(e - (long long)row * cols4) * 4;
+        const float inv = stat[row].inv;
+        const float4 v = rms_in4(x, r, (size_t)row * cols + c);
+        const float4 wv = *reinterpret_cast<const float4*>(w + c);
+        char4 o;
+        o.x = quant1(v.x * inv * wv.x, inv_s);
+        o.y = quant1(v.y * inv * wv.y, inv_s);
+        o.z = quant1(v.z * inv * wv.z, inv_s);
+        o.w = quant1(v.w * inv * wv.w, inv_s);
+        *reinterpret_cast<char4*>(q + 4 * e) = o;
+    }
+}
+
+template <typename T>
+void rmsnorm_quant_run(const T* x, const float* w, const T* r, signed char* q,
+                       float* scale_out, int rows, int cols, float eps,
+                       hipStream_t s) {
+    if (rows < 0 || cols <= 0) inval("rows must be >= 0 and cols must be > 0");
+    if (cols % 4 != 0) inval("rmsnorm_quant: cols must be a multiple of 4");
+    if (rows == 0) return;
+    if (!x || !w || !q || !scale_out) inval("rmsnorm_quant: null operand");
+    const size_t a16 = 4 * sizeof(T);
+    if ((uintptr_t)x % a16 || (r && (uintptr_t)r % a16) || (uintptr_t)w % 16 ||
+        (uintptr_t)q % 4)
+        inval("rmsnorm_quant: operands must be aligned to 4 elements");
+    RowStat* stat = (RowStat*)scratch(Scratch::QuantMax, (size_t)rows * sizeof(RowStat), s);
+    rmsq_rows<T><<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps);
+    launch_check("rmsnorm_quant row kernel launch");
+    const long long n4 = (long long)rows * cols / 4;
+    const unsigned grid = grid_1d(n4, kFNT, dev_info().cu_count * 4);
+    rmsq_quant<T><<<grid, kFNT, 0, s>>>(x, r, w, stat, q, scale_out, rows, cols);
+    launch_check("rmsnorm_quant quantize kernel launch");
+}
+
+// ---------------------------------------------------------------------------
+// swiglu_quant: element (row, c) of gate / up at row * ld + c
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return g / (1.0f + expf(-g)) * u;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kFNT) void swq_absmax(
+    const T* __restrict__ g, const T* __restrict__ u, float* __restrict__ part,
+    int rows, int cols, long long ld) {
+    __shared__ float red[kFNT / 64];
+    const long long n = (long long)rows * cols;
+    float m = 0.0f;
+    for (long long e = (long long)blockIdx.x * kFNT + threadIdx.x; e < n;
+         e += (long long)gridDim.x * kFNT) {
+        const long long row = e / cols;
+        const size_t off = (size_t)(row * ld + (e - row * cols));
+        m = fmaxf(m, fabsf(silu_mul(St<T>::ld(g + off), St<T>::ld(u + off))));
+    }
+    m = block_max<kFNT>(m, red);
+    if (threadIdx.x == 0) part[blockIdx.x] = m;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kFNT) void swq_quant(
+    const T* __restrict__ g, const T* __restrict__ u, const float* __restrict__ part,
+    int nparts, signed char* __restrict__ q, float* __restrict__ scale_out, int rows,
+    int cols, long long ld) {
+    __shared__ float red[kFNT / 64];
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < nparts; i += kFNT) m = fmaxf(m, part[i]);
+    m = block_max<kFNT>(m, red);
+    const float scale = make_scale(m);
+    const float inv_s = 1.0f / scale;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+    const long long n = (long long)rows * cols;
+    for (long long e = (long long)blockIdx.x * kFNT + threadIdx.x; e < n;
+         e += (long long)gridDim.x * kFNT) {
+        const long long row = e / cols;
+        const size_t off = (size_t)(row * ld + (e - row * cols));
+        q[e] = quant1(silu_mul(St<T>::ld(g + off), St<T>::ld(u + off)), inv_s);
+    }
+}
+
+constexpr int kSwqParts = 1024;
+
+template <typename T>
+void swiglu_quant_run(const T* g, const T* u, signed char* q, float* scale_out,
+                      int rows, int cols, long long ld, hipStream_t s) {
+    if (rows < 0 || cols < 0) inval("rows and cols must be >= 0");
+    if (ld < cols) inval("swiglu_quant: row stride must be >= cols");
+    if ((long long)rows * cols == 0) return;
+    if (!g || !u || !q || !scale_out) inval("swiglu_quant: null operand");
+    const long long n = (long long)rows * cols;
+    float* part = (float*)scratch(Scratch::QuantMax, kSwqParts * sizeof(float), s);
+    const unsigned g1 = grid_1d(n, kFNT, kSwqParts);
+    swq_absmax<T><<<g1, kFNT, 0, s>>>(g, u, part, rows, cols, ld);
+    launch_check("swiglu_quant absmax kernel launch");
+    const unsigned g2 = grid_1d(n, kFNT, dev_info().cu_count * 4);
+    swq_quant<T><<<g2, kFNT, 0, s>>>(g, u, part, (int)g1, q, scale_out, rows, cols, ld);
+    launch_check("swiglu_quant quantize kernel launch");
+}
+
+// ---------------------------------------------------------------------------
+// rope_kv_append_paged: one thread per (sequence b, head, pair j) of the
+// Hq + Hkv rotated heads, plus one per (b, v head, pair) copied. The QKV row
+// of sequence b is qkv[b * ld + (head * D ..)], heads ordered q | k | v.
+// ---------------------------------------------------------------------------
+template <typename T, bool NEOX>
+__global__ __launch_bounds__(256) void rope_kv_kernel(
+    const T* __restrict__ qkv, long long ld, const int* __restrict__ lens,
+    const int* __restrict__ table, T* __restrict__ q_out, T* __restrict__ k_pool,
+    T* __restrict__ v_pool, int batch, int hq, int hkv, int dim, int page,
+    int tbl_width, double theta, int pos_offset) {
+    const int half = dim >> 1;
+    const int heads = hq + 2 * hkv;
+    const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= (long long)batch * heads * half) return;
+    const int b = (int)(p / ((long long)heads * half));
+    const int rem = (int)(p - (long long)b * heads * half);
+    const int h = rem / half, j = rem - (rem / half) * half;
+    const int slot = lens[b];
+    const T* src = qkv + (size_t)b * ld + (size_t)h * dim;
+    const int i1 = NEOX ? j : 2 * j;
+    const int i2 = NEOX ? j + half : 2 * j + 1;
+    // destination row of a K / V head: skipped if the slot is outside the
+    // table's capacity (the device lengths are trusted, never read back)
+    auto cache_row = [&](T* pool, int kv) -> T* {
+        if (slot < 0 || slot >= tbl_width * page) return nullptr;
+        const int blk = table[(size_t)b * tbl_width + slot / page];
+        return pool + (((size_t)blk * hkv + kv) * page + slot % page) * dim;
+    };
+    if (h >= hq + hkv) {  // v head: copy two elements
+        T* dst = cache_row(v_pool, h - hq - hkv);
+        if (dst) {
+            dst[i1] = src[i1];
+            dst[i2] = src[i2];
+        }
+        return;
+    }
+    const long long m = (long long)slot + pos_offset;
+    const double angle = (double)m * pow(theta, -2.0 * j / dim);
+    double sn, cs;
+    sincos(angle, &sn, &cs);
+    const float x1 = St<T>::ld(src + i1), x2 = St<T>::ld(src + i2);
+    const float y1 = (float)(x1 * cs - x2 * sn);
+    const float y2 = (float)(x1 * sn + x2 * cs);
+    T* dst = h < hq ? q_out + ((size_t)b * hq + h) * dim : cache_row(k_pool, h - hq);
+    if (dst) {
+        St<T>::st(dst + i1, y1);
+        St<T>::st(dst + i2, y2);
+    }
+}
+
+template <typename T>
+void rope_kv_run(const T* qkv, long long ld, const int* lens, const int* table,
+                 T* q_out, T* k_pool, T* v_pool, int batch, int hq, int hkv,
+                 int dim, int page, int tbl_width, float theta, int pos_offset,
+                 bool neox, hipStream_t s) {
+    if (batch < 0 || hq < 1 || hkv < 1 || dim < 2 || dim % 2 != 0)
+        inval("rope_kv_append: batch >= 0, heads >= 1 and an even dim >= 2 are required");
+    if (page < 1 || tbl_width < 0) inval("rope_kv_append: page >= 1, table width >= 0");
+    if (ld < (long long)(hq + 2 * hkv) * dim) inval("rope_kv_append: qkv row stride too small");
+    if (pos_offset < 0) inval("pos_offset must be >= 0");
+    if ((long long)tbl_width * page > (1LL << 30)) inval("table capacity too large");
+    if (batch == 0) return;
+    if (!qkv || !lens || !table || !q_out || !k_pool || !v_pool)
+        inval("rope_kv_append: null operand");
+    const long long threads = (long long)batch * (hq + 2 * hkv) * (dim / 2);
+    if (threads > (1LL << 40)) inval("rope_kv_append: problem too large");
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    if (neox)
+        rope_kv_kernel<T, true><<<grid, 256, 0, s>>>(qkv, ld, lens, table, q_out, k_pool,
+                                                     v_pool, batch, hq, hkv, dim, page,
+                                                     tbl_width, (double)theta, pos_offset);
+    else
+        rope_kv_kernel<T, false><<<grid, 256, 0, s>>>(qkv, ld, lens, table, q_out, k_pool,
+                                                      v_pool, batch, hq, hkv, dim, page,
+                                                      tbl_width, (double)theta, pos_offset);
+    launch_check("rope_kv_append kernel launch");
+}
+
+}  // namespace
+}  // namespace ft
+
+extern "C" {
+
+int ft_rmsnorm_quant_launch(const void* x, int x_dtype, const float* w,
+                            const void* residual, signed char* q,
+                            float* scale_out, int rows, int cols, float eps,
+                            uintptr_t stream) {
+    return ft::guarded([&] {
+        hipStream_t s = ft::as_stream(stream);
+        switch (x_dtype) {
+        case FT_DT_F32:
+            ft::rmsnorm_quant_run<float>((const float*)x, w, (const float*)residual, q,
+                                         scale_out, rows, cols, eps, s);
+            break;
+        case FT_DT_BF16:
+            ft::rmsnorm_quant_run<ft::bf16>((const ft::bf16*)x, w, (const ft::bf16*)residual,
+                                            q, scale_out, rows, cols, eps, s);
+            break;
+        case FT_DT_F16:
+            ft::rmsnorm_quant_run<ft::f16>((const ft::f16*)x, w, (const ft::f16*)residual,
+                                           q, scale_out, rows, cols, eps, s);
+            break;
+        default:
+            ft::inval("rmsnorm_quant: unknown dtype code");
+        }
+    });
+}
+
+int ft_swiglu_quant_launch(const void* gate, const void* up, int dtype,
+                           signed char* q, float* scale_out, int rows, int cols,
+                           long long ld, uintptr_t stream) {
+    return ft::guarded([&] {
+        hipStream_t s = ft::as_stream(stream);
+        switch (dtype) {
+        case FT_DT_F32:
+            ft::swiglu_quant_run<float>((const float*)gate, (const float*)up, q, scale_out,
+                                        rows, cols, ld, s);
+            break;
+        case FT_DT_BF16:
+            ft::swiglu_quant_run<ft::bf16>((const ft::bf16*)gate, (const ft::bf16*)up, q,
+                                           scale_out, rows, cols, ld, s);
+            break;
+        case FT_DT_F16:
+            ft::swiglu_quant_run<ft::f16>((const ft::f16*)gate, (const ft::f16*)up, q,
+                                          scale_out, rows, cols, ld, s);
+            break;
+        default:
+            ft::inval("swiglu_quant: unknown dtype code");
+        }
+    });
+}
+
+int ft_rope_kv_append_paged_launch(const void* qkv, int dtype, long long ld,
+                                   const int* lens, const int* table, void* q_out,
+                                   void* k_pool, void* v_pool, int batch,
+                                   int q_heads, int kv_heads, int dim, int page,
+                                   int tbl_width, float theta, int pos_offset,
+                                   int neox, uintptr_t stream) {
+    return ft::guarded([&] {
+        hipStream_t s = ft::as_stream(stream);
+        switch (dtype) {
+        case FT_DT_F32:
+            ft::rope_kv_run<float>((const float*)qkv, ld, lens, table, (float*)q_out,
+                                   (float*)k_pool, (float*)v_pool, batch, q_heads,
+                                   kv_heads, dim, page, tbl_width, theta, pos_offset,
+                                   neox != 0, s);
+            break;
+        case FT_DT_BF16:
+            ft::rope_kv_run<ft::bf16>((const ft::bf16*)qkv, ld, lens, table,
+                                      (ft::bf16*)q_out, (ft::bf16*)k_pool,
+                                      (ft::bf16*)v_pool, batch, q_heads, kv_heads, dim,
+                                      page, tbl_width, theta, pos_offset, neox != 0, s);
+            break;
+        case FT_DT_F16:
+            ft::rope_kv_run<ft::f16>((const ft::f16*)qkv, ld, lens, table,
+                                     (ft::f16*)q_out, (ft::f16*)k_pool,
+                                     (ft::f16*)v_pool, batch, q_heads, kv_heads, dim,
+                                     page, tbl_width, theta, pos_offset, neox != 0, s);
+            break;
+        default:
+            ft::inval("rope_kv_append: unknown dtype code");
+        }
+    });
+}
+
+}  // extern "C"

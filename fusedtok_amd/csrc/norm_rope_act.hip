@@ -39,15 +39,15 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(
                 const float4 b = St<T>::ld4(rr + 4 * c);
                 v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
             }
-            acc += v.x * v.x;
-            acc += v.y * v.y;
-            acc += v.z * v.z;
-            acc += v.w * v.w;
+            acc = fmaf(v.x, v.x, acc);
+            acc = fmaf(v.y, v.y, acc);
+            acc = fmaf(v.z, v.z, acc);
+            acc = fmaf(v.w, v.w, acc);
         }
     } else {
         for (int i = threadIdx.x; i < cols; i += NT) {
             const float v = St<T>::ld(xr + i) + (rr ? St<T>::ld(rr + i) : 0.0f);
-            acc += v * v;
+            acc = fmaf(v, v, acc);
         }
     }
     const float total = block_sum<NT>(acc, red);

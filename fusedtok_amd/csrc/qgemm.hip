@@ -9,9 +9,13 @@
 // value rounded to nearest-even.
 //
 // Kernels
-//   qgemv_dot4     M <= 8 (decode GEMV, no MFMA): v_dot4_i32_i8 over 16-byte
-//                  K pieces, several W rows in flight per wave, wave sums.
-//   qgemm_skinny   8 < M <= 64: W streamed once into the B operand of
+//   qgemv_dot4     M == 1 (any M <= 8 when forced; decode GEMV, no MFMA):
+//                  v_dot4_i32_i8 over 16-byte K pieces, several W rows in
+//                  flight per wave, wave sums.
+//   qgemm_dec      2 <= M <= 16: 16 columns per workgroup over all of K, K
+//                  split across the workgroup's waves, operands double-
+//                  buffered in registers, partials folded in LDS.
+//   qgemm_skinny   16 < M <= 64: W streamed once into the B operand of
 //                  v_mfma_i32_16x16x64_i8, 64 columns per workgroup (A shared
 //                  through L1), K split across workgroups when N alone cannot
 //                  fill the chip; int32 partials folded by qgemm_ksum.
@@ -174,6 +178,100 @@ __global__ __launch_bounds__(256) void qgemv_dot4(const i8* __restrict__ a,
                 if (lane == r * M_ + mm && j0 + r < n)
                     epi_store<OUT>(e, sa, n, mm, j0 + r, acc[r][mm]);
     }
+}
+
+// ---------------------------------------------------------------------------
+// decode MFMA GEMM (M <= 16): a workgroup owns 16 output columns (W rows
+// n0 .. n0 + 15) over the whole of K; its KW waves split K into 512-byte
+// chunks taken round robin (wave w: chunks w, w + KW, ...), so each wave
+// streams 16 rows x 512 B per chunk and no second launch is needed to fold
+// a K split: the KW partial accumulators meet in LDS at the end (integer
+// sums, exact in any order). Per 64-byte K step, lane (r, g) holds
+// W[n0 + r][k + 16 g .. +15] (B operand of v_mfma_i32_16x16x64_i8) and
+// A[r][k + 16 g .. +15] (A operand; rows past M read row M - 1 and only feed
+// output rows that are never stored). Both operands are loaded straight to
+// registers, double-buffered: chunk c + KW is in flight while chunk c is
+// multiplied. Every load is unconditional (clamped address), so the
+// compiler's vmcnt bookkeeping sees one fixed count per chunk; K pieces past
+// the end are zeroed by a select on W.
+// ---------------------------------------------------------------------------
+constexpr int kDecChunk = 512;                // K bytes per chunk
+constexpr int kDecSteps = kDecChunk / 64;     // MFMA K steps per chunk
+
+template <int KW, int OUT>
+__global__ __launch_bounds__(64 * KW) void qgemm_dec(
+    const i8* __restrict__ a, const i8* __restrict__ b, Epi e, int m, int n,
+    int k) {
+    __shared__ i32x4 red[KW > 1 ? KW - 1 : 1][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const i8* brow = b + (size_t)min(n0 + r, n - 1) * k;
+    const i8* arow = a + (size_t)min(r, m - 1) * k;
+    const int chunks = (k + kDecChunk - 1) / kDecChunk;
+    // K byte of step u's piece for this lane (lanes of one row group read
+    // 64 contiguous bytes per step; wider per-lane runs measured no faster)
+    auto piece = [&](int c, int u) { return c * kDecChunk + 64 * u + 16 * g; };
+
+    i32x4 w0[kDecSteps], a0[kDecSteps], w1[kDecSteps], a1[kDecSteps];
+    auto load = [&](int c, i32x4 (&wv)[kDecSteps], i32x4 (&av)[kDecSteps]) {
+#pragma unroll
+        for (int u = 0; u < kDecSteps; ++u) {
+            // a piece past the end reads the row's last 16 bytes instead
+            const int kb = min(piece(c, u), k - 16);
+            wv[u] = *reinterpret_cast<const i32x4*>(brow + kb);
+            av[u] = *reinterpret_cast<const i32x4*>(arow + kb);
+        }
+    };
+    // the zeroing of pieces past K is applied here, next to the MFMA that
+    // needs the value anyway (a select right after the load would make the
+    // wave wait for each load in turn)
+    auto mul = [&](int c, const i32x4 (&wv)[kDecSteps], const i32x4 (&av)[kDecSteps],
+                   i32x4 acc) {
+#pragma unroll
+        for (int u = 0; u < kDecSteps; ++u) {
+            const i32x4 wz = piece(c, u) < k ? wv[u] : i32x4{0, 0, 0, 0};
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[u], wz, acc, 0, 0, 0);
+        }
+        return acc;
+    };
+
+    // The loop body is one basic block: prefetches are issued whether or not
+    // their chunk exists (clamped index), and a chunk past the end is
+    // multiplied too, contributing zero (mul zeroes every W piece at or past
+    // K). A load skipped or sunk on one path would make the compiler's wait
+    // counts conservative, and the wave would wait for the prefetch it just
+    // issued; sched_barrier keeps the scheduler from sinking a prefetch below
+    // the multiplies it is meant to overlap.
+    i32x4 acc = {0, 0, 0, 0};
+    const int last = chunks - 1;
+    load(min(wave, last), w0, a0);
+    for (int c = wave; c < chunks; c += 2 * KW) {
+        load(min(c + KW, last), w1, a1);
+        __builtin_amdgcn_sched_barrier(0);
+        acc = mul(c, w0, a0, acc);
+        load(min(c + 2 * KW, last), w0, a0);
+        __builtin_amdgcn_sched_barrier(0);
+        acc = mul(c + KW, w1, a1, acc);
+    }
+    if (KW > 1) {
+        if (wave > 0) red[wave - 1][lane] = acc;
+        __syncthreads();
+        if (wave > 0) return;
+#pragma unroll
+        for (int w = 0; w < KW - 1; ++w) {
+            const i32x4 p = red[w][lane];
+            acc[0] += p[0]; acc[1] += p[1]; acc[2] += p[2]; acc[3] += p[3];
+        }
+    }
+    // lane (r, g) holds C[4 g + i][r] = (A row 4 g + i, W row n0 + r)
+    const int col = n0 + r;
+    if (col >= n) return;
+    const float sa = epi_sa(e);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (4 * g + i < m) epi_store<OUT>(e, sa, n, 4 * g + i, col, acc[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -858,7 +956,7 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
                     hipStream_t s) {
     const bool aligned = (k % 16 == 0) && ((uintptr_t)a % 16 == 0) &&
                          ((uintptr_t)b % 16 == 0);
-    // FT_QGEMM_KERNEL: 1 skinny, 2 tiled, 3 scalar, 4 big, 5 gemv
+    // FT_QGEMM_KERNEL: 1 skinny, 2 tiled, 3 scalar, 4 big, 5 gemv, 6 decode
     const int force = env_int("FT_QGEMM_KERNEL", 0);
     if (!aligned || force == 3) {
         const long long total = (long long)m * n;
@@ -866,7 +964,13 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         launch_check("qgemm scalar kernel launch");
         return;
     }
-    if ((m <= 8 && force == 0) || force == 5) {
+    // decode shapes. Measured on MI355X (HIP-graph replays, weights cycled
+    // past the 256 MB last-level cache): at M = 1 the dot4 GEMV streams W
+    // fastest (1 KB contiguous per load instruction; N=28672 K=4096:
+    // 24.1 us vs 28.3 us), from M = 2 the MFMA decode kernel wins (its dot
+    // products cost 1/16 of the dot4 instructions; N=11008 K=4096 M=8:
+    // 14.0 us vs 37.1 us).
+    if ((m == 1 && force == 0) || force == 5) {
         if (m > 8) inval("gemv qgemm supports m <= 8");
         const long long waves = std::min<long long>((n + kGemvRows - 1) / kGemvRows,
                                                     (long long)dev_info().cu_count * 16);
@@ -882,6 +986,26 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         default: qgemv_dot4<8, OUT><<<grid, 256, 0, s>>>(a, b, e, n, k); break;
         }
         launch_check("qgemm gemv kernel launch");
+        return;
+    }
+    if ((m <= 16 && force == 0) || force == 6) {
+        if (m > 16) inval("decode qgemm supports m <= 16");
+        const int tiles = (n + 15) / 16;
+        const unsigned grid = (unsigned)tiles;
+        // waves per 16-column tile: one long stream per wave when there are
+        // enough tiles, else split K so that every CU still gets waves
+        // (N=6144: 1 wave per tile 8.3 us vs 9.3 us; N=4096 K=14336: 2 waves
+        // 13.4 us vs 18.9 us)
+        int kw = tiles >= 320 ? 1 : tiles >= 128 ? 2 : 4;
+        const int kw_env = env_int("FT_QGEMM_DEC_KW", 0);
+        if (kw_env == 1 || kw_env == 2 || kw_env == 4) kw = kw_env;
+        if (kw == 1)
+            qgemm_dec<1, OUT><<<grid, 64, 0, s>>>(a, b, e, m, n, k);
+        else if (kw == 2)
+            qgemm_dec<2, OUT><<<grid, 128, 0, s>>>(a, b, e, m, n, k);
+        else
+            qgemm_dec<4, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k);
+        launch_check("qgemm decode kernel launch");
         return;
     }
     if ((m <= 64 && force != 2 && force != 4) || force == 1) {

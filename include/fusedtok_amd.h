@@ -251,6 +251,49 @@ int ft_swiglu_launch_bf16(const void* gate, const void* up, void* y,
 int ft_swiglu_launch_fp16(const void* gate, const void* up, void* y,
                           long long n, uintptr_t stream);
 
+/* ------------------------------------------------------------------ */
+/* Fused decode-chain steps. The reference has no fused layer op: a    */
+/* decode layer calls rmsnorm_launch -> quantize_int8_launch,          */
+/* swiglu_launch -> quantize_int8_launch and rope_launch ->            */
+/* kv_append_paged_launch one after another (cuda_launch.hpp:40,       */
+/* 44-45, 56-59, 191-192, 324-460). Each entry below is a build        */
+/* addition that computes what that chain computes, without the float  */
+/* intermediate in HBM. x_dtype / dtype are FT_DT_*.                   */
+/* ------------------------------------------------------------------ */
+/* RMSNorm (+ optional residual) then per-tensor int8 quantize of the
+ * float32 result: q[rows, cols] int8 and *scale_out (DEVICE float) are
+ * bit-identical to ft_rmsnorm_launch (float32 storage) followed by
+ * ft_quantize_int8_launch. cols must be a multiple of 4 and x, residual
+ * aligned to 4 elements, w to 16 bytes, q to 4 bytes. */
+int ft_rmsnorm_quant_launch(const void* x, int x_dtype, const float* w,
+                            const void* residual, signed char* q,
+                            float* scale_out, int rows, int cols, float eps,
+                            uintptr_t stream);
+/* SwiGLU then per-tensor int8 quantize: gate / up element (r, c) at
+ * r * ld + c (so the two halves of one [rows, 2*cols] gate|up GEMM
+ * output are passed as base and base + cols with ld = 2*cols); q is the
+ * dense [rows, cols] int8 result and *scale_out a DEVICE float. Equal to
+ * ft_swiglu_launch (float32 storage) followed by ft_quantize_int8_launch. */
+int ft_swiglu_quant_launch(const void* gate, const void* up, int dtype,
+                           signed char* q, float* scale_out, int rows,
+                           int cols, long long ld, uintptr_t stream);
+/* RoPE of the decode token's q and k heads plus the paged KV append, in
+ * one launch. qkv row b (element stride ld) holds q_heads, then kv_heads
+ * k heads, then kv_heads v heads of `dim` elements. Sequence b's token
+ * sits at position lens[b] + pos_offset: its q heads are rotated into
+ * q_out [batch, q_heads, dim], its k heads rotated and its v heads copied
+ * into slot lens[b] of the paged pools ([blocks, kv_heads, page, dim],
+ * table [batch, tbl_width]), exactly as ft_rope_launch_ex with positions
+ * = lens followed by ft_kv_append_paged_launch*. lens is NOT advanced; a
+ * slot outside [0, tbl_width * page) is skipped. */
+int ft_rope_kv_append_paged_launch(const void* qkv, int dtype, long long ld,
+                                   const int* lens, const int* table,
+                                   void* q_out, void* k_pool, void* v_pool,
+                                   int batch, int q_heads, int kv_heads,
+                                   int dim, int page, int tbl_width,
+                                   float theta, int pos_offset, int neox,
+                                   uintptr_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -187,3 +187,65 @@ def swiglu(g, u):
     y = np.empty_like(g)
     _call("or_swiglu", _p(g), _p(u), ctypes.c_longlong(g.size), _p(y))
     return y
+
+
+def rmsnorm_blocked(x, w, residual=None, eps=1e-6):
+    """RMSNorm in the GPU kernels' summation order (cols % 4 == 0)."""
+    x = _f32(x)
+    w = _f32(w)
+    r = None if residual is None else _f32(residual)
+    rows, cols = (1, x.shape[0]) if x.ndim == 1 else x.shape
+    y = np.empty_like(x)
+    _call("or_rmsnorm_blocked", _p(x), _p(w), _p(r), rows, cols,
+          ctypes.c_float(eps), _p(y))
+    return y
+
+
+def rmsnorm_quant(x, w, residual=None, eps=1e-6):
+    """rmsnorm_blocked -> quantize_int8 over the whole output."""
+    x = _f32(x)
+    w = _f32(w)
+    r = None if residual is None else _f32(residual)
+    rows, cols = (1, x.shape[0]) if x.ndim == 1 else x.shape
+    q = np.empty(x.shape, np.int8)
+    s = ctypes.c_float(0.0)
+    _call("or_rmsnorm_quant", _p(x), _p(w), _p(r), rows, cols,
+          ctypes.c_float(eps), _p(q), ctypes.byref(s))
+    return q, float(s.value)
+
+
+def swiglu_quant(g, u):
+    """swiglu_cpu -> quantize_int8 on [rows, cols] gate / up (any row
+    stride: the arrays may be column slices of one [rows, 2*cols] array)."""
+    g = np.asarray(g, dtype=np.float32)
+    u = np.asarray(u, dtype=np.float32)
+    rows, cols = g.shape
+    both = np.ascontiguousarray(np.concatenate([g, u], axis=1))
+    q = np.empty((rows, cols), np.int8)
+    s = ctypes.c_float(0.0)
+    gp = both.ctypes.data
+    up = gp + cols * 4
+    _call("or_swiglu_quant", ctypes.c_void_p(gp), ctypes.c_void_p(up), rows,
+          cols, ctypes.c_longlong(2 * cols), _p(q), ctypes.byref(s))
+    return q, float(s.value)
+
+
+def rope_kv_append_paged(qkv, q_heads, kv_heads, k_pool, v_pool, table, lens,
+                         theta=10000.0, pos_offset=0, neox=False):
+    """rope (q and k heads of sequence b at position lens[b] + pos_offset),
+    then kv_append_paged of the rotated k and the v heads. qkv is
+    [batch, (q_heads + 2 * kv_heads) * dim] float32; returns q_out
+    [batch, q_heads, dim] and updates the pools in place."""
+    qkv = _f32(qkv)
+    batch = qkv.shape[0]
+    dim = qkv.shape[1] // (q_heads + 2 * kv_heads)
+    heads = qkv.reshape(batch, q_heads + 2 * kv_heads, dim)
+    lens = _i32(lens)
+    rot = np.empty((batch, q_heads + kv_heads, dim), np.float32)
+    for b in range(batch):
+        for h in range(q_heads + kv_heads):
+            rot[b, h] = rope(heads[b, h][None, :], theta,
+                             int(lens[b]) + pos_offset, neox)[0]
+    kv_append_paged(k_pool, v_pool, table, rot[:, q_heads:],
+                    np.ascontiguousarray(heads[:, q_heads + kv_heads:]), lens)
+    return rot[:, :q_heads].copy()

@@ -313,6 +313,95 @@ int or_rmsnorm(const float* x, const float* w, const float* residual, int rows,
 }
 
 // ---------------------------------------------------------------------------
+// RMSNorm in the summation order of this library's GPU kernels (the math of
+// rmsnorm_cpu, reference rmsnorm.cu:110-130; only the rounding order
+// differs): 256 threads, thread t accumulates fmaf(v, v, acc) over the
+// 4-element chunks t, t + 256, ... in element order; each 64-lane wave adds
+// lane l and lane l ^ o for o = 32, 16, ..., 1; the 4 wave totals are added
+// in order. inv = 1 / sqrtf(total / cols + eps), y = (v * inv) * w.
+// cols must be a multiple of 4.
+// ---------------------------------------------------------------------------
+static void rms_blocked_rows(const float* x, const float* w, const float* residual,
+                             int rows, int cols, float eps, float* y) {
+    constexpr int NT = 256;
+    const int chunks = cols / 4;
+    float lane[NT];
+    for (int row = 0; row < rows; ++row) {
+        const size_t base = (size_t)row * cols;
+        auto val = [&](int i) {
+            return x[base + i] + (residual ? residual[base + i] : 0.0f);
+        };
+        for (int t = 0; t < NT; ++t) {
+            float acc = 0.0f;
+            for (int c = t; c < chunks; c += NT)
+                for (int e = 0; e < 4; ++e) {
+                    const float v = val(4 * c + e);
+                    acc = std::fma(v, v, acc);
+                }
+            lane[t] = acc;
+        }
+        float total = 0.0f;
+        for (int wv = 0; wv < NT / 64; ++wv) {
+            float* l = lane + 64 * wv;
+            for (int o = 32; o > 0; o >>= 1) {
+                float nxt[64];
+                for (int i = 0; i < 64; ++i) nxt[i] = l[i] + l[i ^ o];
+                for (int i = 0; i < 64; ++i) l[i] = nxt[i];
+            }
+            total += l[0];
+        }
+        const float inv = 1.0f / std::sqrt(total / (float)cols + eps);
+        for (int i = 0; i < cols; ++i) y[base + i] = val(i) * inv * w[i];
+    }
+}
+
+int or_rmsnorm_blocked(const float* x, const float* w, const float* residual, int rows,
+                       int cols, float eps, float* y) {
+    return run([&] {
+        if (rows < 0 || cols <= 0) throw Inval{"rows must be >= 0 and cols must be > 0"};
+        if (cols % 4 != 0) throw Inval{"cols must be a multiple of 4"};
+        rms_blocked_rows(x, w, residual, rows, cols, eps, y);
+    });
+}
+
+// rmsnorm_quant: or_rmsnorm_blocked then or_quantize_int8 over the whole
+// (rows, cols) output (the reference chain rmsnorm -> quantize_int8).
+int or_rmsnorm_quant(const float* x, const float* w, const float* residual, int rows,
+                     int cols, float eps, signed char* q, float* scale_out) {
+    int rc = 0;
+    std::vector<float> y;
+    rc = run([&] {
+        if (rows < 0 || cols <= 0) throw Inval{"rows must be >= 0 and cols must be > 0"};
+        if (cols % 4 != 0) throw Inval{"cols must be a multiple of 4"};
+        y.resize((size_t)rows * cols);
+        rms_blocked_rows(x, w, residual, rows, cols, eps, y.data());
+    });
+    if (rc != 0) return rc;
+    return or_quantize_int8(y.data(), (long long)rows * cols, q, scale_out);
+}
+
+// swiglu_quant: swiglu_cpu on rows of a strided gate / up view (element
+// (r, c) at r * ld + c), then quantize_int8 over the dense (rows, cols)
+// result.
+int or_swiglu_quant(const float* g, const float* u, int rows, int cols, long long ld,
+                    signed char* q, float* scale_out) {
+    int rc = 0;
+    std::vector<float> y;
+    rc = run([&] {
+        if (rows < 0 || cols < 0) throw Inval{"rows and cols must be >= 0"};
+        if (ld < cols) throw Inval{"row stride must be >= cols"};
+        y.resize((size_t)rows * cols);
+        for (int r = 0; r < rows; ++r)
+            for (int c = 0; c < cols; ++c) {
+                const float gv = g[(size_t)r * ld + c];
+                y[(size_t)r * cols + c] = gv / (1.0f + std::exp(-gv)) * u[(size_t)r * ld + c];
+            }
+    });
+    if (rc != 0) return rc;
+    return or_quantize_int8(y.data(), (long long)rows * cols, q, scale_out);
+}
+
+// ---------------------------------------------------------------------------
 // rope_cpu / rope_neox_cpu (reference rope.cu:96-143): angle = m *
 // pow((double)theta, -2.0*j/dim) in double, cos/sin in double, the rotation
 // in double, rounded to float. Row r sits at position r + pos_offset.

@@ -129,3 +129,36 @@ def test_norm_rope_swiglu_invalid_arguments(lib):
     qz.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
                    ctypes.c_longlong, ctypes.c_size_t]
     assert qz(None, 9, None, None, 4, 0) == FT_EINVAL                  # bad dtype
+
+
+def test_fused_invalid_arguments(lib):
+    rq = lib.ft_rmsnorm_quant_launch
+    rq.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                   ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_float, ctypes.c_size_t]
+    assert rq(None, 0, None, None, None, None, 2, 6, 1e-6, 0) == FT_EINVAL  # cols % 4
+    assert rq(None, 0, None, None, None, None, 2, 0, 1e-6, 0) == FT_EINVAL
+    assert rq(None, 9, None, None, None, None, 2, 8, 1e-6, 0) == FT_EINVAL  # dtype
+    assert rq(None, 1, None, None, None, None, 0, 8, 1e-6, 0) == FT_OK      # no rows
+    sq = lib.ft_swiglu_quant_launch
+    sq.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                   ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_longlong,
+                   ctypes.c_size_t]
+    assert sq(None, None, 0, None, None, 2, 8, 4, 0) == FT_EINVAL          # ld < cols
+    assert sq(None, None, 0, None, None, -1, 8, 8, 0) == FT_EINVAL
+    assert sq(None, None, 2, None, None, 0, 8, 16, 0) == FT_OK
+    rk = lib.ft_rope_kv_append_paged_launch
+    rk.argtypes = ([ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong] +
+                   [ctypes.c_void_p] * 5 + [ctypes.c_int] * 6 +
+                   [ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_size_t])
+    ok = dict(batch=2, hq=4, hkv=2, dim=8, page=16, width=3)
+
+    def call(ld=64, batch=2, hq=4, hkv=2, dim=8, page=16, width=3, off=0):
+        return rk(None, 1, ld, None, None, None, None, None, batch, hq, hkv, dim,
+                  page, width, 10000.0, off, 0, 0)
+    assert call(dim=7) == FT_EINVAL
+    assert call(ld=63) == FT_EINVAL              # (4 + 2*2) * 8 = 64
+    assert call(page=0) == FT_EINVAL
+    assert call(off=-1) == FT_EINVAL
+    assert call(batch=0) == FT_OK
+    assert call(**ok) == FT_EINVAL               # null operands

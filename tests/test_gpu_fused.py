@@ -1,0 +1,267 @@
+"""GPU parity of the fused decode-chain steps (rmsnorm_quant, swiglu_quant,
+rope_kv_append_paged):
+  - against the CPU oracle on the same seeded inputs: int8 codes and the
+    scale bit-exact for rmsnorm_quant (the oracle follows the kernel's
+    summation order); within one code step for swiglu_quant (device expf vs
+    the host's); RoPE within 1e-6 (f32) / one storage ulp (bf16, fp16);
+  - against this library's unfused GPU chain (rmsnorm -> quantize_int8,
+    swiglu -> quantize_int8, rope(positions=lens) -> kv_append_paged):
+    bit-exact, which is the fused ops' contract."""
+
+import numpy as np
+import pytest
+import torch
+
+import fusedtok_amd as ft
+import oracle
+from tests import refs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ALL = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def t(a, dtype=None):
+    x = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    return x if dtype is None else x.to(dtype)
+
+
+def as_f32(x):
+    return x.float().cpu().numpy()
+
+
+def raw(x):
+    if x.dtype is torch.float32:
+        return x.cpu().view(torch.int32).numpy()
+    return x.cpu().view(torch.int16).numpy()
+
+
+# ---------------------------------------------------------------------------
+# rmsnorm_quant
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dt", ALL)
+@pytest.mark.parametrize("rows,cols", [(1, 4096), (8, 4096), (16, 4096), (5, 1028),
+                                       (3, 8), (2, 5000)])
+@pytest.mark.parametrize("with_res", [False, True])
+def test_rmsnorm_quant_matches_oracle_and_chain(dt, rows, cols, with_res):
+    rng = np.random.default_rng(rows * 7919 + cols + with_res)
+    x = t(rng.standard_normal((rows, cols)).astype(np.float32) * 2, dt)
+    w = t(rng.uniform(0.5, 1.5, cols).astype(np.float32))
+    r = t(rng.standard_normal((rows, cols)).astype(np.float32), dt) if with_res else None
+    q, s = ft.rmsnorm_quant(x, w, residual=r, eps=1e-5)
+    eq, es = oracle.rmsnorm_quant(as_f32(x), w.cpu().numpy(),
+                                  None if r is None else as_f32(r), 1e-5)
+    np.testing.assert_array_equal(q.cpu().numpy(), eq)
+    assert s == es
+    # unfused GPU chain on float32 storage
+    y = ft.rmsnorm(x.float(), w, residual=None if r is None else r.float(), eps=1e-5)
+    np.testing.assert_array_equal(
+        y.cpu().numpy(), oracle.rmsnorm_blocked(as_f32(x), w.cpu().numpy(),
+                                                None if r is None else as_f32(r), 1e-5))
+    q2, s2 = ft.quantize_int8(y)
+    np.testing.assert_array_equal(q.cpu().numpy(), q2.cpu().numpy())
+    assert s == s2
+
+
+def test_rmsnorm_quant_device_scale_zero_rows_and_1d():
+    rng = np.random.default_rng(3)
+    x = t(rng.standard_normal(512).astype(np.float32), torch.bfloat16)
+    w = t(np.ones(512, np.float32))
+    q, s = ft.rmsnorm_quant(x, w, device_scale=True)
+    assert q.shape == (512,) and s.shape == (1,) and s.is_cuda
+    q1, s1 = ft.rmsnorm_quant(x, w)
+    assert float(s) == s1 and torch.equal(q, q1)
+    q0, s0 = ft.rmsnorm_quant(torch.empty((0, 64), device=DEV), t(np.ones(64, np.float32)))
+    assert q0.shape == (0, 64) and s0 == 1.0
+    with pytest.raises(ValueError):
+        ft.rmsnorm_quant(torch.ones((2, 6), device=DEV), torch.ones(6, device=DEV))
+    with pytest.raises(TypeError):
+        ft.rmsnorm_quant(np.ones((2, 8), np.float32), np.ones(8, np.float32))
+
+
+def test_rmsnorm_quant_repeatable_over_growing_shapes():
+    # the per-row statistics live in a scratch slot that grows; a smaller call
+    # after a larger one must not read stale rows
+    rng = np.random.default_rng(4)
+    w = t(rng.uniform(0.5, 1.5, 2048).astype(np.float32))
+    big = t(rng.standard_normal((64, 2048)).astype(np.float32) * 50)
+    small = t(rng.standard_normal((3, 2048)).astype(np.float32))
+    ft.rmsnorm_quant(big, w)
+    q, s = ft.rmsnorm_quant(small, w)
+    eq, es = oracle.rmsnorm_quant(small.cpu().numpy(), w.cpu().numpy())
+    np.testing.assert_array_equal(q.cpu().numpy(), eq)
+    assert s == es
+
+
+# ---------------------------------------------------------------------------
+# swiglu_quant
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dt", ALL)
+@pytest.mark.parametrize("rows,cols", [(1, 11008), (8, 14336), (64, 300), (3, 1)])
+def test_swiglu_quant_halves_match_chain_and_oracle(dt, rows, cols):
+    rng = np.random.default_rng(rows * 31 + cols)
+    h = t((rng.standard_normal((rows, 2 * cols)) * 3).astype(np.float32), dt)
+    g, u = h[:, :cols], h[:, cols:]
+    q, s = ft.swiglu_quant(g, u)
+    # unfused GPU chain on float32 storage
+    y = ft.swiglu(g.float().contiguous(), u.float().contiguous())
+    q2, s2 = ft.quantize_int8(y)
+    np.testing.assert_array_equal(q.cpu().numpy(), q2.cpu().numpy())
+    assert s == s2
+    # oracle (host expf): scale within rounding, codes within one step
+    eq, es = oracle.swiglu_quant(as_f32(g), as_f32(u))
+    assert s == pytest.approx(es, rel=1e-6)
+    assert np.abs(q.cpu().numpy().astype(int) - eq.astype(int)).max() <= 1
+
+
+def test_swiglu_quant_contiguous_pair_and_errors():
+    rng = np.random.default_rng(8)
+    g = t(rng.standard_normal((4, 256)).astype(np.float32), torch.float16)
+    u = t(rng.standard_normal((4, 256)).astype(np.float32), torch.float16)
+    q, s = ft.swiglu_quant(g, u, device_scale=True)
+    q2, s2 = ft.quantize_int8(ft.swiglu(g.float(), u.float()))
+    assert torch.equal(q, q2) and float(s) == s2
+    with pytest.raises(TypeError):
+        ft.swiglu_quant(g, u.float())
+    with pytest.raises(ValueError):
+        ft.swiglu_quant(g, u[:, :128])
+    q0, s0 = ft.swiglu_quant(g[:0], u[:0])
+    assert q0.shape == (0, 256) and s0 == 1.0
+
+
+# ---------------------------------------------------------------------------
+# rope_kv_append_paged
+# ---------------------------------------------------------------------------
+
+
+def rope_kv_case(rng, b, hq, hkv, d, lens, page=16, extra=3):
+    width = max(1, max((l + 1 + page - 1) // page for l in lens))
+    nb = b * width + extra
+    qkv = rng.standard_normal((b, (hq + 2 * hkv) * d)).astype(np.float32)
+    kp = rng.standard_normal((nb, hkv, page, d)).astype(np.float32)
+    vp = rng.standard_normal((nb, hkv, page, d)).astype(np.float32)
+    tbl = rng.permutation(nb)[: b * width].reshape(b, width).astype(np.int32)
+    return qkv, kp, vp, tbl, np.array(lens, np.int32)
+
+
+@pytest.mark.parametrize("dt", ALL)
+@pytest.mark.parametrize("neox", [False, True])
+@pytest.mark.parametrize("off", [0, 5])
+def test_rope_kv_append_matches_chain_and_oracle(dt, neox, off):
+    rng = np.random.default_rng(100 + 10 * neox + off)
+    b, hq, hkv, d, page = 5, 32, 8, 128, 16
+    qkv, kp, vp, tbl, lens = rope_kv_case(rng, b, hq, hkv, d, [0, 15, 16, 700, 8191],
+                                          page)
+    qkv_d = t(qkv, dt)
+    kp_d, vp_d = t(kp, dt), t(vp, dt)
+    kp_c, vp_c = kp_d.clone(), vp_d.clone()
+    tbl_d, lens_d = t(tbl), t(lens)
+    qo = ft.rope_kv_append_paged(qkv_d, hq, hkv, kp_d, vp_d, tbl_d, lens_d,
+                                 theta=500000.0, pos_offset=off, neox=neox)
+    # unfused GPU chain
+    qh = qkv_d[:, : hq * d].reshape(b * hq, d).contiguous()
+    kh = qkv_d[:, hq * d:(hq + hkv) * d].reshape(b * hkv, d).contiguous()
+    vh = qkv_d[:, (hq + hkv) * d:].reshape(b, hkv, d).contiguous()
+    qr, _ = ft.rope(qh, theta=500000.0, pos_offset=off, neox=neox, positions=lens_d,
+                    rows_per_position=hq)
+    kr, _ = ft.rope(kh, theta=500000.0, pos_offset=off, neox=neox, positions=lens_d,
+                    rows_per_position=hkv)
+    ft.kv_append_paged(kp_c, vp_c, tbl_d, kr.reshape(b, hkv, d), vh, lens_d)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(raw(qo.reshape(b * hq, d)), raw(qr))
+    np.testing.assert_array_equal(raw(kp_d), raw(kp_c))
+    np.testing.assert_array_equal(raw(vp_d), raw(vp_c))
+    # oracle on the storage-rounded inputs
+    ek, ev = as_f32(t(kp, dt)), as_f32(t(vp, dt))
+    eq = oracle.rope_kv_append_paged(as_f32(qkv_d), hq, hkv, ek, ev, tbl, lens,
+                                     500000.0, off, neox)
+    if dt is torch.float32:
+        tol = dict(rtol=0, atol=1e-6)
+    else:
+        rnd = refs.bf16_round if dt is torch.bfloat16 else refs.f16_round
+        eq, ek = rnd(eq), rnd(ek)
+        tol = dict(rtol=1e-2 if dt is torch.bfloat16 else 2e-3, atol=1e-6)
+    np.testing.assert_allclose(as_f32(qo), eq, **tol)
+    np.testing.assert_allclose(as_f32(kp_d), ek, **tol)
+    np.testing.assert_array_equal(as_f32(vp_d), ev)
+
+
+def test_rope_kv_append_strided_rows_and_errors():
+    rng = np.random.default_rng(9)
+    b, hq, hkv, d = 3, 8, 2, 64
+    qkv, kp, vp, tbl, lens = rope_kv_case(rng, b, hq, hkv, d, [3, 40, 0])
+    wide = np.zeros((b, (hq + 2 * hkv) * d + 64), np.float32)
+    wide[:, : qkv.shape[1]] = qkv
+    kp_a, vp_a = t(kp), t(vp)
+    kp_b, vp_b = t(kp), t(vp)
+    qa = ft.rope_kv_append_paged(t(qkv), hq, hkv, kp_a, vp_a, t(tbl), t(lens))
+    qb = ft.rope_kv_append_paged(t(wide)[:, : qkv.shape[1]], hq, hkv, kp_b, vp_b,
+                                 tbl, lens)          # host table / lens
+    assert torch.equal(qa, qb) and torch.equal(kp_a, kp_b) and torch.equal(vp_a, vp_b)
+    with pytest.raises(ValueError):                   # slot beyond capacity
+        ft.rope_kv_append_paged(t(qkv), hq, hkv, kp_a, vp_a, tbl,
+                                np.array([3, 40, tbl.shape[1] * 16], np.int32))
+    with pytest.raises(ValueError):
+        ft.rope_kv_append_paged(t(qkv), hq, 3, kp_a, vp_a, tbl, lens)
+    with pytest.raises(TypeError):
+        ft.rope_kv_append_paged(t(qkv, torch.bfloat16), hq, hkv, kp_a, vp_a, tbl, lens)
+
+
+# ---------------------------------------------------------------------------
+# a whole W8A8 decode layer (the chain bench.py times as a HIP graph):
+# captured once, replayed several times with eager work in between; every
+# replay must equal the eager layer bit for bit (all kernels here are
+# deterministic: fixed reduction orders, integer GEMM sums)
+# ---------------------------------------------------------------------------
+
+
+def test_decode_layer_graph_replays_equal_eager():
+    dev = torch.device(DEV)
+    gen = torch.Generator(device=dev).manual_seed(77)
+    b, hq, hkv, d, hid, inter, page = 4, 8, 2, 64, 512, 768, 16
+    bf = torch.bfloat16
+
+    def wq(rows, cols):
+        return (torch.randint(-127, 128, (rows, cols), device=dev, generator=gen,
+                              dtype=torch.int32).to(torch.int8),
+                (torch.rand((rows,), device=dev, generator=gen) * 9e-3 + 1e-3).float())
+    wn1 = (torch.rand((hid,), device=dev, generator=gen) + 0.5).float()
+    wn2 = (torch.rand((hid,), device=dev, generator=gen) + 0.5).float()
+    wqkv, wo, wgu, wd = wq((hq + 2 * hkv) * d, hid), wq(hid, hq * d), wq(2 * inter, hid), \
+        wq(hid, inter)
+    lens = torch.tensor([5, 300, 17, 100], dtype=torch.int32, device=dev)
+    npg = (301 + page - 1) // page
+    table = torch.arange(b * npg, dtype=torch.int32, device=dev).reshape(b, npg)
+    kp = torch.randn((b * npg, hkv, page, d), device=dev, generator=gen, dtype=bf)
+    vp = torch.randn((b * npg, hkv, page, d), device=dev, generator=gen, dtype=bf)
+    x = torch.randn((b, hid), device=dev, generator=gen).to(bf)
+
+    def layer():
+        q1, s1 = ft.rmsnorm_quant(x, wn1, eps=1e-5, device_scale=True)
+        qkv = ft.qgemm_perchannel(q1, s1, *wqkv, out_dtype=bf)
+        qr = ft.rope_kv_append_paged(qkv, hq, hkv, kp, vp, table, lens,
+                                     theta=500000.0, neox=True)
+        att = ft.attention_decode_paged(qr, kp, vp, table, lens + 1)
+        qa, sa = ft.quantize_int8(att.reshape(b, hq * d), device_scale=True)
+        o = ft.qgemm_perchannel(qa, sa, *wo, out_dtype=bf)
+        q2, s2 = ft.rmsnorm_quant(o, wn2, residual=x, eps=1e-5, device_scale=True)
+        h = ft.qgemm_perchannel(q2, s2, *wgu, out_dtype=bf)
+        q3, s3 = ft.swiglu_quant(h[:, :inter], h[:, inter:], device_scale=True)
+        return ft.qgemm_perchannel(q3, s3, *wd, out_dtype=bf)
+
+    ref = layer().clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = layer()
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), f"replay {rep} differs from the eager layer"
+        eager = layer()               # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(eager, ref)

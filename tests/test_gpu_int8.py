@@ -1,9 +1,10 @@
 """GPU parity, bit-exact: INT8 quantize codes and scale, int32 GEMM
 accumulators and the float32 GEMM epilogue equal the CPU oracle exactly;
 bf16 / fp16 GEMM outputs equal the oracle's float32 value rounded to
-nearest-even. Every GEMM kernel is exercised: skinny (M <= 64, with and
-without the cross-workgroup K split), tiled (M > 64), scalar fallback
-(K % 16 != 0) and the K == 0 zero fill."""
+nearest-even. Every GEMM kernel is exercised: GEMV (M == 1, or forced up to
+8), decode (2 <= M <= 16, 1 / 2 / 4 waves per tile), skinny (M <= 64, with
+and without the cross-workgroup K split), tiled, big (M, N >= 256, DMA and
+register-staged), scalar fallback (K % 16 != 0) and the K == 0 zero fill."""
 
 import numpy as np
 import pytest
@@ -87,13 +88,15 @@ def test_quantize_misaligned_view_and_staged():
 # ---------------------------------------------------------------------------
 
 GEMM_SHAPES = [
-    (1, 8, 16),            # skinny, tiny
-    (1, 1000, 4096),       # skinny, decode-like
+    (1, 8, 16),            # GEMV, tiny
+    (1, 1000, 4096),       # GEMV, decode-like
+    (2, 1000, 4096),       # decode kernel, 2 waves per tile
     (3, 5, 7),             # scalar fallback (odd K)
     (8, 11008, 4096),      # BASELINE config 2, M = 8
     (16, 11008, 4096),     # BASELINE config 2, M = 16
     (1, 11008, 4096),      # BASELINE config 2, M = 1
     (33, 300, 1024),       # skinny MT = 4, K split
+    (16, 6144, 4096),      # decode kernel, 1 wave per tile
     (64, 4096, 4096),      # BASELINE config 4 o_proj shape
     (64, 512, 14336),      # BASELINE config 4 down-proj K, fewer rows
     (65, 63, 33),          # scalar fallback
@@ -124,16 +127,35 @@ def test_qgemm_bit_exact(m, n, k):
                                   oracle.qgemm_perchannel(a, 0.031, b, sb))
 
 
-@pytest.mark.parametrize("kernel", ["1", "2", "3", "4", "5"])
+@pytest.mark.parametrize("kernel", ["1", "2", "3", "4", "5", "6"])
 def test_every_gemm_kernel_bit_exact(kernel, monkeypatch):
     monkeypatch.setenv("FT_QGEMM_KERNEL", kernel)
     rng = np.random.default_rng(int(kernel))
-    m = {"1": 48, "5": 7}.get(kernel, 80)
+    m = {"1": 48, "5": 7, "6": 13}.get(kernel, 80)
     a, b = rand_q(rng, m, 640), rand_q(rng, 200, 640)
     sb = rng.uniform(1e-3, 1e-2, 200).astype(np.float32)
     y = ft.qgemm_perchannel(t(a), 0.5, t(b), t(sb))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(y.cpu().numpy(), oracle.qgemm_perchannel(a, 0.5, b, sb))
+
+
+@pytest.mark.parametrize("kw", ["1", "2", "4"])
+@pytest.mark.parametrize("m,n,k", [(1, 200, 640), (5, 33, 4096), (16, 200, 640),
+                                   (3, 16, 80), (16, 40, 16), (8, 1000, 14336)])
+def test_decode_gemm_kernel_bit_exact(kw, m, n, k, monkeypatch):
+    # the K-split-in-workgroup decode kernel: ragged chunks (K % 512 != 0),
+    # K below one MFMA step, waves with no chunk, N % 16 != 0
+    monkeypatch.setenv("FT_QGEMM_KERNEL", "6")
+    monkeypatch.setenv("FT_QGEMM_DEC_KW", kw)
+    rng = np.random.default_rng(m * 100 + n + k + int(kw))
+    a, b = rand_q(rng, m, k), rand_q(rng, n, k)
+    sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    acc = ft.qgemm_i32(t(a), t(b))
+    y = ft.qgemm_perchannel(t(a), 0.021, t(b), t(sb), out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(acc.cpu().numpy(), oracle.qgemm_i32(a, b))
+    ref = torch.from_numpy(oracle.qgemm_perchannel(a, 0.021, b, sb)).to(torch.bfloat16)
+    assert torch.equal(y.cpu(), ref)
 
 
 @pytest.mark.parametrize("ksplit", ["1", "2", "4", "7"])

@@ -287,6 +287,102 @@ def test_swiglu_closed_form_and_extremes():
 
 
 # ---------------------------------------------------------------------------
+# fused decode-chain steps: compositions of the pinned functions above, plus
+# the GPU-order RMSNorm (rmsnorm_blocked)
+# ---------------------------------------------------------------------------
+
+
+def test_rmsnorm_blocked_exact_on_integer_data_and_close_otherwise():
+    rng = np.random.default_rng(12)
+    # integer data: every partial sum is exact, so any order gives the same
+    # bits -> blocked == sequential reference order, bit for bit
+    x = rng.integers(-8, 9, (5, 4096)).astype(np.float32)
+    w = rng.integers(1, 4, 4096).astype(np.float32)
+    r = rng.integers(-3, 4, x.shape).astype(np.float32)
+    np.testing.assert_array_equal(oracle.rmsnorm_blocked(x, w, r, 1e-5),
+                                  oracle.rmsnorm(x, w, r, 1e-5))
+    # known answer (test_rmsnorm.py:37-43 padded to 4 columns)
+    y = oracle.rmsnorm_blocked(np.array([[3.0, 4.0, 0.0, 0.0]], np.float32),
+                               np.ones(4, np.float32), eps=1e-12)
+    inv = 1.0 / math.sqrt(25.0 / 4)
+    assert y[0] == pytest.approx([3.0 * inv, 4.0 * inv, 0, 0], abs=1e-6)
+    # random data, ragged chunk counts (cols / 4 not a multiple of 256)
+    for cols in (4, 1028, 4096, 5000):
+        x = rng.standard_normal((3, cols)).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+        np.testing.assert_allclose(oracle.rmsnorm_blocked(x, w),
+                                   refs.ref_rmsnorm(x, w, 1e-6), rtol=2e-6, atol=1e-7)
+    with pytest.raises(ValueError):
+        oracle.rmsnorm_blocked(np.ones((1, 6), np.float32), np.ones(6, np.float32))
+
+
+def test_rmsnorm_quant_is_the_chain_and_near_the_reference_order():
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal((4, 2048)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 2048).astype(np.float32)
+    r = rng.standard_normal(x.shape).astype(np.float32)
+    q, s = oracle.rmsnorm_quant(x, w, r, 1e-5)
+    q2, s2 = oracle.quantize_int8(oracle.rmsnorm_blocked(x, w, r, 1e-5))
+    np.testing.assert_array_equal(q, q2)
+    assert s == s2
+    # the reference's own order (rmsnorm_cpu -> quantize_int8_cpu): the sums
+    # differ in rounding only, so codes move by at most one step
+    q3, s3 = oracle.quantize_int8(oracle.rmsnorm(x, w, r, 1e-5))
+    assert s == pytest.approx(s3, rel=1e-5)
+    assert np.abs(q.astype(int) - q3.astype(int)).max() <= 1
+    # known answer: [3, 4, 0, 0] -> y = [0.6, 0.8, 0, 0] * 2 -> scale 1.6/127
+    q, s = oracle.rmsnorm_quant(np.array([[3.0, 4.0, 0.0, 0.0]], np.float32),
+                                np.ones(4, np.float32), eps=1e-12)
+    assert s == pytest.approx(1.6 / 127, rel=1e-6)
+    np.testing.assert_array_equal(q, [[95, 127, 0, 0]])
+
+
+def test_swiglu_quant_strided_halves_and_closed_form():
+    rng = np.random.default_rng(14)
+    h = (rng.standard_normal((6, 2 * 300)) * 3).astype(np.float32)
+    g, u = h[:, :300], h[:, 300:]
+    q, s = oracle.swiglu_quant(g, u)
+    q2, s2 = oracle.quantize_int8(oracle.swiglu(np.ascontiguousarray(g),
+                                                np.ascontiguousarray(u)))
+    np.testing.assert_array_equal(q, q2)
+    assert s == s2
+    y = refs.ref_swiglu(g, u)
+    assert s == pytest.approx(np.abs(y).max() / 127, rel=1e-6)
+    np.testing.assert_array_equal(q, np.clip(np.rint(y / s), -127, 127))
+    q, s = oracle.swiglu_quant(np.zeros((2, 8), np.float32), np.ones((2, 8), np.float32))
+    assert s == 1.0 and not q.any()
+
+
+@pytest.mark.parametrize("neox", [False, True])
+def test_rope_kv_append_oracle_positions_and_slots(neox):
+    rng = np.random.default_rng(15 + neox)
+    b, hq, hkv, d, page, width = 3, 4, 2, 16, 4, 3
+    nb = b * width + 1
+    qkv = rng.standard_normal((b, (hq + 2 * hkv) * d)).astype(np.float32)
+    kp = rng.standard_normal((nb, hkv, page, d)).astype(np.float32)
+    vp = rng.standard_normal((nb, hkv, page, d)).astype(np.float32)
+    tbl = rng.permutation(nb)[: b * width].reshape(b, width).astype(np.int32)
+    lens = np.array([0, 5, 11], np.int32)
+    k0, v0 = kp.copy(), vp.copy()
+    qo = oracle.rope_kv_append_paged(qkv, hq, hkv, kp, vp, tbl, lens, 10000.0, 7, neox)
+    heads = qkv.reshape(b, hq + 2 * hkv, d)
+    for i in range(b):
+        pos = int(lens[i]) + 7
+        np.testing.assert_allclose(qo[i], refs.ref_rope(heads[i, :hq], 10000.0, 0, neox,
+                                                        positions=np.full(hq, pos)),
+                                   atol=1e-6)
+        blk, off = tbl[i, lens[i] // page], lens[i] % page
+        np.testing.assert_allclose(kp[blk, :, off],
+                                   refs.ref_rope(heads[i, hq:hq + hkv], 10000.0, 0, neox,
+                                                 positions=np.full(hkv, pos)), atol=1e-6)
+        np.testing.assert_array_equal(vp[blk, :, off], heads[i, hq + hkv:])
+        kp[blk, :, off] = k0[blk, :, off]
+        vp[blk, :, off] = v0[blk, :, off]
+    np.testing.assert_array_equal(kp, k0)      # nothing else written
+    np.testing.assert_array_equal(vp, v0)
+
+
+# ---------------------------------------------------------------------------
 # golden vectors (tests/golden/make_golden.py: numpy float64 / exact ints)
 # ---------------------------------------------------------------------------
 
