@@ -701,6 +701,8 @@ def quantize_int8(x, *, device_scale=False):
         _check_dtype(x, "x", _FLOAT_DTYPES)
         q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
         scale = torch.empty(1, dtype=torch.float32, device=x.device)
+        if x.numel() == 0:
+            scale.fill_(1.0)   # all-zero (here: empty) input -> scale 1.0
         if x.dtype is torch.float32:
             _fusedtok.quantize_launch(x.data_ptr(), q.data_ptr(), scale.data_ptr(),
                                       x.numel(), _stream())
@@ -757,7 +759,11 @@ def rmsnorm_quant(x, weight, *, residual=None, eps=1e-6, device_scale=False):
             raise ValueError("residual must have the same shape as x")
         r_ptr = residual.data_ptr()
     q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
-    scale = torch.ones(1, dtype=torch.float32, device=x.device)
+    # the kernel writes the scale; an empty input has none to compute (1.0,
+    # as quantize_int8), set here so the common path launches no fill kernel
+    scale = torch.empty(1, dtype=torch.float32, device=x.device)
+    if rows == 0:
+        scale.fill_(1.0)
     _fusedtok.rmsnorm_quant_launch(x.data_ptr(), _DT_CODE[x.dtype],
                                    weight.data_ptr(), r_ptr, q.data_ptr(),
                                    scale.data_ptr(), rows, cols, float(eps),
@@ -791,7 +797,9 @@ def swiglu_quant(gate, up, *, device_scale=False):
             raise ValueError("gate and up must have unit column stride and "
                              "the same row stride")
     q = torch.empty((rows, cols), dtype=torch.int8, device=gate.device)
-    scale = torch.ones(1, dtype=torch.float32, device=gate.device)
+    scale = torch.empty(1, dtype=torch.float32, device=gate.device)
+    if rows * cols == 0:
+        scale.fill_(1.0)
     _fusedtok.swiglu_quant_launch(gate.data_ptr(), up.data_ptr(),
                                   _DT_CODE[gate.dtype], q.data_ptr(),
                                   scale.data_ptr(), rows, cols, ld, _stream())

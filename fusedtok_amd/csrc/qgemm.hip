@@ -685,157 +685,16 @@ __device__ __forceinline__ float epi_val(int acc, float s) {
     return val;
 }
 
+// Epilogue of the DMA-fed big kernels. acc[i][j] holds C^T: lane (r32, h),
+// register t -> C[row = i*32 + r32][col = j*32 + 8(t/4) + 4h + t%4] of the
+// wave's 128 x 128 sub-tile at (row0, col0), i.e. 4 consecutive columns per
+// register quad. lds must hold 4 * 64 * kEpiPitch bytes no wave still reads.
 template <int OUT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void qgemm_big_dma(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
-                   int m, int n, int k) {
-    __shared__ __attribute__((aligned(16))) i8 lds[kDmaStages * kSlabBytes];
-
-    const int tm = (m + kBigT - 1) / kBigT, tn = (n + kBigT - 1) / kBigT;
-    const int ntiles = tm * tn;
-    int pid = blockIdx.x;
-    if (ntiles % 8 == 0) pid = (pid % 8) * (ntiles / 8) + pid / 8;
-    const int band = pid / (kBigBand * tn);
-    const int first_m = band * kBigBand;
-    const int band_m = min(tm - first_m, kBigBand);
-    const int in_band = pid - band * kBigBand * tn;
-    const int bm = (first_m + in_band % band_m) * kBigT;
-    const int bn = (in_band / band_m) * kBigT;
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
-    const int r32 = lane & 31, h = lane >> 5;
-
-    // this lane's sources: LDS chunk q = tid + 256 j holds tile row
-    // q/4 = tid/4 + 64 j, logical chunk (q%4) ^ big_swz(row), which is
-    // the same for all j. Addresses = wave-uniform tile base (scalar) + a
-    // 32-bit per-lane offset (rows past the edge clamp to the last row).
-    const int c16 = 16 * ((tid & 3) ^ big_swz(tid >> 2));
-    unsigned aoff[4], boff[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int row = (tid >> 2) + 64 * j;
-        aoff[j] = (unsigned)(min(row, m - 1 - bm) * k + c16);
-        boff[j] = (unsigned)(min(row, n - 1 - bn) * k + c16);
-    }
-    const i8* const abase = a + (size_t)bm * k;
-    const i8* const bbase = b + (size_t)bn * k;
-    auto stage_a = [&](int st) { return lds + st * kSlabBytes; };
-    auto stage_b = [&](int st) { return lds + st * kSlabBytes + kBigT * kBigK; };
-    auto issue = [&](int kt, int st) {
-        const i8* ak = abase + (size_t)kt * kBigK;
-        const i8* bk = bbase + (size_t)kt * kBigK;
-        i8* la = stage_a(st);
-        i8* lb = stage_b(st);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int dst = (256 * j + 64 * wave) * 16;  // this wave's 1 KB
-            __builtin_amdgcn_global_load_lds(ak + aoff[j], (lds_void_p)(la + dst), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(bk + boff[j], (lds_void_p)(lb + dst), 16, 0, 0);
-        }
-    };
-
-    i32x16 acc[4][4];  // acc[i][j] = C^T block (n block j, m block i)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int t = 0; t < 16; ++t) acc[i][j][t] = 0;
-
-    // Operand fragments of one 32-byte K step: f[0..3] A row blocks,
-    // f[4..7] B column blocks; two sets (f0, f1) alternate. Row offsets of
-    // this lane's fragment rows within a stage, chunk 0; chunk c of a row
-    // sits at 16 * (c ^ big_swz(row)), i.e. XOR (c << 4) into the offset.
-    unsigned arow_off[4], brow_off[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        arow_off[i] = (unsigned)big_lds_off(wm * 128 + i * 32 + r32, 0);
-        brow_off[i] = (unsigned)big_lds_off(wn * 128 + i * 32 + r32, 0);
-    }
-    const unsigned lds0 = lds_addr(lds);
-    auto read_frags = [&](int st, int sub, i32x4 (&f)[8]) {
-        const unsigned la = lds0 + st * kSlabBytes, lb = la + kBigT * kBigK;
-        const unsigned cx = (unsigned)((2 * sub + h) << 4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) f[i] = lds_read16(la + (arow_off[i] ^ cx));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) f[4 + j] = lds_read16(lb + (brow_off[j] ^ cx));
-    };
-    // 16 MFMAs on f; with rd, the next fragment set's 8 reads go out between
-    // them (one after every second MFMA)
-    auto mfma_and_read = [&](const i32x4 (&f)[8], bool rd, int st, int sub,
-                             i32x4 (&nf)[8]) {
-        const unsigned la = lds0 + st * kSlabBytes, lb = la + kBigT * kBigK;
-        const unsigned cx = (unsigned)((2 * sub + h) << 4);
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int i = q >> 2, j = q & 3;
-            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[4 + j], f[i], acc[i][j], 0, 0, 0);
-            if (rd && (q & 1)) {
-                const int x = q >> 1;  // 0..7
-                __builtin_amdgcn_sched_barrier(0);
-                nf[x] = lds_read16(x < 4 ? la + (arow_off[x] ^ cx)
-                                         : lb + (brow_off[x - 4] ^ cx));
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-    };
-
-    // Per slab kt (in stage st = kt % kDmaStages), with f0 = (kt, sub 0) in
-    // registers:
-    //   16 MFMAs on f0 while f1 = (kt, sub 1) is read; wait f1;
-    //   wait for slab kt+1's DMA, barrier (every wave is past its reads of
-    //   stage st, and slab kt+1 is visible); refill stage st with slab
-    //   kt + kDmaStages;
-    //   16 MFMAs on f1 while f0 = (kt+1, sub 0) is read; wait f0.
-    const int nk = k / kBigK;
-    const int pre = min(kDmaStages, nk);
-    for (int s = 0; s < pre; ++s) issue(s, s);
-    // slab 0 landed: at most pre - 1 slabs issued after it still in flight
-    switch (pre - 1) {
-    case 4: wait_vmcnt<4 * kSlabLoads>(); break;
-    case 3: wait_vmcnt<3 * kSlabLoads>(); break;
-    case 2: wait_vmcnt<2 * kSlabLoads>(); break;
-    case 1: wait_vmcnt<1 * kSlabLoads>(); break;
-    default: wait_vmcnt<0>(); break;
-    }
-    __builtin_amdgcn_s_barrier();
-    i32x4 f0[8], f1[8];
-    read_frags(0, 0, f0);
-    lds_wait(f0);
-    int st = 0;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int st_next = st + 1 == kDmaStages ? 0 : st + 1;
-        mfma_and_read(f0, true, st, 1, f1);
-        lds_wait(f1);
-        // slabs issued after kt+1: kt+2 .. min(nk, kt + kDmaStages) - 1
-        const int after = min(kDmaStages - 2, nk - 2 - kt);
-        switch (after) {
-        case 3: wait_vmcnt<3 * kSlabLoads>(); break;
-        case 2: wait_vmcnt<2 * kSlabLoads>(); break;
-        case 1: wait_vmcnt<1 * kSlabLoads>(); break;
-        default: wait_vmcnt<0>(); break;
-        }
-        // bare barrier: this wave's slab kt+1 DMAs and stage-st reads are
-        // already waited for; __syncthreads() would add a release fence that
-        // drains every in-flight DMA (the later slabs too)
-        __builtin_amdgcn_s_barrier();
-        if (kt + kDmaStages < nk) issue(kt + kDmaStages, st);
-        const bool more = kt + 1 < nk;
-        mfma_and_read(f1, more, st_next, 0, f0);
-        if (more) lds_wait(f0);
-        st = st_next;
-    }
-
-    // ---- epilogue. acc[i][j] holds C^T: lane (r32, h), register t ->
-    // C[row = i*32 + r32][col = j*32 + 8(t/4) + 4h + t%4] of this wave's
-    // 128 x 128 sub-tile, i.e. 4 consecutive columns per register quad.
+__device__ __forceinline__ void big_epilogue(i32x16 (&acc)[4][4], i8* lds, const Epi& e,
+                                             int m, int n, int row0, int col0,
+                                             int lane, int wave, int r32, int h) {
     __syncthreads();  // every wave is done with the stages: LDS is reused
     const float sa = epi_sa(e);
-    const int row0 = bm + wm * 128, col0 = bn + wn * 128;
     auto scales4 = [&](int col) {  // f32(sa * sb[col .. col+3]), clamped at n
         float4 s4;
         if (e.sb_vec) {
@@ -928,6 +787,564 @@ void qgemm_big_dma(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
                     }
                 }
             }
+    }
+}
+
+template <int OUT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void qgemm_big_dma(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
+                   int m, int n, int k) {
+    __shared__ __attribute__((aligned(16))) i8 lds[kDmaStages * kSlabBytes];
+
+    const int tm = (m + kBigT - 1) / kBigT, tn = (n + kBigT - 1) / kBigT;
+    const int ntiles = tm * tn;
+    int pid = blockIdx.x;
+    if (ntiles % 8 == 0) pid = (pid % 8) * (ntiles / 8) + pid / 8;
+    const int band = pid / (kBigBand * tn);
+    const int first_m = band * kBigBand;
+    const int band_m = min(tm - first_m, kBigBand);
+    const int in_band = pid - band * kBigBand * tn;
+    const int bm = (first_m + in_band % band_m) * kBigT;
+    const int bn = (in_band / band_m) * kBigT;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r32 = lane & 31, h = lane >> 5;
+
+    // this lane's sources: LDS chunk q = tid + 256 j holds tile row
+    // q/4 = tid/4 + 64 j, logical chunk (q%4) ^ big_swz(row), which is
+    // the same for all j. Addresses = wave-uniform tile base (scalar) + a
+    // 32-bit per-lane offset (rows past the edge clamp to the last row).
+    const int c16 = 16 * ((tid & 3) ^ big_swz(tid >> 2));
+    unsigned aoff[4], boff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = (tid >> 2) + 64 * j;
+        aoff[j] = (unsigned)(min(row, m - 1 - bm) * k + c16);
+        boff[j] = (unsigned)(min(row, n - 1 - bn) * k + c16);
+    }
+    const i8* const abase = a + (size_t)bm * k;
+    const i8* const bbase = b + (size_t)bn * k;
+    auto stage_a = [&](int st) { return lds + st * kSlabBytes; };
+    auto stage_b = [&](int st) { return lds + st * kSlabBytes + kBigT * kBigK; };
+    auto issue = [&](int kt, int st) {
+        const i8* ak = abase + (size_t)kt * kBigK;
+        const i8* bk = bbase + (size_t)kt * kBigK;
+        i8* la = stage_a(st);
+        i8* lb = stage_b(st);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int dst = (256 * j + 64 * wave) * 16;  // this wave's 1 KB
+            __builtin_amdgcn_global_load_lds(ak + aoff[j], (lds_void_p)(la + dst), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(bk + boff[j], (lds_void_p)(lb + dst), 16, 0, 0);
+        }
+    };
+
+    i32x16 acc[4][4];  // acc[i][j] = C^T block (n block j, m block i)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) acc[i][j][t] = 0;
+
+    // Operand fragments of one 32-byte K step: f[0..3] A row blocks,
+    // f[4..7] B column blocks; two sets (f0, f1) alternate. Row offsets of
+    // this lane's fragment rows within a stage, chunk 0; chunk c of a row
+    // sits at 16 * (c ^ big_swz(row)), i.e. XOR (c << 4) into the offset.
+    unsigned arow_off[4], brow_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        arow_off[i] = (unsigned)big_lds_off(wm * 128 + i * 32 + r32, 0);
+        brow_off[i] = (unsigned)big_lds_off(wn * 128 + i * 32 + r32, 0);
+    }
+    const unsigned lds0 = lds_addr(lds);
+    // Fragment reads go out in the order their first use in the MFMA
+    // sequence below needs them: A0, B0..B3, A1, A2, A3.
+    auto frag_off = [&](int x, unsigned la, unsigned lb, unsigned cx) {
+        constexpr int order[8] = {0, 4, 5, 6, 7, 1, 2, 3};
+        const int fi = order[x];
+        return fi < 4 ? la + (arow_off[fi] ^ cx) : lb + (brow_off[fi - 4] ^ cx);
+    };
+    auto read_frags = [&](int st, int sub, i32x4 (&f)[8]) {
+        const unsigned la = lds0 + st * kSlabBytes, lb = la + kBigT * kBigK;
+        const unsigned cx = (unsigned)((2 * sub + h) << 4);
+        constexpr int order[8] = {0, 4, 5, 6, 7, 1, 2, 3};
+#pragma unroll
+        for (int x = 0; x < 8; ++x) f[order[x]] = lds_read16(frag_off(x, la, lb, cx));
+    };
+    // Wait until LDS reads leave at most N outstanding; the named fragments
+    // are in/out operands, so nothing that uses them moves above the wait.
+#define FT_LGKM_WAIT(N, ...)                                                    \
+    do {                                                                       \
+        __builtin_amdgcn_sched_barrier(0);                                     \
+        asm volatile("s_waitcnt lgkmcnt(" #N ")" : __VA_ARGS__);               \
+        __builtin_amdgcn_sched_barrier(0);                                     \
+    } while (0)
+
+    // 16 MFMAs on f while the next fragment set's 8 reads go out between
+    // them (one after every odd MFMA); with a DMA tag, the 8 DMA
+    // instructions of slab dma_kt into stage dma_st go out after the even
+    // ones. (Issued in a burst right after the barrier, the four waves' 32
+    // DMA instructions would queue at the CU's texture addresser with the
+    // MFMA pipe idle until the last wave's had gone out.)
+    // f was read in the previous call, in first-use order, and is waited for
+    // piecewise: before MFMA q, floor(q/2) reads of this call are in flight
+    // too, so "read r of f landed" is lgkmcnt(7 - r + floor(q/2)) (LDS
+    // reads complete in order). The MFMA pipe never waits on the last
+    // reads of f (A3 is first needed at q = 12).
+    auto mfma_and_read = [&](i32x4 (&f)[8], int st, int sub, i32x4 (&nf)[8],
+                             auto dma, int dma_kt, int dma_st) {
+        const unsigned la = lds0 + st * kSlabBytes, lb = la + kBigT * kBigK;
+        const unsigned cx = (unsigned)((2 * sub + h) << 4);
+        const i8* ak = abase + (size_t)dma_kt * kBigK;
+        const i8* bk = bbase + (size_t)dma_kt * kBigK;
+        i8* da = stage_a(dma_st);
+        i8* db = stage_b(dma_st);
+        constexpr int order[8] = {0, 4, 5, 6, 7, 1, 2, 3};
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int i = q >> 2, j = q & 3;
+            if (q == 0) FT_LGKM_WAIT(6, "+v"(f[0]), "+v"(f[4]));
+            if (q == 1) FT_LGKM_WAIT(5, "+v"(f[5]));
+            if (q == 2) FT_LGKM_WAIT(5, "+v"(f[6]));
+            if (q == 3) FT_LGKM_WAIT(4, "+v"(f[7]));
+            if (q == 4) FT_LGKM_WAIT(4, "+v"(f[1]));
+            if (q == 8) FT_LGKM_WAIT(5, "+v"(f[2]));
+            if (q == 12) FT_LGKM_WAIT(6, "+v"(f[3]));
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[4 + j], f[i], acc[i][j], 0, 0, 0);
+            const int x = q >> 1;  // 0..7
+            if (q & 1) {
+                __builtin_amdgcn_sched_barrier(0);
+                nf[order[x]] = lds_read16(frag_off(x, la, lb, cx));
+                __builtin_amdgcn_sched_barrier(0);
+            } else if constexpr (decltype(dma)::value) {
+                // x = 2 jj: A rows 64 jj + ..; x = 2 jj + 1: B rows (the order
+                // of issue(): A, B per jj)
+                const int jj = x >> 1;
+                const int dst = (256 * jj + 64 * wave) * 16;
+                __builtin_amdgcn_sched_barrier(0);
+                if (x & 1)
+                    __builtin_amdgcn_global_load_lds(bk + boff[jj], (lds_void_p)(db + dst), 16, 0, 0);
+                else
+                    __builtin_amdgcn_global_load_lds(ak + aoff[jj], (lds_void_p)(da + dst), 16, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+#undef FT_LGKM_WAIT
+
+    // Per slab kt (in stage st = kt % kDmaStages), with f0 = (kt, sub 0)
+    // read:
+    //   16 MFMAs on f0 while f1 = (kt, sub 1) is read;
+    //   wait for slab kt+1's DMA, barrier;
+    //   16 MFMAs on f1 while f0 = (kt+1, sub 0) is read and the stage of
+    //   slab kt-1 is refilled with slab kt-1 + kDmaStages.
+    // The barrier of slab kt certifies that every wave has consumed slab
+    // kt-1 (its fragments fed MFMAs before the barrier, which needs them
+    // landed), so that stage is free; and that slab kt+1's DMAs, waited for
+    // by each wave before it, are visible to all. (After the last slab f0
+    // reads a stale stage: in bounds, never used.)
+    const int nk = k / kBigK;
+    const int pre = min(kDmaStages, nk);
+    for (int s = 0; s < pre; ++s) issue(s, s);
+    // slab 0 landed: at most pre - 1 slabs issued after it still in flight
+    switch (pre - 1) {
+    case 4: wait_vmcnt<4 * kSlabLoads>(); break;
+    case 3: wait_vmcnt<3 * kSlabLoads>(); break;
+    case 2: wait_vmcnt<2 * kSlabLoads>(); break;
+    case 1: wait_vmcnt<1 * kSlabLoads>(); break;
+    default: wait_vmcnt<0>(); break;
+    }
+    __builtin_amdgcn_s_barrier();
+    i32x4 f0[8], f1[8];
+    read_frags(0, 0, f0);
+    int st = 0;
+    auto slab = [&](int kt, auto dma) {
+        const int st_next = st + 1 == kDmaStages ? 0 : st + 1;
+        const int st_prev = st == 0 ? kDmaStages - 1 : st - 1;
+        mfma_and_read(f0, st, 1, f1, std::false_type{}, 0, 0);
+        // slabs issued after kt+1: kt+2 .. min(nk - 1, kt + kDmaStages - 2)
+        const int after = min(kDmaStages - 3, nk - 2 - kt);
+        switch (after) {
+        case 3: wait_vmcnt<3 * kSlabLoads>(); break;
+        case 2: wait_vmcnt<2 * kSlabLoads>(); break;
+        case 1: wait_vmcnt<1 * kSlabLoads>(); break;
+        default: wait_vmcnt<0>(); break;
+        }
+        // bare barrier: __syncthreads() would add a release fence that
+        // drains every in-flight DMA (the later slabs too)
+        __builtin_amdgcn_s_barrier();
+        mfma_and_read(f1, st_next, 0, f0, dma, kt - 1 + kDmaStages, st_prev);
+        st = st_next;
+    };
+    // slab 0 has no previous stage to refill; slabs 1 .. nk - kDmaStages do
+    int kt = 0;
+    if (nk > 0) slab(kt++, std::false_type{});
+    for (; kt - 1 + kDmaStages < nk; ++kt) slab(kt, std::true_type{});
+    for (; kt < nk; ++kt) slab(kt, std::false_type{});
+    // the last reads (stale, unused) still land in f0's registers: wait for
+    // them before those registers can be given to anything else
+    lds_wait(f0);
+
+    big_epilogue<OUT>(acc, lds, e, m, n, bm + wm * 128, bn + wn * 128, lane, wave,
+                      r32, h);
+}
+
+// ---------------------------------------------------------------------------
+// big, DMA-fed, 128-byte slabs (K % 128 == 0): the tiles, order and operand
+// layout of qgemm_big_dma, with each slab covering 128 bytes of K, a whole
+// cache line per row:
+//  - a DMA instruction moves 8 rows x 128 B (8 full lines) instead of
+//    16 rows x 64 B (16 half lines); streaming this kernel's operand traffic
+//    alone (7.5 GB for 4096 x 8192 x 28672) runs at 18.5 TB/s L2 -> LDS this
+//    way against 15.6 TB/s with 64-byte rows, at any ring depth;
+//  - LDS rows are 128 B = eight 16-byte chunks, chunk c of row r at
+//    position c ^ ((r >> 1) & 7): the 16 rows of a 16-lane ds_read_b128
+//    group then hit 16 distinct 16-byte bank groups;
+//  - two 64 KB stages: slab kt+1 lands while slab kt is multiplied; one
+//    barrier per slab (four MFMA sub-steps of 32 bytes), placed before the
+//    last sub-step so that sub-step's MFMAs overlap both the refill DMA of
+//    the stage just consumed and the first fragment reads of slab kt+1;
+//  - persistent: min(tiles, CUs) workgroups walk the tiles (XCD-aware
+//    order kept: the grid is a multiple of 8), and the next tile's first two
+//    slabs are in flight while the current tile's epilogue runs, out of a
+//    separate LDS region (per-wave 16-row output staging and the tile's 256
+//    column scales, fetched by DMA when the tile starts), so the epilogue
+//    needs no barrier and the next tile no cold start.
+// ---------------------------------------------------------------------------
+constexpr int kK2 = 128;                     // K bytes per slab
+constexpr int kSlab2 = 2 * kBigT * kK2;      // A + B, 64 KB
+constexpr int kLoads2 = 16;                  // DMA instructions per thread per slab
+constexpr int kK2Stg = 16 * kEpiPitch;       // per-wave output staging, 16 rows
+constexpr int kK2Spare = 2 * kSlab2;         // LDS offset of the staging
+constexpr int kK2Scl = kK2Spare + 4 * kK2Stg;  // LDS offset of the 256 column scales
+constexpr int kK2Lds = kK2Scl + 4 * kBigT;   // 149,504 bytes
+
+// Epilogue of qgemm_big_k128 for the wave's 128 x 128 sub-tile at (row0,
+// col0). acc[i][j] holds C^T (lane (r32, h), register t -> row i*32 + r32,
+// column j*32 + 8(t/4) + 4h + t%4). scw: the sub-tile's 128 column scales in
+// LDS, or null (read sb_vec from global). 2-byte outputs go through this
+// wave's 16-row staging stg in 8 passes and leave as 16-byte row stores;
+// 4-byte outputs are stored from registers.
+template <int OUT>
+__device__ __forceinline__ void k128_epilogue(i32x16 (&acc)[4][4], i8* stg, const float* scw,
+                                              const Epi& e, int m, int n, int row0,
+                                              int col0, int lane, int r32, int h) {
+    const float sa = epi_sa(e);
+    auto scales4 = [&](int jc) {  // f32(sa * sb[col0 + jc .. + 3]), clamped at n
+        float4 s4;
+        if (scw) {
+            const float4 v = *reinterpret_cast<const float4*>(scw + jc);
+            s4 = make_float4(sa * v.x, sa * v.y, sa * v.z, sa * v.w);
+        } else if (e.sb_vec) {
+            const int col = col0 + jc;
+            s4.x = sa * e.sb_vec[min(col, n - 1)];
+            s4.y = sa * e.sb_vec[min(col + 1, n - 1)];
+            s4.z = sa * e.sb_vec[min(col + 2, n - 1)];
+            s4.w = sa * e.sb_vec[min(col + 3, n - 1)];
+        } else {
+            const float sc = sa * e.sb;
+            s4 = make_float4(sc, sc, sc, sc);
+        }
+        return s4;
+    };
+    if constexpr (OUT == kOutBF16 || OUT == kOutF16) {
+        typedef typename std::conditional<OUT == kOutBF16, bf16, f16>::type OT;
+        typedef OT ot4 __attribute__((ext_vector_type(4)));
+        OT* const y = static_cast<OT*>(e.y);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            ot4 v[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 s4 = scales4(j * 32 + 8 * g + 4 * h);
+                    v[j][g][0] = (OT)epi_val(acc[i][j][4 * g + 0], s4.x);
+                    v[j][g][1] = (OT)epi_val(acc[i][j][4 * g + 1], s4.y);
+                    v[j][g][2] = (OT)epi_val(acc[i][j][4 * g + 2], s4.z);
+                    v[j][g][3] = (OT)epi_val(acc[i][j][4 * g + 3], s4.w);
+                }
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                if ((r32 >> 4) == p) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+#pragma unroll
+                        for (int g = 0; g < 4; ++g)
+                            *reinterpret_cast<ot4*>(stg + (r32 & 15) * kEpiPitch +
+                                                    (j * 32 + 8 * g + 4 * h) * 2) = v[j][g];
+                }
+                // 16 rows x 256 bytes back out: 16 lanes per row, 16 bytes each
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int lr = rr * 4 + (lane >> 4);
+                    const int row = row0 + i * 32 + 16 * p + lr;
+                    const int cb = (lane & 15) * 8;  // first of 8 columns
+                    const i8* src = stg + lr * kEpiPitch + cb * 2;
+                    if (row >= m) continue;
+                    OT* dst = y + (size_t)row * n + col0 + cb;
+                    if ((n & 7) == 0) {
+                        if (col0 + cb < n)
+                            *reinterpret_cast<i32x4*>(dst) = *reinterpret_cast<const i32x4*>(src);
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 8; ++c)
+                            if (col0 + cb + c < n) dst[c] = reinterpret_cast<const OT*>(src)[c];
+                    }
+                }
+            }
+        }
+    } else {  // 4-byte outputs: 16-byte stores of 4 consecutive columns
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int col = col0 + j * 32 + 8 * g + 4 * h;
+                float4 s4;
+                if constexpr (OUT == kOutF32) s4 = scales4(j * 32 + 8 * g + 4 * h);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = row0 + i * 32 + r32;
+                    if (row >= m || col >= n) continue;
+                    i32x4 o;
+                    if constexpr (OUT == kOutI32) {
+                        o = i32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1],
+                                  acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                    } else {
+                        o = i32x4{__float_as_int(epi_val(acc[i][j][4 * g], s4.x)),
+                                  __float_as_int(epi_val(acc[i][j][4 * g + 1], s4.y)),
+                                  __float_as_int(epi_val(acc[i][j][4 * g + 2], s4.z)),
+                                  __float_as_int(epi_val(acc[i][j][4 * g + 3], s4.w))};
+                    }
+                    int* dst = static_cast<int*>(e.y) + (size_t)row * n + col;
+                    if ((n & 3) == 0) {
+                        *reinterpret_cast<i32x4*>(dst) = o;
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            if (col + c < n) dst[c] = o[c];
+                    }
+                }
+            }
+    }
+}
+
+// scales_dma: the host checked that sb_vec is 16-byte aligned and n % 4 == 0,
+// so lane l's DMA of sb_vec[bn + 4 l .. + 3] (clamped to the last 4) is one
+// aligned 16-byte piece.
+template <int OUT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void qgemm_big_k128(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
+                    int m, int n, int k, int scales_dma) {
+    __shared__ __attribute__((aligned(16))) i8 lds[kK2Lds];
+
+    const int tm = (m + kBigT - 1) / kBigT, tn = (n + kBigT - 1) / kBigT;
+    const int ntiles = tm * tn;
+    // tile t -> (bm, bn) in the XCD-aware order (tile t runs on XCD t % 8
+    // because the grid is a multiple of 8)
+    auto tile_origin = [&](int t, int& bm, int& bn) {
+        int pid = t;
+        if (ntiles % 8 == 0) pid = (pid % 8) * (ntiles / 8) + pid / 8;
+        const int band = pid / (kBigBand * tn);
+        const int first_m = band * kBigBand;
+        const int band_m = min(tm - first_m, kBigBand);
+        const int in_band = pid - band * kBigBand * tn;
+        bm = (first_m + in_band % band_m) * kBigT;
+        bn = (in_band / band_m) * kBigT;
+    };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r32 = lane & 31, h = lane >> 5;
+    const int nk = k / kK2;
+
+    // DMA: instruction j (0..7) of this wave fills tile rows 32 j + 8 wave +
+    // lane / 8 (1 KB of LDS at row (32 j + 8 wave) * 128); lane's LDS chunk
+    // position is lane % 8, so it fetches logical chunk (lane % 8) ^ swz,
+    // where swz = (row >> 1) & 7 = (4 wave + lane / 16) & 7 for every j.
+    // Rows past M / N read a clamped (real) row; they only feed outputs that
+    // are never stored.
+    const int c16 = 16 * ((lane & 7) ^ ((4 * wave + (lane >> 4)) & 7));
+    unsigned aoff[8], boff[8];
+    const i8* abase;
+    const i8* bbase;
+    auto set_tile = [&](int bm, int bn) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int row = 32 * j + 8 * wave + (lane >> 3);
+            aoff[j] = (unsigned)(min(row, m - 1 - bm) * k + c16);
+            boff[j] = (unsigned)(min(row, n - 1 - bn) * k + c16);
+        }
+        abase = a + (size_t)bm * k;
+        bbase = b + (size_t)bn * k;
+    };
+    // instruction x (0..15) of a slab: A rows for even x, B rows for odd x
+    auto dma1 = [&](int kt, int st, int x) {
+        const int j = x >> 1;
+        i8* dst = lds + st * kSlab2 + (x & 1) * (kBigT * kK2) + (32 * j + 8 * wave) * kK2;
+        if (x & 1)
+            __builtin_amdgcn_global_load_lds(bbase + (size_t)kt * kK2 + boff[j],
+                                             (lds_void_p)dst, 16, 0, 0);
+        else
+            __builtin_amdgcn_global_load_lds(abase + (size_t)kt * kK2 + aoff[j],
+                                             (lds_void_p)dst, 16, 0, 0);
+    };
+    // slabs 0 and 1 of the tile at (bm, bn), with offsets computed here
+    // (not kept: they would stay live through the previous tile's epilogue)
+    auto first_slabs = [&](int bm, int bn) {
+        const int nsl = nk > 1 ? 2 : 1;
+        for (int sl = 0; sl < nsl; ++sl) {
+            const i8* ab = a + (size_t)bm * k + (size_t)sl * kK2;
+            const i8* bb = b + (size_t)bn * k + (size_t)sl * kK2;
+#pragma unroll
+            for (int x = 0; x < kLoads2; ++x) {
+                const int j = x >> 1;
+                const int row = 32 * j + 8 * wave + (lane >> 3);
+                i8* dst = lds + sl * kSlab2 + (x & 1) * (kBigT * kK2) + (32 * j + 8 * wave) * kK2;
+                const unsigned off = (x & 1) ? (unsigned)(min(row, n - 1 - bn) * k + c16)
+                                             : (unsigned)(min(row, m - 1 - bm) * k + c16);
+                __builtin_amdgcn_global_load_lds(((x & 1) ? bb : ab) + off, (lds_void_p)dst,
+                                                 16, 0, 0);
+            }
+        }
+    };
+
+    // fragment rows: A block i = tile row wm*128 + 32 i + r32, B block j
+    // likewise; offset of chunk c = (row << 7) | 16 (c ^ swz(row)); for
+    // sub-step s the lane's chunk is 2 s + h, so the offset is
+    // base ^ (32 s) with base = (row << 7) | 16 (h ^ swz(row)).
+    unsigned arow[4], brow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int ra = wm * 128 + 32 * i + r32, rb = wn * 128 + 32 * i + r32;
+        arow[i] = (unsigned)((ra << 7) | (16 * (h ^ ((ra >> 1) & 7))));
+        brow[i] = (unsigned)((rb << 7) | (16 * (h ^ ((rb >> 1) & 7))));
+    }
+    const unsigned lds0 = lds_addr(lds);
+    constexpr int order[8] = {0, 4, 5, 6, 7, 1, 2, 3};  // first-use order
+    auto frag_addr = [&](int st, int s, int x) {
+        const int fi = order[x];
+        const unsigned base = lds0 + st * kSlab2;
+        return fi < 4 ? base + (arow[fi] ^ (32u * s))
+                      : base + kBigT * kK2 + (brow[fi - 4] ^ (32u * s));
+    };
+    auto read_frags = [&](int st, int s, i32x4 (&f)[8]) {
+#pragma unroll
+        for (int x = 0; x < 8; ++x) f[order[x]] = lds_read16(frag_addr(st, s, x));
+    };
+
+    i32x16 acc[4][4];  // acc[i][j] = C^T block (n block j, m block i)
+#define FT_LGKM_WAIT(N, ...)                                                    \
+    do {                                                                       \
+        __builtin_amdgcn_sched_barrier(0);                                     \
+        asm volatile("s_waitcnt lgkmcnt(" #N ")" : __VA_ARGS__);               \
+        __builtin_amdgcn_sched_barrier(0);                                     \
+    } while (0)
+    // 16 MFMAs on f (read in first-use order by the previous call and
+    // waited for piecewise: before MFMA q, floor(q/2) reads of this call
+    // are in flight too), the 8 reads of nf = (rst, rs) after the odd
+    // MFMAs, and with a DMA tag the 16 DMA instructions of slab dkt into
+    // stage dst, one after every MFMA.
+    auto step = [&](i32x4 (&f)[8], bool piecewise, int rst, int rs, i32x4 (&nf)[8],
+                    auto dma, int dkt, int dst) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int i = q >> 2, j = q & 3;
+            if (piecewise) {
+                if (q == 0) FT_LGKM_WAIT(6, "+v"(f[0]), "+v"(f[4]));
+                if (q == 1) FT_LGKM_WAIT(5, "+v"(f[5]));
+                if (q == 2) FT_LGKM_WAIT(5, "+v"(f[6]));
+                if (q == 3) FT_LGKM_WAIT(4, "+v"(f[7]));
+                if (q == 4) FT_LGKM_WAIT(4, "+v"(f[1]));
+                if (q == 8) FT_LGKM_WAIT(5, "+v"(f[2]));
+                if (q == 12) FT_LGKM_WAIT(6, "+v"(f[3]));
+            }
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[4 + j], f[i], acc[i][j], 0, 0, 0);
+            if constexpr (decltype(dma)::value) {
+                __builtin_amdgcn_sched_barrier(0);
+                dma1(dkt, dst, q);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (q & 1) {
+                __builtin_amdgcn_sched_barrier(0);
+                nf[order[q >> 1]] = lds_read16(frag_addr(rst, rs, q >> 1));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+#undef FT_LGKM_WAIT
+
+    int t = blockIdx.x;
+    if (t < ntiles) {
+        int bm0, bn0;
+        tile_origin(t, bm0, bn0);
+        first_slabs(bm0, bn0);
+    }
+    for (; t < ntiles; t += gridDim.x) {
+        int bm, bn;
+        tile_origin(t, bm, bn);
+        set_tile(bm, bn);
+        // slabs 0 and 1 of this tile were issued (before the previous tile's
+        // epilogue, or just above); wait for them and for that epilogue's
+        // stores, then every wave's DMAs are visible after the barrier
+        wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        if (scales_dma && wave == 0) {
+            const int c = min(bn + 4 * lane, n - 4);
+            __builtin_amdgcn_global_load_lds(e.sb_vec + c, (lds_void_p)(lds + kK2Scl), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) acc[i][j][q] = 0;
+
+        // Per slab kt (stage st = kt & 1), with F0 = (kt, 0) read:
+        //   sub-steps 0, 1, 2: MFMAs on (kt, s) while (kt, s + 1) is read;
+        //   wait for (kt, 3) and for slab kt+1's DMA (and the scales); barrier:
+        //   every wave is past its reads of stage st, and slab kt+1 is
+        //   visible;
+        //   sub-step 3: MFMAs on (kt, 3) while (kt+1, 0) is read from stage
+        //   st ^ 1 and stage st is refilled with slab kt + 2.
+        // (After the last slab, F0 reads a stale stage: in bounds, unused.)
+        i32x4 f0[8], f1[8];
+        read_frags(0, 0, f0);
+        auto slab = [&](int kt, auto dma) {
+            const int st = kt & 1;
+            step(f0, true, st, 1, f1, std::false_type{}, 0, 0);
+            step(f1, true, st, 2, f0, std::false_type{}, 0, 0);
+            step(f0, true, st, 3, f1, std::false_type{}, 0, 0);
+            lds_wait(f1);
+            wait_vmcnt<0>();  // slab kt+1 (the only DMA in flight) and the scales
+            __builtin_amdgcn_s_barrier();
+            step(f1, false, st ^ 1, 0, f0, dma, kt + 2, st);
+        };
+        int kt = 0;
+        for (; kt + 2 < nk; ++kt) slab(kt, std::true_type{});
+        for (; kt < nk; ++kt) slab(kt, std::false_type{});
+        lds_wait(f0);  // the last (unused) reads land before f0's registers are reused
+        wait_vmcnt<0>();  // the scales of a one-slab tile
+        // every wave is done with both stages: the next tile's first slabs
+        // may land while this tile's epilogue runs
+        __builtin_amdgcn_s_barrier();
+        const int row0 = bm + wm * 128, col0 = bn + wn * 128;
+        const int tn_ = t + gridDim.x;
+        if (tn_ < ntiles) {
+            int nbm, nbn;
+            tile_origin(tn_, nbm, nbn);
+            first_slabs(nbm, nbn);
+        }
+        k128_epilogue<OUT>(acc, lds + kK2Spare + wave * kK2Stg,
+                           scales_dma ? reinterpret_cast<const float*>(lds + kK2Scl) + wn * 128
+                                      : nullptr,
+                           e, m, n, row0, col0, lane, r32, h);
     }
 }
 
@@ -1041,7 +1458,19 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
     if ((m >= kBigT && n >= kBigT && force != 2) || force == 4) {
         const long long tiles = (long long)((m + kBigT - 1) / kBigT) * ((n + kBigT - 1) / kBigT);
         if (tiles > (1LL << 30)) inval("qgemm problem too large for one launch");
-        if (k % kBigK == 0 && env_int("FT_QGEMM_NO_DMA", 0) == 0)
+        const int big = env_int("FT_QGEMM_BIG", 0);  // 1: 64-byte slabs, 2: register-staged
+        if (k % kK2 == 0 && big == 0) {
+            // persistent: a multiple of 8 workgroups (XCD-aware order), at
+            // most one per CU
+            const long long cus = dev_info().cu_count;
+            long long grid = std::min<long long>(tiles, cus);
+            if (grid >= 8) grid -= grid % 8;
+            if (env_int("FT_QGEMM_ONE_TILE", 0)) grid = tiles;  // A/B: no persistence
+            const int scales_dma = e.sb_vec && (n % 4 == 0) &&
+                                   ((uintptr_t)e.sb_vec % 16 == 0);
+            qgemm_big_k128<OUT><<<(unsigned)grid, 256, 0, s>>>(a, b, e, m, n, k, scales_dma);
+        }
+        else if (k % kBigK == 0 && big != 2 && env_int("FT_QGEMM_NO_DMA", 0) == 0)
             qgemm_big_dma<OUT><<<(unsigned)tiles, 256, 0, s>>>(a, b, e, m, n, k);
         else
             qgemm_big<OUT><<<(unsigned)tiles, 256, 0, s>>>(a, b, e, m, n, k);

@@ -62,6 +62,8 @@ def test_quantize_known_answers_and_device_scale():
     assert s == 1.0 and (q == 0).all()
     q, s = ft.quantize_int8(t(np.array([1e30, -1e30], np.float32)))
     assert q.cpu().tolist() == [127, -127]
+    q, s = ft.quantize_int8(torch.empty(0, device=DEV))   # empty: scale 1.0
+    assert s == 1.0 and q.numel() == 0
     x = np.random.default_rng(2).standard_normal((16, 4096)).astype(np.float32)
     q, sd = ft.quantize_int8(t(x), device_scale=True)
     assert sd.is_cuda and sd.dtype == torch.float32 and sd.numel() == 1
@@ -108,7 +110,47 @@ GEMM_SHAPES = [
     (1024, 1024, 1024),    # big tiles (256 x 256)
     (257, 300, 80),        # big tiles, ragged M/N, K not a multiple of 64
     (512, 256, 1040),      # big tiles, K tail
+    (256, 256, 128),       # 128-byte-slab kernel, one slab
+    (512, 768, 256),       # 128-byte-slab kernel, two slabs (no refill)
+    (300, 520, 384),       # 128-byte-slab kernel, ragged M/N, one refill
 ]
+
+
+def test_big_persistent_tiles_bit_exact():
+    # 9 x 33 = 297 tiles of 256 x 256 > one workgroup per CU: the persistent
+    # 128-byte-slab kernel walks several tiles per workgroup, with the next
+    # tile's first slabs loading during the previous tile's epilogue. Rows
+    # from every 256-row band are checked against the oracle over all
+    # columns, so every tile is covered.
+    rng = np.random.default_rng(77)
+    m, n, k = 2304, 8448, 384
+    a, b = rand_q(rng, m, k), rand_q(rng, n, k)
+    sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    at, bt = t(a), t(b)
+    acc = ft.qgemm_i32(at, bt).cpu().numpy()
+    y = ft.qgemm_perchannel(at, 0.011, bt, t(sb), out_dtype=torch.bfloat16).cpu()
+    rows = sorted({0, 255, 2303} | {256 * bb + (bb * 37) % 256 for bb in range(9)})
+    ra = np.ascontiguousarray(a[rows])
+    np.testing.assert_array_equal(acc[rows], oracle.qgemm_i32(ra, b))
+    ref = torch.from_numpy(oracle.qgemm_perchannel(ra, 0.011, b, sb)).to(torch.bfloat16)
+    assert torch.equal(y[rows], ref)
+
+
+@pytest.mark.parametrize("big", ["0", "1", "2"])
+def test_big_kernels_bit_exact(big, monkeypatch):
+    # the three big-tile kernels on one K % 128 == 0 shape with ragged edges:
+    # 128-byte DMA slabs (default), 64-byte DMA slabs, register-staged
+    monkeypatch.setenv("FT_QGEMM_BIG", big)
+    rng = np.random.default_rng(400 + int(big))
+    m, n, k = 520, 777, 1280
+    a, b = rand_q(rng, m, k), rand_q(rng, n, k)
+    sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    acc = ft.qgemm_i32(t(a), t(b))
+    y = ft.qgemm_perchannel(t(a), 0.017, t(b), t(sb), out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(acc.cpu().numpy(), oracle.qgemm_i32(a, b))
+    ref = torch.from_numpy(oracle.qgemm_perchannel(a, 0.017, b, sb)).to(torch.bfloat16)
+    assert torch.equal(y.cpu(), ref)
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
