@@ -194,7 +194,7 @@ def bench_c5a(torch, ft, dev, steps, warmup):
                           "peak": INT8_PEAK_TOPS, "unit": "TOPS",
                           "frac": round(tops / INT8_PEAK_TOPS, 4),
                           "traffic": traffic_for("qgemm_c5a"),
-                          "kernel": "qgemm_big_dma"})
+                          "kernel": "qgemm_big_k128"})
 
 
 # ---------------------------------------------------------------------------
