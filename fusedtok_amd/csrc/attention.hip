@@ -243,7 +243,7 @@ __global__ __launch_bounds__(kGenNT) void attn_chunk_generic(
 // laid end to end, b-major then kv: row (b, kv) owns the flat positions
 // [Hkv*pref[b] + kv*len_b, + len_b) with pref the exclusive prefix of the
 // lengths. The G workgroups of the grid each take one equal contiguous
-// segment of that flat range (at least kStreamMinSeg tokens), so every
+// segment of that flat range (at least min_seg tokens), so every
 // workgroup streams the same number of K/V bytes whatever the length mix,
 // and the per-workgroup set-up is paid once per segment, not per chunk. A
 // segment crossing row ends is processed as consecutive pieces, one per row
@@ -309,7 +309,12 @@ template <> struct Mfma<f16> {
 constexpr int kMfmaDim = 128;
 constexpr int kMfmaAccPitch = kMfmaDim + 4;  // LDS row pitch (bank spread)
 constexpr int kStreamScanRows = 2048;        // sequences per launch (LDS prefix)
-constexpr long long kStreamMinSeg = 1024;    // minimum tokens per segment
+// Default minimum tokens per segment. Large decode batches are unaffected
+// (C3's segments hold ~8.9k tokens); for a small one the floor trades
+// per-segment set-up and combine work against idle CUs: 1 x 32 rows x 4096
+// tokens (fp16, HIP-graph replays) takes 24.6 us at 1024 (128 segments),
+// 20.0 us at 512, 21.3 us at 256.
+constexpr int kStreamMinSeg = 512;
 
 // Row addressing modes of attn_decode_stream.
 enum RowMode { kRowsContig = 0, kRowsPagedPow2 = 1, kRowsPagedDiv = 2 };
@@ -347,9 +352,9 @@ __device__ __forceinline__ long long uniform64(long long x) {
     return (long long)(((unsigned long long)hi << 32) | lo);
 }
 
-__device__ __forceinline__ long long stream_seg_len(long long total, int nseg) {
+__device__ __forceinline__ long long stream_seg_len(long long total, int nseg, int min_seg) {
     const long long s = (total + nseg - 1) / nseg;
-    return s < kStreamMinSeg ? kStreamMinSeg : s;
+    return s < min_seg ? (long long)min_seg : s;
 }
 
 template <typename T, int MODE>
@@ -360,7 +365,7 @@ void attn_decode_stream(
     float* __restrict__ ws_ml, float* __restrict__ ws_acc,
     long long* __restrict__ pref_out, T* __restrict__ out, int batch, int hq,
     int hkv, int group, int rows_or_page, int page_shift, int tbl_width,
-    int span, float scale_log2) {
+    int span, float scale_log2, int min_seg) {
     using M = Mfma<T>;
     using V8 = typename M::v8;
     constexpr int D = kMfmaDim;
@@ -381,7 +386,7 @@ void attn_decode_stream(
         for (int i = tid; i <= batch; i += 256) pref_out[i] = s_pref[i];
     const long long total = uniform64(s_pref[batch]) * hkv;
     const int nseg = gridDim.x;
-    const long long S = stream_seg_len(total, nseg);
+    const long long S = stream_seg_len(total, nseg, min_seg);
     const long long seg_lo = (long long)blockIdx.x * S;
     if (seg_lo >= total) return;
     const long long seg_hi = min(seg_lo + S, total);
@@ -611,7 +616,7 @@ template <typename T>
 __global__ __launch_bounds__(64) void attn_combine_stream(
     const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
     const long long* __restrict__ pref, T* __restrict__ out, int batch, int hq,
-    int hkv, int group, int nseg) {
+    int hkv, int group, int nseg, int min_seg) {
     constexpr int D = kMfmaDim;
     const int b = blockIdx.x / hq;
     const int h = blockIdx.x - b * hq;
@@ -623,7 +628,7 @@ __global__ __launch_bounds__(64) void attn_combine_stream(
         if (lane < D / 4) St<T>::st4(o + 4 * lane, make_float4(0.f, 0.f, 0.f, 0.f));
         return;
     }
-    const long long S = stream_seg_len(pref[batch] * hkv, nseg);
+    const long long S = stream_seg_len(pref[batch] * hkv, nseg, min_seg);
     const long long start = pref[b] * hkv + (long long)kv * len;
     const int s_lo = (int)(start / S), s_hi = (int)((start + len - 1) / S);
     if (s_lo == s_hi) return;  // stored whole by the decode kernel
@@ -809,6 +814,7 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
             // (the kernel's register budget allows exactly two per CU)
             int nseg = env_int("FT_ATTN_SEGS", 2 * dev_info().cu_count);
             nseg = std::max(1, std::min(nseg, 1 << 20));
+            const int min_seg = std::max(32, env_int("FT_ATTN_MIN_SEG", kStreamMinSeg));
             const size_t nslots = ((size_t)nseg + (size_t)batch * hkv) * group;
             const size_t ml_floats = (nslots * 2 + 63) & ~(size_t)63;
             const size_t acc_floats = nslots * dim;
@@ -821,18 +827,18 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
             if (paged && page_shift >= 0)
                 attn_decode_stream<T, kRowsPagedPow2><<<(unsigned)nseg, 256, 0, s>>>(
                     q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv,
-                    group, rows_or_page, page_shift, tbl_width, (int)span, scale_log2);
+                    group, rows_or_page, page_shift, tbl_width, (int)span, scale_log2, min_seg);
             else if (paged)
                 attn_decode_stream<T, kRowsPagedDiv><<<(unsigned)nseg, 256, 0, s>>>(
                     q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv,
-                    group, rows_or_page, -1, tbl_width, (int)span, scale_log2);
+                    group, rows_or_page, -1, tbl_width, (int)span, scale_log2, min_seg);
             else
                 attn_decode_stream<T, kRowsContig><<<(unsigned)nseg, 256, 0, s>>>(
                     q, k, v, nullptr, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv,
-                    group, rows_or_page, -1, 0, (int)span, scale_log2);
+                    group, rows_or_page, -1, 0, (int)span, scale_log2, min_seg);
             launch_check("attention decode kernel launch");
             attn_combine_stream<T><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
-                ws_ml, ws_acc, pref, out, batch, hq, hkv, group, nseg);
+                ws_ml, ws_acc, pref, out, batch, hq, hkv, group, nseg, min_seg);
             launch_check("attention combine kernel launch");
             return;
         }

@@ -116,12 +116,14 @@ GEMM_SHAPES = [
 ]
 
 
-def test_big_persistent_tiles_bit_exact():
+@pytest.mark.parametrize("big", ["0", "3"])
+def test_big_persistent_tiles_bit_exact(big, monkeypatch):
     # 9 x 33 = 297 tiles of 256 x 256 > one workgroup per CU: the persistent
-    # 128-byte-slab kernel walks several tiles per workgroup, with the next
-    # tile's first slabs loading during the previous tile's epilogue. Rows
-    # from every 256-row band are checked against the oracle over all
-    # columns, so every tile is covered.
+    # 128-byte-slab kernels (8 waves, default, and 4 waves) walk several tiles per
+    # workgroup, with the next tile's first slabs loading during the
+    # previous tile's epilogue. Rows from every 256-row band are checked
+    # against the oracle over all columns, so every tile is covered.
+    monkeypatch.setenv("FT_QGEMM_BIG", big)
     rng = np.random.default_rng(77)
     m, n, k = 2304, 8448, 384
     a, b = rand_q(rng, m, k), rand_q(rng, n, k)
@@ -136,10 +138,11 @@ def test_big_persistent_tiles_bit_exact():
     assert torch.equal(y[rows], ref)
 
 
-@pytest.mark.parametrize("big", ["0", "1", "2"])
+@pytest.mark.parametrize("big", ["0", "1", "2", "3"])
 def test_big_kernels_bit_exact(big, monkeypatch):
-    # the three big-tile kernels on one K % 128 == 0 shape with ragged edges:
-    # 128-byte DMA slabs (default), 64-byte DMA slabs, register-staged
+    # the four big-tile kernels on one K % 128 == 0 shape with ragged edges:
+    # 128-byte DMA slabs with 8 waves (default), 64-byte DMA slabs,
+    # register-staged, 128-byte DMA slabs with 4 waves
     monkeypatch.setenv("FT_QGEMM_BIG", big)
     rng = np.random.default_rng(400 + int(big))
     m, n, k = 520, 777, 1280
