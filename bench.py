@@ -34,7 +34,9 @@ lens[b] + 1 tokens.
               eight caches cycled in one HIP graph so the 67 MB working set
               is not served by the last-level cache) and config 5b
               (long-context paged decode, B=8 Hq=64 Hkv=8, 131072 tokens per
-              row), each as K+V+q+out bytes per call over its time.
+              row), each as K+V+q+out bytes per call over its time; and
+              the int8 storage ops dequantize_int8 / qadd_int8 over 2^28
+              elements.
   cpu_baseline = the C++ restatement of the reference's single-threaded
               attention_decode_paged_cpu / kv_append_paged_cpu (oracle/),
               on a bounded sample of the same rows, one core.
@@ -80,7 +82,8 @@ def parse():
                    help="skip the secondary W8A8 GEMM measurement")
     p.add_argument("--no-chains", action="store_true",
                    help="skip the config 2 / config 4 chain measurements")
-    p.add_argument("--only", choices=["decode", "gemm", "copy", "c1", "c2", "c4", "c5b"],
+    p.add_argument("--only", choices=["decode", "gemm", "copy", "c1", "c2", "c4", "c5b",
+                            "int8"],
                    default=None,
                    help="run one workload only (profiling runs); 'copy' is "
                         "the HBM-counter calibration: a plain 1 GiB "
@@ -400,6 +403,53 @@ def bench_c5b(torch, np, ft, dev, steps):
 
 
 # ---------------------------------------------------------------------------
+# int8 storage neighbours: dequantize_int8 and qadd_int8 (HBM-bound)
+# ---------------------------------------------------------------------------
+INT8 = dict(n=1 << 28, seed=8, steps=10)
+
+
+def bench_int8(torch, ft, dev):
+    """dequantize (n int8 -> n float32) and qadd (two n-element int8 inputs,
+    device scales, device out scale) over n = 2^28 elements. Algorithmic
+    bytes: dequantize n + 4n; qadd 2n read per pass (absmax, then quantize)
+    + n written = 5n."""
+    c = INT8
+    n = c["n"]
+    gen = torch.Generator(device=dev).manual_seed(c["seed"])
+    qa = torch.randint(-127, 128, (n,), device=dev, generator=gen,
+                       dtype=torch.int32).to(torch.int8)
+    qb = torch.randint(-127, 128, (n,), device=dev, generator=gen,
+                       dtype=torch.int32).to(torch.int8)
+    sa = torch.full((1,), 0.013, device=dev)
+    sb = torch.full((1,), 0.021, device=dev)
+    x = ft.dequantize_int8(qa, sa)          # allocate once, warm up
+    ft.qadd_int8(qa, sa, qb, sb, device_scale=True)
+    stream = torch.cuda.current_stream()
+    res = {}
+    for name, fn, nbytes in (
+            ("dequantize_int8 (f32 out)", lambda: ft.dequantize_int8(qa, sa), 5 * n),
+            ("qadd_int8 (device scales)",
+             lambda: ft.qadd_int8(qa, sa, qb, sb, device_scale=True), 5 * n)):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(c["steps"]):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / c["steps"]
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"us_per_call": round(us, 1), "GB/s": round(gbs, 1),
+                     "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                     "bytes_per_call": nbytes}
+    del qa, qb, x
+    return {"metric": "int8 storage ops GB/s", "unit": "GB/s", "dtype": "int8",
+            "config": {"workload": f"n = 2^28 elements, seed {c['seed']}"},
+            "results": res}
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline: the oracle on a bounded sample of config 3's rows
 # ---------------------------------------------------------------------------
 def cpu_baseline_c3(torch, np, w, budget_s=12.0):
@@ -487,6 +537,9 @@ def main():
     if args.only == "c5b":
         log("c5b", json.dumps(bench_c5b(torch, np, ft, dev, args.steps)))
         return
+    if args.only == "int8":
+        log("int8", json.dumps(bench_int8(torch, ft, dev)))
+        return
 
     log(f"config 3: building workload (seed {C3['seed']})")
     w, wall, attn_ms = bench_c3(torch, np, ft, dev, args.steps, args.warmup)
@@ -527,6 +580,9 @@ def main():
         torch.cuda.empty_cache()
         decode_more.append(bench_c5b(torch, np, ft, dev, max(5, args.steps // 2)))
         log(f"config 5b: {decode_more[1]['value']} GB/s")
+        torch.cuda.empty_cache()
+        decode_more.append(bench_int8(torch, ft, dev))
+        log("int8 storage:", json.dumps(decode_more[2]["results"]))
         torch.cuda.empty_cache()
 
     cpu = None

@@ -7,7 +7,8 @@ contract for the decode hot path (reference python/fusedtok/__init__.py):
   attention over contiguous / paged KV caches (f32, bf16, fp16 storage);
 - ``kv_append`` / ``kv_append_paged``: one fresh token's K/V rows per
   sequence written in place at position ``lens[b]``;
-- ``quantize_int8``: symmetric per-tensor INT8 quantize;
+- ``quantize_int8``: symmetric per-tensor INT8 quantize; ``dequantize_int8``
+  and the fused dequantize-add-requantize ``qadd_int8``;
 - ``qgemm`` / ``qgemm_perchannel``: W8A8 GEMM with exact int32 accumulation;
 - ``rmsnorm`` (+ residual), ``rope`` (interleaved / NeoX, ``pos_offset``),
   ``swiglu``.
@@ -63,6 +64,8 @@ __all__ = [
     "rope",
     "swiglu",
     "quantize_int8",
+    "dequantize_int8",
+    "qadd_int8",
     "qgemm",
     "qgemm_perchannel",
     "qgemm_i32",
@@ -717,6 +720,94 @@ def quantize_int8(x, *, device_scale=False):
     dev = _need_device()
     q, s = quantize_int8(_upload(arr, dev))
     return (q.cpu() if _is_torch(x) else q.cpu().numpy()), s
+
+
+def _dev_scale(s, name):
+    """Python float -> (float, None); 1-element GPU float32 tensor -> (0.0, ptr)."""
+    if _on_gpu(s):
+        if s.dtype is not torch.float32 or s.numel() != 1:
+            raise TypeError(f"a device {name} must be a 1-element float32 tensor")
+        return 0.0, s.data_ptr()
+    if _is_torch(s):
+        s = s.item()
+    return float(s), None
+
+
+def dequantize_int8(q, scale, *, out_dtype=None):
+    """Dequantize int8: ``x = q * scale`` in float32 (one rounding).
+
+    Takes the UNPACKED pair from :func:`quantize_int8`
+    (``dequantize_int8(*quantize_int8(x))``), as the reference
+    (``__init__.py:1428-1449``). Build additions: ``scale`` may be the
+    1-element GPU tensor of ``quantize_int8(..., device_scale=True)``, and
+    ``out_dtype`` bf16 / fp16 stores the float32 value rounded to
+    nearest-even (GPU path).
+    """
+    if _on_gpu(q):
+        if q.dtype is not torch.int8:
+            raise TypeError(f"q must be int8, got {q.dtype}")
+        _check_contiguous(q, "q")
+        odt = torch.float32 if out_dtype is None else out_dtype
+        if odt not in _DT_CODE:
+            raise TypeError("out_dtype must be float32, bfloat16 or float16")
+        sc, sc_ptr = _dev_scale(scale, "scale")
+        x = torch.empty(q.shape, dtype=odt, device=q.device)
+        if q.numel():
+            if odt is torch.float32 and sc_ptr is None:
+                _fusedtok.dequantize_launch(q.data_ptr(), x.data_ptr(), sc, q.numel(),
+                                            _stream())
+            else:
+                _fusedtok.dequantize_launch_ex(q.data_ptr(), sc, sc_ptr, x.data_ptr(),
+                                               _DT_CODE[odt], q.numel(), _stream())
+        return x
+    if _is_torch(q):
+        if q.dtype is not torch.int8:
+            raise TypeError(f"q must be int8, got {q.dtype}")
+        arr = q.detach().numpy()
+    else:
+        arr = np.asarray(q)
+        if arr.size and not np.issubdtype(arr.dtype, np.integer):
+            raise TypeError(f"q must be int8, got {arr.dtype}")
+    dev = _need_device()
+    x = dequantize_int8(_upload(np.ascontiguousarray(arr, dtype=np.int8), dev),
+                        float(scale))
+    return _result(x, q)
+
+
+def qadd_int8(qa, sa, qb, sb, *, device_scale=False):
+    """Fused dequantize-add-requantize of two int8 tensors:
+    ``v = f32(qa * sa) + f32(qb * sb)``, requantized with v's own per-tensor
+    scale. Returns ``(qy, out_scale)``, equal bit for bit to
+    ``quantize_int8(dequantize_int8(qa, sa) + dequantize_int8(qb, sb))``.
+    GPU int8 tensors only (TypeError otherwise, as the reference's
+    ``__init__.py:1452-1473``). Build additions: ``sa`` / ``sb`` may be
+    1-element GPU float32 tensors, and ``device_scale=True`` returns
+    out_scale as one without synchronising the stream.
+    """
+    if not (_on_gpu(qa) and _on_gpu(qb)):
+        raise TypeError("qadd_int8 needs GPU int8 tensors")
+    if qa.dtype is not torch.int8 or qb.dtype is not torch.int8:
+        raise TypeError("inputs must be int8")
+    _check_contiguous(qa, "qa")
+    _check_contiguous(qb, "qb")
+    if qa.shape != qb.shape:
+        raise ValueError("inputs must have the same shape")
+    fa, pa = _dev_scale(sa, "sa")
+    fb, pb = _dev_scale(sb, "sb")
+    qy = torch.empty(qa.shape, dtype=torch.int8, device=qa.device)
+    out_scale = torch.empty(1, dtype=torch.float32, device=qa.device)
+    n = qa.numel()
+    if n == 0:
+        out_scale.fill_(1.0)   # no values: the all-zero scale
+    elif pa is None and pb is None:
+        _fusedtok.qadd_launch(qa.data_ptr(), qb.data_ptr(), fa, fb, qy.data_ptr(),
+                              out_scale.data_ptr(), n, _stream())
+    else:
+        _fusedtok.qadd_launch_ex(qa.data_ptr(), qb.data_ptr(), fa, fb, pa, pb,
+                                 qy.data_ptr(), out_scale.data_ptr(), n, _stream())
+    if device_scale:
+        return qy, out_scale
+    return qy, float(out_scale)
 
 
 # ---------------------------------------------------------------------------

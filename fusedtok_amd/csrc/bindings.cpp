@@ -140,6 +140,43 @@ PYBIND11_MODULE(_fusedtok, m) {
           },
           py::arg("x"), py::arg("dtype"), py::arg("q"), py::arg("scale"),
           py::arg("n"), py::arg("stream") = 0);
+    m.def("dequantize_launch",
+          [](uintptr_t q, uintptr_t x, float scale, long long n, uintptr_t stream) {
+              check(ft_dequantize_int8_launch(P<const signed char>(q), P<float>(x),
+                                              scale, n, stream));
+          },
+          py::arg("q"), py::arg("x"), py::arg("scale"), py::arg("n"),
+          py::arg("stream") = 0);
+    m.def("dequantize_launch_ex",
+          [](uintptr_t q, float scale, py::object scale_dev, uintptr_t x, int dtype,
+             long long n, uintptr_t stream) {
+              check(ft_dequantize_int8_launch_ex(P<const signed char>(q), scale,
+                                                 P<const float>(opt_ptr(scale_dev)),
+                                                 P<void>(x), dtype, n, stream));
+          },
+          py::arg("q"), py::arg("scale"), py::arg("scale_dev"), py::arg("x"),
+          py::arg("dtype"), py::arg("n"), py::arg("stream") = 0);
+    m.def("qadd_launch",
+          [](uintptr_t qa, uintptr_t qb, float sa, float sb, uintptr_t qy,
+             uintptr_t out_scale, long long n, uintptr_t stream) {
+              check(ft_qadd_int8_launch(P<const signed char>(qa), P<const signed char>(qb),
+                                        sa, sb, P<signed char>(qy), P<float>(out_scale),
+                                        n, stream));
+          },
+          py::arg("qa"), py::arg("qb"), py::arg("sa"), py::arg("sb"), py::arg("qy"),
+          py::arg("out_scale"), py::arg("n"), py::arg("stream") = 0);
+    m.def("qadd_launch_ex",
+          [](uintptr_t qa, uintptr_t qb, float sa, float sb, py::object sa_dev,
+             py::object sb_dev, uintptr_t qy, uintptr_t out_scale, long long n,
+             uintptr_t stream) {
+              check(ft_qadd_int8_launch_ex(
+                  P<const signed char>(qa), P<const signed char>(qb), sa, sb,
+                  P<const float>(opt_ptr(sa_dev)), P<const float>(opt_ptr(sb_dev)),
+                  P<signed char>(qy), P<float>(out_scale), n, stream));
+          },
+          py::arg("qa"), py::arg("qb"), py::arg("sa"), py::arg("sb"),
+          py::arg("sa_dev"), py::arg("sb_dev"), py::arg("qy"), py::arg("out_scale"),
+          py::arg("n"), py::arg("stream") = 0);
 
     // ---- qgemm --------------------------------------------------------------
     m.def("qgemm_launch",

@@ -15,6 +15,9 @@
 //                  (identical result everywhere), quantize its share, and
 //                  workgroup 0 store the scale.
 // No memset, no atomics, no host sync: stream-ordered and capturable.
+//
+// Also here: dequantize (q * scale) and the fused dequantize-add-requantize
+// qadd, with the same device-resident-scale structure.
 #include "ft_common.hpp"
 
 namespace ft {
@@ -154,10 +157,256 @@ void quantize_run(const T* x, signed char* q, float* scale_out, long long n,
     launch_check("quantize kernel launch");
 }
 
+// ---------------------------------------------------------------------------
+// dequantize: x = (float)q * scale (reference quantize.cu:101-108), one
+// rounding; 2-byte outputs are that f32 value rounded to nearest-even.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float dq1(signed char q, float sc) {
+    float v = (float)q * sc;
+    asm("" : "+v"(v));  // rounded to f32 before any narrowing (no mixed FMA)
+    return v;
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void dequantize_kernel(
+    const signed char* __restrict__ q, T* __restrict__ x, float scale,
+    const float* __restrict__ scale_dev, long long n) {
+    const float sc = scale_dev ? *scale_dev : scale;
+    const long long stride = (long long)gridDim.x * 256;
+    const long long tid = (long long)blockIdx.x * 256 + threadIdx.x;
+    long long done = 0;
+    if (VEC) {
+        const long long n4 = n >> 2;
+        for (long long c = tid; c < n4; c += stride) {
+            const char4 v = *reinterpret_cast<const char4*>(q + 4 * c);
+            St<T>::st4(x + 4 * c, make_float4(dq1(v.x, sc), dq1(v.y, sc),
+                                              dq1(v.z, sc), dq1(v.w, sc)));
+        }
+        done = n4 << 2;
+    }
+    for (long long i = done + tid; i < n; i += stride) St<T>::st(x + i, dq1(q[i], sc));
+}
+
+template <typename T>
+void dequantize_run(const signed char* q, T* x, float scale, const float* scale_dev,
+                    long long n, hipStream_t s) {
+    if (n < 0) inval("n must be >= 0");
+    if (n == 0) return;
+    if (!q || !x) inval("dequantize: null operand");
+    const unsigned grid = grid_1d((n + 3) / 4, 256, dev_info().cu_count * 8);
+    if ((uintptr_t)q % 4 == 0 && (uintptr_t)x % (4 * sizeof(T)) == 0)
+        dequantize_kernel<T, true><<<grid, 256, 0, s>>>(q, x, scale, scale_dev, n);
+    else
+        dequantize_kernel<T, false><<<grid, 256, 0, s>>>(q, x, scale, scale_dev, n);
+    launch_check("dequantize kernel launch");
+}
+
+// ---------------------------------------------------------------------------
+// qadd: y = requantize(fl(qa*sa) + fl(qb*sb)) with the sum's own per-tensor
+// scale (reference quantize.cu:110-138,217-246): the dequantize -> add ->
+// quantize_int8 chain in one pass per phase. Each product is rounded to f32
+// on its own (the empty asm keeps the backend from contracting one product
+// and the sum into an FMA), so the codes and scale equal
+// quantize_int8(dequantize(qa, sa) + dequantize(qb, sb)) bit for bit.
+// Same two-phase structure as quantize: one workgroup for small n, else
+// per-workgroup maxima in scratch folded by every quantizing workgroup.
+// ---------------------------------------------------------------------------
+struct QaddSrc {
+    const signed char* qa;
+    const signed char* qb;
+    float sa, sb;
+    __device__ __forceinline__ float one(signed char a, signed char b) const {
+        float pa = (float)a * sa;
+        asm("" : "+v"(pa));
+        float pb = (float)b * sb;
+        asm("" : "+v"(pb));
+        return pa + pb;
+    }
+    __device__ __forceinline__ float val(long long i) const { return one(qa[i], qb[i]); }
+    // the 16 values of 16-byte chunk c (VEC paths: both inputs 16-byte aligned)
+    __device__ __forceinline__ void chunk(long long c, float (&v)[16]) const {
+        const int4 a4 = *reinterpret_cast<const int4*>(qa + 16 * c);
+        const int4 b4 = *reinterpret_cast<const int4*>(qb + 16 * c);
+        const signed char* a = reinterpret_cast<const signed char*>(&a4);
+        const signed char* b = reinterpret_cast<const signed char*>(&b4);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = one(a[j], b[j]);
+    }
+};
+
+__device__ __forceinline__ QaddSrc qadd_src(const signed char* qa, const signed char* qb,
+                                            float sa, float sb, const float* sa_dev,
+                                            const float* sb_dev) {
+    return QaddSrc{qa, qb, sa_dev ? *sa_dev : sa, sb_dev ? *sb_dev : sb};
+}
+
+// max |v| over the elements a thread owns: 16-byte chunks tid, tid + stride,
+// ... (VEC), then single elements of the tail (or of everything)
+template <bool VEC>
+__device__ __forceinline__ float qadd_local_max(const QaddSrc& src, long long n,
+                                                long long tid, long long stride) {
+    float m = 0.0f;
+    long long done = 0;
+    if (VEC) {
+        const long long nc = n >> 4;
+        for (long long c = tid; c < nc; c += stride) {
+            float v[16];
+            src.chunk(c, v);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(v[j]));
+        }
+        done = nc << 4;
+    }
+    for (long long i = done + tid; i < n; i += stride) m = fmaxf(m, fabsf(src.val(i)));
+    return m;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void qadd_quant_range(const QaddSrc& src, signed char* qy,
+                                                 long long n, float inv, long long tid,
+                                                 long long stride) {
+    long long done = 0;
+    if (VEC) {
+        const long long nc = n >> 4;
+        for (long long c = tid; c < nc; c += stride) {
+            float v[16];
+            src.chunk(c, v);
+            int4 o;
+            signed char* ob = reinterpret_cast<signed char*>(&o);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) ob[j] = quant1(v[j], inv);
+            *reinterpret_cast<int4*>(qy + 16 * c) = o;
+        }
+        done = nc << 4;
+    }
+    for (long long i = done + tid; i < n; i += stride) qy[i] = quant1(src.val(i), inv);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(1024) void qadd_small_kernel(
+    const signed char* __restrict__ qa, const signed char* __restrict__ qb, float sa,
+    float sb, const float* __restrict__ sa_dev, const float* __restrict__ sb_dev,
+    signed char* __restrict__ qy, float* __restrict__ scale_out, long long n) {
+    __shared__ float red[16];
+    const QaddSrc src = qadd_src(qa, qb, sa, sb, sa_dev, sb_dev);
+    const float m = block_max<1024>(qadd_local_max<VEC>(src, n, threadIdx.x, 1024), red);
+    const float scale = make_scale(m);
+    const float inv = 1.0f / scale;
+    if (threadIdx.x == 0) *scale_out = scale;
+    qadd_quant_range<VEC>(src, qy, n, inv, threadIdx.x, 1024);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void qadd_absmax_kernel(
+    const signed char* __restrict__ qa, const signed char* __restrict__ qb, float sa,
+    float sb, const float* __restrict__ sa_dev, const float* __restrict__ sb_dev,
+    float* __restrict__ partial, long long n) {
+    __shared__ float red[4];
+    const QaddSrc src = qadd_src(qa, qb, sa, sb, sa_dev, sb_dev);
+    const float m = block_max<256>(
+        qadd_local_max<VEC>(src, n, (long long)blockIdx.x * 256 + threadIdx.x,
+                            (long long)gridDim.x * 256), red);
+    if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void qadd_fold_kernel(
+    const signed char* __restrict__ qa, const signed char* __restrict__ qb, float sa,
+    float sb, const float* __restrict__ sa_dev, const float* __restrict__ sb_dev,
+    const float* __restrict__ partial, int nparts, signed char* __restrict__ qy,
+    float* __restrict__ scale_out, long long n) {
+    __shared__ float red[4];
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < nparts; i += 256) m = fmaxf(m, partial[i]);
+    m = block_max<256>(m, red);
+    const float scale = make_scale(m);
+    const float inv = 1.0f / scale;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+    const QaddSrc src = qadd_src(qa, qb, sa, sb, sa_dev, sb_dev);
+    qadd_quant_range<VEC>(src, qy, n, inv, (long long)blockIdx.x * 256 + threadIdx.x,
+                          (long long)gridDim.x * 256);
+}
+
+template <bool VEC>
+void qadd_launch(const signed char* qa, const signed char* qb, float sa, float sb,
+                 const float* sa_dev, const float* sb_dev, signed char* qy,
+                 float* scale_out, long long n, hipStream_t s) {
+    if (n <= kSmallN) {
+        qadd_small_kernel<VEC><<<1, 1024, 0, s>>>(qa, qb, sa, sb, sa_dev, sb_dev, qy,
+                                                  scale_out, n);
+        launch_check("qadd kernel launch");
+        return;
+    }
+    float* partial =
+        (float*)scratch(Scratch::QuantMax, kPass1Blocks * sizeof(float), s);
+    const long long units = VEC ? (n + 15) / 16 : n;
+    const int g1 = (int)grid_1d(units, 256, kPass1Blocks);
+    const unsigned g2 = grid_1d(units, 256, dev_info().cu_count * 8);
+    qadd_absmax_kernel<VEC><<<g1, 256, 0, s>>>(qa, qb, sa, sb, sa_dev, sb_dev, partial, n);
+    launch_check("qadd absmax kernel launch");
+    qadd_fold_kernel<VEC><<<g2, 256, 0, s>>>(qa, qb, sa, sb, sa_dev, sb_dev, partial, g1,
+                                             qy, scale_out, n);
+    launch_check("qadd kernel launch");
+}
+
+void qadd_run(const signed char* qa, const signed char* qb, float sa, float sb,
+              const float* sa_dev, const float* sb_dev, signed char* qy,
+              float* scale_out, long long n, hipStream_t s) {
+    if (n < 0) inval("n must be >= 0");
+    if (n == 0) return;
+    if (!qa || !qb || !qy || !scale_out) inval("qadd: null operand");
+    const bool vec = ((uintptr_t)qa % 16 == 0) && ((uintptr_t)qb % 16 == 0) &&
+                     ((uintptr_t)qy % 16 == 0);
+    if (vec)
+        qadd_launch<true>(qa, qb, sa, sb, sa_dev, sb_dev, qy, scale_out, n, s);
+    else
+        qadd_launch<false>(qa, qb, sa, sb, sa_dev, sb_dev, qy, scale_out, n, s);
+}
+
 }  // namespace
 }  // namespace ft
 
 extern "C" {
+
+int ft_dequantize_int8_launch(const signed char* q, float* x, float scale,
+                              long long n, uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::dequantize_run<float>(q, x, scale, nullptr, n, ft::as_stream(stream));
+    });
+}
+
+int ft_dequantize_int8_launch_ex(const signed char* q, float scale,
+                                 const float* scale_dev, void* x, int x_dtype,
+                                 long long n, uintptr_t stream) {
+    return ft::guarded([&] {
+        hipStream_t s = ft::as_stream(stream);
+        switch (x_dtype) {
+        case FT_DT_F32: ft::dequantize_run<float>(q, (float*)x, scale, scale_dev, n, s); break;
+        case FT_DT_BF16: ft::dequantize_run<ft::bf16>(q, (ft::bf16*)x, scale, scale_dev, n, s); break;
+        case FT_DT_F16: ft::dequantize_run<ft::f16>(q, (ft::f16*)x, scale, scale_dev, n, s); break;
+        default: ft::inval("dequantize: unknown dtype code");
+        }
+    });
+}
+
+int ft_qadd_int8_launch(const signed char* qa, const signed char* qb, float sa,
+                        float sb, signed char* qy, float* out_scale, long long n,
+                        uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::qadd_run(qa, qb, sa, sb, nullptr, nullptr, qy, out_scale, n,
+                     ft::as_stream(stream));
+    });
+}
+
+int ft_qadd_int8_launch_ex(const signed char* qa, const signed char* qb, float sa,
+                           float sb, const float* sa_dev, const float* sb_dev,
+                           signed char* qy, float* out_scale, long long n,
+                           uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::qadd_run(qa, qb, sa, sb, sa_dev, sb_dev, qy, out_scale, n,
+                     ft::as_stream(stream));
+    });
+}
 
 int ft_quantize_int8_launch(const float* x, signed char* q, float* scale_out,
                             long long n, uintptr_t stream) {

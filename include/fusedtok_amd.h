@@ -163,6 +163,39 @@ int ft_quantize_int8_launch_ex(const void* x, int x_dtype, signed char* q,
                                uintptr_t stream);
 
 /* ------------------------------------------------------------------ */
+/* INT8 dequantize: x[i] = (float)q[i] * scale (one f32 rounding).     */
+/* Replaces dequantize_int8_launch (cuda_launch.hpp:194-195;           */
+/* quantize.cu:101-108,188-193).                                       */
+/* ------------------------------------------------------------------ */
+int ft_dequantize_int8_launch(const signed char* q, float* x, float scale,
+                              long long n, uintptr_t stream);
+/* Build addition: scale_dev (a DEVICE float, e.g. a quantize scale_out)
+ * overrides scale when non-NULL; x_dtype FT_DT_BF16 / FT_DT_F16 store the
+ * f32 value rounded to nearest-even. */
+int ft_dequantize_int8_launch_ex(const signed char* q, float scale,
+                                 const float* scale_dev, void* x, int x_dtype,
+                                 long long n, uintptr_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Fused dequantize-add-requantize:                                    */
+/*   v = f32(qa*sa) + f32(qb*sb) (each product rounded on its own);    */
+/*   out_scale = max|v|/127 (1.0 if all zero), a DEVICE float;         */
+/*   qy = clamp(rint(v * (1.0f/out_scale)), -127, 127).                */
+/* Equals quantize_int8(dequantize(qa,sa) + dequantize(qb,sb)) bit for */
+/* bit. Replaces qadd_int8_launch (cuda_launch.hpp:198-200;            */
+/* quantize.cu:110-138,217-246) without its host readback.             */
+/* ------------------------------------------------------------------ */
+int ft_qadd_int8_launch(const signed char* qa, const signed char* qb, float sa,
+                        float sb, signed char* qy, float* out_scale, long long n,
+                        uintptr_t stream);
+/* Build addition: DEVICE input scales (sa_dev / sb_dev override sa / sb
+ * when non-NULL), e.g. the scale_out of an earlier quantize. */
+int ft_qadd_int8_launch_ex(const signed char* qa, const signed char* qb, float sa,
+                           float sb, const float* sa_dev, const float* sb_dev,
+                           signed char* qy, float* out_scale, long long n,
+                           uintptr_t stream);
+
+/* ------------------------------------------------------------------ */
 /* W8A8 GEMM: y[M,N] = float(int32(A_q[M,K] . B_q[N,K]^T)) * scale     */
 /* Replaces qgemm_launch (cuda_launch.hpp:202-204; qgemm.cu:659-703)   */
 /* and qgemm_perchannel_launch (cuda_launch.hpp:211-214;               */

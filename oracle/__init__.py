@@ -122,6 +122,27 @@ def quantize_int8(x):
     return q, float(s.value)
 
 
+def dequantize_int8(q, scale):
+    """dequantize_int8_cpu -> float32 q * scale."""
+    q = np.ascontiguousarray(q, np.int8)
+    x = np.empty(q.shape, np.float32)
+    _call("or_dequantize_int8", _p(q), ctypes.c_longlong(q.size),
+          ctypes.c_float(scale), _p(x))
+    return x
+
+
+def qadd_int8(qa, sa, qb, sb):
+    """quantize_int8(f32(qa*sa) + f32(qb*sb)) -> (q int8, scale float)."""
+    qa = np.ascontiguousarray(qa, np.int8)
+    qb = np.ascontiguousarray(qb, np.int8)
+    assert qa.shape == qb.shape
+    q = np.empty(qa.shape, np.int8)
+    s = ctypes.c_float(0.0)
+    _call("or_qadd_int8", _p(qa), _p(qb), ctypes.c_longlong(qa.size),
+          ctypes.c_float(sa), ctypes.c_float(sb), _p(q), ctypes.byref(s))
+    return q, float(s.value)
+
+
 def qgemm_i32(a, b):
     """Exact int32 accumulators A_q . B_q^T."""
     a = np.ascontiguousarray(a, np.int8)

@@ -234,6 +234,32 @@ int or_quantize_int8(const float* x, long long n, signed char* q, float* scale_o
 }
 
 // ---------------------------------------------------------------------------
+// dequantize_int8_cpu (reference quantize.cu:188-193): x = (float)q * scale.
+// ---------------------------------------------------------------------------
+int or_dequantize_int8(const signed char* q, long long n, float scale, float* x) {
+    return run([&] {
+        for (long long i = 0; i < n; ++i) x[i] = (float)q[i] * scale;
+    });
+}
+
+// ---------------------------------------------------------------------------
+// qadd_int8 (reference quantize.cu:110-138,217-246; its only CPU statement is
+// the explicit pipeline its test compares against, test_quantize.py:48-66):
+// v = f32(qa*sa) + f32(qb*sb) (each product rounded, then the sum; no FMA
+// contraction in this build of the oracle), then quantize_int8 of v.
+// ---------------------------------------------------------------------------
+int or_qadd_int8(const signed char* qa, const signed char* qb, long long n, float sa,
+                 float sb, signed char* qy, float* scale_out) {
+    std::vector<float> v((size_t)n);
+    for (long long i = 0; i < n; ++i) {
+        const float pa = (float)qa[i] * sa;
+        const float pb = (float)qb[i] * sb;
+        v[(size_t)i] = pa + pb;
+    }
+    return or_quantize_int8(v.data(), n, qy, scale_out);
+}
+
+// ---------------------------------------------------------------------------
 // qgemm_cpu / qgemm_perchannel_cpu (reference qgemm.cu:612-652): exact int32
 // dot products, then (float)acc * f32(sa*sb) or (float)acc * f32(sa*sb[j]).
 // ---------------------------------------------------------------------------

@@ -38,7 +38,8 @@ def test_header_declares_the_hot_path():
                  "ft_kv_append_paged_launch", "ft_kv_append_launch_fp16",
                  "ft_quantize_int8_launch", "ft_qgemm_launch",
                  "ft_qgemm_perchannel_launch", "ft_rmsnorm_launch_bf16",
-                 "ft_rope_neox_launch", "ft_swiglu_launch_bf16"]:
+                 "ft_rope_neox_launch", "ft_swiglu_launch_bf16",
+                 "ft_dequantize_int8_launch", "ft_qadd_int8_launch"]:
         assert name in syms
     assert len(syms) >= 30
 
@@ -109,6 +110,25 @@ def test_qgemm_invalid_arguments(lib):
                   ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                   ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_size_t]
     assert h(None, None, None, 1.0, 1.0, None, None, 7, 4, 4, 4, 0) == FT_EINVAL
+
+
+def test_dequantize_qadd_invalid_arguments(lib):
+    d = lib.ft_dequantize_int8_launch
+    d.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_longlong,
+                  ctypes.c_size_t]
+    assert d(None, None, 1.0, -1, 0) == FT_EINVAL
+    assert d(None, None, 1.0, 8, 0) == FT_EINVAL and b"null" in lib.ft_last_error()
+    assert d(None, None, 1.0, 0, 0) == FT_OK                      # empty
+    dx = lib.ft_dequantize_int8_launch_ex
+    dx.argtypes = [ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p,
+                   ctypes.c_int, ctypes.c_longlong, ctypes.c_size_t]
+    assert dx(None, 1.0, None, None, 9, 8, 0) == FT_EINVAL       # dtype code
+    q = lib.ft_qadd_int8_launch
+    q.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_float,
+                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_size_t]
+    assert q(None, None, 1.0, 1.0, None, None, -2, 0) == FT_EINVAL
+    assert q(None, None, 1.0, 1.0, None, None, 16, 0) == FT_EINVAL
+    assert q(None, None, 1.0, 1.0, None, None, 0, 0) == FT_OK
 
 
 def test_norm_rope_swiglu_invalid_arguments(lib):

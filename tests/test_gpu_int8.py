@@ -72,6 +72,81 @@ def test_quantize_known_answers_and_device_scale():
     np.testing.assert_array_equal(q.cpu().numpy(), rq)
 
 
+@pytest.mark.parametrize("n", [1, 3, 4096, 65536, 65537, 1 << 20])
+def test_dequantize_bit_exact(n):
+    rng = np.random.default_rng(n + 5)
+    q = rand_q(rng, 1, n).reshape(n)
+    x = ft.dequantize_int8(t(q), 0.0173)
+    assert x.dtype == torch.float32
+    np.testing.assert_array_equal(x.cpu().numpy(), oracle.dequantize_int8(q, 0.0173))
+    # bf16 / fp16 out: the float32 value rounded once; device scale operand
+    sd = t(np.array([0.0173], np.float32))
+    ref = torch.from_numpy(oracle.dequantize_int8(q, 0.0173))
+    for dt in (torch.bfloat16, torch.float16):
+        y = ft.dequantize_int8(t(q), sd, out_dtype=dt)
+        assert torch.equal(y.cpu(), ref.to(dt))
+
+
+def test_dequantize_roundtrip_views_and_staged():
+    # test_quantize.py:25-31 on the GPU, an odd-offset int8 view (scalar
+    # path), and host input staged through the device
+    x = np.random.default_rng(0).standard_normal(10001).astype(np.float32)
+    q, s = ft.quantize_int8(t(x))
+    back = ft.dequantize_int8(q, s).cpu().numpy()
+    assert np.abs(back - x).max() <= s * 0.51
+    v = ft.dequantize_int8(q[1:], s).cpu().numpy()
+    np.testing.assert_array_equal(v, oracle.dequantize_int8(q[1:].cpu().numpy(), s))
+    qh = q.cpu().numpy()
+    np.testing.assert_array_equal(ft.dequantize_int8(qh, s), oracle.dequantize_int8(qh, s))
+    with pytest.raises(TypeError):
+        ft.dequantize_int8(t(x), s)                      # float "codes"
+
+
+@pytest.mark.parametrize("n", [1, 1000, 65536, 65537, 3_000_001])
+def test_qadd_bit_exact(n):
+    rng = np.random.default_rng(n + 9)
+    a = rng.standard_normal(n).astype(np.float32)
+    b = (rng.standard_normal(n) * 4).astype(np.float32)
+    qa, sa = oracle.quantize_int8(a)
+    qb, sb = oracle.quantize_int8(b)
+    qy, sy = ft.qadd_int8(t(qa), sa, t(qb), sb)
+    rq, rs = oracle.qadd_int8(qa, sa, qb, sb)
+    assert isinstance(sy, float) and sy == rs
+    np.testing.assert_array_equal(qy.cpu().numpy(), rq)
+
+
+def test_qadd_device_scales_chain_and_contract():
+    # quantize (device scale) -> qadd with device scales -> device out scale:
+    # no host sync, same bits as the host-scale call
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((64, 4096)).astype(np.float32)
+    b = rng.standard_normal((64, 4096)).astype(np.float32)
+    qa, sa_d = ft.quantize_int8(t(a), device_scale=True)
+    qb, sb_d = ft.quantize_int8(t(b), device_scale=True)
+    qy, sy_d = ft.qadd_int8(qa, sa_d, qb, sb_d, device_scale=True)
+    assert sy_d.is_cuda and sy_d.numel() == 1
+    rq, rs = oracle.qadd_int8(qa.cpu().numpy(), float(sa_d), qb.cpu().numpy(), float(sb_d))
+    assert float(sy_d) == rs
+    np.testing.assert_array_equal(qy.cpu().numpy(), rq)
+    # 1-byte-offset views (scalar path), both sizes of the two-phase split
+    for n in (1000, 70001):
+        qa1 = qa.reshape(-1)[1:n + 1]
+        qb1 = qb.reshape(-1)[1:n + 1]
+        qy1, sy1 = ft.qadd_int8(qa1, 0.02, qb1, 0.03)
+        rq1, rs1 = oracle.qadd_int8(qa1.cpu().numpy(), 0.02, qb1.cpu().numpy(), 0.03)
+        assert sy1 == rs1
+        np.testing.assert_array_equal(qy1.cpu().numpy(), rq1)
+    # reference contract: GPU int8 only, equal shapes; empty -> scale 1.0
+    with pytest.raises(TypeError):
+        ft.qadd_int8(np.ones(4, np.int8), 1.0, np.ones(4, np.int8), 1.0)
+    with pytest.raises(TypeError):
+        ft.qadd_int8(t(a), 1.0, t(b), 1.0)
+    with pytest.raises(ValueError):
+        ft.qadd_int8(qa, 1.0, qb[:3], 1.0)
+    q0, s0 = ft.qadd_int8(qa[:0], 1.0, qb[:0], 1.0)
+    assert s0 == 1.0 and q0.numel() == 0
+
+
 def test_quantize_misaligned_view_and_staged():
     x = np.random.default_rng(3).standard_normal(1001).astype(np.float32)
     xt = t(x)

@@ -60,6 +60,53 @@ def test_quantize_half_even_ties():
     assert list(q) == [127, 0, 2, 2, 0, -2, 4]
 
 
+def test_dequantize_closed_form_and_roundtrip():
+    # dequantize_int8_cpu is q * scale in float32 (quantize.cu:188-193); the
+    # reference's round-trip bound test_quantize.py:25-31 goes through it
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal(10000).astype(np.float32)
+    q, s = oracle.quantize_int8(x)
+    back = oracle.dequantize_int8(q, s)
+    assert back.dtype == np.float32
+    assert np.abs(back - x).max() <= s * 0.51
+    np.testing.assert_array_equal(back, q.astype(np.float32) * np.float32(s))
+    # every code, an awkward scale: exact float32 products
+    codes = np.arange(-128, 128, dtype=np.int8)
+    sc = np.float32(0.0123456)
+    np.testing.assert_array_equal(oracle.dequantize_int8(codes, float(sc)),
+                                  codes.astype(np.float64).astype(np.float32) * sc)
+
+
+def test_qadd_is_the_explicit_pipeline():
+    # test_quantize.py:48-66: qadd equals dequant -> add -> requant; here the
+    # pipeline is evaluated independently in numpy float32 (two rounded
+    # products, a rounded sum) and quantized by the numpy closed form
+    rng = np.random.default_rng(1)
+    for n in (1, 7, 1000, 65537):
+        a = rng.standard_normal(n).astype(np.float32)
+        b = (rng.standard_normal(n) * 3).astype(np.float32)
+        qa, sa = oracle.quantize_int8(a)
+        qb, sb = oracle.quantize_int8(b)
+        v = (qa.astype(np.float32) * np.float32(sa)) + (qb.astype(np.float32) * np.float32(sb))
+        rq, rs = refs.ref_quantize(v)
+        q, s = oracle.qadd_int8(qa, sa, qb, sb)
+        assert s == rs
+        np.testing.assert_array_equal(q, rq)
+        # the reference test's tolerance statement holds too
+        assert np.abs(q.astype(np.float32) * s - v).max() <= s * 0.51
+
+
+def test_qadd_cancellation_and_zero():
+    # qa*sa + qb*sb == 0 everywhere: scale 1.0, all codes 0 (make_scale)
+    qa = np.array([5, -7, 0, 127], np.int8)
+    q, s = oracle.qadd_int8(qa, 0.5, -qa, 0.5)
+    assert s == 1.0 and (q == 0).all()
+    # one dominant element maps to +-127; the sum saturates nothing else
+    q, s = oracle.qadd_int8(np.array([127, 1], np.int8), 1.0,
+                            np.array([127, -1], np.int8), 1.0)
+    assert s == pytest.approx(254.0 / 127.0) and list(q) == [127, 0]
+
+
 # ---------------------------------------------------------------------------
 # qgemm (reference tests/test_qgemm.py, test_qgemm_perchannel.py)
 # ---------------------------------------------------------------------------
