@@ -30,13 +30,15 @@ lens[b] + 1 tokens.
               a decode loop without per-call Python cost); weights are
               cycled over enough copies to exceed the 256 MB last-level
               cache, as a model's successive layers would.
-  decode_more = BASELINE config 1 (contiguous fp16 decode, B=1 H=32 T=4096,
+  more      = BASELINE config 1 (contiguous fp16 decode, B=1 H=32 T=4096,
               eight caches cycled in one HIP graph so the 67 MB working set
               is not served by the last-level cache) and config 5b
               (long-context paged decode, B=8 Hq=64 Hkv=8, 131072 tokens per
               row), each as K+V+q+out bytes per call over its time; and
               the int8 storage ops dequantize_int8 / qadd_int8 over 2^28
-              elements.
+              elements; and attention_prefill (bf16, 32 / 8 heads, D=128,
+              S=4096, causal and bidirectional) in TFLOP/s against the
+              2.5 PFLOP/s dense bf16 MFMA peak.
   cpu_baseline = the C++ restatement of the reference's single-threaded
               attention_decode_paged_cpu / kv_append_paged_cpu (oracle/),
               on a bounded sample of the same rows, one core.
@@ -83,7 +85,7 @@ def parse():
     p.add_argument("--no-chains", action="store_true",
                    help="skip the config 2 / config 4 chain measurements")
     p.add_argument("--only", choices=["decode", "gemm", "copy", "c1", "c2", "c4", "c5b",
-                            "int8"],
+                            "int8", "prefill"],
                    default=None,
                    help="run one workload only (profiling runs); 'copy' is "
                         "the HBM-counter calibration: a plain 1 GiB "
@@ -450,6 +452,53 @@ def bench_int8(torch, ft, dev):
 
 
 # ---------------------------------------------------------------------------
+# prefill attention (the step before decode)
+# ---------------------------------------------------------------------------
+PREFILL = dict(batch=1, hq=32, hkv=8, seq=4096, dim=128, seed=12, steps=10)
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def bench_prefill(torch, ft, dev):
+    """attention_prefill, bf16, Llama-3-8B heads (32 q / 8 kv, D=128) over a
+    4096-token prompt, causal and bidirectional. FLOPs: 4·S_eff·D per
+    (query row, head) with S_eff the keys it attends to (QK^T and PV, 2
+    flops per multiply-add): causal sum_i (i+1) = S(S+1)/2 keys per head."""
+    c = PREFILL
+    gen = torch.Generator(device=dev).manual_seed(c["seed"])
+    b, hq, hkv, s, d = c["batch"], c["hq"], c["hkv"], c["seq"], c["dim"]
+    bf = torch.bfloat16
+    q = torch.randn((b, hq, s, d), device=dev, generator=gen).to(bf)
+    k = torch.randn((b, hkv, s, d), device=dev, generator=gen).to(bf)
+    v = torch.randn((b, hkv, s, d), device=dev, generator=gen).to(bf)
+    stream = torch.cuda.current_stream()
+    res = {}
+    for causal in (True, False):
+        for _ in range(3):
+            ft.attention_prefill(q, k, v, causal=causal)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(c["steps"]):
+            ft.attention_prefill(q, k, v, causal=causal)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / c["steps"]
+        keys = s * (s + 1) // 2 if causal else s * s
+        flops = 4.0 * b * hq * keys * d
+        tf = flops / (us * 1e-6) / 1e12
+        res["causal" if causal else "bidirectional"] = {
+            "us_per_call": round(us, 1), "TFLOP/s": round(tf, 1),
+            "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), "flops": flops}
+    del q, k, v
+    return {"metric": "prefill attention TFLOP/s", "unit": "TFLOP/s", "dtype": "bf16",
+            "config": {"workload": "attention_prefill bf16 B=1 Hq=32 Hkv=8 S=4096 D=128",
+                       "seed": c["seed"]},
+            "roofline": {"bound": "mfma", "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "kernel": "attn_prefill_mfma<bf16, 128>"},
+            "results": res}
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline: the oracle on a bounded sample of config 3's rows
 # ---------------------------------------------------------------------------
 def cpu_baseline_c3(torch, np, w, budget_s=12.0):
@@ -540,6 +589,9 @@ def main():
     if args.only == "int8":
         log("int8", json.dumps(bench_int8(torch, ft, dev)))
         return
+    if args.only == "prefill":
+        log("prefill", json.dumps(bench_prefill(torch, ft, dev)))
+        return
 
     log(f"config 3: building workload (seed {C3['seed']})")
     w, wall, attn_ms = bench_c3(torch, np, ft, dev, args.steps, args.warmup)
@@ -584,6 +636,9 @@ def main():
         decode_more.append(bench_int8(torch, ft, dev))
         log("int8 storage:", json.dumps(decode_more[2]["results"]))
         torch.cuda.empty_cache()
+        decode_more.append(bench_prefill(torch, ft, dev))
+        log("prefill:", json.dumps(decode_more[3]["results"]))
+        torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu and args.only is None:
@@ -620,7 +675,7 @@ def main():
         "cpu_baseline": cpu,
         "secondary": secondary,
         "chains": chains,
-        "decode_more": decode_more,
+        "more": decode_more,
     }
     print(json.dumps(line), flush=True)
 

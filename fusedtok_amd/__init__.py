@@ -5,6 +5,8 @@ contract for the decode hot path (reference python/fusedtok/__init__.py):
 
 - ``attention_decode`` / ``attention_decode_paged``: flash-decoding GQA
   attention over contiguous / paged KV caches (f32, bf16, fp16 storage);
+- ``attention_prefill``: causal / bidirectional attention over a fresh
+  sequence's S query rows (the step before decode);
 - ``kv_append`` / ``kv_append_paged``: one fresh token's K/V rows per
   sequence written in place at position ``lens[b]``;
 - ``quantize_int8``: symmetric per-tensor INT8 quantize; ``dequantize_int8``
@@ -71,6 +73,7 @@ __all__ = [
     "qgemm_i32",
     "attention_decode",
     "attention_decode_paged",
+    "attention_prefill",
     "kv_append",
     "kv_append_paged",
     "rmsnorm_quant",
@@ -482,6 +485,59 @@ def attention_decode(q, k_cache, v_cache, lens=None, *, cuda=False):
     res = attention_decode(_upload(arr_q, dev), _upload(arr_k, dev),
                            _upload(arr_v, dev),
                            None if arr_l is None else _upload(arr_l, dev))
+    return _result(res, q)
+
+
+def attention_prefill(q, k, v, causal=True, *, cuda=False):
+    """Prefill (fresh-sequence) attention over S query rows:
+
+    ``out[b, h, i] = softmax(q[b,h,i] . K[b,kv(h)]^T / sqrt(D)) . V[b,kv(h)]``
+    where query row i attends to key rows ``[0, i]`` (``causal=True``) or to
+    all S rows (``causal=False``). q: [B, Hq, S, D]; k / v: [B, Hkv, S, D];
+    out: [B, Hq, S, D] in q's dtype (f32 / bf16 / fp16 storage, float32
+    softmax and accumulators). GQA as :func:`attention_decode`; D a multiple
+    of 4, at most 512 (reference ``__init__.py:791-846``).
+    """
+    if _on_gpu(q):
+        for name, t in (("q", q), ("k", k), ("v", v)):
+            _check_dtype(t, name, _FLOAT_DTYPES)
+        for name, t in (("k", k), ("v", v)):
+            if t.dtype is not q.dtype:
+                raise TypeError(f"{name} must have the same dtype as q")
+        if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+            raise ValueError("q/k/v must be [B, heads, S, D]")
+        b, hq, s, d = q.shape
+        b2, hkv, s2, d2 = k.shape
+        if (b2, s2, d2) != (b, s, d) or v.shape != k.shape:
+            raise ValueError("k/v must match q's batch, seq and dim")
+        if hq < 1 or hkv < 1:
+            raise ValueError("head counts must be >= 1")
+        if hq % hkv:
+            raise ValueError("q heads must be a multiple of kv heads")
+        out = torch.empty((b, hq, s, d), dtype=q.dtype, device=q.device)
+        if b * hq * s > 0:
+            _launcher("attention_prefill_launch", q.dtype)(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                b, hq, hkv, s, d, bool(causal), _stream())
+        return out
+    arr_q = _host_f32(q, "q")
+    arr_k = _host_f32(k, "k")
+    arr_v = _host_f32(v, "v")
+    if arr_q.ndim != 4 or arr_k.ndim != 4 or arr_v.ndim != 4:
+        raise ValueError("q/k/v must be [B, heads, S, D]")
+    b, hq, s, d = arr_q.shape
+    b2, hkv, s2, d2 = arr_k.shape
+    if (b2, s2, d2) != (b, s, d) or arr_v.shape != arr_k.shape:
+        raise ValueError("k/v must match q's batch, seq and dim")
+    if hq < 1 or hkv < 1:
+        raise ValueError("head counts must be >= 1")
+    if hq % hkv:
+        raise ValueError("q heads must be a multiple of kv heads")
+    if d % 4 or d > 512:
+        raise ValueError("dim must be a multiple of 4 and at most 512")
+    dev = _need_device()
+    res = attention_prefill(_upload(arr_q, dev), _upload(arr_k, dev),
+                            _upload(arr_v, dev), causal)
     return _result(res, q)
 
 

@@ -63,6 +63,23 @@ PYBIND11_MODULE(_fusedtok, m) {
     FT_ATT("attention_decode_launch_fp16", ft_attention_decode_launch_fp16, void);
 #undef FT_ATT
 
+    // ---- attention, prefill -------------------------------------------------
+#define FT_PRE(NAME, FN, T)                                                    \
+    m.def(NAME,                                                                \
+          [](uintptr_t q, uintptr_t k, uintptr_t v, uintptr_t out, int batch,  \
+             int hq, int hkv, int seq, int dim, bool causal, uintptr_t stream) { \
+              check(FN(P<const T>(q), P<const T>(k), P<const T>(v), P<T>(out), \
+                       batch, hq, hkv, seq, dim, causal ? 1 : 0, stream));     \
+          },                                                                   \
+          py::arg("q"), py::arg("k"), py::arg("v"), py::arg("out"),            \
+          py::arg("batch"), py::arg("q_heads"), py::arg("kv_heads"),           \
+          py::arg("seq"), py::arg("dim"), py::arg("causal"),                   \
+          py::arg("stream") = 0)
+    FT_PRE("attention_prefill_launch", ft_attention_prefill_launch, float);
+    FT_PRE("attention_prefill_launch_bf16", ft_attention_prefill_launch_bf16, void);
+    FT_PRE("attention_prefill_launch_fp16", ft_attention_prefill_launch_fp16, void);
+#undef FT_PRE
+
     // ---- attention, paged -----------------------------------------------
 #define FT_ATTP(NAME, FN, T)                                                   \
     m.def(NAME,                                                                \

@@ -1,0 +1,423 @@
+// Prefill (fresh-sequence) attention for gfx950:
+//
+//   out[b, h, i] = softmax(q[b,h,i] . K[b,kv]^T / sqrt(D)) . V[b,kv],
+//   kv = h / (Hq / Hkv), over key rows [0, i] (causal) or all S rows.
+//   q, out: [B, Hq, S, D]; k, v: [B, Hkv, S, D]; D % 4 == 0, D <= 512.
+//
+// (reference attention.hpp:64-81 semantics, attention.cu:1591-1639 CPU
+// path, attention.cu:1649-1739 launcher contract: no workspace, stream-
+// ordered, capturable.)
+//
+// attn_prefill_mfma<T, D>: bf16 / fp16 storage, D in {64, 128}. A
+// workgroup owns 128 query rows of one (b, q head), 32 per wave; 64-row K
+// and V tiles stream through two LDS stages, V transposed on the way in.
+// Everything is computed transposed, so every accumulator a lane holds
+// belongs to one query row (r = lane % 16, g = lane / 16; operand layout
+// of v_mfma_f32_16x16x32: A[r][8g+j], B[8g+j][r], C[4g+i][r]):
+//
+//   scores  S^T[kv][q] = K[kv][:] . Q[q][:]     A = K rows from LDS,
+//           B = Q^T (the wave's Q in registers for the whole kernel);
+//           lane (q, g) gets keys 4g + i of each 16-key block.
+//   softmax online per query row: the 64 keys of a row sit in the 4 lanes
+//           {q, q+16, q+32, q+48}: two xor shuffles for the tile maximum;
+//           the rescale of the running output is a per-lane multiply.
+//   PV      O^T[d][q] += V^T[d][kv] . P^T[kv][q]: B = P straight from the
+//           score accumulators: for a 32-key step, lane (q, g) holds keys
+//           {4g+i} of block 2ks and {16+4g+i} of block 2ks+1, so the k
+//           slots are permuted (slot 8g+i <-> key 4g+i, slot 8g+4+i <->
+//           key 16+4g+i) and V^T is stored in LDS in that key order, so its
+//           A fragments are single 16-byte reads.
+//   bf16:   P is split into hi + lo bf16 parts (two MFMAs), so the weights
+//           carry ~16 mantissa bits; fp16 P carries 11.
+//
+// Causal work is uneven across query tiles: the grid runs the last (most
+// keys) tiles of every head first.
+//
+// attn_prefill_generic<T>: f32 storage, and half storage with other D: one
+// wave per query row, lanes across D in float4 chunks, online softmax over
+// the keys (a parity path).
+#include "ft_common.hpp"
+
+#include <cstdlib>
+#include <type_traits>
+
+namespace ft {
+namespace {
+
+constexpr float kLog2eP = 1.4426950408889634f;
+constexpr int kPQ = 128;                  // query rows per workgroup
+constexpr int kPKV = 64;                  // key rows per tile
+constexpr int kVtPitch = kPKV * 2 + 16;   // bytes per V^T row (one d)
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T> struct PMma;
+template <> struct PMma<bf16> {
+    typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+    static constexpr bool kSplit = true;
+    __device__ __forceinline__ static f32x4 mma(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct PMma<f16> {
+    typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+    static constexpr bool kSplit = false;
+    __device__ __forceinline__ static f32x4 mma(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <int D>
+struct PCfg {
+    static constexpr int kKPitch = D * 2 + 16;                 // bytes per K row
+    static constexpr int kStage = kPKV * kKPitch + D * kVtPitch;
+    static constexpr int kKChunks = kPKV * D / 8 / 256;        // 16-byte K chunks per thread
+    static constexpr int kVPieces = 16 * (D / 8);              // 4 keys x 8 d pieces
+    static constexpr int kS = D / 32;                          // score k-steps
+    static constexpr int kDB = D / 16;                         // output d blocks
+};
+
+// position (in 4-key units) of key group G (keys 4G .. 4G+3 of a 64-key
+// tile) in a V^T row: the PV k-slot order described above
+__device__ __forceinline__ int vt_pos(int G) {
+    return 8 * (G >> 3) + 2 * (G & 3) + ((G & 7) >= 4 ? 1 : 0);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
+                       const T* __restrict__ v, T* __restrict__ out, int batch,
+                       int hq, int hkv, int seq, int causal, float scale_log2) {
+    using M = PMma<T>;
+    using V8 = typename M::v8;
+    using C = PCfg<D>;
+    __shared__ __attribute__((aligned(16))) char smem[2 * C::kStage];
+
+    const int nqt = (seq + kPQ - 1) / kPQ;
+    const int nbh = batch * hq;
+    const int qt = nqt - 1 - (int)(blockIdx.x / (unsigned)nbh);
+    const int bh = (int)(blockIdx.x % (unsigned)nbh);
+    const int b = bh / hq, h = bh - b * hq;
+    const int kvh = h / (hq / hkv);
+    const int q0 = qt * kPQ;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+
+    const T* qh = q + ((size_t)b * hq + h) * seq * D;
+    const T* kh = k + ((size_t)b * hkv + kvh) * seq * D;
+    const T* vh = v + ((size_t)b * hkv + kvh) * seq * D;
+
+    // the wave's Q as B operands: row q0 + 32 wave + 16 qb + r16, elements
+    // 32 s + 8 g .. +7 (rows past S read row S - 1; never stored)
+    V8 qf[2][C::kS];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const int row = min(q0 + 32 * wave + 16 * qb + r16, seq - 1);
+#pragma unroll
+        for (int s = 0; s < C::kS; ++s)
+            qf[qb][s] = *reinterpret_cast<const V8*>(qh + (size_t)row * D + 32 * s + 8 * g);
+    }
+
+    const int nkv_all = (seq + kPKV - 1) / kPKV;
+    const int nkt = causal ? min(nkv_all, min(q0 + kPQ - 1, seq - 1) / kPKV + 1) : nkv_all;
+
+    // ---- staging: K rows as is, V transposed into the PV slot order -------
+    i32x4_t kreg[C::kKChunks];
+    i32x4_t vreg[4];
+    const bool vthr = tid < C::kVPieces;
+    const int vG = tid & 15, vc = tid >> 4;   // key group, d chunk of this thread's piece
+    auto load_tile = [&](int kt) {
+        const int kv0 = kt * kPKV;
+#pragma unroll
+        for (int j = 0; j < C::kKChunks; ++j) {
+            const int c = tid + 256 * j;
+            const int row = min(kv0 + c / (D / 8), seq - 1);
+            kreg[j] = *reinterpret_cast<const i32x4_t*>(kh + (size_t)row * D + 8 * (c % (D / 8)));
+        }
+        if (vthr) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = min(kv0 + 4 * vG + r, seq - 1);
+                vreg[r] = *reinterpret_cast<const i32x4_t*>(vh + (size_t)row * D + 8 * vc);
+            }
+        }
+    };
+    auto store_tile = [&](int st) {
+        char* ks = smem + st * C::kStage;
+        char* vt = ks + kPKV * C::kKPitch;
+#pragma unroll
+        for (int j = 0; j < C::kKChunks; ++j) {
+            const int c = tid + 256 * j;
+            *reinterpret_cast<i32x4_t*>(ks + (c / (D / 8)) * C::kKPitch + 16 * (c % (D / 8))) =
+                kreg[j];
+        }
+        if (vthr) {
+            char* dst = vt + (8 * vc) * kVtPitch + 8 * vt_pos(vG);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {  // dwords w of the 4 rows: d = 8 vc + 2 w, +1
+                const unsigned a0 = (unsigned)vreg[0][w], a1 = (unsigned)vreg[1][w];
+                const unsigned a2 = (unsigned)vreg[2][w], a3 = (unsigned)vreg[3][w];
+                uint2 lo, hi;  // keys 0..3 of element 2w (low halves), 2w + 1 (high)
+                lo.x = (a0 & 0xffffu) | (a1 << 16);
+                lo.y = (a2 & 0xffffu) | (a3 << 16);
+                hi.x = (a0 >> 16) | (a1 & 0xffff0000u);
+                hi.y = (a2 >> 16) | (a3 & 0xffff0000u);
+                *reinterpret_cast<uint2*>(dst + (2 * w) * kVtPitch) = lo;
+                *reinterpret_cast<uint2*>(dst + (2 * w + 1) * kVtPitch) = hi;
+            }
+        }
+    };
+
+    f32x4 o[C::kDB][2];
+#pragma unroll
+    for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) o[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run[2] = {-INFINITY, -INFINITY};
+    float l_run[2] = {0.f, 0.f};
+    const int wrow0 = q0 + 32 * wave;  // first query row of this wave
+
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    for (int kt = 0; kt < nkt; ++kt) {
+        if (kt + 1 < nkt) load_tile(kt + 1);
+        const int kv0 = kt * kPKV;
+        const bool active = !causal || kv0 <= wrow0 + 31;
+        if (active) {
+            const char* ks = smem + (kt & 1) * C::kStage;
+            const char* vt = ks + kPKV * C::kKPitch;
+            // scores S^T for 4 key blocks x 2 query blocks
+            f32x4 sc[4][2];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                sc[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+                sc[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < C::kS; ++s) {
+                    const V8 kf = *reinterpret_cast<const V8*>(
+                        ks + (16 * kb + r16) * C::kKPitch + (32 * s + 8 * g) * 2);
+                    sc[kb][0] = M::mma(kf, qf[0][s], sc[kb][0]);
+                    sc[kb][1] = M::mma(kf, qf[1][s], sc[kb][1]);
+                }
+            }
+            // online softmax per query row; P fragments for the PV product
+            V8 ph[2][2], pl[2][2];
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                const int qrow = wrow0 + 16 * qb + r16;
+                float t[4][4];
+                float mt = -INFINITY;
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int key = kv0 + 16 * kb + 4 * g + i;
+                        const bool valid = key < seq && (!causal || key <= qrow);
+                        t[kb][i] = valid ? sc[kb][qb][i] * scale_log2 : -INFINITY;
+                        mt = fmaxf(mt, t[kb][i]);
+                    }
+                mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+                mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+                const float m_new = fmaxf(m_run[qb], mt);
+                const float m_use = m_new == -INFINITY ? 0.f : m_new;
+                const float alpha = exp2f(m_run[qb] - m_use);
+                float psum = 0.f;
+                float p[4][4];
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        p[kb][i] = exp2f(t[kb][i] - m_use);
+                        psum += p[kb][i];
+                    }
+                l_run[qb] = l_run[qb] * alpha + psum;
+                m_run[qb] = m_new;
+#pragma unroll
+                for (int db = 0; db < C::kDB; ++db) o[db][qb] *= alpha;
+#pragma unroll
+                for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float pv = p[2 * ks2 + (j >> 2)][j & 3];
+                        const T hv = (T)pv;
+                        ph[qb][ks2][j] = hv;
+                        if constexpr (M::kSplit) pl[qb][ks2][j] = (T)(pv - (float)hv);
+                    }
+            }
+            // O^T += V^T . P^T
+#pragma unroll
+            for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+                for (int ks2 = 0; ks2 < 2; ++ks2) {
+                    const V8 vf = *reinterpret_cast<const V8*>(
+                        vt + (16 * db + r16) * kVtPitch + (32 * ks2 + 8 * g) * 2);
+#pragma unroll
+                    for (int qb = 0; qb < 2; ++qb) {
+                        o[db][qb] = M::mma(vf, ph[qb][ks2], o[db][qb]);
+                        if constexpr (M::kSplit) o[db][qb] = M::mma(vf, pl[qb][ks2], o[db][qb]);
+                    }
+                }
+        }
+        if (kt + 1 < nkt) store_tile((kt + 1) & 1);
+        __syncthreads();
+    }
+
+    // normalise and store: lane (q, g) holds d = 16 db + 4 g + i of row q
+    T* oh = out + ((size_t)b * hq + h) * seq * D;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        float l = l_run[qb];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        const float inv = 1.0f / l;
+        const int qrow = wrow0 + 16 * qb + r16;
+        if (qrow >= seq) continue;
+#pragma unroll
+        for (int db = 0; db < C::kDB; ++db)
+            St<T>::st4(oh + (size_t)qrow * D + 16 * db + 4 * g,
+                       make_float4(o[db][qb][0] * inv, o[db][qb][1] * inv,
+                                   o[db][qb][2] * inv, o[db][qb][3] * inv));
+    }
+}
+
+// one wave per (b, q head, query row); lanes hold float4 chunks c = lane,
+// lane + 64 of D
+template <typename T>
+__global__ __launch_bounds__(64) void attn_prefill_generic(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    T* __restrict__ out, int hq, int hkv, int seq, int dim, int causal, float scale) {
+    const long long id = blockIdx.x;
+    const int i = (int)(id % seq);
+    const long long bh = id / seq;
+    const int h = (int)(bh % hq);
+    const long long b = bh / hq;
+    const int kvh = h / (hq / hkv);
+    const int lane = threadIdx.x;
+    const int nc = dim / 4;
+    const T* qr = q + ((size_t)bh * seq + i) * dim;
+    const T* kh = k + ((size_t)b * hkv + kvh) * seq * dim;
+    const T* vh = v + ((size_t)b * hkv + kvh) * seq * dim;
+    const bool c0 = lane < nc, c1 = lane + 64 < nc;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 q0 = c0 ? St<T>::ld4(qr + 4 * lane) : z;
+    const float4 q1 = c1 ? St<T>::ld4(qr + 4 * (lane + 64)) : z;
+    float4 a0 = z, a1 = z;
+    float m = -INFINITY, l = 0.f;
+    const int lim = causal ? i + 1 : seq;
+    for (int t = 0; t < lim; ++t) {
+        const T* kr = kh + (size_t)t * dim;
+        float d = 0.f;
+        if (c0) {
+            const float4 kk = St<T>::ld4(kr + 4 * lane);
+            d = q0.x * kk.x + q0.y * kk.y + q0.z * kk.z + q0.w * kk.w;
+        }
+        if (c1) {
+            const float4 kk = St<T>::ld4(kr + 4 * (lane + 64));
+            d += q1.x * kk.x + q1.y * kk.y + q1.z * kk.z + q1.w * kk.w;
+        }
+        const float s = wave_sum(d) * scale;
+        const float m_new = fmaxf(m, s);
+        const float a = expf(m - m_new);
+        const float p = expf(s - m_new);
+        l = l * a + p;
+        m = m_new;
+        const T* vr = vh + (size_t)t * dim;
+        if (c0) {
+            const float4 vv = St<T>::ld4(vr + 4 * lane);
+            a0 = make_float4(a0.x * a + p * vv.x, a0.y * a + p * vv.y,
+                             a0.z * a + p * vv.z, a0.w * a + p * vv.w);
+        }
+        if (c1) {
+            const float4 vv = St<T>::ld4(vr + 4 * (lane + 64));
+            a1 = make_float4(a1.x * a + p * vv.x, a1.y * a + p * vv.y,
+                             a1.z * a + p * vv.z, a1.w * a + p * vv.w);
+        }
+    }
+    const float inv = 1.0f / l;
+    T* orow = out + ((size_t)bh * seq + i) * dim;
+    if (c0) St<T>::st4(orow + 4 * lane, make_float4(a0.x * inv, a0.y * inv, a0.z * inv, a0.w * inv));
+    if (c1)
+        St<T>::st4(orow + 4 * (lane + 64),
+                   make_float4(a1.x * inv, a1.y * inv, a1.z * inv, a1.w * inv));
+}
+
+int env_flag(const char* name) {
+    const char* s = getenv(name);
+    return (s && *s) ? atoi(s) : 0;
+}
+
+template <typename T>
+void prefill_run(const T* q, const T* k, const T* v, T* out, int batch, int hq, int hkv,
+                 int seq, int dim, bool causal, hipStream_t s) {
+    if (batch < 0 || hq < 1 || hkv < 1 || seq < 0 || dim < 1)
+        inval("attention shapes must satisfy batch>=0, heads>=1, rows>=0, dim>=1");
+    if (hq % hkv != 0)
+        inval("q heads must be a multiple of kv heads (contiguous GQA groups)");
+    if (dim % 4 != 0 || dim > 512) inval("dim must be a multiple of 4 and at most 512");
+    if (batch == 0 || seq == 0) return;  // nothing to compute
+    if (!q || !k || !v || !out) inval("attention prefill: null operand");
+    const float scale = 1.0f / sqrtf((float)dim);
+    if constexpr (!std::is_same<T, float>::value) {
+        const bool aligned = ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) % 16 == 0;
+        if ((dim == 64 || dim == 128) && aligned && !env_flag("FT_PREFILL_FORCE_GENERIC")) {
+            const long long nqt = (seq + kPQ - 1) / kPQ;
+            const long long grid = (long long)batch * hq * nqt;
+            if (grid > 0x7fffffffLL) inval("attention prefill problem too large for one launch");
+            const float sl2 = scale * kLog2eP;
+            if (dim == 128)
+                attn_prefill_mfma<T, 128><<<(unsigned)grid, 256, 0, s>>>(
+                    q, k, v, out, batch, hq, hkv, seq, causal ? 1 : 0, sl2);
+            else
+                attn_prefill_mfma<T, 64><<<(unsigned)grid, 256, 0, s>>>(
+                    q, k, v, out, batch, hq, hkv, seq, causal ? 1 : 0, sl2);
+            launch_check("attention prefill kernel launch");
+            return;
+        }
+    }
+    const long long grid = (long long)batch * hq * seq;
+    if (grid > 0x7fffffffLL) inval("attention prefill problem too large for one launch");
+    attn_prefill_generic<T><<<(unsigned)grid, 64, 0, s>>>(q, k, v, out, hq, hkv, seq, dim,
+                                                          causal ? 1 : 0, scale);
+    launch_check("attention prefill kernel launch");
+}
+
+}  // namespace
+}  // namespace ft
+
+extern "C" {
+
+int ft_attention_prefill_launch(const float* q, const float* k, const float* v, float* out,
+                                int batch, int q_heads, int kv_heads, int seq, int dim,
+                                int causal, uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::prefill_run<float>(q, k, v, out, batch, q_heads, kv_heads, seq, dim, causal != 0,
+                               ft::as_stream(stream));
+    });
+}
+
+int ft_attention_prefill_launch_bf16(const void* q, const void* k, const void* v, void* out,
+                                     int batch, int q_heads, int kv_heads, int seq, int dim,
+                                     int causal, uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::prefill_run<ft::bf16>((const ft::bf16*)q, (const ft::bf16*)k, (const ft::bf16*)v,
+                                  (ft::bf16*)out, batch, q_heads, kv_heads, seq, dim,
+                                  causal != 0, ft::as_stream(stream));
+    });
+}
+
+int ft_attention_prefill_launch_fp16(const void* q, const void* k, const void* v, void* out,
+                                     int batch, int q_heads, int kv_heads, int seq, int dim,
+                                     int causal, uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::prefill_run<ft::f16>((const ft::f16*)q, (const ft::f16*)k, (const ft::f16*)v,
+                                 (ft::f16*)out, batch, q_heads, kv_heads, seq, dim,
+                                 causal != 0, ft::as_stream(stream));
+    });
+}
+
+}  // extern "C"

@@ -147,6 +147,26 @@ int ft_kv_append_launch_fp16(const void* k_new, const void* v_new,
                              uintptr_t stream);
 
 /* ------------------------------------------------------------------ */
+/* Prefill (fresh-sequence) attention: q [B,Hq,S,D] attends over k / v  */
+/* [B,Hkv,S,D]; causal != 0 masks query row i to key rows [0, i],      */
+/* causal == 0 attends to all S rows; out [B,Hq,S,D] in q's dtype,     */
+/* float32 softmax and accumulators. Same GQA grouping and D contract  */
+/* as decode (D % 4 == 0, D <= 512). No workspace; capturable.         */
+/* Replaces attention_prefill_launch{,_bf16,_fp16}                     */
+/* (cuda_launch.hpp:362-378; attention.cu:1649-1739); causal is an int */
+/* here (bool in the reference).                                       */
+/* ------------------------------------------------------------------ */
+int ft_attention_prefill_launch(const float* q, const float* k, const float* v,
+                                float* out, int batch, int q_heads, int kv_heads,
+                                int seq, int dim, int causal, uintptr_t stream);
+int ft_attention_prefill_launch_bf16(const void* q, const void* k, const void* v,
+                                     void* out, int batch, int q_heads, int kv_heads,
+                                     int seq, int dim, int causal, uintptr_t stream);
+int ft_attention_prefill_launch_fp16(const void* q, const void* k, const void* v,
+                                     void* out, int batch, int q_heads, int kv_heads,
+                                     int seq, int dim, int causal, uintptr_t stream);
+
+/* ------------------------------------------------------------------ */
 /* INT8 per-tensor symmetric quantize                                  */
 /* scale = max|x|/127 (1.0 for all-zero input); inv = 1.0f/scale;      */
 /* q = clamp(rint(x*inv), -127, 127). scale_out is a DEVICE float.     */

@@ -75,6 +75,17 @@ def attention_decode(q, k, v, lens=None):
     return out
 
 
+def attention_prefill(q, k, v, causal=True):
+    """attention_prefill_cpu: q [B,Hq,S,D], k/v [B,Hkv,S,D] -> [B,Hq,S,D] f32."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    b, hq, s, d = q.shape
+    hkv = k.shape[1]
+    out = np.zeros((b, hq, s, d), np.float32)
+    _call("or_attention_prefill", _p(q), _p(k), _p(v), _p(out), b, hq, hkv, s, d,
+          1 if causal else 0)
+    return out
+
+
 def attention_decode_paged(q, k_pool, v_pool, table, lens=None):
     """attention_decode_paged_cpu: pools [Nb,Hkv,P,D], table [B,S]."""
     q, k_pool, v_pool = _f32(q), _f32(k_pool), _f32(v_pool)

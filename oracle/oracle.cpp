@@ -100,6 +100,48 @@ int or_attention_decode(const float* q, const float* k, const float* v,
 }
 
 // ---------------------------------------------------------------------------
+// attention_prefill_cpu (reference attention.cu:1591-1639): per (b, h, row
+// i), keys [0, i] (causal) or [0, S): the same two-pass float32 softmax as
+// the decode step (scores = (q . k_t) * (1/sqrtf(D)), m, l = sum expf(s - m),
+// out += (expf(s - m) / l) * v_t).
+// ---------------------------------------------------------------------------
+int or_attention_prefill(const float* q, const float* k, const float* v, float* out,
+                         int batch, int hq, int hkv, int seq, int dim, int causal) {
+    return run([&] {
+        attention_check(batch, hq, hkv, seq, dim);
+        const int group = hq / hkv;
+        const float scale = 1.0f / sqrtf((float)dim);
+        std::memset(out, 0, sizeof(float) * (size_t)batch * hq * seq * dim);
+        std::vector<float> scores(seq > 0 ? seq : 1);
+        for (int bi = 0; bi < batch; ++bi)
+            for (int h = 0; h < hq; ++h) {
+                const int kv = h / group;
+                const float* qp = q + (((size_t)bi * hq + h) * seq) * dim;
+                const float* kp = k + (((size_t)bi * hkv + kv) * seq) * dim;
+                const float* vp = v + (((size_t)bi * hkv + kv) * seq) * dim;
+                for (int i = 0; i < seq; ++i) {
+                    const int lim = causal ? i + 1 : seq;
+                    const float* qr = qp + (size_t)i * dim;
+                    float m = -INFINITY;
+                    for (int t = 0; t < lim; ++t) {
+                        float dot = 0.0f;
+                        for (int d = 0; d < dim; ++d) dot += qr[d] * kp[(size_t)t * dim + d];
+                        scores[t] = dot * scale;
+                        m = fmaxf(m, scores[t]);
+                    }
+                    float l = 0.0f;
+                    for (int t = 0; t < lim; ++t) l += expf(scores[t] - m);
+                    float* op = out + (((size_t)bi * hq + h) * seq + i) * dim;
+                    for (int t = 0; t < lim; ++t) {
+                        const float p = expf(scores[t] - m) / l;
+                        for (int d = 0; d < dim; ++d) op[d] += p * vp[(size_t)t * dim + d];
+                    }
+                }
+            }
+    });
+}
+
+// ---------------------------------------------------------------------------
 // attention_decode_paged_cpu (reference attention.cu:1382-1456): the same
 // walk with row(t) = pool[table[b*S + t/P], kv, t%P, :]; validates lens and
 // the table entries of the pages in use.

@@ -67,6 +67,30 @@ def ref_qgemm_pc(a, sa, b, sb):
     return acc.astype(np.int32).astype(np.float32) * scales
 
 
+def ref_prefill(q, k, v, causal=True, rows=None):
+    """float64 prefill attention (reference tests/test_attention.py:155-173
+    conventions): query row i of [B,Hq,S,D] attends to key rows [0, i]
+    (causal) or all S rows, kv head h // G. rows: optional subset of query
+    rows (the others stay 0)."""
+    b, hq, s, d = q.shape
+    hkv = k.shape[1]
+    group = hq // hkv
+    out = np.zeros((b, hq, s, d), dtype=np.float64)
+    rows = range(s) if rows is None else rows
+    for bi in range(b):
+        for h in range(hq):
+            kv = h // group
+            kd = k[bi, kv].astype(np.float64)
+            vd = v[bi, kv].astype(np.float64)
+            for i in rows:
+                lim = i + 1 if causal else s
+                sc = kd[:lim] @ q[bi, h, i].astype(np.float64) / math.sqrt(d)
+                p = np.exp(sc - sc.max())
+                p /= p.sum()
+                out[bi, h, i] = p @ vd[:lim]
+    return out
+
+
 def ref_quantize(x):
     """float32 closed form of the symmetric quantizer, with numpy rounding
     (np.rint: half to even)."""

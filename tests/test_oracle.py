@@ -246,6 +246,51 @@ def test_paged_single_token_is_v_and_errors():
         oracle.attention_decode_paged(q, kp, vp, bad, lens)
 
 
+PREFILL_SHAPES = [  # reference tests/test_attention.py:176-184
+    (1, 4, 2, 1, 32), (1, 8, 8, 5, 64), (2, 6, 3, 17, 16), (1, 32, 8, 40, 128),
+    (1, 4, 1, 33, 8), (1, 8, 2, 64, 256), (1, 4, 2, 9, 512),
+]
+
+
+@pytest.mark.parametrize("b,hq,hkv,s,d", PREFILL_SHAPES)
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_matches_float64(b, hq, hkv, s, d, causal):
+    # test_attention.py:187-197: rtol 1e-4, atol 1e-5 against float64
+    rng = np.random.default_rng(b * 100 + hq * 17 + s * 3 + d + causal)
+    q = rng.standard_normal((b, hq, s, d)).astype(np.float32)
+    k = rng.standard_normal((b, hkv, s, d)).astype(np.float32)
+    v = rng.standard_normal((b, hkv, s, d)).astype(np.float32)
+    y = oracle.attention_prefill(q, k, v, causal)
+    np.testing.assert_allclose(y, refs.ref_prefill(q, k, v, causal), rtol=1e-4, atol=1e-5)
+
+
+def test_prefill_first_row_s1_decode_and_errors():
+    rng = np.random.default_rng(50)
+    # test_attention.py:200-210: causal row 0 attends only to key 0 -> v[0]
+    q = rng.standard_normal((1, 4, 9, 32)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 9, 32)).astype(np.float32)
+    v = rng.standard_normal((1, 2, 9, 32)).astype(np.float32)
+    y = oracle.attention_prefill(q, k, v, True)
+    for h in range(4):
+        np.testing.assert_array_equal(y[0, h, 0], v[0, h // 2, 0])
+    # causal row i is the decode step over keys [0, i] (bit-identical loops)
+    for i in (3, 8):
+        dec = oracle.attention_decode(q[:, :, i], k[:, :, :i + 1], v[:, :, :i + 1])
+        np.testing.assert_array_equal(y[:, :, i], dec)
+    # bidirectional: every row is the decode step over all S keys
+    yb = oracle.attention_prefill(q, k, v, False)
+    np.testing.assert_array_equal(yb[:, :, 2], oracle.attention_decode(q[:, :, 2], k, v))
+    # test_attention.py:227-238: shape contract
+    with pytest.raises(ValueError):
+        oracle.attention_prefill(np.zeros((1, 5, 8, 32), np.float32),
+                                 np.zeros((1, 2, 8, 32), np.float32),
+                                 np.zeros((1, 2, 8, 32), np.float32))
+    with pytest.raises(ValueError):
+        oracle.attention_prefill(np.zeros((1, 4, 8, 30), np.float32),
+                                 np.zeros((1, 2, 8, 30), np.float32),
+                                 np.zeros((1, 2, 8, 30), np.float32))
+
+
 def test_kv_append_copies_and_bounds():
     rng = np.random.default_rng(9)
     b, hkv, t, d = 3, 2, 10, 8
