@@ -48,6 +48,7 @@ constexpr float kLog2eP = 1.4426950408889634f;
 constexpr int kPQ = 128;                  // query rows per workgroup
 constexpr int kPKV = 64;                  // key rows per tile
 constexpr int kVtPitch = kPKV * 2 + 16;   // bytes per V^T row (one d)
+constexpr float kLazy = 8.0f;             // log2 of the largest unnormalised weight
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
@@ -77,6 +78,14 @@ struct PCfg {
     static constexpr int kS = D / 32;                          // score k-steps
     static constexpr int kDB = D / 16;                         // output d blocks
 };
+
+// two floats -> one dword of two T values (round to nearest even)
+template <typename T>
+__device__ __forceinline__ int pack2(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef T t2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(int, __builtin_convertvector(f2{a, b}, t2));
+}
 
 // position (in 4-key units) of key group G (keys 4G .. 4G+3 of a 64-key
 // tile) in a V^T row: the PV k-slot order described above
@@ -180,6 +189,7 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
     float m_run[2] = {-INFINITY, -INFINITY};
     float l_run[2] = {0.f, 0.f};
     const int wrow0 = q0 + 32 * wave;  // first query row of this wave
+    const float lazy_raw = kLazy / scale_log2;
 
     load_tile(0);
     store_tile(0);
@@ -205,48 +215,78 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
                     sc[kb][1] = M::mma(kf, qf[1][s], sc[kb][1]);
                 }
             }
-            // online softmax per query row; P fragments for the PV product
-            V8 ph[2][2], pl[2][2];
+            // online softmax per query row, on raw scores (the 1/sqrt(D) *
+            // log2(e) factor c > 0 commutes with max and folds into one FMA
+            // per score: p = exp2(s c - m c)); masks only on the tiles that
+            // cross this wave's diagonal or the sequence end
+            const bool need_mask = (causal && kv0 + kPKV - 1 > wrow0) || kv0 + kPKV > seq;
+            i32x4_t ph[2][2], pl[2][2];
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
-                const int qrow = wrow0 + 16 * qb + r16;
-                float t[4][4];
                 float mt = -INFINITY;
+                if (need_mask) {
+                    const int qrow = wrow0 + 16 * qb + r16;
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int key = kv0 + 16 * kb + 4 * g + i;
+                            const bool valid = key < seq && (!causal || key <= qrow);
+                            if (!valid) sc[kb][qb][i] = -INFINITY;
+                        }
+                }
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int key = kv0 + 16 * kb + 4 * g + i;
-                        const bool valid = key < seq && (!causal || key <= qrow);
-                        t[kb][i] = valid ? sc[kb][qb][i] * scale_log2 : -INFINITY;
-                        mt = fmaxf(mt, t[kb][i]);
-                    }
+                    for (int i = 0; i < 4; ++i) mt = fmaxf(mt, sc[kb][qb][i]);
                 mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
                 mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-                const float m_new = fmaxf(m_run[qb], mt);
+                // lazy rescale: the running maximum moves only when the tile's
+                // exceeds it by more than kLazy / c (weights then stay
+                // <= 2^kLazy); a wave whose rows all keep theirs skips the
+                // output rescale
+                const bool upd = mt > m_run[qb] + lazy_raw;
+                const float m_new = upd ? mt : m_run[qb];
                 const float m_use = m_new == -INFINITY ? 0.f : m_new;
-                const float alpha = exp2f(m_run[qb] - m_use);
-                float psum = 0.f;
+                // v_exp_f32 directly: exp2f's expansion adds a denormal-range
+                // rescale per call; weights below 2^-126 of the row maximum
+                // flush to 0, which changes no sum at float precision
+                const float alpha = __builtin_amdgcn_exp2f((m_run[qb] - m_use) * scale_log2);
+                const float nmc = -m_use * scale_log2;
                 float p[4][4];
+                float psum = 0.f;
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        p[kb][i] = exp2f(t[kb][i] - m_use);
+                        p[kb][i] = __builtin_amdgcn_exp2f(fmaf(sc[kb][qb][i], scale_log2, nmc));
                         psum += p[kb][i];
                     }
                 l_run[qb] = l_run[qb] * alpha + psum;
                 m_run[qb] = m_new;
+                if (__builtin_amdgcn_ballot_w64(upd)) {
 #pragma unroll
-                for (int db = 0; db < C::kDB; ++db) o[db][qb] *= alpha;
+                    for (int db = 0; db < C::kDB; ++db) o[db][qb] *= alpha;
+                }
+                // P^T fragments: dword w of step ks2 holds slots 8g + 2w, +1
 #pragma unroll
                 for (int ks2 = 0; ks2 < 2; ++ks2)
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const float pv = p[2 * ks2 + (j >> 2)][j & 3];
-                        const T hv = (T)pv;
-                        ph[qb][ks2][j] = hv;
-                        if constexpr (M::kSplit) pl[qb][ks2][j] = (T)(pv - (float)hv);
+                    for (int w = 0; w < 4; ++w) {
+                        const float p0 = p[2 * ks2 + (w >> 1)][2 * (w & 1)];
+                        const float p1 = p[2 * ks2 + (w >> 1)][2 * (w & 1) + 1];
+                        if constexpr (M::kSplit) {
+                            // hi: the top 16 bits (truncation, exact); lo: the
+                            // exact remainder rounded to bf16; hi + lo carries
+                            // ~16 significant bits of p
+                            const unsigned u0 = __float_as_uint(p0), u1 = __float_as_uint(p1);
+                            ph[qb][ks2][w] = (int)((u0 >> 16) | (u1 & 0xffff0000u));
+                            const float r0 = p0 - __uint_as_float(u0 & 0xffff0000u);
+                            const float r1 = p1 - __uint_as_float(u1 & 0xffff0000u);
+                            pl[qb][ks2][w] = pack2<T>(r0, r1);
+                        } else {
+                            ph[qb][ks2][w] = pack2<T>(p0, p1);
+                        }
                     }
             }
             // O^T += V^T . P^T
@@ -258,8 +298,9 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
                         vt + (16 * db + r16) * kVtPitch + (32 * ks2 + 8 * g) * 2);
 #pragma unroll
                     for (int qb = 0; qb < 2; ++qb) {
-                        o[db][qb] = M::mma(vf, ph[qb][ks2], o[db][qb]);
-                        if constexpr (M::kSplit) o[db][qb] = M::mma(vf, pl[qb][ks2], o[db][qb]);
+                        o[db][qb] = M::mma(vf, __builtin_bit_cast(V8, ph[qb][ks2]), o[db][qb]);
+                        if constexpr (M::kSplit)
+                            o[db][qb] = M::mma(vf, __builtin_bit_cast(V8, pl[qb][ks2]), o[db][qb]);
                     }
                 }
         }
