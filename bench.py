@@ -38,7 +38,8 @@ lens[b] + 1 tokens.
               the int8 storage ops dequantize_int8 / qadd_int8 over 2^28
               elements; and attention_prefill (bf16, 32 / 8 heads, D=128,
               S=4096, causal and bidirectional) in TFLOP/s against the
-              2.5 PFLOP/s dense bf16 MFMA peak.
+              2.5 PFLOP/s dense bf16 MFMA peak; and the post-logits step
+              (decode_step_batched, argmax_batched) at 64 rows x 128256.
   cpu_baseline = the C++ restatement of the reference's single-threaded
               attention_decode_paged_cpu / kv_append_paged_cpu (oracle/),
               on a bounded sample of the same rows, one core.
@@ -85,7 +86,7 @@ def parse():
     p.add_argument("--no-chains", action="store_true",
                    help="skip the config 2 / config 4 chain measurements")
     p.add_argument("--only", choices=["decode", "gemm", "copy", "c1", "c2", "c4", "c5b",
-                            "int8", "prefill"],
+                            "int8", "prefill", "sampling"],
                    default=None,
                    help="run one workload only (profiling runs); 'copy' is "
                         "the HBM-counter calibration: a plain 1 GiB "
@@ -499,6 +500,54 @@ def bench_prefill(torch, ft, dev):
 
 
 # ---------------------------------------------------------------------------
+# post-logits step: decode_step_batched and argmax_batched
+# ---------------------------------------------------------------------------
+SAMPLE = dict(rows=64, vocab=128256, hist=64, seed=13, steps=20)
+
+
+def bench_sampling(torch, ft, dev):
+    """The step after the LM head at config 4's batch: 64 rows of Llama-3's
+    128256-entry vocabulary (float32 logits, N(0, 2^2)), repetition penalty
+    over a 64-token history per row, temperature 0.8, nucleus p = 0.9, tokens
+    left on the device; and greedy argmax_batched. Bytes: the logits read
+    once (rows x vocab x 4)."""
+    import numpy as np
+    c = SAMPLE
+    rows, n = c["rows"], c["vocab"]
+    gen = torch.Generator(device=dev).manual_seed(c["seed"])
+    logits = torch.randn((rows, n), device=dev, generator=gen) * 2.0
+    rng = np.random.default_rng(c["seed"])
+    hist = rng.integers(0, n, size=(rows, c["hist"]))
+    stream = torch.cuda.current_stream()
+    res = {}
+    calls = {
+        "decode_step_batched": lambda: ft.decode_step_batched(
+            logits, hist, 1.2, p=0.9, temperature=0.8, device_out=True),
+        "argmax_batched": lambda: ft.argmax_batched(logits),
+    }
+    for name, fn in calls.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(c["steps"]):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / c["steps"]
+        gbs = rows * n * 4 / (us * 1e-6) / 1e9
+        res[name] = {"us_per_call": round(us, 1), "GB/s": round(gbs, 1),
+                     "us_per_row": round(us / rows, 3)}
+    del logits
+    return {"metric": "post-logits step, us per call", "unit": "us", "dtype": "f32",
+            "config": {"workload": f"decode_step_batched / argmax_batched, {rows} rows x "
+                                   f"{n} vocab, penalty 1.2 over {c['hist']} ids, T=0.8, "
+                                   "p=0.9", "seed": c["seed"]},
+            "results": res}
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline: the oracle on a bounded sample of config 3's rows
 # ---------------------------------------------------------------------------
 def cpu_baseline_c3(torch, np, w, budget_s=12.0):
@@ -592,6 +641,9 @@ def main():
     if args.only == "prefill":
         log("prefill", json.dumps(bench_prefill(torch, ft, dev)))
         return
+    if args.only == "sampling":
+        log("sampling", json.dumps(bench_sampling(torch, ft, dev)))
+        return
 
     log(f"config 3: building workload (seed {C3['seed']})")
     w, wall, attn_ms = bench_c3(torch, np, ft, dev, args.steps, args.warmup)
@@ -638,6 +690,9 @@ def main():
         torch.cuda.empty_cache()
         decode_more.append(bench_prefill(torch, ft, dev))
         log("prefill:", json.dumps(decode_more[3]["results"]))
+        torch.cuda.empty_cache()
+        decode_more.append(bench_sampling(torch, ft, dev))
+        log("sampling:", json.dumps(decode_more[4]["results"]))
         torch.cuda.empty_cache()
 
     cpu = None

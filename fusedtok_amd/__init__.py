@@ -13,7 +13,11 @@ contract for the decode hot path (reference python/fusedtok/__init__.py):
   and the fused dequantize-add-requantize ``qadd_int8``;
 - ``qgemm`` / ``qgemm_perchannel``: W8A8 GEMM with exact int32 accumulation;
 - ``rmsnorm`` (+ residual), ``rope`` (interleaved / NeoX, ``pos_offset``),
-  ``swiglu``.
+  ``swiglu``;
+- the post-logits step: ``argmax`` / ``argmax_batched`` (greedy),
+  ``sample_topp`` / ``sample_topp_batched`` and ``decode_step`` /
+  ``decode_step_batched`` (repetition penalty -> temperature -> nucleus
+  sampling, deterministic per seed).
 
 Execution paths:
 
@@ -79,6 +83,12 @@ __all__ = [
     "rmsnorm_quant",
     "swiglu_quant",
     "rope_kv_append_paged",
+    "argmax",
+    "argmax_batched",
+    "sample_topp",
+    "sample_topp_batched",
+    "decode_step",
+    "decode_step_batched",
 ]
 
 # C-ABI dtype codes (include/fusedtok_amd.h)
@@ -1147,3 +1157,283 @@ def qgemm_i32(a_q, b_q):
         raise ValueError("operands must be 2-D [rows, K] with matching K")
     dev = _need_device()
     return _result(qgemm_i32(_upload(a, dev), _upload(b, dev)), a_q)
+
+
+# ---------------------------------------------------------------------------
+# post-logits sampling (reference __init__.py:1120-1176, 1602-1632,
+# 2292-2316, 2366-2540; sampling.cu, topk.cu)
+# ---------------------------------------------------------------------------
+
+
+def _logits_f32(t, name="logits"):
+    if not t.is_cuda:
+        raise TypeError(f"{name} must be a GPU tensor (got a CPU tensor on the "
+                        "zero-copy path)")
+    if t.dtype is not torch.float32:
+        raise TypeError(f"{name} must be float32, got {t.dtype}")
+    _check_contiguous(t, name)
+
+
+def _sampling_params(p, temperature, penalty=1.0):
+    if not penalty > 0.0:
+        raise ValueError("penalty must be > 0")
+    if not 0.0 < p <= 1.0:
+        raise ValueError("p must be in (0, 1]")
+    if not temperature > 0.0:
+        raise ValueError("temperature must be > 0")
+
+
+def _host_logits(x, ndim, what):
+    arr = _host_f32(x, "logits")
+    if arr.ndim != ndim:
+        raise ValueError(what)
+    return arr
+
+
+def _ids_arg(ids, vocab, device, name="sampled_ids"):
+    """1-D int64 ids on `device`: host values range-checked against
+    [0, vocab) (ValueError); a GPU tensor is trusted (the kernels drop
+    out-of-range entries) - the reference's boundary (__init__.py:322-343)."""
+    if _on_gpu(ids):
+        it = ids if ids.dtype is torch.int64 else ids.to(torch.int64)
+        if not it.is_contiguous():
+            it = it.contiguous()
+        if it.ndim != 1:
+            raise ValueError(f"{name} must be 1-D")
+        return it
+    host = _host_int_array(ids, name)
+    host = np.ascontiguousarray(host, dtype=np.int64)
+    if host.ndim != 1:
+        raise ValueError(f"{name} must be 1-D")
+    if host.size and (host.min() < 0 or host.max() >= vocab):
+        raise ValueError(f"{name} values must be in [0, {vocab})")
+    return torch.from_numpy(host).to(device)
+
+
+def _batch_seeds(seeds, rows, name="seeds"):
+    """None -> 0..rows-1; else one non-negative integer per row
+    (reference __init__.py:370-395)."""
+    if seeds is None:
+        return np.arange(rows, dtype=np.int64)
+    if _is_torch(seeds):
+        seeds = seeds.detach().cpu().numpy()
+    arr = np.asarray(seeds)
+    if arr.dtype.kind not in "iu":
+        raise TypeError(f"{name} must contain integers")
+    if arr.ndim != 1:
+        raise ValueError(f"{name} must be 1-D")
+    if arr.shape[0] != rows:
+        raise ValueError(f"{name} must have one entry per row")
+    out = np.ascontiguousarray(arr, dtype=np.int64)
+    if out.size and out.min() < 0:
+        raise ValueError(f"{name} values must be in [0, 2**63)")
+    return out
+
+
+def _batch_ids(sampled_ids, ids_offsets, rows, n):
+    """Per-row histories -> (flat int64 ids, int64 offsets), host side:
+    ragged sequences, a 2-D array (every row contributes all columns), or
+    flat ids plus ids_offsets (reference __init__.py:2415-2481)."""
+    if ids_offsets is not None:
+        if _is_torch(sampled_ids):
+            sampled_ids = sampled_ids.detach().cpu().numpy()
+        if _is_torch(ids_offsets):
+            ids_offsets = ids_offsets.detach().cpu().numpy()
+        ids = np.ascontiguousarray(sampled_ids)
+        if ids.ndim != 1:
+            raise ValueError("sampled_ids with ids_offsets must be a flat 1-D array")
+        offs = np.ascontiguousarray(ids_offsets)
+        if offs.ndim != 1 or offs.size != rows + 1:
+            raise ValueError("ids_offsets must be 1-D with rows + 1 entries")
+        if ids.size and not np.issubdtype(ids.dtype, np.integer):
+            raise TypeError("sampled_ids entries must be integers")
+        if offs.size and not np.issubdtype(offs.dtype, np.integer):
+            raise TypeError("ids_offsets entries must be integers")
+        ids = ids.astype(np.int64, copy=False)
+        offs = offs.astype(np.int64, copy=False)
+        if offs[0] != 0 or offs[-1] != ids.size or (np.diff(offs) < 0).any():
+            raise ValueError("ids_offsets must start at 0, end at len(sampled_ids) "
+                             "and be non-decreasing")
+    elif isinstance(sampled_ids, (list, tuple)):
+        if len(sampled_ids) != rows:
+            raise ValueError("sampled_ids must have one entry per row")
+        flat, offs = [], [0]
+        for row_ids in sampled_ids:
+            row = np.asarray(row_ids)
+            if row.size and not np.issubdtype(row.dtype, np.integer):
+                raise TypeError("sampled_ids entries must be integers")
+            flat.extend(int(i) for i in row.reshape(-1))
+            offs.append(len(flat))
+        ids = np.asarray(flat, dtype=np.int64)
+        offs = np.asarray(offs, dtype=np.int64)
+    else:
+        arr = sampled_ids
+        if _is_torch(arr):
+            arr = arr.detach().cpu().numpy()
+        arr = np.asarray(arr)
+        if arr.ndim != 2:
+            raise ValueError("sampled_ids must be per-row sequences, a 2-D array, "
+                             "or flat ids plus ids_offsets")
+        if arr.shape[0] != rows:
+            raise ValueError("sampled_ids must have one entry per row")
+        if arr.size and not np.issubdtype(arr.dtype, np.integer):
+            raise TypeError("sampled_ids entries must be integers")
+        ids = np.ascontiguousarray(arr, dtype=np.int64).reshape(-1)
+        offs = np.arange(rows + 1, dtype=np.int64) * arr.shape[1]
+    if ids.size and (ids.min() < 0 or ids.max() >= n):
+        raise ValueError(f"sampled_ids values must be in [0, {n})")
+    return ids, offs
+
+
+def argmax(x, *, cuda=False):
+    """Index of the largest element (earliest index on ties)."""
+    if _on_gpu(x):
+        _logits_f32(x, "x")
+        if x.ndim != 1:
+            raise ValueError("x must be 1-D for argmax")
+        if x.numel() == 0:
+            raise ValueError("argmax of empty input")
+        out = torch.empty(1, dtype=torch.int32, device=x.device)
+        _fusedtok.argmax_launch(x.data_ptr(), x.numel(), out.data_ptr(), _stream())
+        return int(out.item())
+    arr = _host_f32(x, "x")
+    if arr.ndim != 1:
+        raise ValueError("x must be 1-D for argmax")
+    if arr.size == 0:
+        raise ValueError("argmax of empty input")
+    return argmax(_upload(arr, _need_device()))
+
+
+def argmax_batched(x, *, cuda=False):
+    """Row-wise argmax of ``[rows, vocab]`` float32 logits, earliest index on
+    ties; one launch. GPU input: an int64 GPU tensor, no host sync."""
+    if _on_gpu(x):
+        _logits_f32(x, "x")
+        if x.ndim != 2:
+            raise ValueError("x must be 2-D [rows, vocab] for argmax_batched")
+        if x.shape[1] == 0:
+            raise ValueError("argmax of empty input")
+        rows, n = x.shape
+        out = torch.empty(rows, dtype=torch.int64, device=x.device)
+        if rows:
+            _fusedtok.argmax_batched_launch(x.data_ptr(), rows, n, out.data_ptr(), _stream())
+        return out
+    arr = _host_f32(x, "x")
+    if arr.ndim != 2:
+        raise ValueError("x must be 2-D [rows, vocab] for argmax_batched")
+    if arr.shape[1] == 0:
+        raise ValueError("argmax of empty input")
+    return _result(argmax_batched(_upload(arr, _need_device())), x)
+
+
+def sample_topp(logits, p, *, temperature=1.0, seed=0, cuda=False):
+    """Fused nucleus sampling: softmax of ``logits / temperature``, truncated
+    to the smallest top-p nucleus, inverse-CDF draw at a splitmix hash
+    uniform of ``seed``. Deterministic per seed. Returns the token id."""
+    _sampling_params(p, temperature)
+    if _on_gpu(logits):
+        _logits_f32(logits)
+        if logits.ndim != 1:
+            raise ValueError("logits must be 1-D")
+        if logits.numel() == 0:
+            raise ValueError("sample of empty logits")
+        out = torch.empty(1, dtype=torch.int64, device=logits.device)
+        _fusedtok.sample_topp_launch(logits.data_ptr(), logits.numel(), float(p),
+                                     float(temperature), int(seed), out.data_ptr(), _stream())
+        return int(out.item())
+    arr = _host_logits(logits, 1, "logits must be 1-D")
+    if arr.size == 0:
+        raise ValueError("sample of empty logits")
+    return sample_topp(_upload(arr, _need_device()), p, temperature=temperature, seed=seed)
+
+
+def _seeds_dev(seeds, rows, device):
+    s = _batch_seeds(seeds, rows)
+    return torch.from_numpy(s).to(device)   # int64 bits = the uint64 seeds
+
+
+def sample_topp_batched(logits, p, *, temperature=1.0, seeds=None, cuda=False,
+                        device_out=False):
+    """Nucleus sampling of every row of ``[rows, vocab]`` float32 logits, one
+    workgroup per row, one launch. ``seeds``: one per row (None: 0..rows-1).
+    Returns int64 tokens on the host (the reference's contract); build
+    addition ``device_out=True`` returns them as a GPU tensor, no sync."""
+    _sampling_params(p, temperature)
+    if _on_gpu(logits):
+        _logits_f32(logits)
+        if logits.ndim != 2:
+            raise ValueError("logits must be 2-D [rows, vocab]")
+        rows, n = logits.shape
+        sd = _seeds_dev(seeds, rows, logits.device)
+        out = torch.empty(rows, dtype=torch.int64, device=logits.device)
+        if rows:
+            if n == 0:
+                raise ValueError("sample of empty logits")
+            _fusedtok.sample_topp_batched_launch(logits.data_ptr(), rows, n, float(p),
+                                                 float(temperature), sd.data_ptr(),
+                                                 out.data_ptr(), _stream())
+        return out if device_out else out.cpu()
+    arr = _host_logits(logits, 2, "logits must be 2-D [rows, vocab]")
+    res = sample_topp_batched(_upload(arr, _need_device()), p, temperature=temperature,
+                              seeds=seeds)
+    return res if _is_torch(logits) else res.numpy()
+
+
+def decode_step(logits, sampled_ids, penalty=1.0, *, p=0.9, temperature=1.0, seed=0,
+                cuda=False):
+    """Fused decode step: CTRL repetition penalty over ``sampled_ids`` (each
+    distinct id once), then ``/ temperature``, then nucleus sampling, in one
+    launch. Returns the token id; deterministic per seed."""
+    _sampling_params(p, temperature, penalty)
+    if _on_gpu(logits):
+        _logits_f32(logits)
+        if logits.ndim != 1:
+            raise ValueError("logits must be 1-D")
+        n = logits.numel()
+        if n == 0:
+            raise ValueError("sample of empty logits")
+        ids = _ids_arg(sampled_ids, n, logits.device)
+        out = torch.empty(1, dtype=torch.int64, device=logits.device)
+        _fusedtok.decode_step_launch(logits.data_ptr(), ids.data_ptr() if ids.numel() else None,
+                                     n, ids.numel(), float(penalty), float(p),
+                                     float(temperature), int(seed), out.data_ptr(), _stream())
+        return int(out.item())
+    arr = _host_logits(logits, 1, "logits must be 1-D")
+    if arr.size == 0:
+        raise ValueError("sample of empty logits")
+    dev = _need_device()
+    ids = _ids_arg(sampled_ids, arr.size, dev)
+    return decode_step(_upload(arr, dev), ids, penalty, p=p, temperature=temperature,
+                       seed=seed)
+
+
+def decode_step_batched(logits, sampled_ids, penalty=1.0, *, p=0.9, temperature=1.0,
+                        seeds=None, ids_offsets=None, cuda=False, device_out=False):
+    """The fused decode step for every row of ``[rows, vocab]`` float32
+    logits, one workgroup per row, one launch. ``sampled_ids``: per-row
+    histories (ragged sequences, a 2-D array, or flat ids with
+    ``ids_offsets``). Returns int64 tokens on the host (the reference's
+    contract); build addition ``device_out=True`` keeps them on the GPU."""
+    _sampling_params(p, temperature, penalty)
+    if _on_gpu(logits):
+        _logits_f32(logits)
+        if logits.ndim != 2:
+            raise ValueError("logits must be 2-D [rows, vocab]")
+        rows, n = logits.shape
+        ids, offs = _batch_ids(sampled_ids, ids_offsets, rows, n)
+        sd = _seeds_dev(seeds, rows, logits.device)
+        out = torch.empty(rows, dtype=torch.int64, device=logits.device)
+        if rows:
+            if n == 0:
+                raise ValueError("sample of empty logits")
+            ids_t = torch.from_numpy(ids).to(logits.device)
+            offs_t = torch.from_numpy(offs).to(logits.device)
+            _fusedtok.decode_step_batched_launch(
+                logits.data_ptr(), rows, n, ids_t.data_ptr() if ids.size else None,
+                offs_t.data_ptr(), float(penalty), float(p), float(temperature),
+                sd.data_ptr(), out.data_ptr(), _stream())
+        return out if device_out else out.cpu()
+    arr = _host_logits(logits, 2, "logits must be 2-D [rows, vocab]")
+    res = decode_step_batched(_upload(arr, _need_device()), sampled_ids, penalty, p=p,
+                              temperature=temperature, seeds=seeds, ids_offsets=ids_offsets)
+    return res if _is_torch(logits) else res.numpy()

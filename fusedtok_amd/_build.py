@@ -39,6 +39,7 @@ HIP_SOURCES = [
     "norm_rope_act.hip",
     "fused.hip",
     "prefill.hip",
+    "sampling.hip",
 ]
 
 HIP_FLAGS = [

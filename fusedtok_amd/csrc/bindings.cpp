@@ -195,6 +195,57 @@ PYBIND11_MODULE(_fusedtok, m) {
           py::arg("sa_dev"), py::arg("sb_dev"), py::arg("qy"), py::arg("out_scale"),
           py::arg("n"), py::arg("stream") = 0);
 
+    // ---- sampling -----------------------------------------------------------
+    m.def("argmax_launch",
+          [](uintptr_t x, int n, uintptr_t out, uintptr_t stream) {
+              check(ft_argmax_launch(P<const float>(x), n, P<int>(out), stream));
+          },
+          py::arg("x"), py::arg("n"), py::arg("out"), py::arg("stream") = 0);
+    m.def("argmax_batched_launch",
+          [](uintptr_t x, int rows, int n, uintptr_t out, uintptr_t stream) {
+              check(ft_argmax_batched_launch(P<const float>(x), rows, n, P<long long>(out),
+                                             stream));
+          },
+          py::arg("x"), py::arg("rows"), py::arg("n"), py::arg("out"), py::arg("stream") = 0);
+    m.def("sample_topp_launch",
+          [](uintptr_t x, int n, float p, float t, unsigned long long seed, uintptr_t out,
+             uintptr_t stream) {
+              check(ft_sample_topp_launch(P<const float>(x), n, p, t, seed, P<long long>(out),
+                                          stream));
+          },
+          py::arg("x"), py::arg("n"), py::arg("p"), py::arg("temperature"), py::arg("seed"),
+          py::arg("out"), py::arg("stream") = 0);
+    m.def("sample_topp_batched_launch",
+          [](uintptr_t x, int rows, int n, float p, float t, uintptr_t seeds, uintptr_t out,
+             uintptr_t stream) {
+              check(ft_sample_topp_batched_launch(P<const float>(x), rows, n, p, t,
+                                                  P<const unsigned long long>(seeds),
+                                                  P<long long>(out), stream));
+          },
+          py::arg("x"), py::arg("rows"), py::arg("n"), py::arg("p"), py::arg("temperature"),
+          py::arg("seeds"), py::arg("out"), py::arg("stream") = 0);
+    m.def("decode_step_launch",
+          [](uintptr_t x, py::object ids, int n, int m_, float penalty, float p, float t,
+             unsigned long long seed, uintptr_t out, uintptr_t stream) {
+              check(ft_decode_step_launch(P<const float>(x), P<const long long>(opt_ptr(ids)),
+                                          n, m_, penalty, p, t, seed, P<long long>(out),
+                                          stream));
+          },
+          py::arg("x"), py::arg("ids"), py::arg("n"), py::arg("m"), py::arg("penalty"),
+          py::arg("p"), py::arg("temperature"), py::arg("seed"), py::arg("out"),
+          py::arg("stream") = 0);
+    m.def("decode_step_batched_launch",
+          [](uintptr_t x, int rows, int n, py::object ids, uintptr_t offs, float penalty,
+             float p, float t, uintptr_t seeds, uintptr_t out, uintptr_t stream) {
+              check(ft_decode_step_batched_launch(
+                  P<const float>(x), rows, n, P<const long long>(opt_ptr(ids)),
+                  P<const long long>(offs), penalty, p, t, P<const unsigned long long>(seeds),
+                  P<long long>(out), stream));
+          },
+          py::arg("x"), py::arg("rows"), py::arg("n"), py::arg("ids"), py::arg("offs"),
+          py::arg("penalty"), py::arg("p"), py::arg("temperature"), py::arg("seeds"),
+          py::arg("out"), py::arg("stream") = 0);
+
     // ---- qgemm --------------------------------------------------------------
     m.def("qgemm_launch",
           [](uintptr_t a, uintptr_t b, uintptr_t y, int mm, int n, int k,

@@ -1,0 +1,551 @@
+// Post-logits sampling step for gfx950: argmax (greedy), nucleus sampling
+// (sample_topp) and the fused decode step (repetition penalty ->
+// temperature -> nucleus sampling), single row or one workgroup per row.
+//
+// Semantics (reference sampling.cu:103-120,466-516,1030-1081, topk.cu:5677,
+// cuda_util.cuh:69-76): the value of token i is
+//     v_i = l_i' * (1/T),  l_i' = (i penalised) ? (l_i > 0 ? l_i / pen : l_i * pen) : l_i
+// tokens are ordered by (v desc, index asc), masses are exp(v - max); the
+// nucleus is the shortest prefix of that order whose mass reaches p * total,
+// and the token is where the prefix mass first reaches u * nucleus mass,
+// u = splitmix_uniform(seed).
+//
+// Algorithm (one 1024-thread workgroup per row; no sort of the vocabulary):
+//   - masses are fixed point, q_i = rint(exp(v_i - max) * 2^40) in 64-bit
+//     integers, so every sum is exact and order-free: the result is
+//     deterministic per seed (no float atomics);
+//   - one pass bins every token by its distance from the maximum in 1/64-nat
+//     steps (2048 bins; the last takes everything from ~32 nats on, whose
+//     mass is 0) with the bins' mass and count; bins are contiguous ranges
+//     of the order, so a scan over them finds the bin where a prefix mass
+//     crosses a threshold;
+//   - the crossing bin's tokens are gathered into LDS (<= 4096), sorted by
+//     the exact order key (value bits, then ~index) with a bitonic network,
+//     and scanned; a larger crossing bin (nearly flat logits) is resolved by
+//     8-bit radix passes over the exact key, restricted to that bin;
+//   - the nucleus cut and the draw are two such threshold queries, the
+//     draw's threshold being u * (prefix mass through the cut).
+// Compared with the reference CPU path (float sums in sorted order, host
+// exp), the token is the same except when a threshold lands within float
+// rounding of a prefix boundary - the limit the reference states for its
+// own GPU path.
+#include "ft_common.hpp"
+
+#include <cstdlib>
+
+namespace ft {
+namespace {
+
+typedef unsigned long long u64;
+
+constexpr int kSmpNT = 1024;
+constexpr int kDistBins = 2048;
+constexpr float kDistScale = 64.0f;       // bins per nat
+constexpr int kGather = 4096;             // exact-sort capacity of one bin
+constexpr int kMaxBitmapVocab = 1 << 19;  // penalty bitmap in LDS (64 KB)
+constexpr float kFx = 1099511627776.0f;   // 2^40: fixed-point mass unit
+
+__device__ __forceinline__ float splitmix_uniform(u64 seed) {
+    u64 z = seed + 0x9E3779B97F4A7C15ULL;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    z ^= z >> 31;
+    return (float)((z >> 11) * (1.0 / 9007199254740992.0));
+}
+
+struct SampleRow {
+    const float* x;
+    int n;
+    float inv_t;
+    float pen;
+    const unsigned* bits;  // penalised-token bitmap in LDS, or null
+    // value of token i from its raw logit l
+    __device__ __forceinline__ float val_of(int i, float l) const {
+        if (bits && ((bits[i >> 5] >> (i & 31)) & 1u)) l = l > 0.0f ? l / pen : l * pen;
+        return l * inv_t + 0.0f;  // -0 -> +0: equal values order by index
+    }
+};
+
+// Visit every token of a row as f(i, v_i): 16-byte loads, four in flight
+// per thread (the rows are read several times; one dependent 4-byte load
+// per thread per step left each pass latency-bound).
+template <int NT, typename F>
+__device__ __forceinline__ void row_scan(const SampleRow& row, F&& f) {
+    const float* x = row.x;
+    const int n = row.n;
+    const int tid = threadIdx.x;
+    int done = 0;
+    if (((uintptr_t)x & 15) == 0) {
+        const int n4 = n >> 2;
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        int c = tid;
+        for (; c + 3 * NT < n4; c += 4 * NT) {
+            float4 q[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) q[u] = x4[c + u * NT];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = 4 * (c + u * NT);
+                f(i, row.val_of(i, q[u].x));
+                f(i + 1, row.val_of(i + 1, q[u].y));
+                f(i + 2, row.val_of(i + 2, q[u].z));
+                f(i + 3, row.val_of(i + 3, q[u].w));
+            }
+        }
+        for (; c < n4; c += NT) {
+            const float4 q = x4[c];
+            const int i = 4 * c;
+            f(i, row.val_of(i, q.x));
+            f(i + 1, row.val_of(i + 1, q.y));
+            f(i + 2, row.val_of(i + 2, q.z));
+            f(i + 3, row.val_of(i + 3, q.w));
+        }
+        done = 4 * n4;
+    }
+    for (int i = done + tid; i < n; i += NT) f(i, row.val_of(i, x[i]));
+}
+
+// order key: larger = earlier in the (value desc, index asc) order
+__device__ __forceinline__ u64 order_key(float v, int i) {
+    const unsigned b = __float_as_uint(v);
+    const unsigned o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((u64)o << 32) | (unsigned)(~(unsigned)i);
+}
+__device__ __forceinline__ int key_index(u64 k) { return (int)~(unsigned)(k & 0xffffffffu); }
+
+// q = trunc(exp(v - vmax) * 2^40): v_exp_f32 on (v - vmax) log2(e), then
+// the product s < 2^41 split into 32-bit halves, each converted exactly
+// (s - hi 2^32 is exact: s >= 2^32 has an exponent of at least 9)
+__device__ __forceinline__ u64 mass_fx(float v, float vmax) {
+    const float m = __builtin_amdgcn_exp2f((v - vmax) * 1.4426950408889634f);
+    if (!(m > 0.0f)) return 0ULL;  // underflow or NaN
+    const float s = m * kFx;
+    const unsigned hi = (unsigned)(s * 2.3283064365386963e-10f);  // s / 2^32
+    const unsigned lo = (unsigned)(s - (float)hi * 4294967296.0f);
+    return ((u64)hi << 32) | lo;
+}
+// k >> s with s in [0, 64] (a shift by 64 gives 0)
+__device__ __forceinline__ u64 shr64(u64 k, int s) { return s >= 64 ? 0ULL : k >> s; }
+__device__ __forceinline__ int dist_bin(float v, float vmax) {
+    const float d = (vmax - v) * kDistScale;  // >= 0; +inf for v = -inf
+    return d < (float)(kDistBins - 1) ? (int)d : kDistBins - 1;
+}
+
+struct SmpShared {
+    u64 h_mass[kDistBins];
+    u64 g_key[kGather];
+    u64 g_q[kGather];
+    u64 wsum[kSmpNT / 64];
+    unsigned r_cnt[256];
+    u64 r_key, r_mass, r_above;
+    int r_bin, g_n, g_bin, g_cnt;
+    float fred[kSmpNT / 64];
+    unsigned bitmap[kMaxBitmapVocab / 32];
+};
+
+// inclusive scan of one value per thread over the workgroup
+__device__ __forceinline__ u64 block_scan(u64 v, u64* wsum) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const u64 y = __shfl_up(v, o, 64);
+        if (lane >= o) v += y;
+    }
+    if (lane == 63) wsum[wave] = v;
+    __syncthreads();
+    u64 off = 0;
+    for (int w = 0; w < wave; ++w) off += wsum[w];
+    __syncthreads();
+    return v + off;
+}
+
+template <bool MAX>
+__device__ __forceinline__ u64 block_minmax(u64 v, u64* wsum) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const u64 y = __shfl_xor(v, o, 64);
+        v = MAX ? (y > v ? y : v) : (y < v ? y : v);
+    }
+    if (lane == 0) wsum[wave] = v;
+    __syncthreads();
+    u64 r = wsum[0];
+    for (int w = 1; w < kSmpNT / 64; ++w) r = MAX ? (wsum[w] > r ? wsum[w] : r) : (wsum[w] < r ? wsum[w] : r);
+    __syncthreads();
+    return r;
+}
+
+// Smallest prefix of the order whose mass reaches T (1 <= T <= total):
+// returns its last key in sh.r_key and the prefix mass in sh.r_mass.
+__device__ void select_prefix(const SampleRow& row, float vmax, u64 T, SmpShared& sh) {
+    const int tid = threadIdx.x;
+    // crossing distance bin: thread t owns bins 2t, 2t + 1 (exactly one
+    // thread matches since 1 <= T <= total; the defaults keep every later
+    // index in range regardless)
+    if (tid == 0) {
+        sh.r_bin = 0;
+        sh.r_above = 0;
+        sh.r_key = 0;
+        sh.r_mass = T;
+    }
+    {
+        const u64 m0 = sh.h_mass[2 * tid], m1 = sh.h_mass[2 * tid + 1];
+        const u64 incl = block_scan(m0 + m1, sh.wsum);
+        const u64 excl = incl - m0 - m1;
+        if (excl < T && T <= incl) {
+            const bool first = excl + m0 >= T;
+            sh.r_bin = first ? 2 * tid : 2 * tid + 1;
+            sh.r_above = first ? excl : excl + m0;
+        }
+        __syncthreads();
+    }
+    const int bin = min(max(sh.r_bin, 0), kDistBins - 1);
+    const u64 above = sh.r_above;
+    // gather the bin and sort it exactly (reused when the previous query
+    // sorted the same bin); a bin with more than kGather tokens goes to the
+    // radix passes below
+    if (sh.g_bin != bin) {
+        if (tid == 0) sh.g_n = 0;
+        __syncthreads();
+        row_scan<kSmpNT>(row, [&](int i, float v) {
+            if (dist_bin(v, vmax) == bin) {
+                const int slot = atomicAdd(&sh.g_n, 1);
+                if (slot < kGather) {
+                    sh.g_key[slot] = order_key(v, i);
+                    sh.g_q[slot] = mass_fx(v, vmax);
+                }
+            }
+        });
+        __syncthreads();
+        const int gcnt = sh.g_n;
+        if (gcnt <= kGather) {
+            int np2 = 1;
+            while (np2 < gcnt) np2 <<= 1;
+            for (int i = gcnt + tid; i < np2; i += kSmpNT) {
+                sh.g_key[i] = 0;
+                sh.g_q[i] = 0;
+            }
+            __syncthreads();
+            // bitonic sort, descending by key
+            for (int k = 2; k <= np2; k <<= 1)
+                for (int j = k >> 1; j > 0; j >>= 1) {
+                    for (int i = tid; i < np2; i += kSmpNT) {
+                        const int ixj = i ^ j;
+                        if (ixj > i) {
+                            const u64 a = sh.g_key[i], b = sh.g_key[ixj];
+                            const bool up = (i & k) == 0;
+                            if (up ? a < b : a > b) {
+                                sh.g_key[i] = b;
+                                sh.g_key[ixj] = a;
+                                const u64 t = sh.g_q[i];
+                                sh.g_q[i] = sh.g_q[ixj];
+                                sh.g_q[ixj] = t;
+                            }
+                        }
+                    }
+                    __syncthreads();
+                }
+        }
+        if (tid == 0) {
+            sh.g_cnt = gcnt;
+            sh.g_bin = gcnt <= kGather ? bin : -2;
+        }
+        __syncthreads();
+    }
+    if (sh.g_bin == bin) {
+        // scan the sorted bin: thread t owns entries 4t .. 4t + 3
+        const int c = sh.g_cnt;
+        u64 q[4], local = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * tid + e;
+            q[e] = i < c ? sh.g_q[i] : 0;
+            local += q[e];
+        }
+        const u64 incl = block_scan(local, sh.wsum) + above;
+        u64 run = incl - local;
+        if (run < T && T <= incl) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (run < T && T <= run + q[e]) {
+                    sh.r_key = sh.g_key[4 * tid + e];
+                    sh.r_mass = run + q[e];
+                }
+                run += q[e];
+            }
+        }
+        __syncthreads();
+        return;
+    }
+    // large bin: radix passes over the exact key, restricted to the bin
+    u64 kmax = 0, kmin = ~0ULL;
+    row_scan<kSmpNT>(row, [&](int i, float v) {
+        if (dist_bin(v, vmax) == bin) {
+            const u64 k = order_key(v, i);
+            kmax = k > kmax ? k : kmax;
+            kmin = k < kmin ? k : kmin;
+        }
+    });
+    kmax = block_minmax<true>(kmax, sh.wsum);
+    kmin = block_minmax<false>(kmin, sh.wsum);
+    const int hb = 63 - __clzll(kmax ^ kmin);  // highest differing bit (cnt > 1: keys unique)
+    int shift = hb >= 7 ? hb - 7 : 0;
+    int width = hb - shift + 1;
+    u64 prefix = shr64(kmax, hb + 1);          // bits above hb (shared by the whole bin)
+    u64 above_r = above;
+    u64* hm = sh.g_key;                        // 256 bins of mass
+    u64* hk = sh.g_q;                          // 256 bins of max key
+    unsigned* hc = sh.r_cnt;                   // 256 bins of count
+    while (true) {
+        for (int b = tid; b < 256; b += kSmpNT) {
+            hm[b] = 0;
+            hk[b] = 0;
+            hc[b] = 0;
+        }
+        __syncthreads();
+        row_scan<kSmpNT>(row, [&](int i, float v) {
+            if (dist_bin(v, vmax) != bin) return;
+            const u64 k = order_key(v, i);
+            if (shr64(k, shift + width) != prefix) return;
+            const int b = (int)((k >> shift) & ((1u << width) - 1u));
+            atomicAdd(&hm[b], mass_fx(v, vmax));
+            atomicAdd(&hc[b], 1u);
+            atomicMax(&hk[b], k);
+        });
+        __syncthreads();
+        // crossing digit from the top: thread t (< 256) owns digit 255 - t
+        if (tid == 0) sh.r_bin = 0;
+        {
+            const int d = 255 - tid;
+            const u64 m = tid < 256 ? hm[d] : 0;
+            const u64 incl = block_scan(m, sh.wsum) + above_r;
+            const u64 excl = incl - m;
+            if (tid < 256 && excl < T && T <= incl) {
+                sh.r_bin = d;
+                sh.r_above = excl;
+            }
+            __syncthreads();
+        }
+        const int d = sh.r_bin & 255;
+        above_r = sh.r_above;
+        prefix = (prefix << width) | (u64)d;
+        if (hc[d] == 1u || shift == 0) {
+            if (tid == 0) {
+                sh.r_key = shift == 0 ? prefix : hk[d];
+                sh.r_mass = above_r + hm[d];
+            }
+            __syncthreads();
+            // the gather buffers held the radix bins: never reuse them
+            if (tid == 0) sh.g_bin = -2;
+            __syncthreads();
+            return;
+        }
+        width = shift >= 8 ? 8 : shift;
+        shift -= width;
+        __syncthreads();
+    }
+}
+
+// One row per workgroup. ids/offs: penalised token ids of row r at
+// ids[offs[r] .. offs[r + 1]) (offs null: ids[0 .. m_single)); seeds: one
+// per row (null: seed0 for a single row).
+__global__ __launch_bounds__(kSmpNT) void sample_topp_rows(
+    const float* __restrict__ x, int n, float p, float inv_t, float pen,
+    const long long* __restrict__ ids, const long long* __restrict__ offs, int m_single,
+    const u64* __restrict__ seeds, u64 seed0, long long* __restrict__ out) {
+    __shared__ SmpShared sh;
+    const int r = blockIdx.x;
+    const int tid = threadIdx.x;
+    SampleRow row{x + (size_t)r * n, n, inv_t, pen, nullptr};
+    const bool penal = ids != nullptr && pen != 1.0f;
+    if (penal) {
+        for (int w = tid; w < (n + 31) / 32; w += kSmpNT) sh.bitmap[w] = 0u;
+        __syncthreads();
+        const long long a = offs ? offs[r] : 0;
+        const long long b = offs ? offs[r + 1] : m_single;
+        for (long long j = a + tid; j < b; j += kSmpNT) {
+            const long long id = ids[j];
+            if (id >= 0 && id < n) atomicOr(&sh.bitmap[id >> 5], 1u << (id & 31));  // others dropped
+        }
+        __syncthreads();
+        row.bits = sh.bitmap;
+    }
+    // row maximum
+    float vmax = -INFINITY;
+    row_scan<kSmpNT>(row, [&](int, float v) { vmax = fmaxf(vmax, v); });
+    vmax = block_max<kSmpNT>(vmax, sh.fred);
+    if (!(vmax > -INFINITY)) {
+        // every value -inf (or NaN): the reference's float path never
+        // reaches its cut and returns the last token of the order
+        if (tid == 0) out[r] = n - 1;
+        return;
+    }
+    // distance histogram (mass and count per bin)
+    for (int b = tid; b < kDistBins; b += kSmpNT) sh.h_mass[b] = 0;
+    if (tid == 0) sh.g_bin = -1;
+    __syncthreads();
+    row_scan<kSmpNT>(row, [&](int, float v) {
+        const u64 q = mass_fx(v, vmax);
+        if (q) atomicAdd(&sh.h_mass[dist_bin(v, vmax)], q);
+    });
+    __syncthreads();
+    u64 total;
+    {
+        const u64 incl = block_scan(sh.h_mass[2 * tid] + sh.h_mass[2 * tid + 1], sh.wsum);
+        if (tid == kSmpNT - 1) sh.r_mass = incl;
+        __syncthreads();
+        total = sh.r_mass;
+        __syncthreads();
+    }
+    // nucleus cut: prefix mass >= p * total
+    double tc = ceil((double)p * (double)total);
+    u64 T = tc < 1.0 ? 1ULL : (u64)tc;
+    if (T > total) T = total;
+    select_prefix(row, vmax, T, sh);
+    const u64 nucleus = sh.r_mass;
+    // draw: prefix mass >= u * nucleus mass
+    const float u = splitmix_uniform(seeds ? seeds[r] : seed0);
+    double td = ceil((double)u * (double)nucleus);
+    T = td < 1.0 ? 1ULL : (u64)td;
+    if (T > nucleus) T = nucleus;
+    select_prefix(row, vmax, T, sh);
+    if (tid == 0) out[r] = key_index(sh.r_key);
+}
+
+// argmax per row (earliest index on ties): a sequential scan with strict >
+// keeps index 0 when x[0] is NaN and never picks a NaN elsewhere, so NaN
+// counts as -inf except at index 0.
+constexpr int kArgNT = 1024;
+
+template <typename OUT>
+__global__ __launch_bounds__(kArgNT) void argmax_rows(const float* __restrict__ x, int n,
+                                                      OUT* __restrict__ out) {
+    __shared__ float sv[kArgNT / 64];
+    __shared__ int si[kArgNT / 64];
+    const SampleRow row{x + (size_t)blockIdx.x * n, n, 1.0f, 1.0f, nullptr};
+    const int tid = threadIdx.x;
+    float bv = -INFINITY;
+    int bi = n;  // sentinel: no candidate
+    row_scan<kArgNT>(row, [&](int i, float v) {
+        if (v != v) v = -INFINITY;
+        if (v > bv || (v == bv && i < bi)) {
+            bv = v;
+            bi = i;
+        }
+    });
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = bv;
+        si[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kArgNT / 64; ++w)
+            if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) {
+                bv = sv[w];
+                bi = si[w];
+            }
+        const float x0 = row.x[0];
+        out[blockIdx.x] = (OUT)((x0 != x0 || bi >= n) ? 0 : bi);
+    }
+}
+
+void sampling_check(int rows, int n, float p, float t) {
+    if (rows < 0) inval("rows must be >= 0");
+    if (n <= 0) inval("sample of empty logits");
+    if (!(p > 0.0f && p <= 1.0f)) inval("p must be in (0, 1]");
+    if (!(t > 0.0f)) inval("temperature must be > 0");
+}
+
+void topp_launch(const float* x, int rows, int n, float p, float t, float pen,
+                 const long long* ids, const long long* offs, int m, const u64* seeds,
+                 u64 seed0, long long* out, hipStream_t s) {
+    sampling_check(rows, n, p, t);
+    if (!(pen > 0.0f)) inval("penalty must be > 0");
+    if (m < 0) inval("id count must be >= 0");
+    const bool penal = pen != 1.0f && ((offs != nullptr) || m > 0);
+    if (penal && n > kMaxBitmapVocab)
+        inval("vocabulary too large for the penalty bitmap (n <= 524288)");
+    if (rows == 0) return;
+    if (!x || !out) inval("sampling: null operand");
+    if (penal && !ids) inval("sampling: null token ids");
+    const float inv_t = 1.0f / t;  // the reference's order (inv_t = 1.0f / t)
+    sample_topp_rows<<<(unsigned)rows, kSmpNT, 0, s>>>(
+        x, n, p, inv_t, pen, penal ? ids : nullptr, penal ? offs : nullptr, m, seeds, seed0, out);
+    launch_check("sampling kernel launch");
+}
+
+}  // namespace
+}  // namespace ft
+
+extern "C" {
+
+int ft_argmax_launch(const float* x, int n, int* out, uintptr_t stream) {
+    return ft::guarded([&] {
+        if (n <= 0) ft::inval("argmax of empty vector");
+        if (!x || !out) ft::inval("argmax: null operand");
+        ft::argmax_rows<int><<<1, ft::kArgNT, 0, ft::as_stream(stream)>>>(x, n, out);
+        ft::launch_check("argmax kernel launch");
+    });
+}
+
+int ft_argmax_batched_launch(const float* x, int rows, int n, long long* out,
+                             uintptr_t stream) {
+    return ft::guarded([&] {
+        if (rows < 0) ft::inval("rows must be >= 0");
+        if (n <= 0) ft::inval("argmax of empty vector");
+        if (rows == 0) return;
+        if (!x || !out) ft::inval("argmax: null operand");
+        ft::argmax_rows<long long><<<(unsigned)rows, ft::kArgNT, 0, ft::as_stream(stream)>>>(x, n, out);
+        ft::launch_check("argmax kernel launch");
+    });
+}
+
+int ft_sample_topp_launch(const float* x, int n, float p, float t, unsigned long long seed,
+                          long long* out, uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::topp_launch(x, 1, n, p, t, 1.0f, nullptr, nullptr, 0, nullptr, seed, out,
+                        ft::as_stream(stream));
+    });
+}
+
+int ft_sample_topp_batched_launch(const float* x, int rows, int n, float p, float t,
+                                  const unsigned long long* seeds, long long* out,
+                                  uintptr_t stream) {
+    return ft::guarded([&] {
+        if (rows > 0 && !seeds) ft::inval("sampling: null seeds");
+        ft::topp_launch(x, rows, n, p, t, 1.0f, nullptr, nullptr, 0, seeds, 0, out,
+                        ft::as_stream(stream));
+    });
+}
+
+int ft_decode_step_launch(const float* x, const long long* ids, int n, int m, float penalty,
+                          float p, float t, unsigned long long seed, long long* out,
+                          uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::topp_launch(x, 1, n, p, t, penalty, ids, nullptr, m, nullptr, seed, out,
+                        ft::as_stream(stream));
+    });
+}
+
+int ft_decode_step_batched_launch(const float* x, int rows, int n, const long long* ids,
+                                  const long long* offs, float penalty, float p, float t,
+                                  const unsigned long long* seeds, long long* out,
+                                  uintptr_t stream) {
+    return ft::guarded([&] {
+        if (rows > 0 && !seeds) ft::inval("sampling: null seeds");
+        if (rows > 0 && !offs) ft::inval("sampling: null id offsets");
+        ft::topp_launch(x, rows, n, p, t, penalty, ids, offs, 0, seeds, 0, out,
+                        ft::as_stream(stream));
+    });
+}
+
+}  // extern "C"

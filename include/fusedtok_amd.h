@@ -347,6 +347,49 @@ int ft_rope_kv_append_paged_launch(const void* qkv, int dtype, long long ld,
                                    float theta, int pos_offset, int neox,
                                    uintptr_t stream);
 
+/* ------------------------------------------------------------------ */
+/* Post-logits sampling                                                */
+/* Greedy argmax: index of the first maximum of each row (a scan with  */
+/* strict >: NaN never wins except at index 0). Replaces argmax_launch */
+/* (cuda_launch.hpp:275) and argmax_batched_launch (:287-288).         */
+/* ------------------------------------------------------------------ */
+int ft_argmax_launch(const float* x, int n, int* out, uintptr_t stream);
+int ft_argmax_batched_launch(const float* x, int rows, int n, long long* out,
+                             uintptr_t stream);
+
+/* Nucleus sampling of float32 logits: order tokens by (logit/T desc,   */
+/* index asc), masses exp(v - max), nucleus = the shortest prefix whose */
+/* mass reaches p * total, token = where the prefix mass first reaches  */
+/* splitmix_uniform(seed) * nucleus mass (splitmix64 finalised to a     */
+/* float in [0,1), reference cuda_util.cuh:69-76). Deterministic per    */
+/* seed. p in (0,1], t > 0. The token is written to the DEVICE int64    */
+/* *out without a host sync (the reference launchers return it after a  */
+/* readback). Replaces sample_topp_launch (cuda_launch.hpp:73-74) and   */
+/* sample_topp_batched_launch (:149-152); seeds: one DEVICE uint64 per  */
+/* row.                                                                 */
+int ft_sample_topp_launch(const float* x, int n, float p, float t,
+                          unsigned long long seed, long long* out, uintptr_t stream);
+int ft_sample_topp_batched_launch(const float* x, int rows, int n, float p, float t,
+                                  const unsigned long long* seeds, long long* out,
+                                  uintptr_t stream);
+
+/* Fused decode step: CTRL repetition penalty over the DEVICE int64 ids  */
+/* (each distinct id once, from the original logit: v > 0 ? v/penalty : */
+/* v*penalty; ids outside [0, n) are dropped), then the temperature,    */
+/* then nucleus sampling as above. penalty > 0 (1.0 disables); with a   */
+/* penalty, n <= 524288. Batched: row r's ids are ids[offs[r] ..        */
+/* offs[r+1]) (DEVICE int64 offsets, rows + 1 entries). Replaces        */
+/* decode_step_launch (cuda_launch.hpp:138-141) and                     */
+/* decode_step_batched_launch (:179-183), writing tokens to DEVICE      */
+/* memory without a host sync.                                          */
+int ft_decode_step_launch(const float* x, const long long* ids, int n, int m,
+                          float penalty, float p, float t, unsigned long long seed,
+                          long long* out, uintptr_t stream);
+int ft_decode_step_batched_launch(const float* x, int rows, int n, const long long* ids,
+                                  const long long* offs, float penalty, float p, float t,
+                                  const unsigned long long* seeds, long long* out,
+                                  uintptr_t stream);
+
 #ifdef __cplusplus
 }
 #endif

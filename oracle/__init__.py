@@ -281,3 +281,58 @@ def rope_kv_append_paged(qkv, q_heads, kv_heads, k_pool, v_pool, table, lens,
     kv_append_paged(k_pool, v_pool, table, rot[:, q_heads:],
                     np.ascontiguousarray(heads[:, q_heads + kv_heads:]), lens)
     return rot[:, :q_heads].copy()
+
+
+# ---------------------------------------------------------------------------
+# post-logits sampling
+# ---------------------------------------------------------------------------
+
+
+def splitmix_uniform(seed):
+    """The shared sampler RNG: splitmix64 finalised to a float in [0, 1)."""
+    lib = _load()
+    lib.or_splitmix_uniform.restype = ctypes.c_float
+    return float(lib.or_splitmix_uniform(ctypes.c_ulonglong(seed)))
+
+
+def argmax_batched(x):
+    """argmax_batched_cpu: [rows, n] f32 -> int64 [rows] (earliest index on ties)."""
+    x = _f32(x)
+    rows, n = x.shape
+    out = np.zeros(rows, np.int64)
+    _call("or_argmax_batched", _p(x), rows, n, _p(out))
+    return out
+
+
+def repetition_penalty(logits, ids, penalty):
+    """repetition_penalty_cpu: each distinct id once, from the original logit."""
+    logits = _f32(logits)
+    ids = np.ascontiguousarray(ids, np.int64)
+    y = np.empty_like(logits)
+    _call("or_repetition_penalty", _p(logits), logits.size, _p(ids), ids.size,
+          ctypes.c_float(penalty), _p(y))
+    return y
+
+
+def sample_topp(logits, p, temperature=1.0, seed=0):
+    """sample_topp_cpu -> token id."""
+    logits = _f32(logits)
+    out = ctypes.c_longlong(0)
+    _call("or_sample_topp", _p(logits), logits.size, ctypes.c_float(p),
+          ctypes.c_float(temperature), ctypes.c_ulonglong(seed), ctypes.byref(out))
+    return int(out.value)
+
+
+def decode_step_batched(logits, ids, offs, penalty, p, temperature, seeds):
+    """Per row: repetition_penalty over ids[offs[r]:offs[r+1]], then
+    sample_topp with seeds[r]. offs=None: no ids."""
+    logits = _f32(logits)
+    rows, n = logits.shape
+    ids = np.ascontiguousarray(np.zeros(0) if ids is None else ids, np.int64)
+    offs_a = None if offs is None else np.ascontiguousarray(offs, np.int64)
+    seeds = np.ascontiguousarray(seeds, np.uint64)
+    out = np.zeros(rows, np.int64)
+    _call("or_decode_step_batched", _p(logits), rows, n, _p(ids), _p(offs_a),
+          ctypes.c_float(penalty), ctypes.c_float(p), ctypes.c_float(temperature),
+          _p(seeds), _p(out))
+    return out

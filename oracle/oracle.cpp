@@ -11,6 +11,7 @@
 // Each function cites the reference function it restates. Exported with a
 // flat C ABI for ctypes: int status (0 ok, 1 invalid argument) and a
 // thread-local message from or_last_error().
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -509,6 +510,122 @@ int or_swiglu(const float* g, const float* u, long long n, float* y) {
         for (long long i = 0; i < n; ++i) {
             const float gv = g[i];
             y[i] = gv / (1.0f + std::exp(-gv)) * u[i];
+        }
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Post-logits sampling (reference sampling.cu, topk.cu, cuda_util.cuh).
+// ---------------------------------------------------------------------------
+
+// splitmix64 finalised to a float uniform in [0, 1) (reference
+// cuda_util.cuh:69-76): the shared sampler RNG of the CPU and GPU paths.
+float or_splitmix_uniform(unsigned long long seed) {
+    unsigned long long z = seed + 0x9E3779B97F4A7C15ULL;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    z ^= z >> 31;
+    return (float)((z >> 11) * (1.0 / 9007199254740992.0));
+}
+
+// argmax_batched_cpu (reference sampling.cu:1065-1081): per row the first
+// index of the maximum (a sequential scan with strict >).
+int or_argmax_batched(const float* x, int rows, int n, long long* out) {
+    return run([&] {
+        if (rows < 0) throw Inval{"rows must be >= 0"};
+        if (n <= 0) throw Inval{"argmax of empty vector"};
+        for (int r = 0; r < rows; ++r) {
+            const float* row = x + (size_t)r * n;
+            long long best = 0;
+            for (int i = 1; i < n; ++i)
+                if (row[i] > row[best]) best = i;
+            out[r] = best;
+        }
+    });
+}
+
+// repetition_penalty_cpu (reference sampling.cu:103-120): each distinct id
+// once, from the original logit: v > 0 ? v / penalty : v * penalty.
+int or_repetition_penalty(const float* logits, int n, const long long* ids, int m,
+                          float penalty, float* y) {
+    return run([&] {
+        if (!(penalty > 0.0f)) throw Inval{"penalty must be > 0"};
+        for (int j = 0; j < m; ++j)
+            if (ids[j] < 0 || ids[j] >= n) throw Inval{"token id out of range"};
+        std::memcpy(y, logits, sizeof(float) * (size_t)n);
+        for (int j = 0; j < m; ++j) {
+            const float v = logits[ids[j]];
+            y[ids[j]] = v > 0.0f ? v / penalty : v * penalty;
+        }
+    });
+}
+
+// sample_topp_cpu (reference sampling.cu:466-516): order by (logit/T desc,
+// index asc), float masses exp(v - max) summed in that order, nucleus = the
+// shortest prefix with cum >= p * total, inverse-CDF draw at
+// splitmix_uniform(seed) * nucleus mass.
+static long long topp_row(const float* logits, int n, float p, float t,
+                          unsigned long long seed) {
+    if (n <= 0) throw Inval{"sample of empty logits"};
+    if (!(p > 0.0f && p <= 1.0f)) throw Inval{"p must be in (0, 1]"};
+    if (!(t > 0.0f)) throw Inval{"temperature must be > 0"};
+    std::vector<unsigned int> order((size_t)n);
+    for (int i = 0; i < n; ++i) order[(size_t)i] = (unsigned int)i;
+    const float inv_t = 1.0f / t;
+    std::sort(order.begin(), order.end(), [&](unsigned int a, unsigned int b) {
+        const float va = logits[a] * inv_t, vb = logits[b] * inv_t;
+        if (va != vb) return va > vb;
+        return a < b;
+    });
+    const float row_max = logits[order[0]] * inv_t;
+    auto mass_at = [&](size_t i) { return std::exp(logits[order[i]] * inv_t - row_max); };
+    float total = 0.0f;
+    for (size_t i = 0; i < (size_t)n; ++i) total += mass_at(i);
+    float cum = 0.0f;
+    size_t nucleus = 0;
+    float nucleus_mass = 0.0f;
+    for (size_t i = 0; i < (size_t)n; ++i) {
+        cum += mass_at(i);
+        nucleus = i + 1;
+        if (cum >= p * total) {
+            nucleus_mass = cum;
+            break;
+        }
+    }
+    const float u = or_splitmix_uniform(seed);
+    const float target = u * nucleus_mass;
+    cum = 0.0f;
+    for (size_t i = 0; i < nucleus; ++i) {
+        cum += mass_at(i);
+        if (cum >= target) return (long long)order[i];
+    }
+    return (long long)order[nucleus - 1];
+}
+
+int or_sample_topp(const float* logits, int n, float p, float t, unsigned long long seed,
+                   long long* out) {
+    return run([&] { *out = topp_row(logits, n, p, t, seed); });
+}
+
+// decode_step / decode_step_batched CPU path (reference __init__.py:2410-2412,
+// sampling.cu:1030-1062): repetition_penalty over the row's ids, then
+// sample_topp with that row's seed.
+int or_decode_step_batched(const float* logits, int rows, int n, const long long* ids,
+                           const long long* offs, float penalty, float p, float t,
+                           const unsigned long long* seeds, long long* out) {
+    return run([&] {
+        if (!(penalty > 0.0f)) throw Inval{"penalty must be > 0"};
+        std::vector<float> row((size_t)n);
+        for (int r = 0; r < rows; ++r) {
+            const float* x = logits + (size_t)r * n;
+            const long long a = offs ? offs[r] : 0, b = offs ? offs[r + 1] : 0;
+            std::memcpy(row.data(), x, sizeof(float) * (size_t)n);
+            for (long long j = a; j < b; ++j) {
+                if (ids[j] < 0 || ids[j] >= n) throw Inval{"token id out of range"};
+                const float v = x[ids[j]];
+                row[(size_t)ids[j]] = v > 0.0f ? v / penalty : v * penalty;
+            }
+            out[r] = topp_row(row.data(), n, p, t, seeds[r]);
         }
     });
 }

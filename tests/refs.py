@@ -137,3 +137,39 @@ def bf16_round(a):
 
 def f16_round(a):
     return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def splitmix_uniform(seed):
+    """splitmix64 finalised to a float32 in [0, 1), in Python integers
+    (reference cuda_util.cuh:69-76)."""
+    mask = (1 << 64) - 1
+    z = (seed + 0x9E3779B97F4A7C15) & mask
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
+    z ^= z >> 31
+    return float(np.float32((z >> 11) * (1.0 / 9007199254740992.0)))
+
+
+def ref_topp(logits, p, t=1.0, seed=0):
+    """float64 nucleus sampling with the reference's order and cut rule:
+    returns (token, margin), margin = the smallest distance (relative to the
+    total mass) between the cut or draw threshold and a prefix boundary -
+    a small margin means float rounding may legitimately move the token."""
+    inv_t = np.float32(1.0) / np.float32(t)
+    v = (np.asarray(logits, np.float32) * inv_t).astype(np.float32)
+    idx = np.arange(v.size)
+    order = np.lexsort((idx, -v.astype(np.float64)))
+    m = np.exp(v[order].astype(np.float64) - float(v[order[0]]))
+    cum = np.cumsum(m)
+    total = cum[-1]
+    thr = p * total
+    k = int(np.searchsorted(cum, thr, side="left"))
+    k = min(k, v.size - 1)
+    nucleus = cum[k]
+    margin = min(abs(cum[k] - thr), abs(thr - (cum[k - 1] if k else 0.0))) / total
+    target = splitmix_uniform(seed) * nucleus
+    j = int(np.searchsorted(cum[:k + 1], target, side="left"))
+    j = min(j, k)
+    margin = min(margin, abs(cum[j] - target) / total,
+                 abs(target - (cum[j - 1] if j else 0.0)) / total)
+    return int(order[j]), margin

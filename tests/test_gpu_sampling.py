@@ -1,0 +1,170 @@
+"""GPU parity for the post-logits step: argmax / argmax_batched (bit-exact
+against the oracle), sample_topp / decode_step (single and batched) against
+the CPU oracle (sample_topp_cpu / repetition_penalty_cpu restatement) and a
+float64 restatement of the same rule.
+
+The GPU sums masses exactly (fixed point) and the oracle in float32 in
+sorted order, so a token may differ only where a threshold sits within
+rounding of a prefix boundary: every mismatch must show a float64 margin
+below 1e-4 of the total mass (the reference states the same limit for its
+own GPU path, test_sample_topp.py:115-123)."""
+
+import numpy as np
+import pytest
+import torch
+
+import fusedtok_amd as ft
+import oracle
+from tests import refs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _agree(got, logits, p, temp, seed, pen_ids=None, pen=1.0):
+    x = logits if pen_ids is None else oracle.repetition_penalty(logits, pen_ids, pen)
+    want = oracle.sample_topp(x, p, temp, seed)
+    if got == want:
+        return True
+    _, margin = refs.ref_topp(x, p, temp, seed)
+    return margin < 1e-4
+
+
+def test_argmax_and_batched_bit_exact():
+    x = np.array([[1, 3, 3, 2], [5, 5, 1, 0], [-np.inf] * 4, [np.nan, 9, 1, 2],
+                  [1, np.nan, 7, 7]], np.float32)
+    got = ft.argmax_batched(t(x))
+    assert got.dtype == torch.int64 and got.is_cuda
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle.argmax_batched(x))
+    rng = np.random.default_rng(0)
+    for rows, n in [(1, 1), (3, 777), (64, 128256), (7, 5000)]:
+        y = rng.integers(-50, 50, (rows, n)).astype(np.float32)   # ties everywhere
+        np.testing.assert_array_equal(ft.argmax_batched(t(y)).cpu().numpy(),
+                                      oracle.argmax_batched(y))
+        assert ft.argmax(t(y[0])) == int(oracle.argmax_batched(y[:1])[0])
+    assert ft.argmax([3.0, 1.0, 3.0]) == 0                      # host input, staged
+    with pytest.raises(ValueError):
+        ft.argmax(torch.zeros(0, device=DEV))
+    with pytest.raises(TypeError):
+        ft.argmax_batched(torch.zeros((2, 3), dtype=torch.float64, device=DEV))
+
+
+@pytest.mark.parametrize("n,scale", [(100, 3.0), (2000, 2.0), (32000, 1.5), (128256, 2.0)])
+@pytest.mark.parametrize("p,temp", [(0.9, 1.0), (0.5, 0.7), (1.0, 1.3), (0.95, 0.1)])
+def test_sample_topp_matches_oracle(n, scale, p, temp):
+    rng = np.random.default_rng(n + int(p * 100))
+    logits = (rng.standard_normal(n) * scale).astype(np.float32)
+    lt = t(logits)
+    seeds = [0, 1, 7, 42, 12345, 2**40 + 9]
+    for seed in seeds:
+        tok = ft.sample_topp(lt, p, temperature=temp, seed=seed)
+        assert 0 <= tok < n
+        assert _agree(tok, logits, p, temp, seed), (n, p, temp, seed, tok)
+    # batched rows are the single-row pipeline, one workgroup each
+    rows = np.repeat(logits[None], len(seeds), 0)
+    bt = ft.sample_topp_batched(t(rows), p, temperature=temp, seeds=seeds)
+    assert bt.dtype == torch.int64 and not bt.is_cuda
+    singles = [ft.sample_topp(lt, p, temperature=temp, seed=s) for s in seeds]
+    assert bt.tolist() == singles
+
+
+def test_sample_topp_known_answers_and_determinism():
+    peak = np.array([10.0] + [0.0] * 49, np.float32)
+    assert {ft.sample_topp(t(peak), 0.9, temperature=0.1, seed=s) for s in range(16)} == {0}
+    assert len({ft.sample_topp(t(peak), 1.0, temperature=1e4, seed=s) for s in range(64)}) > 10
+    # flat logits: token = ceil(u n) - 1 (index order, equal masses)
+    flat = t(np.zeros(32, np.float32))
+    for s in range(40):
+        assert ft.sample_topp(flat, 1.0, seed=s) == max(0, int(np.ceil(refs.splitmix_uniform(s) * 32)) - 1)
+    rng = np.random.default_rng(6)
+    x = t((rng.standard_normal(1000) * 2).astype(np.float32))
+    first = ft.sample_topp(x, 0.9, seed=9)
+    assert all(ft.sample_topp(x, 0.9, seed=9) == first for _ in range(5))
+    # host input is staged through the device
+    assert ft.sample_topp(x.cpu().numpy(), 0.9, seed=9) == first
+
+
+def test_sample_topp_large_flat_bin_radix_path():
+    # 8192 equal logits fall in one distance bin (> the 4096-entry exact
+    # sort): the radix passes over the exact key resolve the index order
+    n = 8192
+    flat = t(np.zeros(n, np.float32))
+    for s in range(20):
+        u = refs.splitmix_uniform(s)
+        want = max(0, int(np.ceil(u * n)) - 1)
+        got = ft.sample_topp(flat, 1.0, seed=s)
+        assert got == want or abs(u * n - round(u * n)) < 1e-3
+    # near-flat: two values interleaved, p cuts inside the top group
+    rng = np.random.default_rng(1)
+    x = np.where(rng.random(20000) < 0.5, 0.0, 0.001).astype(np.float32)
+    for s in range(10):
+        assert _agree(ft.sample_topp(t(x), 0.3, seed=s), x, 0.3, 1.0, s)
+
+
+@pytest.mark.parametrize("pen", [1.0, 1.3, 0.7, 100.0])
+def test_decode_step_matches_oracle(pen):
+    rng = np.random.default_rng(37)
+    n = 3000
+    logits = (rng.standard_normal(n) * 2).astype(np.float32)
+    ids = rng.integers(0, n, size=50)
+    for seed in (0, 11, 99):
+        tok = ft.decode_step(t(logits), t(ids), pen, p=0.9, temperature=0.7, seed=seed)
+        assert _agree(tok, logits, 0.9, 0.7, seed, ids, pen), (pen, seed, tok)
+        # host ids are range-checked and give the same token
+        assert ft.decode_step(t(logits), ids.tolist(), pen, p=0.9, temperature=0.7,
+                              seed=seed) == tok
+
+
+def test_decode_step_batched_matches_rows_and_oracle():
+    rng = np.random.default_rng(41)
+    rows, n = 16, 32000
+    logits = (rng.standard_normal((rows, n)) * 2).astype(np.float32)
+    hist = [rng.integers(0, n, size=int(rng.integers(0, 60))).tolist() for _ in range(rows)]
+    seeds = list(range(100, 100 + rows))
+    got = ft.decode_step_batched(t(logits), hist, 1.25, p=0.9, temperature=0.8, seeds=seeds)
+    assert got.shape == (rows,) and got.dtype == torch.int64
+    for r in range(rows):
+        assert _agree(int(got[r]), logits[r], 0.9, 0.8, seeds[r], np.array(hist[r], np.int64),
+                      1.25), r
+        assert int(got[r]) == ft.decode_step(t(logits[r]), hist[r], 1.25, p=0.9,
+                                             temperature=0.8, seed=seeds[r])
+    # flat ids + offsets and device output give the same tokens
+    flat = np.concatenate([np.array(h, np.int64) for h in hist])
+    offs = np.cumsum([0] + [len(h) for h in hist])
+    dev = ft.decode_step_batched(t(logits), flat, 1.25, p=0.9, temperature=0.8, seeds=seeds,
+                                 ids_offsets=offs, device_out=True)
+    assert dev.is_cuda and dev.cpu().tolist() == got.tolist()
+
+
+def test_decode_step_device_ids_out_of_range_are_dropped():
+    # device ids are trusted (no sync); entries outside [0, n) are dropped
+    rng = np.random.default_rng(38)
+    logits = (rng.standard_normal(3000) * 2).astype(np.float32)
+    good = rng.integers(0, 3000, size=50).tolist()
+    bad = [3000, -7, 2**31 - 1]
+    a = ft.decode_step(t(logits), t(np.array(good + bad, np.int64)), 1.5, p=0.9, seed=4)
+    b = ft.decode_step(t(logits), t(np.array(good, np.int64)), 1.5, p=0.9, seed=4)
+    assert a == b
+    with pytest.raises(ValueError):                       # host ids are checked
+        ft.decode_step(t(logits), good + bad, 1.5, p=0.9, seed=4)
+
+
+def test_sampling_contract():
+    x = t(np.ones(4, np.float32))
+    for kw in [dict(p=0.0), dict(p=1.5), dict(p=0.9, temperature=0.0)]:
+        pp = kw.pop("p")
+        with pytest.raises(ValueError):
+            ft.sample_topp(x, pp, **kw)
+    with pytest.raises(ValueError):
+        ft.sample_topp(t(np.ones((2, 2), np.float32)), 0.9)
+    with pytest.raises(ValueError):
+        ft.decode_step(x, [1], 0.0)
+    with pytest.raises(TypeError):
+        ft.sample_topp(torch.ones(4, dtype=torch.float64, device=DEV), 0.9)
+    with pytest.raises(ValueError):
+        ft.sample_topp_batched(t(np.ones((3, 4), np.float32)), 0.9, seeds=[1, 2])
+    assert ft.sample_topp_batched(t(np.ones((0, 4), np.float32)), 0.9).numel() == 0

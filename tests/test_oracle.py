@@ -523,3 +523,120 @@ def test_pins_catch_round_half_away():
     away = np.sign(x) * np.floor(np.abs(x) + 0.5)
     q, _ = oracle.quantize_int8(np.concatenate([x, [127.0]]).astype(np.float32))
     assert not np.array_equal(q[:4], away.astype(np.int8))
+
+
+# ---------------------------------------------------------------------------
+# post-logits sampling (reference tests/test_sampling.py, test_sample_topp.py,
+# test_decode_step.py, test_argmax_batched.py)
+# ---------------------------------------------------------------------------
+
+
+def test_splitmix_uniform_matches_integer_restatement():
+    for seed in [0, 1, 7, 42, 123, 12345, 2**40 + 3, 2**63 - 1]:
+        assert oracle.splitmix_uniform(seed) == refs.splitmix_uniform(seed)
+    us = [oracle.splitmix_uniform(s) for s in range(2000)]
+    assert min(us) >= 0.0 and max(us) < 1.0 and 0.45 < np.mean(us) < 0.55
+
+
+def test_argmax_batched_ties_nan_and_numpy():
+    # test_sampling.py:79-82 / test_argmax_batched.py:41-53: earliest index
+    x = np.array([[1, 3, 3, 2], [5, 5, 1, 0], [-np.inf, -np.inf, -np.inf, -np.inf],
+                  [np.nan, 9, 1, 2], [1, np.nan, 7, 7]], np.float32)
+    np.testing.assert_array_equal(oracle.argmax_batched(x), [1, 0, 0, 0, 2])
+    rng = np.random.default_rng(0)
+    y = rng.integers(-5, 5, (64, 300)).astype(np.float32)   # many ties
+    np.testing.assert_array_equal(oracle.argmax_batched(y), np.argmax(y, axis=1))
+
+
+def test_repetition_penalty_closed_form():
+    # test_sampling.py:104-125: positive logits divide, negative multiply,
+    # zero unchanged, duplicates applied once, empty ids = identity
+    x = np.array([2.0, -2.0, 0.0, 4.0], np.float32)
+    y = oracle.repetition_penalty(x, [0, 1, 2, 0, 0], 2.0)
+    np.testing.assert_array_equal(y, [1.0, -4.0, 0.0, 4.0])
+    np.testing.assert_array_equal(oracle.repetition_penalty(x, [], 3.0), x)
+    with pytest.raises(ValueError):
+        oracle.repetition_penalty(x, [4], 2.0)
+    with pytest.raises(ValueError):
+        oracle.repetition_penalty(x, [0], 0.0)
+
+
+def test_sample_topp_known_answers():
+    # test_sample_topp.py:37-43: peaked logits at low temperature -> the peak
+    peak = np.array([10.0] + [0.0] * 49, np.float32)
+    assert {oracle.sample_topp(peak, 0.9, 0.1, s) for s in range(16)} == {0}
+    # :45-50: a very high temperature spreads the draws
+    assert len({oracle.sample_topp(peak, 1.0, 1e4, s) for s in range(64)}) > 10
+    # flat logits, p = 1: the order is the index order and every mass is 1,
+    # so the token is the first prefix reaching u * n: ceil(u n) - 1
+    flat = np.zeros(32, np.float32)
+    for s in range(50):
+        u = refs.splitmix_uniform(s)
+        assert oracle.sample_topp(flat, 1.0, 1.0, s) == max(0, int(np.ceil(u * 32)) - 1)
+    # :99-111: parameter contract
+    for args in [(0.0, 1.0), (1.5, 1.0), (0.9, 0.0)]:
+        with pytest.raises(ValueError):
+            oracle.sample_topp(np.ones(4, np.float32), *args)
+    with pytest.raises(ValueError):
+        oracle.sample_topp(np.zeros(0, np.float32), 0.9)
+
+
+def test_sample_topp_matches_float64_reference_and_nucleus():
+    # the oracle against an independent float64 restatement of the same rule;
+    # a differing token is only allowed where a threshold sits within float32
+    # summation error of a prefix boundary
+    rng = np.random.default_rng(5)
+    for n, scale in [(100, 3.0), (2000, 2.0), (50000, 1.0)]:
+        logits = (rng.standard_normal(n) * scale).astype(np.float32)
+        for p, t in [(0.9, 1.0), (0.5, 0.7), (1.0, 1.3)]:
+            for seed in range(25):
+                got = oracle.sample_topp(logits, p, t, seed)
+                want, margin = refs.ref_topp(logits, p, t, seed)
+                assert got == want or margin < 1e-4, (n, p, t, seed, got, want, margin)
+    # test_sample_topp.py:87-96: never outside the nucleus
+    logits = (rng.standard_normal(100) * 3).astype(np.float32)
+    probs = np.exp(logits.astype(np.float64) - logits.max())
+    probs /= probs.sum()
+    order = np.argsort(-probs, kind="stable")
+    nucleus = set(order[:np.searchsorted(np.cumsum(probs[order]), 0.7) + 1].tolist())
+    assert all(oracle.sample_topp(logits, 0.7, 1.0, s) in nucleus for s in range(200))
+
+
+def test_sample_topp_distribution_matches_softmax():
+    # test_sample_topp.py:67-84: frequencies track the renormalised nucleus
+    rng = np.random.default_rng(3)
+    logits = (rng.standard_normal(8) * 2).astype(np.float32)
+    probs = np.exp(logits.astype(np.float64) - logits.max())
+    probs /= probs.sum()
+    n = 6000
+    counts = np.bincount([oracle.sample_topp(logits, 0.95, 1.0, s) for s in range(n)],
+                         minlength=8)
+    order = np.argsort(-probs)
+    keep = order[:np.searchsorted(np.cumsum(probs[order]), 0.95) + 1]
+    kp = probs[keep] / probs[keep].sum()
+    for tok, pr in zip(keep, kp):
+        assert abs(counts[tok] / n - pr) < 5 * np.sqrt(pr * (1 - pr) / n) + 1e-4
+
+
+def test_decode_step_is_penalty_then_topp():
+    # test_decode_step.py:30-60: the composed order; penalty 1.0 or no ids
+    # is plain sample_topp; a heavy penalty moves the draw off the top token
+    rng = np.random.default_rng(31)
+    logits = (rng.standard_normal((3, 900)) * 2).astype(np.float32)
+    ids = rng.integers(0, 900, size=(3, 40))
+    offs = np.arange(4) * 40
+    seeds = np.array([0, 7, 123], np.uint64)
+    for pen in (1.0, 1.3, 0.7):
+        got = oracle.decode_step_batched(logits, ids.reshape(-1), offs, pen, 0.9, 0.8, seeds)
+        for r in range(3):
+            want = oracle.sample_topp(oracle.repetition_penalty(logits[r], ids[r], pen),
+                                      0.9, 0.8, int(seeds[r]))
+            assert got[r] == want
+    plain = oracle.decode_step_batched(logits, None, None, 2.0, 0.9, 1.0, seeds)
+    for r in range(3):
+        assert plain[r] == oracle.sample_topp(logits[r], 0.9, 1.0, int(seeds[r]))
+    top = int(np.argmax(logits[0]))
+    draws = oracle.decode_step_batched(np.repeat(logits[:1], 40, 0), np.array([top] * 40),
+                                       np.arange(41), 100.0, 0.8, 1.0,
+                                       np.arange(40, dtype=np.uint64))
+    assert top not in set(draws.tolist())
