@@ -131,6 +131,33 @@ def test_dequantize_qadd_invalid_arguments(lib):
     assert q(None, None, 1.0, 1.0, None, None, 0, 0) == FT_OK
 
 
+def test_prefill_and_sampling_invalid_arguments(lib):
+    f = lib.ft_attention_prefill_launch_bf16
+    f.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 6 + [ctypes.c_size_t]
+    assert f(None, None, None, None, 1, 5, 2, 8, 64, 1, 0) == FT_EINVAL     # GQA
+    assert f(None, None, None, None, 1, 4, 2, 8, 30, 1, 0) == FT_EINVAL     # dim % 4
+    assert f(None, None, None, None, 1, 4, 2, 8, 516, 1, 0) == FT_EINVAL    # dim > 512
+    assert f(None, None, None, None, 1, 4, 2, 8, 64, 1, 0) == FT_EINVAL     # null
+    assert f(None, None, None, None, 0, 4, 2, 8, 64, 1, 0) == FT_OK         # empty
+    s = lib.ft_sample_topp_launch
+    s.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_float,
+                  ctypes.c_ulonglong, ctypes.c_void_p, ctypes.c_size_t]
+    assert s(None, 8, 0.0, 1.0, 0, None, 0) == FT_EINVAL                   # p
+    assert s(None, 8, 0.9, 0.0, 0, None, 0) == FT_EINVAL                   # temperature
+    assert s(None, 0, 0.9, 1.0, 0, None, 0) == FT_EINVAL                   # empty
+    d = lib.ft_decode_step_launch
+    d.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                  ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_ulonglong,
+                  ctypes.c_void_p, ctypes.c_size_t]
+    assert d(None, None, 8, 1, 0.0, 0.9, 1.0, 0, None, 0) == FT_EINVAL     # penalty
+    assert d(None, None, 1 << 20, 1, 1.5, 0.9, 1.0, 0, None, 0) == FT_EINVAL  # bitmap cap
+    a = lib.ft_argmax_batched_launch
+    a.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                  ctypes.c_size_t]
+    assert a(None, 2, 0, None, 0) == FT_EINVAL
+    assert a(None, 0, 4, None, 0) == FT_OK
+
+
 def test_norm_rope_swiglu_invalid_arguments(lib):
     r = lib.ft_rmsnorm_launch
     r.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_int, ctypes.c_float,
