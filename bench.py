@@ -207,7 +207,7 @@ def bench_c5a(torch, ft, dev, steps, warmup):
                           "peak": INT8_PEAK_TOPS, "unit": "TOPS",
                           "frac": round(tops / INT8_PEAK_TOPS, 4),
                           "traffic": traffic_for("qgemm_c5a"),
-                          "kernel": "qgemm_big_w8"})
+                          "kernel": "qgemm_big_w16"})
 
 
 # ---------------------------------------------------------------------------
@@ -621,7 +621,9 @@ def main():
         log(f"copy: {args.warmup + args.steps} x 1 GiB read + 1 GiB written")
         return
     if args.only == "gemm":
-        log("gemm", json.dumps(bench_c5a(torch, ft, dev, args.steps, args.warmup)))
+        # the main run's C5a leg: ~0.25 s of warm-up launches, then timed
+        log("gemm", json.dumps(bench_c5a(torch, ft, dev, max(50, args.steps * 5),
+                                         max(300, args.warmup))))
         return
     if args.only == "c2":
         log("c2", json.dumps(bench_c2(torch, ft, dev)))
@@ -661,9 +663,9 @@ def main():
         del w["kp"], w["vp"]
         torch.cuda.empty_cache()
         # sustained rate: ~0.25 s of launches first, so the power manager
-        # has settled at the board limit (measured: the clock falls from
-        # 2.4 GHz to ~1.5 GHz, socket power 1400 W, within the first few
-        # launches)
+        # has settled at the board limit (measured: socket power 1400 W, the
+        # clock falls from 2.4 GHz to ~1.8 GHz, with a deeper dip during the
+        # first ~100 launches)
         secondary = bench_c5a(torch, ft, dev, max(50, args.steps * 5), 300)
         log(f"config 5a: {secondary['value']} TOPS")
 

@@ -19,9 +19,11 @@
 //                  v_mfma_i32_16x16x64_i8, 64 columns per workgroup (A shared
 //                  through L1), K split across workgroups when N alone cannot
 //                  fill the chip; int32 partials folded by qgemm_ksum.
-//   qgemm_big_w8   M, N >= 256, K % 128 == 0 (default): persistent 256x256
-//                  tiles, 8 waves (two per SIMD, 64x128 each), 128-byte K
-//                  slabs DMA'd global->LDS into two stages.
+//   qgemm_big_w16  M, N >= 256, K % 128 == 0 (default): persistent 256x256
+//                  tiles, 8 waves (two per SIMD, 64x128 each, on
+//                  v_mfma_i32_16x16x64_i8), 128-byte K slabs DMA'd
+//                  global->LDS into two stages.
+//   qgemm_big_w8   the same on v_mfma_i32_32x32x32_i8.
 //   qgemm_big_k128 the same with 4 waves of 128x128 (one per SIMD).
 //   qgemm_big_dma  M, N >= 256, K % 64 == 0: 256x256 tiles on
 //                  v_mfma_i32_32x32x32_i8 fed by a 5-stage global->LDS DMA
@@ -1695,6 +1697,338 @@ void qgemm_big_w8(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
 }
 
 // ---------------------------------------------------------------------------
+// big, 8 waves, 16x16x64 MFMAs: qgemm_big_w8's tiles, tile order, DMA slabs,
+// LDS layout and barriers, with each wave's 64 x 128 sub-tile computed as
+// 4 x 8 blocks of v_mfma_i32_16x16x64_i8 (128 accumulators per lane, as
+// before). The fragment bytes per MAC are the same as with 32x32x32; what
+// changes is the instruction: under the board power limit of random int8
+// operands the 16x16x64 form sustains more operations per second (all CUs,
+// operands cycling through 8 random register sets: 3.24 vs 2.91 POP/s).
+// Lane (r16, q4) = (lane % 16, lane / 16) holds 16 bytes (chunk 4 s + q4 of
+// 64-byte sub-step s) of row r16 of a 16-row block; the accumulator register
+// t of block (i, j) is C[row 16 i + r16][col 16 j + 4 q4 + t].
+// ---------------------------------------------------------------------------
+
+// s_waitcnt lgkmcnt(n) for a compile-time n (after unrolling) in 6..11,
+// tying the fragments x and y so that their uses stay below the wait.
+__device__ __forceinline__ void lgkm_wait_xy(int n, i32x4& x, i32x4& y) {
+    __builtin_amdgcn_sched_barrier(0);
+    switch (n) {
+    case 6: asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(x), "+v"(y)); break;
+    case 7: asm volatile("s_waitcnt lgkmcnt(7)" : "+v"(x), "+v"(y)); break;
+    case 8: asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(x), "+v"(y)); break;
+    case 9: asm volatile("s_waitcnt lgkmcnt(9)" : "+v"(x), "+v"(y)); break;
+    case 10: asm volatile("s_waitcnt lgkmcnt(10)" : "+v"(x), "+v"(y)); break;
+    case 11: asm volatile("s_waitcnt lgkmcnt(11)" : "+v"(x), "+v"(y)); break;
+    default: asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x), "+v"(y)); break;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Read schedule of the 16x16x64 sub-step (32 MFMAs, q = 4 j + i multiplies
+// B block j by A block i). The next sub-step's 12 fragments are read in
+// their first-use order B0 A0 A1 A2 A3 B1 .. B7 (fragment index: A i = i,
+// B j = 4 + j): read kW16Rd[q] goes out after MFMA q (-1: none), B j's once
+// the current B j is dead. kW16Wait[q] is the lgkmcnt bound before MFMA q
+// in a sub-step whose fragments are still landing (-1: no wait): the reads
+// that MFMA q needs first have landed once at most (11 - their position)
+// reads of the previous sub-step plus this sub-step's reads issued before
+// MFMA q are outstanding (LDS reads return in order).
+constexpr int kW16Rd[32] = {-1, -1, -1, 4, 0, 1, 2, 3, 5, -1, -1, -1, 6, -1, -1, -1,
+                            7,  -1, -1, -1, 8, -1, -1, -1, 9, -1, -1, -1, 10, -1, -1, 11};
+constexpr int kW16Wait[32] = {10, 9, 8, 7, 7, -1, -1, -1, 10, -1, -1, -1, 10, -1, -1, -1,
+                              10, -1, -1, -1, 10, -1, -1, -1, 10, -1, -1, -1, 10, -1, -1, -1};
+
+// Epilogue of qgemm_big_w16: the wave's 64 x 128 sub-tile at (row0, col0),
+// acc[i][j] as above; scw and the staging as in w8_epilogue (16 rows x 64
+// columns per pass, 128-byte row pieces out).
+template <int OUT>
+__device__ __forceinline__ void w16_epilogue(i32x4 (&acc)[4][8], i8* stg, const float* scw,
+                                             const Epi& e, int m, int n, int row0,
+                                             int col0, int lane, int r16, int q4) {
+    const float sa = epi_sa(e);
+    auto scales4 = [&](int jc) {  // f32(sa * sb[col0 + jc .. + 3]), clamped at n
+        float4 s4;
+        if (scw) {
+            const float4 v = *reinterpret_cast<const float4*>(scw + jc);
+            s4 = make_float4(sa * v.x, sa * v.y, sa * v.z, sa * v.w);
+        } else if (e.sb_vec) {
+            const int col = col0 + jc;
+            s4.x = sa * e.sb_vec[min(col, n - 1)];
+            s4.y = sa * e.sb_vec[min(col + 1, n - 1)];
+            s4.z = sa * e.sb_vec[min(col + 2, n - 1)];
+            s4.w = sa * e.sb_vec[min(col + 3, n - 1)];
+        } else {
+            const float sc = sa * e.sb;
+            s4 = make_float4(sc, sc, sc, sc);
+        }
+        return s4;
+    };
+    if constexpr (OUT == kOutBF16 || OUT == kOutF16) {
+        typedef typename std::conditional<OUT == kOutBF16, bf16, f16>::type OT;
+        typedef OT ot4 __attribute__((ext_vector_type(4)));
+        OT* const y = static_cast<OT*>(e.y);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int jp = 0; jp < 2; ++jp) {
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int j = 4 * jp + jj;
+                    const float4 s4 = scales4(16 * j + 4 * q4);
+                    ot4 v;
+                    v[0] = (OT)epi_val(acc[i][j][0], s4.x);
+                    v[1] = (OT)epi_val(acc[i][j][1], s4.y);
+                    v[2] = (OT)epi_val(acc[i][j][2], s4.z);
+                    v[3] = (OT)epi_val(acc[i][j][3], s4.w);
+                    *reinterpret_cast<ot4*>(stg + r16 * kW8Pitch + (16 * jj + 4 * q4) * 2) = v;
+                }
+                // 16 rows x 128 bytes back out: 8 lanes per row, 16 bytes each
+#pragma unroll
+                for (int rr = 0; rr < 2; ++rr) {
+                    const int lr = rr * 8 + (lane >> 3);
+                    const int row = row0 + i * 16 + lr;
+                    const int cb = (lane & 7) * 8;  // first of 8 columns
+                    const int col = col0 + jp * 64 + cb;
+                    const i8* src = stg + lr * kW8Pitch + cb * 2;
+                    if (row >= m) continue;
+                    OT* dst = y + (size_t)row * n + col;
+                    if ((n & 7) == 0) {
+                        if (col < n)
+                            *reinterpret_cast<i32x4*>(dst) = *reinterpret_cast<const i32x4*>(src);
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 8; ++c)
+                            if (col + c < n) dst[c] = reinterpret_cast<const OT*>(src)[c];
+                    }
+                }
+            }
+        }
+    } else {  // 4-byte outputs: 16-byte stores of 4 consecutive columns
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int col = col0 + 16 * j + 4 * q4;
+            float4 s4;
+            if constexpr (OUT == kOutF32) s4 = scales4(16 * j + 4 * q4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = row0 + i * 16 + r16;
+                if (row >= m || col >= n) continue;
+                i32x4 o;
+                if constexpr (OUT == kOutI32) {
+                    o = acc[i][j];
+                } else {
+                    o = i32x4{__float_as_int(epi_val(acc[i][j][0], s4.x)),
+                              __float_as_int(epi_val(acc[i][j][1], s4.y)),
+                              __float_as_int(epi_val(acc[i][j][2], s4.z)),
+                              __float_as_int(epi_val(acc[i][j][3], s4.w))};
+                }
+                int* dst = static_cast<int*>(e.y) + (size_t)row * n + col;
+                if ((n & 3) == 0) {
+                    *reinterpret_cast<i32x4*>(dst) = o;
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (col + c < n) dst[c] = o[c];
+                }
+            }
+        }
+    }
+}
+
+template <int OUT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void qgemm_big_w16(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
+                   int m, int n, int k, int scales_dma, int band) {
+    __shared__ __attribute__((aligned(16))) i8 lds[kW8Lds];
+
+    const int tm = (m + kBigT - 1) / kBigT, tn = (n + kBigT - 1) / kBigT;
+    const int ntiles = tm * tn;
+    // qgemm_big_k128's order with `band` tile rows per band
+    auto tile_origin = [&](int t, int& bm, int& bn) {
+        int pid = t;
+        if (ntiles % 8 == 0) pid = (pid % 8) * (ntiles / 8) + pid / 8;
+        const int bi = pid / (band * tn);
+        const int first_m = bi * band;
+        const int band_m = min(tm - first_m, band);
+        const int in_band = pid - bi * band * tn;
+        bm = (first_m + in_band % band_m) * kBigT;
+        bn = (in_band / band_m) * kBigT;
+    };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..7
+    const int wr = 128 * (wave >> 2) + 64 * ((wave & 3) >> 1);  // sub-tile row
+    const int wc = 128 * (wave & 1);                            // sub-tile column
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const int nk = k / kK2;
+
+    // DMA exactly as qgemm_big_w8: instruction j (0..3) of this wave fills
+    // tile rows 64 j + 8 wave + lane / 8 of A and of B; the lane's LDS chunk
+    // position lane % 8 holds logical chunk (lane % 8) ^ swz, swz = (row >> 1)
+    // & 7. Rows past M / N read a clamped (real) row.
+    const int c16 = 16 * ((lane & 7) ^ ((4 * wave + (lane >> 4)) & 7));
+    unsigned aoff[4], boff[4];
+    const i8* abase;
+    const i8* bbase;
+    auto set_tile = [&](int bm, int bn) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = 64 * j + 8 * wave + (lane >> 3);
+            aoff[j] = (unsigned)(min(row, m - 1 - bm) * k + c16);
+            boff[j] = (unsigned)(min(row, n - 1 - bn) * k + c16);
+        }
+        abase = a + (size_t)bm * k;
+        bbase = b + (size_t)bn * k;
+    };
+    auto dma1 = [&](int kt, int st, int x) {  // instruction x (0..7): A for even x
+        const int j = x >> 1;
+        i8* dst = lds + st * kSlab2 + (x & 1) * (kBigT * kK2) + (64 * j + 8 * wave) * kK2;
+        if (x & 1)
+            __builtin_amdgcn_global_load_lds(bbase + (size_t)kt * kK2 + boff[j],
+                                             (lds_void_p)dst, 16, 0, 0);
+        else
+            __builtin_amdgcn_global_load_lds(abase + (size_t)kt * kK2 + aoff[j],
+                                             (lds_void_p)dst, 16, 0, 0);
+    };
+    auto first_slabs = [&](int bm, int bn) {
+        const int nsl = nk > 1 ? 2 : 1;
+        for (int sl = 0; sl < nsl; ++sl) {
+            const i8* ab = a + (size_t)bm * k + (size_t)sl * kK2;
+            const i8* bb = b + (size_t)bn * k + (size_t)sl * kK2;
+#pragma unroll
+            for (int x = 0; x < 8; ++x) {
+                const int j = x >> 1;
+                const int row = 64 * j + 8 * wave + (lane >> 3);
+                i8* dst = lds + sl * kSlab2 + (x & 1) * (kBigT * kK2) + (64 * j + 8 * wave) * kK2;
+                const unsigned off = (x & 1) ? (unsigned)(min(row, n - 1 - bn) * k + c16)
+                                             : (unsigned)(min(row, m - 1 - bm) * k + c16);
+                __builtin_amdgcn_global_load_lds(((x & 1) ? bb : ab) + off, (lds_void_p)dst,
+                                                 16, 0, 0);
+            }
+        }
+    };
+
+    // Fragment x (A block i: x = i; B block j: x = 4 + j) of sub-step s in
+    // stage st: row R = (wr or wc) + 16 block + r16, chunk 4 s + q4 at offset
+    // (R << 7) | 16 ((4 s + q4) ^ swz(R)). swz(R) = (r16 >> 1) & 7 for every
+    // block (wr, wc and 16 block are multiples of 16), so the offset is a
+    // per-sub-step base plus 2048 block.
+    const unsigned lds0 = lds_addr(lds);
+    unsigned abase_s[2], bbase_s[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const unsigned sw = 16u * ((4 * s + q4) ^ ((r16 >> 1) & 7));
+        abase_s[s] = lds0 + (unsigned)((wr + r16) << 7) + sw;
+        bbase_s[s] = lds0 + (unsigned)(kBigT * kK2) + (unsigned)((wc + r16) << 7) + sw;
+    }
+    auto frag_addr = [&](int st, int s, int x) {
+        return (x < 4 ? abase_s[s] + 2048u * x : bbase_s[s] + 2048u * (x - 4)) +
+               (unsigned)(st * kSlab2);
+    };
+    auto read_frags = [&](int st, int s, i32x4 (&f)[12]) {
+        // first-use order: B0 A0 A1 A2 A3 B1 .. B7
+        f[4] = lds_read16(frag_addr(st, s, 4));
+#pragma unroll
+        for (int x = 0; x < 4; ++x) f[x] = lds_read16(frag_addr(st, s, x));
+#pragma unroll
+        for (int x = 5; x < 12; ++x) f[x] = lds_read16(frag_addr(st, s, x));
+    };
+    auto frags_wait = [&](i32x4 (&f)[12]) {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]),
+                       "+v"(f[5]), "+v"(f[6]), "+v"(f[7]), "+v"(f[8]), "+v"(f[9]),
+                       "+v"(f[10]), "+v"(f[11]));
+    };
+
+    i32x4 acc[4][8];  // acc[i][j] = C^T block (n block j, m block i)
+    // 32 MFMAs on f (read in first-use order by the previous call), reading
+    // the next sub-step (rst, rs) into nf on the kW16Rd schedule. With a DMA
+    // tag, the 8 DMA instructions of slab dkt into stage dst go out after
+    // MFMAs 1, 5, .., 29.
+    auto step = [&](i32x4 (&f)[12], bool piecewise, int rst, int rs, i32x4 (&nf)[12],
+                    auto dma, int dkt, int dst) {
+#pragma unroll
+        for (int q = 0; q < 32; ++q) {
+            const int i = q & 3, j = q >> 2;
+            if (piecewise && kW16Wait[q] >= 0) lgkm_wait_xy(kW16Wait[q], f[4 + j], f[i]);
+            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f[4 + j], f[i], acc[i][j], 0, 0, 0);
+            if constexpr (decltype(dma)::value) {
+                if ((q & 3) == 1) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    dma1(dkt, dst, q >> 2);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            if (kW16Rd[q] >= 0) {
+                __builtin_amdgcn_sched_barrier(0);
+                nf[kW16Rd[q]] = lds_read16(frag_addr(rst, rs, kW16Rd[q]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+
+    int t = blockIdx.x;
+    if (t < ntiles) {
+        int bm0, bn0;
+        tile_origin(t, bm0, bn0);
+        first_slabs(bm0, bn0);
+    }
+    for (; t < ntiles; t += gridDim.x) {
+        int bm, bn;
+        tile_origin(t, bm, bn);
+        set_tile(bm, bn);
+        // slabs 0 and 1 of this tile are in flight (issued before the
+        // previous tile's epilogue, or just above): wait for them and for
+        // that epilogue's stores; after the barrier every wave's DMAs are
+        // visible
+        wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        if (scales_dma && wave == 0) {
+            const int c = min(bn + 4 * lane, n - 4);
+            __builtin_amdgcn_global_load_lds(e.sb_vec + c, (lds_void_p)(lds + kW8Scl), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+
+        // Per slab kt (stage st = kt & 1), with F0 = (kt, 0) read: sub-step 0
+        // multiplies (kt, 0) while (kt, 1) is read; wait for (kt, 1) and slab
+        // kt+1's DMA; barrier (every wave is past its reads of stage st; slab
+        // kt+1 is visible); sub-step 1 multiplies (kt, 1) while (kt+1, 0) is
+        // read from stage st ^ 1 and stage st is refilled with slab kt + 2.
+        // After the last slab, F0 reads a stale stage: in bounds, unused.
+        i32x4 f0[12], f1[12];
+        read_frags(0, 0, f0);
+        auto slab = [&](int kt, auto dma) {
+            const int st = kt & 1;
+            step(f0, true, st, 1, f1, std::false_type{}, 0, 0);
+            frags_wait(f1);
+            wait_vmcnt<0>();  // slab kt+1 (the only DMA in flight) and the scales
+            __builtin_amdgcn_s_barrier();
+            step(f1, false, st ^ 1, 0, f0, dma, kt + 2, st);
+        };
+        int kt = 0;
+        for (; kt + 2 < nk; ++kt) slab(kt, std::true_type{});
+        for (; kt < nk; ++kt) slab(kt, std::false_type{});
+        frags_wait(f0);   // the last (unused) reads land before f0's registers are reused
+        wait_vmcnt<0>();  // the scales of a one-slab tile
+        __builtin_amdgcn_s_barrier();
+        const int tn_ = t + gridDim.x;
+        if (tn_ < ntiles) {
+            int nbm, nbn;
+            tile_origin(tn_, nbm, nbn);
+            first_slabs(nbm, nbn);
+        }
+        w16_epilogue<OUT>(acc, lds + kW8Spare + wave * kW8Stg,
+                          scales_dma ? reinterpret_cast<const float*>(lds + kW8Scl) + wc : nullptr,
+                          e, m, n, bm + wr, bn + wc, lane, r16, q4);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // dispatch
 // ---------------------------------------------------------------------------
 int env_int(const char* name, int dflt) {
@@ -1805,23 +2139,29 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         const long long tiles = (long long)((m + kBigT - 1) / kBigT) * ((n + kBigT - 1) / kBigT);
         if (tiles > (1LL << 30)) inval("qgemm problem too large for one launch");
         // FT_QGEMM_BIG: 1: 64-byte slabs, 2: register-staged, 3: 128-byte
-        // slabs with 4 waves (one per SIMD)
+        // slabs with 4 waves (one per SIMD), 4: 8 waves on 32x32x32 MFMAs
         const int big = env_int("FT_QGEMM_BIG", 0);
-        if (k % kK2 == 0 && (big == 0 || big == 3)) {
+        if (k % kK2 == 0 && (big == 0 || big == 3 || big == 4)) {
             // persistent: a multiple of 8 workgroups (XCD-aware order), at
             // most one per CU. 8 waves by default: on C5a (4096 x 8192 x
             // 28672, random int8) the MFMA pipes are busy 70% of the cycles
-            // against 60% with 4 waves (0.88 vs 0.93 ms)
+            // against 60% with 4 waves (0.88 vs 0.93 ms); 16x16x64 MFMAs by
+            // default: 0.807 vs 0.885 ms with 32x32x32 (same schedule; the
+            // board power limit admits more 16x16x64 work per second)
             const long long cus = dev_info().cu_count;
             long long grid = std::min<long long>(tiles, cus);
             if (grid >= 8) grid -= grid % 8;
             if (env_int("FT_QGEMM_ONE_TILE", 0)) grid = tiles;  // A/B: no persistence
+            const int band = std::max(1, env_int("FT_QGEMM_BAND", kBigBand));
             const int scales_dma = e.sb_vec && (n % 4 == 0) &&
                                    ((uintptr_t)e.sb_vec % 16 == 0);
             if (big == 3)
                 qgemm_big_k128<OUT><<<(unsigned)grid, 256, 0, s>>>(a, b, e, m, n, k, scales_dma);
-            else
+            else if (big == 4)
                 qgemm_big_w8<OUT><<<(unsigned)grid, 512, 0, s>>>(a, b, e, m, n, k, scales_dma);
+            else
+                qgemm_big_w16<OUT><<<(unsigned)grid, 512, 0, s>>>(a, b, e, m, n, k, scales_dma,
+                                                                  band);
         }
         else if (k % kBigK == 0 && big != 2 && env_int("FT_QGEMM_NO_DMA", 0) == 0)
             qgemm_big_dma<OUT><<<(unsigned)tiles, 256, 0, s>>>(a, b, e, m, n, k);

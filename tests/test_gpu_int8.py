@@ -191,10 +191,11 @@ GEMM_SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("big", ["0", "3"])
+@pytest.mark.parametrize("big", ["0", "3", "4"])
 def test_big_persistent_tiles_bit_exact(big, monkeypatch):
     # 9 x 33 = 297 tiles of 256 x 256 > one workgroup per CU: the persistent
-    # 128-byte-slab kernels (8 waves, default, and 4 waves) walk several tiles per
+    # 128-byte-slab kernels (8 waves with 16x16x64 MFMAs, default, or
+    # 32x32x32, and 4 waves) walk several tiles per
     # workgroup, with the next tile's first slabs loading during the
     # previous tile's epilogue. Rows from every 256-row band are checked
     # against the oracle over all columns, so every tile is covered.
@@ -213,22 +214,31 @@ def test_big_persistent_tiles_bit_exact(big, monkeypatch):
     assert torch.equal(y[rows], ref)
 
 
-@pytest.mark.parametrize("big", ["0", "1", "2", "3"])
+@pytest.mark.parametrize("big", ["0", "1", "2", "3", "4"])
 def test_big_kernels_bit_exact(big, monkeypatch):
-    # the four big-tile kernels on one K % 128 == 0 shape with ragged edges:
-    # 128-byte DMA slabs with 8 waves (default), 64-byte DMA slabs,
-    # register-staged, 128-byte DMA slabs with 4 waves
+    # the five big-tile kernels on one K % 128 == 0 shape with ragged edges:
+    # 128-byte DMA slabs with 8 waves on 16x16x64 MFMAs (default), 64-byte
+    # DMA slabs, register-staged, 128-byte DMA slabs with 4 waves, 8 waves on
+    # 32x32x32 MFMAs; every output type (i32, f32 per-tensor and per-channel,
+    # bf16, f16)
     monkeypatch.setenv("FT_QGEMM_BIG", big)
     rng = np.random.default_rng(400 + int(big))
     m, n, k = 520, 777, 1280
     a, b = rand_q(rng, m, k), rand_q(rng, n, k)
     sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
-    acc = ft.qgemm_i32(t(a), t(b))
-    y = ft.qgemm_perchannel(t(a), 0.017, t(b), t(sb), out_dtype=torch.bfloat16)
+    at, bt = t(a), t(b)
+    acc = ft.qgemm_i32(at, bt)
+    y = ft.qgemm_perchannel(at, 0.017, bt, t(sb), out_dtype=torch.bfloat16)
+    yh = ft.qgemm_perchannel(at, 0.017, bt, t(sb), out_dtype=torch.float16)
+    yf = ft.qgemm_perchannel(at, 0.017, bt, t(sb))
+    yt = ft.qgemm(at, 0.03, bt, 0.02)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(acc.cpu().numpy(), oracle.qgemm_i32(a, b))
-    ref = torch.from_numpy(oracle.qgemm_perchannel(a, 0.017, b, sb)).to(torch.bfloat16)
-    assert torch.equal(y.cpu(), ref)
+    pc = oracle.qgemm_perchannel(a, 0.017, b, sb)
+    np.testing.assert_array_equal(yf.cpu().numpy(), pc)
+    np.testing.assert_array_equal(yt.cpu().numpy(), oracle.qgemm(a, 0.03, b, 0.02))
+    assert torch.equal(y.cpu(), torch.from_numpy(pc).to(torch.bfloat16))
+    assert torch.equal(yh.cpu(), torch.from_numpy(pc).to(torch.float16))
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
