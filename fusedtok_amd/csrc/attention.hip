@@ -357,7 +357,7 @@ __device__ __forceinline__ long long stream_seg_len(long long total, int nseg, i
     return s < min_seg ? (long long)min_seg : s;
 }
 
-template <typename T, int MODE>
+template <typename T, int MODE, bool WIDE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_decode_stream(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
@@ -471,8 +471,71 @@ void attn_decode_stream(
                 }
             }
         };
-        auto compute_step = [&](int st, const V8 (&kt)[2][4], const V8 (&vt)[2][4]) {
+        // WIDE: load p (0..3) of tile h reads 4 whole rows, tile rows 4p ..
+        // 4p + 3: lane l takes 16-byte chunk l % 16 of tile row 4p + l / 16,
+        // whose table entry is held by lane 4p + l / 16. Whole 128-byte lines
+        // per instruction, non-temporal: the pages are read once per launch
+        // (a read of C3's pages in this pattern runs at 6.7 TB/s, against
+        // 5.6 TB/s for half lines per instruction, non-temporal, and 5.1 TB/s
+        // for plain loads either way).
+        auto kv_load_wide = [&](int st, const int (&e)[2], V8 (&kt)[2][4], V8 (&vt)[2][4]) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const int rho = 4 * p + (lane >> 4);
+                    const int t = t0 + min((st << 5) + 16 * h + rho, n - 1);
+                    size_t off;
+                    if constexpr (MODE == kRowsContig) {
+                        off = ((size_t)row * rows_or_page + t) * D;
+                    } else {
+                        const int ent = __shfl(e[h], rho, 64);
+                        const int in_pg = MODE == kRowsPagedPow2 ? (t & (rows_or_page - 1))
+                                                                 : (t % rows_or_page);
+                        off = (((size_t)ent * hkv + kv) * rows_or_page + in_pg) * D;
+                    }
+                    off += 8 * (lane & 15);
+                    kt[h][p] = __builtin_nontemporal_load(reinterpret_cast<const V8*>(k + off));
+                    vt[h][p] = __builtin_nontemporal_load(reinterpret_cast<const V8*>(v + off));
+                }
+            }
+        };
+        // WIDE staging: the wave's 32 rows x 256 B of K (then V) in its own
+        // s_acc slot (8448 B, written as s_acc only after the wave's last
+        // step). Chunk c of row w sits at 16 (c ^ (w & 15)): the 16 lanes of
+        // a write (one row) and of a fragment read (16 rows, one chunk) hit
+        // 16 different 16-byte bank groups.
+        char* const stg = reinterpret_cast<char*>(&s_acc[wave][0][0]);
+        auto stage_write = [&](const V8 (&x)[2][4]) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const int w = 16 * h + 4 * p + (lane >> 4);
+                    *reinterpret_cast<V8*>(stg + w * 256 + 16 * ((lane & 15) ^ (w & 15))) = x[h][p];
+                }
+        };
+        auto stage_read = [&](V8 (&f)[2][4]) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int w = 16 * h + r;
+                    f[h][j] = *reinterpret_cast<const V8*>(stg + w * 256 + 16 * ((4 * j + g) ^ r));
+                }
+        };
+        auto compute_step = [&](int st, const V8 (&kin)[2][4], const V8 (&vin)[2][4]) {
             const int tb = st << 5;
+            // WIDE: K through the staging, then V written behind K's
+            // fragment reads (one wave's LDS operations run in order), so
+            // V's load registers are free during the softmax
+            V8 kw[2][4], vw[2][4];
+            if constexpr (WIDE) {
+                stage_write(kin);
+                stage_read(kw);
+                stage_write(vin);
+            }
+            const V8 (&kt)[2][4] = WIDE ? kw : kin;
             f32x4 s[2];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -512,6 +575,8 @@ void attn_decode_stream(
                 pb[i] = (T)p[i];
                 if (M::kSplitP) pl[i] = (T)(p[i] - (float)pb[i]);
             }
+            if constexpr (WIDE) stage_read(vw);
+            const V8 (&vt)[2][4] = WIDE ? vw : vin;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -538,18 +603,22 @@ void attn_decode_stream(
         if (st < nsteps) {
             V8 ka[2][4], va_[2][4], kb[2][4], vb[2][4];
             int ea[2] = {0, 0}, eb[2] = {0, 0};
+            auto kvl = [&](int s_, const int (&e)[2], V8 (&kt)[2][4], V8 (&vt)[2][4]) {
+                if constexpr (WIDE) kv_load_wide(s_, e, kt, vt);
+                else kv_load(s_, e, kt, vt);
+            };
             tbl_load(st, ea);
             tbl_load(min(st + 4, last), eb);
-            kv_load(st, ea, ka, va_);
+            kvl(st, ea, ka, va_);
             for (; st + 4 < nsteps; st += 8) {
                 tbl_load(min(st + 8, last), ea);
-                kv_load(st + 4, eb, kb, vb);
+                kvl(st + 4, eb, kb, vb);
                 // keep the prefetch ahead of the compute that follows it (the
                 // scheduler would otherwise sink the loads below the waits)
                 __builtin_amdgcn_sched_barrier(0);
                 compute_step(st, ka, va_);
                 tbl_load(min(st + 12, last), eb);
-                kv_load(min(st + 8, last), ea, ka, va_);
+                kvl(min(st + 8, last), ea, ka, va_);
                 __builtin_amdgcn_sched_barrier(0);
                 compute_step(st + 4, kb, vb);
             }
@@ -775,6 +844,28 @@ int env_int(const char* name, int dflt) {
     return (s && *s) ? atoi(s) : dflt;
 }
 
+// attn_decode_stream in the row mode of the layout (paged with a power-of-2
+// page, paged with any page, contiguous).
+template <typename T, bool WIDE>
+void launch_stream(bool paged, int page_shift, int nseg, hipStream_t s, const T* q,
+                   const T* k, const T* v, const int* table, const int* lens, float* ws_ml,
+                   float* ws_acc, long long* pref, T* out, int batch, int hq, int hkv,
+                   int group, int rows_or_page, int tbl_width, int span, float scale_log2,
+                   int min_seg) {
+    if (paged && page_shift >= 0)
+        attn_decode_stream<T, kRowsPagedPow2, WIDE><<<(unsigned)nseg, 256, 0, s>>>(
+            q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
+            rows_or_page, page_shift, tbl_width, span, scale_log2, min_seg);
+    else if (paged)
+        attn_decode_stream<T, kRowsPagedDiv, WIDE><<<(unsigned)nseg, 256, 0, s>>>(
+            q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
+            rows_or_page, -1, tbl_width, span, scale_log2, min_seg);
+    else
+        attn_decode_stream<T, kRowsContig, WIDE><<<(unsigned)nseg, 256, 0, s>>>(
+            q, k, v, nullptr, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
+            rows_or_page, -1, 0, span, scale_log2, min_seg);
+}
+
 template <typename T>
 void attention_run(const T* q, const T* k, const T* v, const int* table,
                    const int* lens, T* out, int batch, int hq, int hkv,
@@ -824,18 +915,17 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
             float* ws_ml = (float*)ws;
             float* ws_acc = ws_ml + ml_floats;
             long long* pref = (long long*)(ws_acc + acc_floats);
-            if (paged && page_shift >= 0)
-                attn_decode_stream<T, kRowsPagedPow2><<<(unsigned)nseg, 256, 0, s>>>(
-                    q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv,
-                    group, rows_or_page, page_shift, tbl_width, (int)span, scale_log2, min_seg);
-            else if (paged)
-                attn_decode_stream<T, kRowsPagedDiv><<<(unsigned)nseg, 256, 0, s>>>(
-                    q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv,
-                    group, rows_or_page, -1, tbl_width, (int)span, scale_log2, min_seg);
+            // FT_ATTN_LOADS=1: the per-lane row loads straight into the MFMA
+            // layout (half a 128-byte line per instruction, plain loads)
+            if (env_int("FT_ATTN_LOADS", 0) == 1)
+                launch_stream<T, false>(paged, page_shift, nseg, s, q, k, v, table, lens, ws_ml,
+                                        ws_acc, pref, out, batch, hq, hkv, group,
+                                        rows_or_page, tbl_width, (int)span, scale_log2,
+                                        min_seg);
             else
-                attn_decode_stream<T, kRowsContig><<<(unsigned)nseg, 256, 0, s>>>(
-                    q, k, v, nullptr, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv,
-                    group, rows_or_page, -1, 0, (int)span, scale_log2, min_seg);
+                launch_stream<T, true>(paged, page_shift, nseg, s, q, k, v, table, lens, ws_ml,
+                                       ws_acc, pref, out, batch, hq, hkv, group, rows_or_page,
+                                       tbl_width, (int)span, scale_log2, min_seg);
             launch_check("attention decode kernel launch");
             attn_combine_stream<T><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
                 ws_ml, ws_acc, pref, out, batch, hq, hkv, group, nseg, min_seg);

@@ -219,6 +219,38 @@ def test_paged_odd_page_sizes(page):
     assert_half_close(out.float().cpu().numpy(), ref, f"page={page}")
 
 
+@pytest.mark.parametrize("dt", HALF)
+def test_stream_load_paths_bit_identical(dt, monkeypatch):
+    # The MFMA kernel reads K / V either as whole rows per load (default:
+    # 128-byte lines, staged through LDS into the MFMA layout) or straight
+    # into the MFMA layout (FT_ATTN_LOADS=1). Only the data movement
+    # differs, so the outputs agree bit for bit; both match the oracle.
+    rng = np.random.default_rng(77)
+    q, k, v, _ = make_case(rng, 3, 32, 8, 700, 128, False)
+    lens = np.array([700, 33, 451], np.int32)
+    pq, kp, vp, tbl, ln = paged_case(rng, 4, 16, 4, 128, [1, 300, 77, 1024])
+    oq, okp, ovp, otbl, oln = paged_case(rng, 3, 8, 2, 128, [40, 77, 3], page=5)
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("FT_ATTN_LOADS", mode)
+        outs[mode] = (
+            ft.attention_decode(t(q, dt), t(k, dt), t(v, dt), t(lens)),
+            ft.attention_decode_paged(t(pq, dt), t(kp, dt), t(vp, dt), t(tbl), t(ln)),
+            ft.attention_decode_paged(t(oq, dt), t(okp, dt), t(ovp, dt), t(otbl), t(oln)))
+    torch.cuda.synchronize()
+    for a, b in zip(outs["0"], outs["1"]):
+        assert torch.equal(a, b)
+    assert_half_close(outs["0"][0].float().cpu().numpy(),
+                      oracle.attention_decode(rounded(q, dt), rounded(k, dt), rounded(v, dt),
+                                              lens), "contiguous")
+    assert_half_close(outs["0"][1].float().cpu().numpy(),
+                      oracle.attention_decode_paged(rounded(pq, dt), rounded(kp, dt),
+                                                    rounded(vp, dt), tbl, ln), "paged")
+    assert_half_close(outs["0"][2].float().cpu().numpy(),
+                      oracle.attention_decode_paged(rounded(oq, dt), rounded(okp, dt),
+                                                    rounded(ovp, dt), otbl, oln), "page 5")
+
+
 def test_paged_equals_contiguous_materialisation():
     rng = np.random.default_rng(41)
     q, kp, vp, tbl, ln = paged_case(rng, 3, 8, 2, 64, [37, 16, 48])
