@@ -147,7 +147,12 @@ __global__ __launch_bounds__(256) void qgemv_dot4(const i8* __restrict__ a,
 #pragma unroll
                 for (int r = 0; r < kGemvRows; ++r) {
                     const int row = min(j0 + r, n - 1);
-                    w[c][r] = kok ? *reinterpret_cast<const i32x4*>(b + (size_t)row * k + kk) : z;
+                    // W is read once: non-temporal (1 KB of a row per
+                    // instruction, whole lines; N=11008 K=4096: 10.6 vs
+                    // 11.7 us with plain loads)
+                    w[c][r] = kok ? __builtin_nontemporal_load(
+                                        reinterpret_cast<const i32x4*>(b + (size_t)row * k + kk))
+                                  : z;
                 }
 #pragma unroll
                 for (int mm = 0; mm < M_; ++mm)
