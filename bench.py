@@ -47,6 +47,9 @@ lens[b] + 1 tokens.
 `traffic` (HBM bytes per launch, from rocprofv3 FETCH_SIZE / WRITE_SIZE
 counters scaled by a copy-kernel calibration) is read from
 profiles/hbm_traffic.json when that file holds an entry for the kernel.
+`roofline.copy_gbs` is a plain 1 GiB device copy measured in the same run
+(read + write bytes per second), and `frac_of_copy` the attention rate
+against it.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
 """
@@ -595,6 +598,28 @@ def traffic_for(key):
         return None
 
 
+def measured_copy_gbs(torch, dev):
+    """Bandwidth of a plain 1 GiB device-to-device copy (torch's copy kernel),
+    counted as bytes read + bytes written per second: the practical HBM
+    figure the decode fractions are also quoted against."""
+    src = torch.ones((1 << 29,), dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(10):
+        dst.copy_(src)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / 10
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2 * (1 << 30) / sec / 1e9
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -647,6 +672,9 @@ def main():
         log("sampling", json.dumps(bench_sampling(torch, ft, dev)))
         return
 
+    copy_gbs = measured_copy_gbs(torch, dev) if args.only is None else None
+    if copy_gbs:
+        log(f"device copy: {copy_gbs:.1f} GB/s (read + write)")
     log(f"config 3: building workload (seed {C3['seed']})")
     w, wall, attn_ms = bench_c3(torch, np, ft, dev, args.steps, args.warmup)
     step_bytes = w["attn_bytes"] + w["append_bytes"]
@@ -728,7 +756,9 @@ def main():
                      "traffic": traffic_for("attention_c3"),
                      "kernel": "attention_decode_paged = attn_decode_stream + attn_combine_stream",
                      "avg_us": round(attn_ms * 1e3, 2),
-                     "bytes_per_launch": w["attn_bytes"]},
+                     "bytes_per_launch": w["attn_bytes"],
+                     "copy_gbs": round(copy_gbs, 1) if copy_gbs else None,
+                     "frac_of_copy": round(attn_gbs / copy_gbs, 4) if copy_gbs else None},
         "cpu_baseline": cpu,
         "secondary": secondary,
         "chains": chains,

@@ -50,6 +50,29 @@ enum OutKind { kOutF32 = 0, kOutBF16 = 1, kOutF16 = 2, kOutI32 = 3 };
 
 typedef __attribute__((address_space(3))) void* lds_void_p;
 
+// s_waitcnt with only the vector-memory count bounded (gfx9 encoding;
+// expcnt and lgkmcnt fields at their maxima = no wait).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+    return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// 16-byte LDS read issued as inline asm, so that the compiler's tracking of
+// global->LDS DMA does not put a vmcnt(0) before it; the value is valid
+// only after an lgkmcnt wait that ties it (asm with the value as an in/out
+// operand, so that its uses stay below the wait).
+__device__ __forceinline__ i32x4 lds_read16(unsigned addr) {
+    i32x4 v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+
 struct Epi {
     void* y;
     float sa;
@@ -660,26 +683,8 @@ constexpr int kSlabBytes = 2 * kBigT * kBigK;  // A + B slab, 32 KB
 constexpr int kSlabLoads = 8;  // DMA instructions per thread per slab (4 A + 4 B)
 constexpr int kEpiPitch = 272;  // LDS row pitch of the output staging (16-byte rows)
 
-// s_waitcnt with only the vector-memory count bounded (gfx9 encoding;
-// expcnt and lgkmcnt fields at their maxima = no wait).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
-// LDS byte address of a __shared__ object.
-__device__ __forceinline__ unsigned lds_addr(const void* p) {
-    return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
-}
 
-// 16-byte LDS read issued as inline asm: invisible to the compiler's
-// memory model (see above). The result is valid only after lds_wait.
-__device__ __forceinline__ i32x4 lds_read16(unsigned addr) {
-    i32x4 v;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
-    return v;
-}
 // Wait for every outstanding LDS read; the fragments are in/out operands, so
 // nothing that uses them can be scheduled above the wait.
 __device__ __forceinline__ void lds_wait(i32x4 (&f)[8]) {
@@ -2115,8 +2120,12 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         const int col_wgs = (n + 63) / 64;
         const int chunks = (k + kSkChunk - 1) / kSkChunk;  // 1 KB K chunks
         const int cus = dev_info().cu_count;
-        // enough workgroups for 2 per CU
-        int ksplit = std::max(1, std::min((2 * cus + col_wgs - 1) / col_wgs, chunks));
+        // no K split once the column workgroups alone cover every CU (M=64,
+        // N=28672, K=4096: 38.9 us against 45.0 us split in two, which also
+        // needs the fold launch); below that, enough workgroups for 2 per CU
+        int ksplit = col_wgs >= cus
+                         ? 1
+                         : std::max(1, std::min((2 * cus + col_wgs - 1) / col_wgs, chunks));
         const int forced_split = env_int("FT_QGEMM_KSPLIT", 0);
         if (forced_split > 0) ksplit = std::min(forced_split, chunks);
         if (ksplit > 65535) ksplit = 65535;

@@ -257,6 +257,32 @@ def test_qgemm_bit_exact(m, n, k):
                                   oracle.qgemm_perchannel(a, 0.031, b, sb))
 
 
+@pytest.mark.parametrize("m,n,k,split", [
+    (20, 200, 640, 0),      # one 16-row tile, K tail inside a chunk
+    (33, 300, 1040, 0),     # two tiles, ragged N, K tail
+    (64, 4096, 4096, 0),    # C4 o_proj shape, auto K split
+    (48, 777, 4112, 3),     # forced split, ragged everything
+    (64, 1000, 2000, 5),    # split leaving an empty K range
+    (17, 64, 16, 0),        # a single 16-byte K piece
+    (64, 16448, 512, 0),    # 257 column workgroups: no K split
+])
+def test_skinny_kernel_bit_exact(m, n, k, split, monkeypatch):
+    # 16 < M <= 64 (qgemm_skinny), with and without K splits (int32 partials
+    # folded by a second launch), including a split that leaves a workgroup
+    # an empty K range
+    if split:
+        monkeypatch.setenv("FT_QGEMM_KSPLIT", str(split))
+    rng = np.random.default_rng(m * 7 + n + k + split)
+    a, b = rand_q(rng, m, k), rand_q(rng, n, k)
+    sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    acc = ft.qgemm_i32(t(a), t(b))
+    y = ft.qgemm_perchannel(t(a), 0.021, t(b), t(sb), out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(acc.cpu().numpy(), oracle.qgemm_i32(a, b))
+    ref = torch.from_numpy(oracle.qgemm_perchannel(a, 0.021, b, sb)).to(torch.bfloat16)
+    assert torch.equal(y.cpu(), ref)
+
+
 @pytest.mark.parametrize("kernel", ["1", "2", "3", "4", "5", "6"])
 def test_every_gemm_kernel_bit_exact(kernel, monkeypatch):
     monkeypatch.setenv("FT_QGEMM_KERNEL", kernel)
