@@ -1778,6 +1778,9 @@ __device__ __forceinline__ void w16_epilogue(i32x4 (&acc)[4][8], i8* stg, const 
         typedef typename std::conditional<OUT == kOutBF16, bf16, f16>::type OT;
         typedef OT ot4 __attribute__((ext_vector_type(4)));
         OT* const y = static_cast<OT*>(e.y);
+        float4 sc[8];  // the lane's column scales, the same for every row block
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sc[j] = scales4(16 * j + 4 * q4);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -1785,7 +1788,7 @@ __device__ __forceinline__ void w16_epilogue(i32x4 (&acc)[4][8], i8* stg, const 
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj) {
                     const int j = 4 * jp + jj;
-                    const float4 s4 = scales4(16 * j + 4 * q4);
+                    const float4 s4 = sc[j];
                     ot4 v;
                     v[0] = (OT)epi_val(acc[i][j][0], s4.x);
                     v[1] = (OT)epi_val(acc[i][j][1], s4.y);
