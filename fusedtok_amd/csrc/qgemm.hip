@@ -1796,14 +1796,19 @@ __device__ __forceinline__ void w16_epilogue(i32x4 (&acc)[4][8], i8* stg, const 
                     v[3] = (OT)epi_val(acc[i][j][3], s4.w);
                     *reinterpret_cast<ot4*>(stg + r16 * kW8Pitch + (16 * jj + 4 * q4) * 2) = v;
                 }
-                // 16 rows x 128 bytes back out: 8 lanes per row, 16 bytes each
+                // 16 rows x 128 bytes back out: 8 lanes per row, 16 bytes each.
+                // Both pieces are read before the guarded stores, so the wave
+                // waits once per pass rather than once per store.
+                const int cb = (lane & 7) * 8;  // first of 8 columns
+                const int col = col0 + jp * 64 + cb;
+                i32x4 piece[2];
+#pragma unroll
+                for (int rr = 0; rr < 2; ++rr)
+                    piece[rr] = *reinterpret_cast<const i32x4*>(
+                        stg + (rr * 8 + (lane >> 3)) * kW8Pitch + cb * 2);
 #pragma unroll
                 for (int rr = 0; rr < 2; ++rr) {
-                    const int lr = rr * 8 + (lane >> 3);
-                    const int row = row0 + i * 16 + lr;
-                    const int cb = (lane & 7) * 8;  // first of 8 columns
-                    const int col = col0 + jp * 64 + cb;
-                    const i8* src = stg + lr * kW8Pitch + cb * 2;
+                    const int row = row0 + i * 16 + rr * 8 + (lane >> 3);
                     if (row >= m) continue;
                     OT* dst = y + (size_t)row * n + col;
                     if ((n & 7) == 0) {
@@ -1812,12 +1817,12 @@ __device__ __forceinline__ void w16_epilogue(i32x4 (&acc)[4][8], i8* stg, const 
                         // drains faster without cache allocation (C5a: 0.690
                         // against 0.732 ms with plain stores)
                         if (col < n)
-                            __builtin_nontemporal_store(*reinterpret_cast<const i32x4*>(src),
-                                                        reinterpret_cast<i32x4*>(dst));
+                            __builtin_nontemporal_store(piece[rr], reinterpret_cast<i32x4*>(dst));
                     } else {
+                        const OT* v = reinterpret_cast<const OT*>(&piece[rr]);
 #pragma unroll
                         for (int c = 0; c < 8; ++c)
-                            if (col + c < n) dst[c] = reinterpret_cast<const OT*>(src)[c];
+                            if (col + c < n) dst[c] = v[c];
                     }
                 }
             }
