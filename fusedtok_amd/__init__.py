@@ -177,6 +177,47 @@ def _upload(arr, device):
     return torch.from_numpy(np.ascontiguousarray(arr)).to(device)
 
 
+# Small per-call int64 arguments (token histories, offsets, seeds) travel in
+# one non-blocking copy from a ring of pinned host buffers: a pageable copy
+# per array made every call wait for the GPU to drain before the host could
+# prepare the next one. A slot is refilled only after the copy that read it
+# has completed (its event).
+_PIN_RING = []
+_PIN_SLOTS = 4
+_pin_next = [0]
+
+
+def _upload_i64(arrays, device):
+    """Host int64 numpy arrays -> device int64 tensors (views of one
+    buffer), ordered on the current stream."""
+    sizes = [int(a.size) for a in arrays]
+    total = max(1, sum(sizes))
+    if len(_PIN_RING) < _PIN_SLOTS:
+        _PIN_RING.append([torch.empty(0, dtype=torch.int64), None])
+    slot = _PIN_RING[_pin_next[0] % len(_PIN_RING)]
+    _pin_next[0] += 1
+    if slot[1] is not None:
+        slot[1].synchronize()
+    if slot[0].numel() < total:
+        slot[0] = torch.empty(max(total, 2 * slot[0].numel(), 1024), dtype=torch.int64,
+                              pin_memory=True)
+    host = slot[0].numpy()
+    at = 0
+    for a, k in zip(arrays, sizes):
+        host[at:at + k] = a.reshape(-1)
+        at += k
+    dev = torch.empty(total, dtype=torch.int64, device=device)
+    dev.copy_(slot[0][:total], non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record(torch.cuda.current_stream(device))
+    slot[1] = ev
+    out, at = [], 0
+    for k in sizes:
+        out.append(dev[at:at + k])
+        at += k
+    return out
+
+
 def _result(res_t, like):
     """Staged result back to the caller's family (torch CPU or numpy)."""
     out = res_t.cpu()
@@ -1349,13 +1390,14 @@ def sample_topp(logits, p, *, temperature=1.0, seed=0, cuda=False):
 
 def _seeds_dev(seeds, rows, device):
     s = _batch_seeds(seeds, rows)
-    return torch.from_numpy(s).to(device)   # int64 bits = the uint64 seeds
+    return _upload_i64([s], device)[0]   # int64 bits = the uint64 seeds
 
 
 def sample_topp_batched(logits, p, *, temperature=1.0, seeds=None, cuda=False,
                         device_out=False):
-    """Nucleus sampling of every row of ``[rows, vocab]`` float32 logits, one
-    workgroup per row, one launch. ``seeds``: one per row (None: 0..rows-1).
+    """Nucleus sampling of every row of ``[rows, vocab]`` float32 logits (each
+    row split across CUs when there are fewer rows than CUs). ``seeds``: one
+    per row (None: 0..rows-1).
     Returns int64 tokens on the host (the reference's contract); build
     addition ``device_out=True`` returns them as a GPU tensor, no sync."""
     _sampling_params(p, temperature)
@@ -1410,7 +1452,8 @@ def decode_step(logits, sampled_ids, penalty=1.0, *, p=0.9, temperature=1.0, see
 def decode_step_batched(logits, sampled_ids, penalty=1.0, *, p=0.9, temperature=1.0,
                         seeds=None, ids_offsets=None, cuda=False, device_out=False):
     """The fused decode step for every row of ``[rows, vocab]`` float32
-    logits, one workgroup per row, one launch. ``sampled_ids``: per-row
+    logits (each row split across CUs when there are fewer rows than CUs).
+    ``sampled_ids``: per-row
     histories (ragged sequences, a 2-D array, or flat ids with
     ``ids_offsets``). Returns int64 tokens on the host (the reference's
     contract); build addition ``device_out=True`` keeps them on the GPU."""
@@ -1421,13 +1464,12 @@ def decode_step_batched(logits, sampled_ids, penalty=1.0, *, p=0.9, temperature=
             raise ValueError("logits must be 2-D [rows, vocab]")
         rows, n = logits.shape
         ids, offs = _batch_ids(sampled_ids, ids_offsets, rows, n)
-        sd = _seeds_dev(seeds, rows, logits.device)
+        ids_t, offs_t, sd = _upload_i64([ids, offs, _batch_seeds(seeds, rows)],
+                                        logits.device)
         out = torch.empty(rows, dtype=torch.int64, device=logits.device)
         if rows:
             if n == 0:
                 raise ValueError("sample of empty logits")
-            ids_t = torch.from_numpy(ids).to(logits.device)
-            offs_t = torch.from_numpy(offs).to(logits.device)
             _fusedtok.decode_step_batched_launch(
                 logits.data_ptr(), rows, n, ids_t.data_ptr() if ids.size else None,
                 offs_t.data_ptr(), float(penalty), float(p), float(temperature),

@@ -92,7 +92,8 @@ enum class Scratch : int {
     AttnPartials = 0,
     QuantMax = 1,
     GemmPartials = 2,
-    kCount = 3
+    Sampling = 3,
+    kCount = 4
 };
 void* scratch(Scratch which, size_t bytes, hipStream_t s);
 // Same, but memory is zero when first allocated (or re-allocated); kernels

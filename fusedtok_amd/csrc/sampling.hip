@@ -10,7 +10,9 @@
 // and the token is where the prefix mass first reaches u * nucleus mass,
 // u = splitmix_uniform(seed).
 //
-// Algorithm (one 1024-thread workgroup per row; no sort of the vocabulary):
+// Algorithm (one 1024-thread workgroup per row, or the row split across CUs
+// by the sliced pipeline below when there are fewer rows than CUs; no sort
+// of the vocabulary):
 //   - masses are fixed point, q_i = rint(exp(v_i - max) * 2^40) in 64-bit
 //     integers, so every sum is exact and order-free: the result is
 //     deterministic per seed (no float atomics);
@@ -19,9 +21,11 @@
 //     mass is 0) with the bins' mass and count; bins are contiguous ranges
 //     of the order, so a scan over them finds the bin where a prefix mass
 //     crosses a threshold;
-//   - the crossing bin's tokens are gathered into LDS (<= 4096), sorted by
-//     the exact order key (value bits, then ~index) with a bitonic network,
-//     and scanned; a larger crossing bin (nearly flat logits) is resolved by
+//   - the crossing bin's tokens are gathered into LDS (<= 4096); up to 1024
+//     are resolved without sorting (an entry's prefix inside the bin is the
+//     mass of the entries with a larger key), more are sorted by the exact
+//     order key (value bits, then ~index) with a bitonic network and
+//     scanned; a larger crossing bin (nearly flat logits) is resolved by
 //     8-bit radix passes over the exact key, restricted to that bin;
 //   - the nucleus cut and the draw are two such threshold queries, the
 //     draw's threshold being u * (prefix mass through the cut).
@@ -31,6 +35,7 @@
 // own GPU path.
 #include "ft_common.hpp"
 
+#include <algorithm>
 #include <cstdlib>
 
 namespace ft {
@@ -58,27 +63,28 @@ struct SampleRow {
     int n;
     float inv_t;
     float pen;
-    const unsigned* bits;  // penalised-token bitmap in LDS, or null
+    const unsigned* bits;  // penalised-token bitmap (LDS or global), or null
+    int bit0;              // first token of bits[0] (a multiple of 32)
     // value of token i from its raw logit l
     __device__ __forceinline__ float val_of(int i, float l) const {
-        if (bits && ((bits[i >> 5] >> (i & 31)) & 1u)) l = l > 0.0f ? l / pen : l * pen;
+        if (bits && ((bits[(i - bit0) >> 5] >> (i & 31)) & 1u))
+            l = l > 0.0f ? l / pen : l * pen;
         return l * inv_t + 0.0f;  // -0 -> +0: equal values order by index
     }
 };
 
-// Visit every token of a row as f(i, v_i): 16-byte loads, four in flight
-// per thread (the rows are read several times; one dependent 4-byte load
-// per thread per step left each pass latency-bound).
+// Visit tokens [lo, hi) of a row (lo a multiple of 4) as f(i, v_i): 16-byte
+// loads, four in flight per thread (the rows are read several times; one
+// dependent 4-byte load per thread per step left each pass latency-bound).
 template <int NT, typename F>
-__device__ __forceinline__ void row_scan(const SampleRow& row, F&& f) {
+__device__ __forceinline__ void slice_scan(const SampleRow& row, int lo, int hi, F&& f) {
     const float* x = row.x;
-    const int n = row.n;
     const int tid = threadIdx.x;
-    int done = 0;
-    if (((uintptr_t)x & 15) == 0) {
-        const int n4 = n >> 2;
+    int done = lo;
+    if (((uintptr_t)(x + lo) & 15) == 0) {
+        const int n4 = hi >> 2;
         const float4* x4 = reinterpret_cast<const float4*>(x);
-        int c = tid;
+        int c = (lo >> 2) + tid;
         for (; c + 3 * NT < n4; c += 4 * NT) {
             float4 q[4];
 #pragma unroll
@@ -102,7 +108,11 @@ __device__ __forceinline__ void row_scan(const SampleRow& row, F&& f) {
         }
         done = 4 * n4;
     }
-    for (int i = done + tid; i < n; i += NT) f(i, row.val_of(i, x[i]));
+    for (int i = done + tid; i < hi; i += NT) f(i, row.val_of(i, x[i]));
+}
+template <int NT, typename F>
+__device__ __forceinline__ void row_scan(const SampleRow& row, F&& f) {
+    slice_scan<NT>(row, 0, row.n, f);
 }
 
 // order key: larger = earlier in the (value desc, index asc) order
@@ -112,6 +122,10 @@ __device__ __forceinline__ u64 order_key(float v, int i) {
     return ((u64)o << 32) | (unsigned)(~(unsigned)i);
 }
 __device__ __forceinline__ int key_index(u64 k) { return (int)~(unsigned)(k & 0xffffffffu); }
+__device__ __forceinline__ float key_value(u64 k) {
+    const unsigned o = (unsigned)(k >> 32);
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
 
 // q = trunc(exp(v - vmax) * 2^40): v_exp_f32 on (v - vmax) log2(e), then
 // the product s < 2^41 split into 32-bit halves, each converted exactly
@@ -131,8 +145,11 @@ __device__ __forceinline__ int dist_bin(float v, float vmax) {
     return d < (float)(kDistBins - 1) ? (int)d : kDistBins - 1;
 }
 
+constexpr int kMaxSlices = 64;
+
 struct SmpShared {
     u64 h_mass[kDistBins];
+    int seg_off[kMaxSlices + 1];  // sliced path: gathered segment offsets
     u64 g_key[kGather];
     u64 g_q[kGather];
     u64 wsum[kSmpNT / 64];
@@ -175,30 +192,45 @@ __device__ __forceinline__ u64 block_minmax(u64 v, u64* wsum) {
     return r;
 }
 
-// Smallest prefix of the order whose mass reaches T (1 <= T <= total):
-// returns its last key in sh.r_key and the prefix mass in sh.r_mass.
-__device__ void select_prefix(const SampleRow& row, float vmax, u64 T, SmpShared& sh) {
+// Distance bin where the prefix mass crosses T (1 <= T <= total), into
+// sh.r_bin, with the mass of the bins before it in sh.r_above: thread t owns
+// bins 2t, 2t + 1 (exactly one thread matches; the defaults keep every
+// later index in range regardless). Sets sh.r_key / sh.r_mass to defaults.
+__device__ void find_bin(u64 T, SmpShared& sh) {
     const int tid = threadIdx.x;
-    // crossing distance bin: thread t owns bins 2t, 2t + 1 (exactly one
-    // thread matches since 1 <= T <= total; the defaults keep every later
-    // index in range regardless)
     if (tid == 0) {
         sh.r_bin = 0;
         sh.r_above = 0;
         sh.r_key = 0;
         sh.r_mass = T;
     }
-    {
-        const u64 m0 = sh.h_mass[2 * tid], m1 = sh.h_mass[2 * tid + 1];
-        const u64 incl = block_scan(m0 + m1, sh.wsum);
-        const u64 excl = incl - m0 - m1;
-        if (excl < T && T <= incl) {
-            const bool first = excl + m0 >= T;
-            sh.r_bin = first ? 2 * tid : 2 * tid + 1;
-            sh.r_above = first ? excl : excl + m0;
-        }
-        __syncthreads();
+    const u64 m0 = sh.h_mass[2 * tid], m1 = sh.h_mass[2 * tid + 1];
+    const u64 incl = block_scan(m0 + m1, sh.wsum);
+    const u64 excl = incl - m0 - m1;
+    if (excl < T && T <= incl) {
+        const bool first = excl + m0 >= T;
+        sh.r_bin = first ? 2 * tid : 2 * tid + 1;
+        sh.r_above = first ? excl : excl + m0;
     }
+    __syncthreads();
+}
+
+// Tokens gathered ahead by the sliced pipeline: every token of the bins a
+// query can cross, in S segments of `cap` entries; segment sg holds
+// sh.seg_off[sg + 1] - sh.seg_off[sg] of them (ok == 0: not gathered, scan
+// the row).
+struct Pregathered {
+    const u64* key;
+    const u64* q;
+    int S, cap, ok;
+};
+
+// Smallest prefix of the order whose mass reaches T (1 <= T <= total):
+// returns its last key in sh.r_key and the prefix mass in sh.r_mass.
+__device__ void select_prefix(const SampleRow& row, float vmax, u64 T, SmpShared& sh,
+                              const Pregathered& pre) {
+    const int tid = threadIdx.x;
+    find_bin(T, sh);
     const int bin = min(max(sh.r_bin, 0), kDistBins - 1);
     const u64 above = sh.r_above;
     // gather the bin and sort it exactly (reused when the previous query
@@ -207,18 +239,37 @@ __device__ void select_prefix(const SampleRow& row, float vmax, u64 T, SmpShared
     if (sh.g_bin != bin) {
         if (tid == 0) sh.g_n = 0;
         __syncthreads();
-        row_scan<kSmpNT>(row, [&](int i, float v) {
-            if (dist_bin(v, vmax) == bin) {
-                const int slot = atomicAdd(&sh.g_n, 1);
-                if (slot < kGather) {
-                    sh.g_key[slot] = order_key(v, i);
-                    sh.g_q[slot] = mass_fx(v, vmax);
+        if (pre.ok) {
+            // one flat pass over all segments: candidate j lies in the
+            // segment whose offsets enclose it
+            const int total = sh.seg_off[pre.S];
+            for (int j = tid; j < total; j += kSmpNT) {
+                int sg = 0;
+                while (sh.seg_off[sg + 1] <= j) ++sg;
+                const size_t at = (size_t)sg * pre.cap + (j - sh.seg_off[sg]);
+                const u64 k = pre.key[at];
+                if (dist_bin(key_value(k), vmax) == bin) {
+                    const int slot = atomicAdd(&sh.g_n, 1);
+                    if (slot < kGather) {
+                        sh.g_key[slot] = k;
+                        sh.g_q[slot] = pre.q[at];
+                    }
                 }
             }
-        });
+        } else {
+            row_scan<kSmpNT>(row, [&](int i, float v) {
+                if (dist_bin(v, vmax) == bin) {
+                    const int slot = atomicAdd(&sh.g_n, 1);
+                    if (slot < kGather) {
+                        sh.g_key[slot] = order_key(v, i);
+                        sh.g_q[slot] = mass_fx(v, vmax);
+                    }
+                }
+            });
+        }
         __syncthreads();
         const int gcnt = sh.g_n;
-        if (gcnt <= kGather) {
+        if (gcnt > kSmpNT && gcnt <= kGather) {  // a small bin needs no sort (below)
             int np2 = 1;
             while (np2 < gcnt) np2 <<= 1;
             for (int i = gcnt + tid; i < np2; i += kSmpNT) {
@@ -251,6 +302,44 @@ __device__ void select_prefix(const SampleRow& row, float vmax, u64 T, SmpShared
             sh.g_bin = gcnt <= kGather ? bin : -2;
         }
         __syncthreads();
+    }
+    if (sh.g_bin == bin && sh.g_cnt <= kSmpNT) {
+        // up to one entry per thread, unsorted. Keys are unique, so the mass
+        // of the bin's order before entry i is the sum over the entries
+        // with a larger key; the entry whose span (above + before, above +
+        // before + q] holds T is the crossing one (every thread reads the
+        // same entry at a time: LDS broadcasts, no barrier per step)
+        // P adjacent threads share an entry (P = 1 .. 16, as many as the
+        // bin's size allows), each summing over a 1/P share of the others,
+        // four at a time; xor shuffles combine the shares.
+        const int c = sh.g_cnt;
+        const int P = c <= kSmpNT / 16 ? 16 : c <= kSmpNT / 8 ? 8 : c <= kSmpNT / 4 ? 4
+                    : c <= kSmpNT / 2 ? 2 : 1;
+        const int e = tid / P, part = tid - e * P;
+        const u64 ki = e < c ? sh.g_key[e] : 0, qi = e < c ? sh.g_q[e] : 0;
+        const int per = (c + P - 1) / P;
+        const int j0 = part * per, j1 = min(c, j0 + per);
+        u64 b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+        int j = j0;
+        for (; j + 4 <= j1; j += 4) {
+            const u64 k0 = sh.g_key[j], k1 = sh.g_key[j + 1], k2 = sh.g_key[j + 2],
+                      k3 = sh.g_key[j + 3];
+            const u64 q0 = sh.g_q[j], q1 = sh.g_q[j + 1], q2 = sh.g_q[j + 2], q3 = sh.g_q[j + 3];
+            b0 += k0 > ki ? q0 : 0ULL;
+            b1 += k1 > ki ? q1 : 0ULL;
+            b2 += k2 > ki ? q2 : 0ULL;
+            b3 += k3 > ki ? q3 : 0ULL;
+        }
+        for (; j < j1; ++j) b0 += sh.g_key[j] > ki ? sh.g_q[j] : 0ULL;
+        u64 before = (b0 + b1) + (b2 + b3);
+        for (int o = 1; o < P; o <<= 1) before += __shfl_xor(before, o, 64);
+        const u64 lo_m = above + before;
+        if (part == 0 && e < c && lo_m < T && T <= lo_m + qi) {
+            sh.r_key = ki;
+            sh.r_mass = lo_m + qi;
+        }
+        __syncthreads();
+        return;
     }
     if (sh.g_bin == bin) {
         // scan the sorted bin: thread t owns entries 4t .. 4t + 3
@@ -356,7 +445,7 @@ __global__ __launch_bounds__(kSmpNT) void sample_topp_rows(
     __shared__ SmpShared sh;
     const int r = blockIdx.x;
     const int tid = threadIdx.x;
-    SampleRow row{x + (size_t)r * n, n, inv_t, pen, nullptr};
+    SampleRow row{x + (size_t)r * n, n, inv_t, pen, nullptr, 0};
     const bool penal = ids != nullptr && pen != 1.0f;
     if (penal) {
         for (int w = tid; w < (n + 31) / 32; w += kSmpNT) sh.bitmap[w] = 0u;
@@ -401,15 +490,284 @@ __global__ __launch_bounds__(kSmpNT) void sample_topp_rows(
     double tc = ceil((double)p * (double)total);
     u64 T = tc < 1.0 ? 1ULL : (u64)tc;
     if (T > total) T = total;
-    select_prefix(row, vmax, T, sh);
+    const Pregathered none{nullptr, nullptr, 0, 0, 0};
+    select_prefix(row, vmax, T, sh, none);
     const u64 nucleus = sh.r_mass;
     // draw: prefix mass >= u * nucleus mass
     const float u = splitmix_uniform(seeds ? seeds[r] : seed0);
     double td = ceil((double)u * (double)nucleus);
     T = td < 1.0 ? 1ULL : (u64)td;
     if (T > nucleus) T = nucleus;
-    select_prefix(row, vmax, T, sh);
+    select_prefix(row, vmax, T, sh, none);
     if (tid == 0) out[r] = key_index(sh.r_key);
+}
+
+// ---------------------------------------------------------------------------
+// Sliced pipeline (fewer rows than CUs): each row is cut into S slices of
+// slen tokens (a multiple of 32), so that S workgroups share a row's passes
+// over the logits; the per-row steps run on one workgroup per row. Same
+// arithmetic and order as sample_topp_rows (integer masses: every merge is
+// exact), so the tokens are identical.
+//   1 smp_slice_max    slice maxima; the slice's penalty bits to global
+//   2 smp_slice_hist   slice distance histograms (mass, count) from the row
+//                      maximum
+//   3 smp_plan         per row: merged histogram, total, the nucleus bin b1
+//                      and the range [c_lo, c_hi] of bins the draw can
+//                      cross (the nucleus mass lies in b1's prefix range and
+//                      the draw threshold is monotone in it)
+//   4 smp_gather       each slice collects the tokens of those bins (order
+//                      key, mass) in LDS, one reservation per wave, and
+//                      copies them to its own segment of the row's buffer
+//                      (no atomics across workgroups: a shared counter per
+//                      row kept this pass at 65 us on 64 x 128k rows)
+//   5 smp_finish       the two threshold queries of sample_topp_rows on the
+//                      merged histogram and the gathered tokens; a row whose
+//                      candidates overflowed the buffer is resolved by full
+//                      row scans, and a crossing bin beyond the exact sort's
+//                      capacity by the radix passes, as in sample_topp_rows
+// ---------------------------------------------------------------------------
+constexpr int kSliceNT = 256;
+constexpr int kMinSlice = 8192;    // tokens per slice at least
+constexpr int kSliceCap = 1024;    // gathered candidates per slice
+// LDS bitmap words of one slice: the sliced path runs with S >= 2, so a
+// slice holds at most ceil(n / 2) + 31 tokens, n <= kMaxBitmapVocab
+constexpr int kSliceWords = (kMaxBitmapVocab / 2 + 32) / 32 + 1;
+
+struct SmpPlan {
+    u64 total;
+    float vmax;
+    int b1, c_lo, c_hi;
+};
+
+struct SliceArgs {
+    const float* x;
+    int n, S, slen, words;     // words: bitmap words per row
+    float inv_t, pen;
+    const long long* ids;      // null: no penalty
+    const long long* offs;     // null: ids[0 .. m_single) for row 0
+    int m_single;
+    unsigned* bits;            // rows x words
+    float* smax;               // rows x S
+    u64* hmass;                // rows x S x kDistBins
+    u64* mhist;                // rows x kDistBins
+    SmpPlan* plan;             // rows
+    int* gcnt;                 // rows x S
+    u64* gkey;                 // rows x S x kSliceCap
+    u64* gq;                   // rows x S x kSliceCap
+    float p;
+    const u64* seeds;
+    u64 seed0;
+    long long* out;
+};
+
+__device__ __forceinline__ SampleRow slice_row(const SliceArgs& a, int r) {
+    SampleRow row{a.x + (size_t)r * a.n, a.n, a.inv_t, a.pen, nullptr, 0};
+    if (a.ids) row.bits = a.bits + (size_t)r * a.words;
+    return row;
+}
+
+// The row with the penalty bits of tokens [lo, hi) copied to LDS (a global
+// bitmap word per token kept each pass waiting on dependent loads). Ends
+// with a workgroup barrier in every case, so LDS set up before the call is
+// visible to the whole workgroup after it.
+__device__ __forceinline__ SampleRow slice_row_lds(const SliceArgs& a, int r, int lo, int hi,
+                                                   unsigned* lbits) {
+    SampleRow row{a.x + (size_t)r * a.n, a.n, a.inv_t, a.pen, nullptr, 0};
+    if (a.ids) {
+        const int w0 = lo >> 5, w1 = (hi + 31) >> 5;
+        const unsigned* g = a.bits + (size_t)r * a.words;
+        for (int w = w0 + (int)threadIdx.x; w < w1; w += kSliceNT) lbits[w - w0] = g[w];
+        row.bits = lbits;
+        row.bit0 = w0 * 32;
+    }
+    __syncthreads();
+    return row;
+}
+
+__global__ __launch_bounds__(kSliceNT) void smp_slice_max(SliceArgs a) {
+    __shared__ unsigned lbits[kSliceWords];
+    __shared__ float red[kSliceNT / 64];
+    const int r = blockIdx.x / a.S, s = blockIdx.x - r * a.S;
+    const int lo = min(a.n, s * a.slen), hi = min(a.n, lo + a.slen);
+    SampleRow row{a.x + (size_t)r * a.n, a.n, a.inv_t, a.pen, nullptr, 0};
+    if (a.ids) {
+        // this slice's words of the row's bitmap (slices own whole words)
+        const int w0 = lo >> 5, w1 = (hi + 31) >> 5;
+        for (int w = w0 + (int)threadIdx.x; w < w1; w += kSliceNT) lbits[w - w0] = 0u;
+        __syncthreads();
+        const long long ja = a.offs ? a.offs[r] : 0;
+        const long long jb = a.offs ? a.offs[r + 1] : a.m_single;
+        for (long long j = ja + threadIdx.x; j < jb; j += kSliceNT) {
+            const long long id = a.ids[j];
+            if (id >= lo && id < hi) atomicOr(&lbits[(id >> 5) - w0], 1u << (id & 31));
+        }
+        __syncthreads();
+        for (int w = w0 + (int)threadIdx.x; w < w1; w += kSliceNT)
+            a.bits[(size_t)r * a.words + w] = lbits[w - w0];
+        row.bits = lbits;
+        row.bit0 = w0 * 32;
+    }
+    float vmax = -INFINITY;
+    slice_scan<kSliceNT>(row, lo, hi, [&](int, float v) { vmax = fmaxf(vmax, v); });
+    vmax = block_max<kSliceNT>(vmax, red);
+    if (threadIdx.x == 0) a.smax[blockIdx.x] = vmax;
+}
+
+__device__ __forceinline__ float row_max_of(const SliceArgs& a, int r) {
+    float vmax = -INFINITY;
+    for (int s = 0; s < a.S; ++s) vmax = fmaxf(vmax, a.smax[r * a.S + s]);
+    return vmax;
+}
+
+__global__ __launch_bounds__(kSliceNT) void smp_slice_hist(SliceArgs a) {
+    __shared__ u64 hm[kDistBins];
+    __shared__ unsigned lbits[kSliceWords];
+    const int r = blockIdx.x / a.S, s = blockIdx.x - r * a.S;
+    const float vmax = row_max_of(a, r);
+    if (!(vmax > -INFINITY)) return;  // smp_plan settles the row
+    const int lo = min(a.n, s * a.slen), hi = min(a.n, lo + a.slen);
+    for (int b = threadIdx.x; b < kDistBins; b += kSliceNT) hm[b] = 0;
+    const SampleRow row = slice_row_lds(a, r, lo, hi, lbits);  // (synchronises)
+    slice_scan<kSliceNT>(row, lo, hi, [&](int, float v) {
+        const u64 q = mass_fx(v, vmax);
+        if (q) atomicAdd(&hm[dist_bin(v, vmax)], q);
+    });
+    __syncthreads();
+    u64* gm = a.hmass + (size_t)blockIdx.x * kDistBins;
+    for (int b = threadIdx.x; b < kDistBins; b += kSliceNT) gm[b] = hm[b];
+}
+
+__global__ __launch_bounds__(kSmpNT) void smp_plan(SliceArgs a) {
+    __shared__ SmpShared sh;
+    const int r = blockIdx.x, tid = threadIdx.x;
+    const float vmax = row_max_of(a, r);
+    if (!(vmax > -INFINITY)) {
+        if (tid == 0) a.plan[r] = SmpPlan{0ULL, vmax, 0, 0, 0};
+        return;
+    }
+    for (int b = tid; b < kDistBins; b += kSmpNT) {
+        u64 m = 0;
+        for (int s = 0; s < a.S; ++s) m += a.hmass[((size_t)r * a.S + s) * kDistBins + b];
+        sh.h_mass[b] = m;
+        a.mhist[(size_t)r * kDistBins + b] = m;
+    }
+    __syncthreads();
+    u64 total;
+    {
+        const u64 incl = block_scan(sh.h_mass[2 * tid] + sh.h_mass[2 * tid + 1], sh.wsum);
+        if (tid == kSmpNT - 1) sh.r_mass = incl;
+        __syncthreads();
+        total = sh.r_mass;
+        __syncthreads();
+    }
+    // the nucleus bin, as smp_finish will find it
+    const double tc = ceil((double)a.p * (double)total);
+    u64 T1 = tc < 1.0 ? 1ULL : (u64)tc;
+    if (T1 > total) T1 = total;
+    find_bin(T1, sh);
+    const int b1 = min(max(sh.r_bin, 0), kDistBins - 1);
+    const u64 after_b1 = sh.r_above + sh.h_mass[b1];  // nucleus mass is in [T1, after_b1]
+    __syncthreads();
+    // the draw threshold for the extreme nucleus masses
+    const float u = splitmix_uniform(a.seeds ? a.seeds[r] : a.seed0);
+    auto draw_t = [&](u64 nucleus) {
+        const double td = ceil((double)u * (double)nucleus);
+        u64 T = td < 1.0 ? 1ULL : (u64)td;
+        return T > nucleus ? nucleus : T;
+    };
+    find_bin(draw_t(T1), sh);
+    const int c_lo = min(max(sh.r_bin, 0), kDistBins - 1);
+    __syncthreads();
+    find_bin(draw_t(after_b1), sh);
+    const int c_hi = min(max(sh.r_bin, 0), kDistBins - 1);
+    __syncthreads();
+    if (tid == 0) a.plan[r] = SmpPlan{total, vmax, b1, c_lo, c_hi};
+}
+
+__global__ __launch_bounds__(kSliceNT) void smp_gather(SliceArgs a) {
+    __shared__ unsigned lbits[kSliceWords];
+    __shared__ u64 lkey[kSliceCap], lq[kSliceCap];
+    __shared__ int lcount;
+    const int r = blockIdx.x / a.S, s = blockIdx.x - r * a.S;
+    const SmpPlan pl = a.plan[r];
+    if (!(pl.vmax > -INFINITY)) return;
+    const int lo = min(a.n, s * a.slen), hi = min(a.n, lo + a.slen);
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x == 0) lcount = 0;
+    const SampleRow row = slice_row_lds(a, r, lo, hi, lbits);  // (synchronises)
+    slice_scan<kSliceNT>(row, lo, hi, [&](int i, float v) {
+        const int b = dist_bin(v, pl.vmax);
+        const bool cand = b == pl.b1 || (b >= pl.c_lo && b <= pl.c_hi);
+        // one reservation per wave: the lowest candidate lane adds the
+        // wave's count, the others take consecutive slots after it
+        const u64 mask = __ballot(cand);
+        if (cand) {
+            const int leader = __ffsll((long long)mask) - 1;
+            int base = 0;
+            if (lane == leader) base = atomicAdd(&lcount, __popcll(mask));
+            base = __shfl(base, leader, 64);
+            const int slot = base + __popcll(mask & ((1ULL << lane) - 1ULL));
+            if (slot < kSliceCap) {  // a larger count sends the row to row scans
+                lkey[slot] = order_key(v, i);
+                lq[slot] = mass_fx(v, pl.vmax);
+            }
+        }
+    });
+    __syncthreads();
+    const int c = lcount;
+    const size_t seg = (size_t)blockIdx.x * kSliceCap;
+    for (int j = threadIdx.x; j < min(c, kSliceCap); j += kSliceNT) {
+        a.gkey[seg + j] = lkey[j];
+        a.gq[seg + j] = lq[j];
+    }
+    if (threadIdx.x == 0) a.gcnt[blockIdx.x] = c;
+}
+
+__global__ __launch_bounds__(kSmpNT) void smp_finish(SliceArgs a) {
+    __shared__ SmpShared sh;
+    const int r = blockIdx.x, tid = threadIdx.x;
+    const SmpPlan pl = a.plan[r];
+    if (!(pl.vmax > -INFINITY)) {
+        // every value -inf (or NaN): as sample_topp_rows
+        if (tid == 0) a.out[r] = a.n - 1;
+        return;
+    }
+    for (int b = tid; b < kDistBins; b += kSmpNT) sh.h_mass[b] = a.mhist[(size_t)r * kDistBins + b];
+    if (tid == 0) sh.g_bin = -1;
+    __syncthreads();
+    const SampleRow row = slice_row(a, r);
+    // the gathered segments of this row (any overflowed: full row scans)
+    if (tid < 64) {
+        const int c = tid < a.S ? a.gcnt[r * a.S + tid] : 0;
+        const unsigned long long over = __ballot(c > kSliceCap);
+        int incl = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (tid >= o) incl += y;
+        }
+        if (tid < a.S) sh.seg_off[tid + 1] = incl;
+        if (tid == 0) {
+            sh.seg_off[0] = 0;
+            sh.g_cnt = over ? 0 : 1;
+        }
+    }
+    __syncthreads();
+    const Pregathered pre{a.gkey + (size_t)r * a.S * kSliceCap, a.gq + (size_t)r * a.S * kSliceCap,
+                          a.S, kSliceCap, sh.g_cnt};
+    __syncthreads();
+    const u64 total = pl.total;
+    const double tc = ceil((double)a.p * (double)total);
+    u64 T = tc < 1.0 ? 1ULL : (u64)tc;
+    if (T > total) T = total;
+    select_prefix(row, pl.vmax, T, sh, pre);
+    const u64 nucleus = sh.r_mass;
+    const float u = splitmix_uniform(a.seeds ? a.seeds[r] : a.seed0);
+    const double td = ceil((double)u * (double)nucleus);
+    T = td < 1.0 ? 1ULL : (u64)td;
+    if (T > nucleus) T = nucleus;
+    select_prefix(row, pl.vmax, T, sh, pre);
+    if (tid == 0) a.out[r] = key_index(sh.r_key);
 }
 
 // argmax per row (earliest index on ties): a sequential scan with strict >
@@ -422,7 +780,7 @@ __global__ __launch_bounds__(kArgNT) void argmax_rows(const float* __restrict__ 
                                                       OUT* __restrict__ out) {
     __shared__ float sv[kArgNT / 64];
     __shared__ int si[kArgNT / 64];
-    const SampleRow row{x + (size_t)blockIdx.x * n, n, 1.0f, 1.0f, nullptr};
+    const SampleRow row{x + (size_t)blockIdx.x * n, n, 1.0f, 1.0f, nullptr, 0};
     const int tid = threadIdx.x;
     float bv = -INFINITY;
     int bi = n;  // sentinel: no candidate
@@ -458,6 +816,11 @@ __global__ __launch_bounds__(kArgNT) void argmax_rows(const float* __restrict__ 
     }
 }
 
+int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return (v && *v) ? atoi(v) : dflt;
+}
+
 void sampling_check(int rows, int n, float p, float t) {
     if (rows < 0) inval("rows must be >= 0");
     if (n <= 0) inval("sample of empty logits");
@@ -478,8 +841,68 @@ void topp_launch(const float* x, int rows, int n, float p, float t, float pen,
     if (!x || !out) inval("sampling: null operand");
     if (penal && !ids) inval("sampling: null token ids");
     const float inv_t = 1.0f / t;  // the reference's order (inv_t = 1.0f / t)
-    sample_topp_rows<<<(unsigned)rows, kSmpNT, 0, s>>>(
-        x, n, p, inv_t, pen, penal ? ids : nullptr, penal ? offs : nullptr, m, seeds, seed0, out);
+    // slices per row: enough workgroups for about two per CU, at least
+    // kMinSlice tokens each; FT_SMP_SINGLE=1 keeps one workgroup per row
+    const int cus = dev_info().cu_count;
+    int S = 1;
+    if (rows < cus && env_int("FT_SMP_SINGLE", 0) == 0)
+        S = std::min({(2 * cus + rows - 1) / rows, std::max(1, n / kMinSlice), kMaxSlices});
+    if (S <= 1) {
+        sample_topp_rows<<<(unsigned)rows, kSmpNT, 0, s>>>(
+            x, n, p, inv_t, pen, penal ? ids : nullptr, penal ? offs : nullptr, m, seeds, seed0,
+            out);
+        launch_check("sampling kernel launch");
+        return;
+    }
+    int slen = (n + S - 1) / S;
+    slen = (slen + 31) & ~31;  // whole bitmap words, 16-byte aligned starts
+    S = (n + slen - 1) / slen;
+    SliceArgs a{};
+    a.x = x;
+    a.n = n;
+    a.S = S;
+    a.slen = slen;
+    a.words = (n + 31) / 32;
+    a.inv_t = inv_t;
+    a.pen = pen;
+    a.ids = penal ? ids : nullptr;
+    a.offs = penal ? offs : nullptr;
+    a.m_single = m;
+    a.p = p;
+    a.seeds = seeds;
+    a.seed0 = seed0;
+    a.out = out;
+    // scratch, 256-byte aligned pieces
+    const size_t R = (size_t)rows;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off += (bytes + 255) & ~(size_t)255;
+        return at;
+    };
+    const size_t o_bits = take(R * a.words * 4), o_smax = take(R * S * 4),
+                 o_hm = take(R * S * kDistBins * 8), o_mh = take(R * kDistBins * 8), o_plan = take(R * sizeof(SmpPlan)),
+                 o_gn = take(R * S * 4), o_gk = take(R * S * kSliceCap * 8),
+                 o_gq = take(R * S * kSliceCap * 8);
+    char* ws = (char*)scratch(Scratch::Sampling, off, s);
+    a.bits = (unsigned*)(ws + o_bits);
+    a.smax = (float*)(ws + o_smax);
+    a.hmass = (u64*)(ws + o_hm);
+    a.mhist = (u64*)(ws + o_mh);
+    a.plan = (SmpPlan*)(ws + o_plan);
+    a.gcnt = (int*)(ws + o_gn);
+    a.gkey = (u64*)(ws + o_gk);
+    a.gq = (u64*)(ws + o_gq);
+    const unsigned grid = (unsigned)(rows * S);
+    smp_slice_max<<<grid, kSliceNT, 0, s>>>(a);
+    launch_check("sampling max kernel launch");
+    smp_slice_hist<<<grid, kSliceNT, 0, s>>>(a);
+    launch_check("sampling histogram kernel launch");
+    smp_plan<<<(unsigned)rows, kSmpNT, 0, s>>>(a);
+    launch_check("sampling plan kernel launch");
+    smp_gather<<<grid, kSliceNT, 0, s>>>(a);
+    launch_check("sampling gather kernel launch");
+    smp_finish<<<(unsigned)rows, kSmpNT, 0, s>>>(a);
     launch_check("sampling kernel launch");
 }
 

@@ -168,3 +168,34 @@ def test_sampling_contract():
     with pytest.raises(ValueError):
         ft.sample_topp_batched(t(np.ones((3, 4), np.float32)), 0.9, seeds=[1, 2])
     assert ft.sample_topp_batched(t(np.ones((0, 4), np.float32)), 0.9).numel() == 0
+
+
+@pytest.mark.parametrize("rows,n", [(1, 128256), (3, 50000), (16, 32000), (64, 128256),
+                                    (2, 16417), (5, 20000)])
+def test_sliced_pipeline_matches_single_workgroup(rows, n, monkeypatch):
+    # Fewer rows than CUs: each row is split over several workgroups (slice
+    # maxima, slice histograms, a per-row plan, a gather of the bins the two
+    # queries can cross, the exact select). Masses are integers, so the
+    # tokens equal those of the one-workgroup-per-row kernel (FT_SMP_SINGLE)
+    # bit for bit, including rows that fall back to full scans.
+    rng = np.random.default_rng(rows * 1000 + n)
+    logits = (rng.standard_normal((rows, n)) * 2).astype(np.float32)
+    if rows >= 3:
+        logits[1] = 0.0                               # flat: the plan overflows
+        logits[2, :] = -np.inf                        # no finite value
+    if rows >= 5:
+        logits[3, rng.integers(0, n, 50)] = np.nan    # NaNs count as mass 0
+        logits[4, :] = -30.0
+        logits[4, n // 3] = 5.0                       # one dominant token
+    seeds = list(range(11, 11 + rows))
+    hist = [rng.integers(0, n, size=int(rng.integers(0, 80))).tolist() for _ in range(rows)]
+    lt = t(logits)
+    for p, temp in [(0.9, 0.8), (0.5, 1.3), (1.0, 1.0), (0.05, 0.3)]:
+        got = {}
+        for mode in ("0", "1"):
+            monkeypatch.setenv("FT_SMP_SINGLE", mode)
+            got[mode] = (ft.decode_step_batched(lt, hist, 1.3, p=p, temperature=temp,
+                                                seeds=seeds).tolist(),
+                         ft.sample_topp_batched(lt, p, temperature=temp, seeds=seeds).tolist(),
+                         ft.sample_topp(lt[0], p, temperature=temp, seed=seeds[0]))
+        assert got["0"] == got["1"], (p, temp)
