@@ -1453,9 +1453,8 @@ def decode_step_batched(logits, sampled_ids, penalty=1.0, *, p=0.9, temperature=
                         seeds=None, ids_offsets=None, cuda=False, device_out=False):
     """The fused decode step for every row of ``[rows, vocab]`` float32
     logits (each row split across CUs when there are fewer rows than CUs).
-    ``sampled_ids``: per-row
-    histories (ragged sequences, a 2-D array, or flat ids with
-    ``ids_offsets``). Returns int64 tokens on the host (the reference's
+    ``sampled_ids``: per-row histories (ragged sequences, a 2-D array, or
+    flat ids with ``ids_offsets``). Returns int64 tokens on the host (the reference's
     contract); build addition ``device_out=True`` keeps them on the GPU."""
     _sampling_params(p, temperature, penalty)
     if _on_gpu(logits):
