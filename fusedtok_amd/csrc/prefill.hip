@@ -87,6 +87,12 @@ __device__ __forceinline__ int pack2(float a, float b) {
     return __builtin_bit_cast(int, __builtin_convertvector(f2{a, b}, t2));
 }
 
+// two bf16 (one dword) -> two fp16, exact for |v| < 2^16 (fp16 keeps
+// every bf16 significand; values below 2^-14 become fp16 subnormals)
+__device__ __forceinline__ unsigned bf2_to_h2(unsigned w) {
+    return (unsigned)pack2<f16>(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
+}
+
 // position (in 4-key units) of key group G (keys 4G .. 4G+3 of a 64-key
 // tile) in a V^T row: the PV k-slot order described above
 __device__ __forceinline__ int vt_pos(int G) {
@@ -101,6 +107,11 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
     using M = PMma<T>;
     using V8 = typename M::v8;
     using C = PCfg<D>;
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    // bf16 inputs: P and V go through an fp16 PV product (P rounded to 11
+    // significant bits) on every tile whose V values are all below 2^16 in
+    // magnitude, bf16 hi + lo P otherwise
+    constexpr bool kF16PV = std::is_same<T, bf16>::value;
     __shared__ __attribute__((aligned(16))) char smem[2 * C::kStage];
 
     const int nqt = (seq + kPQ - 1) / kPQ;
@@ -155,7 +166,8 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
             }
         }
     };
-    auto store_tile = [&](int st) {
+    // f16v (bf16 inputs): V^T stored as fp16 for the fp16 PV product
+    auto store_tile = [&](int st, bool f16v) {
         char* ks = smem + st * C::kStage;
         char* vt = ks + kPKV * C::kKPitch;
 #pragma unroll
@@ -168,8 +180,14 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
             char* dst = vt + (8 * vc) * kVtPitch + 8 * vt_pos(vG);
 #pragma unroll
             for (int w = 0; w < 4; ++w) {  // dwords w of the 4 rows: d = 8 vc + 2 w, +1
-                const unsigned a0 = (unsigned)vreg[0][w], a1 = (unsigned)vreg[1][w];
-                const unsigned a2 = (unsigned)vreg[2][w], a3 = (unsigned)vreg[3][w];
+                unsigned a0 = (unsigned)vreg[0][w], a1 = (unsigned)vreg[1][w];
+                unsigned a2 = (unsigned)vreg[2][w], a3 = (unsigned)vreg[3][w];
+                if (kF16PV && f16v) {
+                    a0 = bf2_to_h2(a0);
+                    a1 = bf2_to_h2(a1);
+                    a2 = bf2_to_h2(a2);
+                    a3 = bf2_to_h2(a3);
+                }
                 uint2 lo, hi;  // keys 0..3 of element 2w (low halves), 2w + 1 (high)
                 lo.x = (a0 & 0xffffu) | (a1 << 16);
                 lo.y = (a2 & 0xffffu) | (a3 << 16);
@@ -191,122 +209,177 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
     const int wrow0 = q0 + 32 * wave;  // first query row of this wave
     const float lazy_raw = kLazy / scale_log2;
 
+    // whether the V tile in vreg fits fp16 exactly (a workgroup vote; every
+    // thread must call it): the largest |v| bit pattern of the thread's
+    // pieces, inf and NaN counting as too large
+    auto v_fits_f16 = [&]() {
+        typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+        us2 mx = {0, 0};
+        if (vthr) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    mx = __builtin_elementwise_max(
+                        mx, __builtin_bit_cast(us2, (unsigned)vreg[r][w] & 0x7fff7fffu));
+        }
+        const bool bad = mx[0] >= 0x4780u || mx[1] >= 0x4780u;  // >= 2^16
+        return __syncthreads_or(bad ? 1 : 0) == 0;
+    };
+
     load_tile(0);
-    store_tile(0);
+    const bool f16_first = kF16PV && v_fits_f16();
+    store_tile(0, f16_first);
     __syncthreads();
-    for (int kt = 0; kt < nkt; ++kt) {
-        if (kt + 1 < nkt) load_tile(kt + 1);
-        const int kv0 = kt * kPKV;
-        const bool active = !causal || kv0 <= wrow0 + 31;
-        if (active) {
-            const char* ks = smem + (kt & 1) * C::kStage;
-            const char* vt = ks + kPKV * C::kKPitch;
-            // scores S^T for 4 key blocks x 2 query blocks
-            f32x4 sc[4][2];
+    // Tiles kt0 .. : the fp16 PV loop (F16) runs while each next tile votes
+    // in range and hands over at the first one that does not (staged in
+    // bf16); the bf16 loop then runs to the end. Two separate loops, so that
+    // neither path's temporaries are live in the other.
+    auto run = [&](auto f16_tag, int kt0) -> int {
+        constexpr bool F16 = decltype(f16_tag)::value;
+        for (int kt = kt0; kt < nkt; ++kt) {
+            if (kt + 1 < nkt) load_tile(kt + 1);
+            const int kv0 = kt * kPKV;
+            const bool active = !causal || kv0 <= wrow0 + 31;
+            if (active) {
+                const char* ks = smem + (kt & 1) * C::kStage;
+                const char* vt = ks + kPKV * C::kKPitch;
+                // scores S^T for 4 key blocks x 2 query blocks
+                f32x4 sc[4][2];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                sc[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-                sc[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int kb = 0; kb < 4; ++kb) {
+                    sc[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    sc[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int s = 0; s < C::kS; ++s) {
-                    const V8 kf = *reinterpret_cast<const V8*>(
-                        ks + (16 * kb + r16) * C::kKPitch + (32 * s + 8 * g) * 2);
-                    sc[kb][0] = M::mma(kf, qf[0][s], sc[kb][0]);
-                    sc[kb][1] = M::mma(kf, qf[1][s], sc[kb][1]);
+                    for (int s = 0; s < C::kS; ++s) {
+                        const V8 kf = *reinterpret_cast<const V8*>(
+                            ks + (16 * kb + r16) * C::kKPitch + (32 * s + 8 * g) * 2);
+                        sc[kb][0] = M::mma(kf, qf[0][s], sc[kb][0]);
+                        sc[kb][1] = M::mma(kf, qf[1][s], sc[kb][1]);
+                    }
                 }
-            }
-            // online softmax per query row, on raw scores (the 1/sqrt(D) *
-            // log2(e) factor c > 0 commutes with max and folds into one FMA
-            // per score: p = exp2(s c - m c)); masks only on the tiles that
-            // cross this wave's diagonal or the sequence end
-            const bool need_mask = (causal && kv0 + kPKV - 1 > wrow0) || kv0 + kPKV > seq;
-            i32x4_t ph[2][2], pl[2][2];
+                // online softmax per query row, on raw scores (the 1/sqrt(D) *
+                // log2(e) factor c > 0 commutes with max and folds into one FMA
+                // per score: p = exp2(s c - m c)); masks only on the tiles that
+                // cross this wave's diagonal or the sequence end
+                const bool need_mask = (causal && kv0 + kPKV - 1 > wrow0) || kv0 + kPKV > seq;
+                i32x4_t ph[2][2], pl[2][2];
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                float mt = -INFINITY;
-                if (need_mask) {
-                    const int qrow = wrow0 + 16 * qb + r16;
+                for (int qb = 0; qb < 2; ++qb) {
+                    float mt = -INFINITY;
+                    if (need_mask) {
+                        const int qrow = wrow0 + 16 * qb + r16;
+#pragma unroll
+                        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const int key = kv0 + 16 * kb + 4 * g + i;
+                                const bool valid = key < seq && (!causal || key <= qrow);
+                                if (!valid) sc[kb][qb][i] = -INFINITY;
+                            }
+                    }
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) mt = fmaxf(mt, sc[kb][qb][i]);
+                    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+                    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+                    // lazy rescale: the running maximum moves only when the tile's
+                    // exceeds it by more than kLazy / c (weights then stay
+                    // <= 2^kLazy); a wave whose rows all keep theirs skips the
+                    // output rescale
+                    const bool upd = mt > m_run[qb] + lazy_raw;
+                    const float m_new = upd ? mt : m_run[qb];
+                    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+                    // v_exp_f32 directly: exp2f's expansion adds a denormal-range
+                    // rescale per call; weights below 2^-126 of the row maximum
+                    // flush to 0, which changes no sum at float precision
+                    const float alpha = __builtin_amdgcn_exp2f((m_run[qb] - m_use) * scale_log2);
+                    const float nmc = -m_use * scale_log2;
+                    float p[4][4];
+                    float psum = 0.f;
 #pragma unroll
                     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            const int key = kv0 + 16 * kb + 4 * g + i;
-                            const bool valid = key < seq && (!causal || key <= qrow);
-                            if (!valid) sc[kb][qb][i] = -INFINITY;
+                            p[kb][i] = __builtin_amdgcn_exp2f(fmaf(sc[kb][qb][i], scale_log2, nmc));
+                            psum += p[kb][i];
+                        }
+                    l_run[qb] = l_run[qb] * alpha + psum;
+                    m_run[qb] = m_new;
+                    if (__builtin_amdgcn_ballot_w64(upd)) {
+#pragma unroll
+                        for (int db = 0; db < C::kDB; ++db) o[db][qb] *= alpha;
+                    }
+                    // P^T fragments: dword w of step ks2 holds slots 8g + 2w, +1
+#pragma unroll
+                    for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+                        for (int w = 0; w < 4; ++w) {
+                            const float p0 = p[2 * ks2 + (w >> 1)][2 * (w & 1)];
+                            const float p1 = p[2 * ks2 + (w >> 1)][2 * (w & 1) + 1];
+                            if constexpr (F16) {
+                                ph[qb][ks2][w] = pack2<f16>(p0, p1);
+                            } else if constexpr (M::kSplit) {
+                                // hi: the top 16 bits (truncation, exact); lo: the
+                                // exact remainder rounded to bf16; hi + lo carries
+                                // ~16 significant bits of p
+                                const unsigned u0 = __float_as_uint(p0), u1 = __float_as_uint(p1);
+                                ph[qb][ks2][w] = (int)((u0 >> 16) | (u1 & 0xffff0000u));
+                                const float r0 = p0 - __uint_as_float(u0 & 0xffff0000u);
+                                const float r1 = p1 - __uint_as_float(u1 & 0xffff0000u);
+                                pl[qb][ks2][w] = pack2<T>(r0, r1);
+                            } else {
+                                ph[qb][ks2][w] = pack2<T>(p0, p1);
+                            }
                         }
                 }
+                // O^T += V^T . P^T
+                if constexpr (F16) {
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
+                    for (int db = 0; db < C::kDB; ++db)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) mt = fmaxf(mt, sc[kb][qb][i]);
-                mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-                mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-                // lazy rescale: the running maximum moves only when the tile's
-                // exceeds it by more than kLazy / c (weights then stay
-                // <= 2^kLazy); a wave whose rows all keep theirs skips the
-                // output rescale
-                const bool upd = mt > m_run[qb] + lazy_raw;
-                const float m_new = upd ? mt : m_run[qb];
-                const float m_use = m_new == -INFINITY ? 0.f : m_new;
-                // v_exp_f32 directly: exp2f's expansion adds a denormal-range
-                // rescale per call; weights below 2^-126 of the row maximum
-                // flush to 0, which changes no sum at float precision
-                const float alpha = __builtin_amdgcn_exp2f((m_run[qb] - m_use) * scale_log2);
-                const float nmc = -m_use * scale_log2;
-                float p[4][4];
-                float psum = 0.f;
+                        for (int ks2 = 0; ks2 < 2; ++ks2) {
+                            const h8 vf = *reinterpret_cast<const h8*>(
+                                vt + (16 * db + r16) * kVtPitch + (32 * ks2 + 8 * g) * 2);
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        p[kb][i] = __builtin_amdgcn_exp2f(fmaf(sc[kb][qb][i], scale_log2, nmc));
-                        psum += p[kb][i];
-                    }
-                l_run[qb] = l_run[qb] * alpha + psum;
-                m_run[qb] = m_new;
-                if (__builtin_amdgcn_ballot_w64(upd)) {
-#pragma unroll
-                    for (int db = 0; db < C::kDB; ++db) o[db][qb] *= alpha;
-                }
-                // P^T fragments: dword w of step ks2 holds slots 8g + 2w, +1
-#pragma unroll
-                for (int ks2 = 0; ks2 < 2; ++ks2)
-#pragma unroll
-                    for (int w = 0; w < 4; ++w) {
-                        const float p0 = p[2 * ks2 + (w >> 1)][2 * (w & 1)];
-                        const float p1 = p[2 * ks2 + (w >> 1)][2 * (w & 1) + 1];
-                        if constexpr (M::kSplit) {
-                            // hi: the top 16 bits (truncation, exact); lo: the
-                            // exact remainder rounded to bf16; hi + lo carries
-                            // ~16 significant bits of p
-                            const unsigned u0 = __float_as_uint(p0), u1 = __float_as_uint(p1);
-                            ph[qb][ks2][w] = (int)((u0 >> 16) | (u1 & 0xffff0000u));
-                            const float r0 = p0 - __uint_as_float(u0 & 0xffff0000u);
-                            const float r1 = p1 - __uint_as_float(u1 & 0xffff0000u);
-                            pl[qb][ks2][w] = pack2<T>(r0, r1);
-                        } else {
-                            ph[qb][ks2][w] = pack2<T>(p0, p1);
+                            for (int qb = 0; qb < 2; ++qb)
+                                o[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                    vf, __builtin_bit_cast(h8, ph[qb][ks2]), o[db][qb], 0, 0, 0);
                         }
-                    }
+                } else {
+#pragma unroll
+                    for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+                        for (int ks2 = 0; ks2 < 2; ++ks2) {
+                            const V8 vf = *reinterpret_cast<const V8*>(
+                                vt + (16 * db + r16) * kVtPitch + (32 * ks2 + 8 * g) * 2);
+#pragma unroll
+                            for (int qb = 0; qb < 2; ++qb) {
+                                o[db][qb] = M::mma(vf, __builtin_bit_cast(V8, ph[qb][ks2]), o[db][qb]);
+                                if constexpr (M::kSplit)
+                                    o[db][qb] = M::mma(vf, __builtin_bit_cast(V8, pl[qb][ks2]),
+                                                       o[db][qb]);
+                            }
+                        }
+                }
             }
-            // O^T += V^T . P^T
-#pragma unroll
-            for (int db = 0; db < C::kDB; ++db)
-#pragma unroll
-                for (int ks2 = 0; ks2 < 2; ++ks2) {
-                    const V8 vf = *reinterpret_cast<const V8*>(
-                        vt + (16 * db + r16) * kVtPitch + (32 * ks2 + 8 * g) * 2);
-#pragma unroll
-                    for (int qb = 0; qb < 2; ++qb) {
-                        o[db][qb] = M::mma(vf, __builtin_bit_cast(V8, ph[qb][ks2]), o[db][qb]);
-                        if constexpr (M::kSplit)
-                            o[db][qb] = M::mma(vf, __builtin_bit_cast(V8, pl[qb][ks2]), o[db][qb]);
-                    }
-                }
+            if (kt + 1 < nkt) {
+                const bool next_f16 = F16 && v_fits_f16();
+                store_tile((kt + 1) & 1, next_f16);
+                __syncthreads();
+                if (F16 && !next_f16) return kt + 1;
+            } else {
+                __syncthreads();
+            }
         }
-        if (kt + 1 < nkt) store_tile((kt + 1) & 1);
-        __syncthreads();
+        return nkt;
+    };
+    int kt_split = 0;
+    if constexpr (kF16PV) {
+        if (f16_first) kt_split = run(std::true_type{}, 0);
     }
+    run(std::false_type{}, kt_split);
 
     // normalise and store: lane (q, g) holds d = 16 db + 4 g + i of row q
     T* oh = out + ((size_t)b * hq + h) * seq * D;

@@ -49,6 +49,29 @@ def test_prefill_mfma_matches_oracle(dt, d, s, causal):
     _check_half(out, q, k, v, causal)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_bf16_large_v_tiles_take_the_split_path(d, causal):
+    # bf16 inputs: a key tile whose V values all stay below 2^16 runs the PV
+    # product in fp16 (exact V, P rounded to 11 bits); from the first tile
+    # holding a larger value on, the workgroup uses bf16 P split hi + lo.
+    # Here keys 130..199 carry V around 7e4 (tiles 2 and 3), so both paths
+    # and the hand-over run; the oracle sees the same rounded inputs. (Large
+    # values of mixed sign would cancel to outputs of order 1 whose error
+    # follows the large terms, for any finite precision of P.)
+    rng = np.random.default_rng(d + int(causal))
+    dt = torch.bfloat16
+    q, k, v = _inputs(rng, 1, 4, 2, 300, d, dt)
+    v2 = v.clone()
+    big = 7.0e4 + 1.0e3 * rng.standard_normal((1, 2, 70, d)).astype(np.float32)
+    v[:, :, 130:200] = torch.from_numpy(big).to(DEV, dt)
+    assert v.float().abs().max().item() >= 65536.0
+    out = ft.attention_prefill(q, k, v, causal=causal)
+    _check_half(out, q, k, v, causal)
+    # and every value in range: the fp16 path alone
+    _check_half(ft.attention_prefill(q, k, v2, causal=causal), q, k, v2, causal)
+
+
 @pytest.mark.parametrize("dt", HALF)
 def test_prefill_mfma_first_row_is_v0_and_s1_is_decode(dt):
     rng = np.random.default_rng(5)
