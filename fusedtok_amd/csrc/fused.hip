@@ -5,7 +5,8 @@
 // launches and no float intermediate in HBM:
 //
 //   rmsnorm_quant   y = RMSNorm(x [+ r]) * w in f32 -> per-tensor int8 codes
-//                   + device scale (2 launches: per-row pass, fold+quantize)
+//                   + device scale (1 launch for up to 4 rows of up to
+//                   4096 columns, else 2: per-row pass, fold+quantize)
 //   swiglu_quant    y = silu(g) * u in f32 -> per-tensor int8 codes + device
 //                   scale (2 launches); g / u may be strided row views (the
 //                   halves of one gate|up GEMM output)
@@ -59,6 +60,10 @@ __device__ __forceinline__ float4 rms_in4(const T* x, const T* r, size_t off) {
     return v;
 }
 
+constexpr int kRowChunks = 4;  // 4-element chunks per thread held in registers
+
+// One workgroup per row: sum of squares -> inv, then the row's max |y|. A row
+// of up to 4096 columns stays in registers between the two passes.
 template <typename T>
 __global__ __launch_bounds__(kFNT) void rmsq_rows(
     const T* __restrict__ x, const T* __restrict__ r, const float* __restrict__ w,
@@ -66,44 +71,98 @@ __global__ __launch_bounds__(kFNT) void rmsq_rows(
     __shared__ float red[kFNT / 64];
     const size_t base = (size_t)blockIdx.x * cols;
     const int chunks = cols >> 2;
-    float acc = 0.0f;
-    for (int c = threadIdx.x; c < chunks; c += kFNT) {
-        const float4 v = rms_in4(x, r, base + 4 * c);
-        acc = fmaf(v.x, v.x, acc);
-        acc = fmaf(v.y, v.y, acc);
-        acc = fmaf(v.z, v.z, acc);
-        acc = fmaf(v.w, v.w, acc);
-    }
-    const float total = block_sum<kFNT>(acc, red);
-    const float inv = 1.0f / sqrtf(total / (float)cols + eps);
     float m = 0.0f;
-    for (int c = threadIdx.x; c < chunks; c += kFNT) {
-        const float4 v = rms_in4(x, r, base + 4 * c);
-        const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c);
-        m = fmaxf(m, fabsf(v.x * inv * wv.x));
-        m = fmaxf(m, fabsf(v.y * inv * wv.y));
-        m = fmaxf(m, fabsf(v.z * inv * wv.z));
-        m = fmaxf(m, fabsf(v.w * inv * wv.w));
+    float inv;
+    if (chunks <= kFNT * kRowChunks) {
+        float4 v[kRowChunks];
+#pragma unroll
+        for (int j = 0; j < kRowChunks; ++j) {
+            const int c = threadIdx.x + j * kFNT;
+            v[j] = c < chunks ? rms_in4(x, r, base + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kRowChunks; ++j) {
+            if ((int)threadIdx.x + j * kFNT < chunks) {
+                acc = fmaf(v[j].x, v[j].x, acc);
+                acc = fmaf(v[j].y, v[j].y, acc);
+                acc = fmaf(v[j].z, v[j].z, acc);
+                acc = fmaf(v[j].w, v[j].w, acc);
+            }
+        }
+        const float total = block_sum<kFNT>(acc, red);
+        inv = 1.0f / sqrtf(total / (float)cols + eps);
+#pragma unroll
+        for (int j = 0; j < kRowChunks; ++j) {
+            const int c = threadIdx.x + j * kFNT;
+            if (c < chunks) {
+                const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c);
+                m = fmaxf(m, fabsf(v[j].x * inv * wv.x));
+                m = fmaxf(m, fabsf(v[j].y * inv * wv.y));
+                m = fmaxf(m, fabsf(v[j].z * inv * wv.z));
+                m = fmaxf(m, fabsf(v[j].w * inv * wv.w));
+            }
+        }
+    } else {
+        float acc = 0.0f;
+        for (int c = threadIdx.x; c < chunks; c += kFNT) {
+            const float4 v = rms_in4(x, r, base + 4 * c);
+            acc = fmaf(v.x, v.x, acc);
+            acc = fmaf(v.y, v.y, acc);
+            acc = fmaf(v.z, v.z, acc);
+            acc = fmaf(v.w, v.w, acc);
+        }
+        const float total = block_sum<kFNT>(acc, red);
+        inv = 1.0f / sqrtf(total / (float)cols + eps);
+        for (int c = threadIdx.x; c < chunks; c += kFNT) {
+            const float4 v = rms_in4(x, r, base + 4 * c);
+            const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c);
+            m = fmaxf(m, fabsf(v.x * inv * wv.x));
+            m = fmaxf(m, fabsf(v.y * inv * wv.y));
+            m = fmaxf(m, fabsf(v.z * inv * wv.z));
+            m = fmaxf(m, fabsf(v.w * inv * wv.w));
+        }
     }
     m = block_max<kFNT>(m, red);
     if (threadIdx.x == 0) stat[blockIdx.x] = RowStat{m, inv};
 }
 
+// Fold of the row maxima -> scale, then the codes. Each thread's first
+// element (x, r, w and its row's inv) is loaded before the fold, so the fold's
+// reads and the data reads share one round trip.
 template <typename T>
 __global__ __launch_bounds__(kFNT) void rmsq_quant(
     const T* __restrict__ x, const T* __restrict__ r, const float* __restrict__ w,
     const RowStat* __restrict__ stat, signed char* __restrict__ q,
     float* __restrict__ scale_out, int rows, int cols) {
     __shared__ float red[kFNT / 64];
+    const long long n4 = (long long)rows * cols / 4;
+    const int cols4 = cols >> 2;
+    const long long e0 = (long long)blockIdx.x * kFNT + threadIdx.x;
+    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), w0 = v0;
+    float inv0 = 0.0f;
+    if (e0 < n4) {
+        const int row = (int)(e0 / cols4);
+        const int c = (int)(e0 - (long long)row * cols4) * 4;
+        v0 = rms_in4(x, r, (size_t)row * cols + c);
+        w0 = *reinterpret_cast<const float4*>(w + c);
+        inv0 = stat[row].inv;
+    }
     float m = 0.0f;
     for (int i = threadIdx.x; i < rows; i += kFNT) m = fmaxf(m, stat[i].absmax);
     m = block_max<kFNT>(m, red);
     const float scale = make_scale(m);
     const float inv_s = 1.0f / scale;
     if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
-    const long long n4 = (long long)rows * cols / 4;
-    const int cols4 = cols >> 2;
-    for (long long e = (long long)blockIdx.x * kFNT + threadIdx.x; e < n4;
+    if (e0 < n4) {
+        char4 o;
+        o.x = quant1(v0.x * inv0 * w0.x, inv_s);
+        o.y = quant1(v0.y * inv0 * w0.y, inv_s);
+        o.z = quant1(v0.z * inv0 * w0.z, inv_s);
+        o.w = quant1(v0.w * inv0 * w0.w, inv_s);
+        *reinterpret_cast<char4*>(q + 4 * e0) = o;
+    }
+    for (long long e = e0 + (long long)gridDim.x * kFNT; e < n4;
          e += (long long)gridDim.x * kFNT) {
         const int row = (int)(e / cols4);
         const int c = (int)(e - (long long)row * cols4) * 4;
@@ -119,6 +178,121 @@ __global__ __launch_bounds__(kFNT) void rmsq_quant(
     }
 }
 
+// Small-M rmsnorm_quant in one launch: one workgroup of 256 * rows threads
+// for up to 4 rows; lane g (256 threads) holds row g in registers, thread t
+// chunks t, t + 256, t + 512, t + 768, so x (and r) are read once and the row
+// pass, the tensor maximum and the codes come from the same registers. The
+// arithmetic is the two-kernel path's: per row the same 256-thread chunk
+// assignment, fmaf order, wave butterfly and in-order sum of the lane's 4
+// wave totals; products (v * inv) * w; maxima are exact in any order. One CU
+// keeps only ~64 cache-line misses in flight (~10 GB/s from HBM), so each
+// further row adds ~0.75 us: past 4 rows the two kernels, which spread the
+// rows over CUs, are faster.
+constexpr int kRmsqRows = 1;    // rows per lane
+constexpr int kRmsqMaxRows = 4 * kRmsqRows;
+constexpr int kRmsqMaxCols = 4 * kFNT * kRowChunks;
+
+template <typename T>
+__global__ __launch_bounds__(4 * kFNT) void rmsq_small(
+    const T* __restrict__ x, const T* __restrict__ r, const float* __restrict__ w,
+    signed char* __restrict__ q, float* __restrict__ scale_out, int rows, int cols,
+    float eps) {
+    __shared__ float red[kRmsqMaxRows][kFNT / 64];
+    __shared__ float redm[4 * kFNT / 64];
+    const int G = blockDim.x / kFNT;
+    const int lane_g = threadIdx.x / kFNT;
+    const int t = threadIdx.x % kFNT;
+    const int wv = t >> 6;
+    const int chunks = cols >> 2;
+
+    float4 v[kRmsqRows][kRowChunks];
+    float4 wc[kRowChunks];
+#pragma unroll
+    for (int j = 0; j < kRowChunks; ++j) {
+        const int c = t + j * kFNT;
+        wc[j] = c < chunks ? *reinterpret_cast<const float4*>(w + 4 * c)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < kRmsqRows; ++i) {
+        const int row = lane_g + i * G;
+#pragma unroll
+        for (int j = 0; j < kRowChunks; ++j) {
+            const int c = t + j * kFNT;
+            v[i][j] = (row < rows && c < chunks)
+                          ? rms_in4(x, r, (size_t)row * cols + 4 * c)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kRmsqRows; ++i) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kRowChunks; ++j) {
+            if (t + j * kFNT < chunks) {
+                acc = fmaf(v[i][j].x, v[i][j].x, acc);
+                acc = fmaf(v[i][j].y, v[i][j].y, acc);
+                acc = fmaf(v[i][j].z, v[i][j].z, acc);
+                acc = fmaf(v[i][j].w, v[i][j].w, acc);
+            }
+        }
+        acc = wave_sum(acc);
+        if ((t & 63) == 0) red[lane_g + i * G][wv] = acc;
+    }
+    __syncthreads();
+    float inv[kRmsqRows];
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRmsqRows; ++i) {
+        const int row = lane_g + i * G;
+        inv[i] = 0.0f;
+        if (row < rows) {
+            float tot = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kFNT / 64; ++k) tot += red[row][k];
+            inv[i] = 1.0f / sqrtf(tot / (float)cols + eps);
+#pragma unroll
+            for (int j = 0; j < kRowChunks; ++j) {
+                if (t + j * kFNT < chunks) {
+                    m = fmaxf(m, fabsf(v[i][j].x * inv[i] * wc[j].x));
+                    m = fmaxf(m, fabsf(v[i][j].y * inv[i] * wc[j].y));
+                    m = fmaxf(m, fabsf(v[i][j].z * inv[i] * wc[j].z));
+                    m = fmaxf(m, fabsf(v[i][j].w * inv[i] * wc[j].w));
+                }
+            }
+        }
+    }
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) redm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = redm[0];
+    for (int k = 1; k < (int)(blockDim.x >> 6); ++k) m = fmaxf(m, redm[k]);
+    const float scale = make_scale(m);
+    const float inv_s = 1.0f / scale;
+    if (threadIdx.x == 0) *scale_out = scale;
+#pragma unroll
+    for (int i = 0; i < kRmsqRows; ++i) {
+        const int row = lane_g + i * G;
+        if (row >= rows) continue;
+#pragma unroll
+        for (int j = 0; j < kRowChunks; ++j) {
+            const int c = t + j * kFNT;
+            if (c >= chunks) continue;
+            char4 o;
+            o.x = quant1(v[i][j].x * inv[i] * wc[j].x, inv_s);
+            o.y = quant1(v[i][j].y * inv[i] * wc[j].y, inv_s);
+            o.z = quant1(v[i][j].z * inv[i] * wc[j].z, inv_s);
+            o.w = quant1(v[i][j].w * inv[i] * wc[j].w, inv_s);
+            *reinterpret_cast<char4*>(q + (size_t)row * cols + 4 * c) = o;
+        }
+    }
+}
+
+bool rmsq_split_forced() {
+    const char* e = getenv("FT_RMSQ_SPLIT");
+    return e && *e && atoi(e) != 0;
+}
+
 template <typename T>
 void rmsnorm_quant_run(const T* x, const float* w, const T* r, signed char* q,
                        float* scale_out, int rows, int cols, float eps,
@@ -131,6 +305,12 @@ void rmsnorm_quant_run(const T* x, const float* w, const T* r, signed char* q,
     if ((uintptr_t)x % a16 || (r && (uintptr_t)r % a16) || (uintptr_t)w % 16 ||
         (uintptr_t)q % 4)
         inval("rmsnorm_quant: operands must be aligned to 4 elements");
+    if (rows <= kRmsqMaxRows && cols <= kRmsqMaxCols && !rmsq_split_forced()) {
+        rmsq_small<T><<<1, (unsigned)(rows * kFNT), 0, s>>>(x, r, w, q, scale_out, rows,
+                                                             cols, eps);
+        launch_check("rmsnorm_quant small kernel launch");
+        return;
+    }
     RowStat* stat = (RowStat*)scratch(Scratch::QuantMax, (size_t)rows * sizeof(RowStat), s);
     rmsq_rows<T><<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps);
     launch_check("rmsnorm_quant row kernel launch");

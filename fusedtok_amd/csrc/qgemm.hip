@@ -12,6 +12,10 @@
 //   qgemv_dot4     M == 1 (any M <= 8 when forced; decode GEMV, no MFMA):
 //                  v_dot4_i32_i8 over 16-byte K pieces, several W rows in
 //                  flight per wave, wave sums.
+//   qgemm_dec_lds  2 <= M <= 16, K % 512 == 0, >= 320 column tiles: one
+//                  wave per 16 columns over all of K; W and A rows DMA'd
+//                  global->LDS in whole lines through a 2-stage ring, read
+//                  back in the MFMA layout through an XOR swizzle.
 //   qgemm_dec      2 <= M <= 16: 16 columns per workgroup over all of K, K
 //                  split across the workgroup's waves, operands double-
 //                  buffered in registers, partials folded in LDS.
@@ -298,6 +302,115 @@ __global__ __launch_bounds__(64 * KW) void qgemm_dec(
             const i32x4 p = red[w][lane];
             acc[0] += p[0]; acc[1] += p[1]; acc[2] += p[2]; acc[3] += p[3];
         }
+    }
+    // lane (r, g) holds C[4 g + i][r] = (A row 4 g + i, W row n0 + r)
+    const int col = n0 + r;
+    if (col >= n) return;
+    const float sa = epi_sa(e);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (4 * g + i < m) epi_store<OUT>(e, sa, n, 4 * g + i, col, acc[i]);
+}
+
+// ---------------------------------------------------------------------------
+// decode MFMA GEMM through LDS (2 <= M <= 16, K % 512 == 0): one wave owns 16
+// output columns over all of K, as qgemm_dec with KW = 1, but both operands
+// arrive by global -> LDS DMA in whole 128-byte lines: one
+// global_load_lds_dwordx4 covers 512 bytes of each of two rows (lanes 0-31
+// the first, 32-63 the second), where the register path reads 64 bytes of
+// each of 16 rows per instruction. An S-stage ring keeps S - 1 chunks of
+// 16 W rows and 16 A rows x 512 bytes in flight.
+//
+// LDS layout of a stage: operand x (0 = A, 1 = W), row r, 16-byte slot s at
+// x * 8192 + 512 r + 16 s holds K piece s ^ r of the chunk (lane l of a DMA
+// reads piece (l & 31) ^ r, a permutation of each aligned group of 8 pieces,
+// so every 8 lanes still cover one whole line). MFMA step u of lane (r, g)
+// needs piece 4 u + g: slot (4 u + g) ^ r, and the 16 lanes of a ds_read_b128
+// quarter (r = 0..15) hit 16 distinct 16-byte bank groups.
+// ---------------------------------------------------------------------------
+constexpr int kDwChunk = 512;
+constexpr int kDwStage = 2 * 16 * kDwChunk;  // A and W, 16 rows each
+
+template <int NSTAGE>
+__device__ __forceinline__ void dw_wait_vm(int pending_chunks) {
+    // 16 DMA instructions per chunk; waits until at most `pending_chunks`
+    // chunks issued after the one needed are still in flight
+    static_assert(NSTAGE >= 2 && NSTAGE <= 3, "stage count");
+    switch (pending_chunks) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<16>(); break;
+    default: wait_vmcnt<32>(); break;
+    }
+}
+
+template <int NSTAGE, int CPOL, int OUT>
+__global__ __launch_bounds__(64) void qgemm_dec_lds(
+    const i8* __restrict__ a, const i8* __restrict__ b, Epi e, int m, int n, int k) {
+    __shared__ __attribute__((aligned(16))) char lds[NSTAGE * kDwStage];
+    const int lane = threadIdx.x;
+    const int r = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int chunks = k / kDwChunk;
+
+    // DMA instruction i (0..7) of an operand: rows 2 i + (lane >> 5)
+    const int hi = lane >> 5;
+    const int sl = lane & 31;
+    size_t aoff[8], boff[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int row = 2 * i + hi;
+        const int piece = sl ^ row;
+        aoff[i] = (size_t)min(row, m - 1) * k + 16 * piece;
+        boff[i] = (size_t)min(n0 + row, n - 1) * k + 16 * piece;
+    }
+    auto issue = [&](int c, int st) {
+        char* dst = lds + st * kDwStage;
+        const size_t kc = (size_t)c * kDwChunk;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_global_load_lds(b + boff[i] + kc,
+                                             (lds_void_p)(dst + 16 * kDwChunk + 1024 * i), 16,
+                                             0, CPOL);
+            __builtin_amdgcn_global_load_lds(a + aoff[i] + kc, (lds_void_p)(dst + 1024 * i),
+                                             16, 0, 0);
+        }
+    };
+
+    const unsigned lds0 = lds_addr(lds);
+    unsigned fo[kDecSteps];  // byte offset of step u's fragment in an operand
+#pragma unroll
+    for (int u = 0; u < kDecSteps; ++u) fo[u] = 512 * r + 16 * ((4 * u + g) ^ r);
+
+#pragma unroll
+    for (int j = 0; j < NSTAGE - 1; ++j)
+        if (j < chunks) issue(j, j);
+
+    i32x4 acc = {0, 0, 0, 0};
+    int st = 0;
+    for (int c = 0; c < chunks; ++c) {
+        const int nxt = c + NSTAGE - 1;
+        if (nxt < chunks) {
+            issue(nxt, nxt % NSTAGE);
+            dw_wait_vm<NSTAGE>(NSTAGE - 1);
+        } else {
+            dw_wait_vm<NSTAGE>(chunks - 1 - c);
+        }
+        const unsigned sa_ = lds0 + st * kDwStage;
+        i32x4 fa[kDecSteps], fw[kDecSteps];
+#pragma unroll
+        for (int u = 0; u < kDecSteps; ++u) {
+            fa[u] = lds_read16(sa_ + fo[u]);
+            fw[u] = lds_read16(sa_ + 16 * kDwChunk + fo[u]);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fa[4]),
+                       "+v"(fa[5]), "+v"(fa[6]), "+v"(fa[7]), "+v"(fw[0]), "+v"(fw[1]),
+                       "+v"(fw[2]), "+v"(fw[3]), "+v"(fw[4]), "+v"(fw[5]), "+v"(fw[6]),
+                       "+v"(fw[7]));
+#pragma unroll
+        for (int u = 0; u < kDecSteps; ++u)
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u], fw[u], acc, 0, 0, 0);
+        st = st + 1 == NSTAGE ? 0 : st + 1;
     }
     // lane (r, g) holds C[4 g + i][r] = (A row 4 g + i, W row n0 + r)
     const int col = n0 + r;
@@ -2119,6 +2232,20 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         int kw = tiles >= 320 ? 1 : tiles >= 128 ? 2 : 4;
         const int kw_env = env_int("FT_QGEMM_DEC_KW", 0);
         if (kw_env == 1 || kw_env == 2 || kw_env == 4) kw = kw_env;
+        // W and A through an LDS ring in whole lines, W non-temporal (C2 chain,
+        // M = 8 / 16: 21.1 / 23.3 us with register operands, 16.5 / 17.4 us
+        // with 2 stages; 3 stages the same, 4 stages slower: 64 KB per wave
+        // leaves 2 waves per CU; plain W loads 19.1 / 19.4 us)
+        const int lds_stages = env_int("FT_QGEMM_DEC_LDS", 2);
+        if (kw == 1 && k % kDwChunk == 0 && (lds_stages == 2 || lds_stages == 3)) {
+            const bool nt = env_int("FT_QGEMM_DEC_NT", 1) != 0;
+#define FT_DEC_LDS(S, C) qgemm_dec_lds<S, C, OUT><<<grid, 64, 0, s>>>(a, b, e, m, n, k)
+            if (lds_stages == 2) { if (nt) FT_DEC_LDS(2, 2); else FT_DEC_LDS(2, 0); }
+            else { if (nt) FT_DEC_LDS(3, 2); else FT_DEC_LDS(3, 0); }
+#undef FT_DEC_LDS
+            launch_check("qgemm decode lds kernel launch");
+            return;
+        }
         if (kw == 1)
             qgemm_dec<1, OUT><<<grid, 64, 0, s>>>(a, b, e, m, n, k);
         else if (kw == 2)

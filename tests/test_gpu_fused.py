@@ -65,6 +65,27 @@ def test_rmsnorm_quant_matches_oracle_and_chain(dt, rows, cols, with_res):
     assert s == s2
 
 
+@pytest.mark.parametrize("dt", ALL)
+@pytest.mark.parametrize("rows,cols", [(1, 4096), (2, 12), (3, 4096), (4, 4096),
+                                       (4, 1000), (1, 4)])
+def test_rmsnorm_quant_one_launch_matches_two_launch_path(dt, rows, cols, monkeypatch):
+    # up to 4 rows of up to 4096 columns run as one workgroup; FT_RMSQ_SPLIT=1
+    # forces the per-row + fold/quantize kernels. Both must agree bit for bit.
+    rng = np.random.default_rng(rows * 131 + cols)
+    x = rng.standard_normal((rows, cols)).astype(np.float32) * 3
+    x[rows // 2, : cols // 3] *= 40.0
+    x = t(x, dt)
+    w = t(rng.uniform(0.5, 1.5, cols).astype(np.float32))
+    r = t(rng.standard_normal((rows, cols)).astype(np.float32), dt)
+    for res in (None, r):
+        q1, s1 = ft.rmsnorm_quant(x, w, residual=res, eps=1e-5)
+        monkeypatch.setenv("FT_RMSQ_SPLIT", "1")
+        q2, s2 = ft.rmsnorm_quant(x, w, residual=res, eps=1e-5)
+        monkeypatch.delenv("FT_RMSQ_SPLIT")
+        np.testing.assert_array_equal(q1.cpu().numpy(), q2.cpu().numpy())
+        assert s1 == s2
+
+
 def test_rmsnorm_quant_device_scale_zero_rows_and_1d():
     rng = np.random.default_rng(3)
     x = t(rng.standard_normal(512).astype(np.float32), torch.bfloat16)

@@ -2,7 +2,8 @@
 accumulators and the float32 GEMM epilogue equal the CPU oracle exactly;
 bf16 / fp16 GEMM outputs equal the oracle's float32 value rounded to
 nearest-even. Every GEMM kernel is exercised: GEMV (M == 1, or forced up to
-8), decode (2 <= M <= 16, 1 / 2 / 4 waves per tile), skinny (M <= 64, with
+8), decode (2 <= M <= 16, 1 / 2 / 4 waves per tile, and the LDS-ring
+variant), skinny (M <= 64, with
 and without the cross-workgroup K split), tiled, big (M, N >= 256, DMA and
 register-staged), scalar fallback (K % 16 != 0) and the K == 0 zero fill."""
 
@@ -312,6 +313,35 @@ def test_decode_gemm_kernel_bit_exact(kw, m, n, k, monkeypatch):
     np.testing.assert_array_equal(acc.cpu().numpy(), oracle.qgemm_i32(a, b))
     ref = torch.from_numpy(oracle.qgemm_perchannel(a, 0.021, b, sb)).to(torch.bfloat16)
     assert torch.equal(y.cpu(), ref)
+
+
+@pytest.mark.parametrize("stages,nt", [("2", "0"), ("2", "1"), ("3", "1")])
+def test_decode_gemm_lds_ring_bit_exact(stages, nt, monkeypatch):
+    # the LDS-staged decode kernel (K % 512 == 0, one wave per 16 columns):
+    # one chunk, fewer chunks than ring stages, ragged N, odd M; the C2 shape
+    # against the register-operand kernel (FT_QGEMM_DEC_LDS=0)
+    monkeypatch.setenv("FT_QGEMM_KERNEL", "6")
+    monkeypatch.setenv("FT_QGEMM_DEC_KW", "1")
+    monkeypatch.setenv("FT_QGEMM_DEC_NT", nt)
+    for m, n, k in [(2, 40, 512), (7, 1000, 1024), (16, 333, 2560), (9, 17, 4608)]:
+        monkeypatch.setenv("FT_QGEMM_DEC_LDS", stages)
+        rng = np.random.default_rng(m * 10 + n + k)
+        a, b = rand_q(rng, m, k), rand_q(rng, n, k)
+        sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+        acc = ft.qgemm_i32(t(a), t(b))
+        y = ft.qgemm_perchannel(t(a), 0.021, t(b), t(sb), out_dtype=torch.float16)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(acc.cpu().numpy(), oracle.qgemm_i32(a, b))
+        ref = torch.from_numpy(oracle.qgemm_perchannel(a, 0.021, b, sb)).to(torch.float16)
+        assert torch.equal(y.cpu(), ref)
+    for m, n, k in [(16, 11008, 4096), (13, 5000, 14336)]:
+        rng = np.random.default_rng(m + n + k)
+        at, bt = t(rand_q(rng, m, k)), t(rand_q(rng, n, k))
+        monkeypatch.setenv("FT_QGEMM_DEC_LDS", stages)
+        acc = ft.qgemm_i32(at, bt)
+        monkeypatch.setenv("FT_QGEMM_DEC_LDS", "0")
+        acc0 = ft.qgemm_i32(at, bt)
+        assert torch.equal(acc, acc0)
 
 
 @pytest.mark.parametrize("ksplit", ["1", "2", "4", "7"])
