@@ -19,6 +19,9 @@
 //   qgemm_dec      2 <= M <= 16: 16 columns per workgroup over all of K, K
 //                  split across the workgroup's waves, operands double-
 //                  buffered in registers, partials folded in LDS.
+//   qgemm_skinny_lds 16 < M <= 64, K % 256 == 0: the skinny tiling below with
+//                  both operands DMA'd global->LDS in whole lines (256-byte
+//                  K chunks, 2-stage ring, XOR-swizzled fragment reads).
 //   qgemm_skinny   16 < M <= 64: W streamed once into the B operand of
 //                  v_mfma_i32_16x16x64_i8, 64 columns per workgroup (A shared
 //                  through L1), K split across workgroups when N alone cannot
@@ -490,6 +493,149 @@ __global__ __launch_bounds__(256) void qgemm_skinny(
     }
     if (!live) return;
     // C layout: lane (r, g) holds C[4g + i][r] = (A row 16t + 4g + i, W row n0 + r)
+    const int col = n0 + r;
+    if (col >= n) return;
+    if (ksplit == 1) {
+        const float sa = epi_sa(e);
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = 16 * t + 4 * g + i;
+                if (row < m) epi_store<OUT>(e, sa, n, row, col, acc[t][i]);
+            }
+    } else {
+        int* mine = part + (size_t)ks * m * n;
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = 16 * t + 4 * g + i;
+                if (row < m) mine[(size_t)row * n + col] = acc[t][i];
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// skinny MFMA GEMM through an LDS ring (M <= 16*MT <= 64, K % 256 == 0): the
+// workgroup, waves and K split of qgemm_skinny, but both operands arrive by
+// global -> LDS DMA in whole lines, 256-byte K chunks, NSTAGE chunks in the
+// ring (NSTAGE - 1 in flight while one is multiplied). One DMA instruction
+// covers 256 bytes of each of 4 rows (16 lanes per row); the A rows are
+// copied once per workgroup (wave w: instructions w, w + 4, ..), each wave
+// copies its own 16 W rows (non-temporal: read once).
+//
+// A stage holds A rows [0, 16 MT) then W rows [0, 64) (wave w's at 16 w),
+// 256 bytes each; slot s of row r holds K piece s ^ (r & 15): lane l of a DMA
+// reads piece (l & 15) ^ (r & 15), and the 16 lanes of a ds_read_b128
+// quarter (rows 16 t + 0..15, piece 4 u + g) hit distinct bank groups.
+// ---------------------------------------------------------------------------
+constexpr int kSlChunk = 256;
+constexpr int kSlSteps = kSlChunk / 64;
+
+// one chunk of qgemm_skinny_lds: this wave's 4 W instructions (non-temporal)
+// and its share of the A instructions, into the stage at dst
+template <int MT>
+__device__ __forceinline__ void sl_issue(const i8* a, const i8* b, const size_t* aoff,
+                                         const size_t* boff, char* dst, size_t kc, int wave) {
+    constexpr int kArows = 16 * MT;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_global_load_lds(
+            b + boff[i] + kc, (lds_void_p)(dst + (kArows + 16 * wave + 4 * i) * kSlChunk), 16,
+            0, 2);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+        __builtin_amdgcn_global_load_lds(a + aoff[i] + kc,
+                                         (lds_void_p)(dst + 4 * (wave + 4 * i) * kSlChunk), 16,
+                                         0, 0);
+}
+
+template <int MT, int NSTAGE, int OUT>
+__global__ __launch_bounds__(256) void qgemm_skinny_lds(
+    const i8* __restrict__ a, const i8* __restrict__ b, Epi e, int m, int n,
+    int k, int ksplit, int* __restrict__ part) {
+    constexpr int kArows = 16 * MT;
+    constexpr int kStage = (kArows + 64) * kSlChunk;
+    constexpr int kAIns = kArows / 4 / 4;  // A DMA instructions per wave per chunk
+    static_assert(NSTAGE == 2 || NSTAGE == 3, "stage count");
+    __shared__ __attribute__((aligned(16))) char lds[NSTAGE * kStage];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int n0 = (blockIdx.x * 4 + wave) * 16;
+    const bool live = n0 < n;
+    const int ks = blockIdx.y;
+    const int chunks = k / kSlChunk;
+    const int per = (chunks + ksplit - 1) / ksplit;
+    const int c0 = min(chunks, ks * per), c1 = min(chunks, c0 + per);
+
+    // DMA lane roles: row (l >> 4) of the instruction's 4, piece (l & 15) ^ row
+    const int drow = lane >> 4;
+    size_t aoff[kAIns], boff[4];
+#pragma unroll
+    for (int i = 0; i < kAIns; ++i) {
+        const int row = 4 * (wave + 4 * i) + drow;  // A row staged by this lane
+        aoff[i] = (size_t)min(row, m - 1) * k + 16 * ((lane & 15) ^ (row & 15));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = 4 * i + drow;  // of this wave's 16 W rows
+        boff[i] = (size_t)min(n0 + row, n - 1) * k + 16 * ((lane & 15) ^ row);
+    }
+    constexpr int kIns = 4 + kAIns;  // DMA instructions per wave per chunk
+
+    const unsigned lds0 = lds_addr(lds);
+    unsigned fo[kSlSteps];  // offset of step u's fragment within a 16-row group
+#pragma unroll
+    for (int u = 0; u < kSlSteps; ++u) fo[u] = kSlChunk * r + 16 * ((4 * u + g) ^ r);
+
+    i32x4 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < NSTAGE - 1; ++j)
+        if (c0 + j < c1)
+            sl_issue<MT>(a, b, aoff, boff, lds + j * kStage, (size_t)(c0 + j) * kSlChunk, wave);
+    int st = 0;
+    for (int c = c0; c < c1; ++c) {
+        // this wave's copies of chunk c landed (the later chunks may still fly)
+        if (NSTAGE == 3 && c + 1 < c1)
+            wait_vmcnt<kIns>();
+        else
+            wait_vmcnt<0>();
+        // everyone's copies of chunk c landed; chunk c - 1 is free. A bare
+        // barrier: __syncthreads() would add a release fence that drains the
+        // chunk still in flight
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const int nxt = c + NSTAGE - 1;
+        if (nxt < c1)
+            sl_issue<MT>(a, b, aoff, boff, lds + ((st + NSTAGE - 1) % NSTAGE) * kStage,
+                         (size_t)nxt * kSlChunk, wave);
+        const unsigned base = lds0 + st * kStage;
+        i32x4 fw[kSlSteps], fa[MT][kSlSteps];
+#pragma unroll
+        for (int u = 0; u < kSlSteps; ++u)
+            fw[u] = lds_read16(base + (kArows + 16 * wave) * kSlChunk + fo[u]);
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int u = 0; u < kSlSteps; ++u)
+                fa[t][u] = lds_read16(base + 16 * t * kSlChunk + fo[u]);
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fw[0]), "+v"(fw[1]), "+v"(fw[2]), "+v"(fw[3]));
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+            asm volatile("" : "+v"(fa[t][0]), "+v"(fa[t][1]), "+v"(fa[t][2]), "+v"(fa[t][3]));
+#pragma unroll
+        for (int u = 0; u < kSlSteps; ++u)
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[t][u], fw[u], acc[t], 0, 0, 0);
+        st = st + 1 == NSTAGE ? 0 : st + 1;
+    }
+    if (!live) return;
     const int col = n0 + r;
     if (col >= n) return;
     if (ksplit == 1) {
@@ -2275,7 +2421,24 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
             part = (int*)scratch(Scratch::GemmPartials,
                                  (size_t)ksplit * m * n * sizeof(int), s);
         dim3 grid(col_wgs, ksplit);
-        if (mt <= 1)
+        // operands through a 2-stage LDS ring in whole lines (C4 layer: 462 us
+        // against 477 us with register W operands; 3 stages 470 us: 96 KB of
+        // LDS leaves one workgroup per CU)
+        const int sk_stages = env_int("FT_QGEMM_SK_LDS", 2);
+        if (k % kSlChunk == 0 && (sk_stages == 2 || sk_stages == 3)) {
+#define FT_SK_LDS(MT, S) \
+    qgemm_skinny_lds<MT, S, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part)
+            if (sk_stages == 2) {
+                if (mt <= 1) FT_SK_LDS(1, 2);
+                else if (mt <= 2) FT_SK_LDS(2, 2);
+                else FT_SK_LDS(4, 2);
+            } else {
+                if (mt <= 1) FT_SK_LDS(1, 3);
+                else if (mt <= 2) FT_SK_LDS(2, 3);
+                else FT_SK_LDS(4, 3);
+            }
+#undef FT_SK_LDS
+        } else if (mt <= 1)
             qgemm_skinny<1, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part);
         else if (mt <= 2)
             qgemm_skinny<2, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part);

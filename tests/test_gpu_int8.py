@@ -284,6 +284,31 @@ def test_skinny_kernel_bit_exact(m, n, k, split, monkeypatch):
     assert torch.equal(y.cpu(), ref)
 
 
+@pytest.mark.parametrize("stages", ["0", "2", "3"])
+@pytest.mark.parametrize("m,n,k,split", [
+    (17, 200, 256, 0),      # one chunk, one 16-row tile
+    (33, 300, 1280, 0),     # three tiles (MT = 4 with one row past M), ragged N
+    (64, 1000, 3072, 3),    # forced split in three
+    (20, 70, 2304, 2),      # split into 5 + 4 chunks; ragged N (dead waves)
+    (64, 16448, 512, 0),    # 257 column workgroups, no split
+])
+def test_skinny_lds_ring_bit_exact(stages, m, n, k, split, monkeypatch):
+    # the LDS-ring skinny kernel (K % 256 == 0) against the oracle, for both
+    # ring depths and the register-operand kernel (FT_QGEMM_SK_LDS=0)
+    monkeypatch.setenv("FT_QGEMM_SK_LDS", stages)
+    if split:
+        monkeypatch.setenv("FT_QGEMM_KSPLIT", str(split))
+    rng = np.random.default_rng(m * 3 + n + k + split)
+    a, b = rand_q(rng, m, k), rand_q(rng, n, k)
+    sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    acc = ft.qgemm_i32(t(a), t(b))
+    y = ft.qgemm_perchannel(t(a), 0.021, t(b), t(sb), out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(acc.cpu().numpy(), oracle.qgemm_i32(a, b))
+    ref = torch.from_numpy(oracle.qgemm_perchannel(a, 0.021, b, sb)).to(torch.bfloat16)
+    assert torch.equal(y.cpu(), ref)
+
+
 @pytest.mark.parametrize("kernel", ["1", "2", "3", "4", "5", "6"])
 def test_every_gemm_kernel_bit_exact(kernel, monkeypatch):
     monkeypatch.setenv("FT_QGEMM_KERNEL", kernel)
