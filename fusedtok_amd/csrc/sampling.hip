@@ -816,9 +816,112 @@ __global__ __launch_bounds__(kArgNT) void argmax_rows(const float* __restrict__ 
     }
 }
 
+// argmax with a row split across workgroups when there are fewer rows than
+// CUs: workgroup (slice, row) reduces tokens [slice * slen, +slen) with the
+// comparator of argmax_rows (value, then earliest index; NaN as -inf), and
+// one wave per row folds the slice winners. The comparator is a total order
+// on (value, -index), so any split gives argmax_rows' result; the index-0
+// NaN rule is applied once, in the fold.
+constexpr int kArgSliceNT = 256;
+constexpr int kArgMaxSlices = 64;
+constexpr int kArgMinSlice = 4096;  // tokens
+
+__device__ __forceinline__ void arg_better(float& bv, int& bi, float ov, int oi) {
+    if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+    }
+}
+
+__global__ __launch_bounds__(kArgSliceNT) void argmax_slices(const float* __restrict__ x, int n,
+                                                             int slen, float* __restrict__ pv,
+                                                             int* __restrict__ pi) {
+    __shared__ float sv[kArgSliceNT / 64];
+    __shared__ int si[kArgSliceNT / 64];
+    const SampleRow row{x + (size_t)blockIdx.y * n, n, 1.0f, 1.0f, nullptr, 0};
+    const int lo = blockIdx.x * slen;
+    const int hi = min(n, lo + slen);
+    const int tid = threadIdx.x;
+    float bv = -INFINITY;
+    int bi = n;
+    slice_scan<kArgSliceNT>(row, lo, hi, [&](int i, float v) {
+        if (v != v) v = -INFINITY;
+        arg_better(bv, bi, v, i);
+    });
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        arg_better(bv, bi, ov, oi);
+    }
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = bv;
+        si[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kArgSliceNT / 64; ++w) arg_better(bv, bi, sv[w], si[w]);
+        pv[(size_t)blockIdx.y * gridDim.x + blockIdx.x] = bv;
+        pi[(size_t)blockIdx.y * gridDim.x + blockIdx.x] = bi;
+    }
+}
+
+template <typename OUT>
+__global__ __launch_bounds__(64) void argmax_fold(const float* __restrict__ x, int n, int S,
+                                                  const float* __restrict__ pv,
+                                                  const int* __restrict__ pi,
+                                                  OUT* __restrict__ out) {
+    const int lane = threadIdx.x;
+    const int r = blockIdx.x;
+    float bv = -INFINITY;
+    int bi = n;
+    if (lane < S) {
+        bv = pv[(size_t)r * S + lane];
+        bi = pi[(size_t)r * S + lane];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        arg_better(bv, bi, ov, oi);
+    }
+    if (lane == 0) {
+        const float x0 = x[(size_t)r * n];
+        out[r] = (OUT)((x0 != x0 || bi >= n) ? 0 : bi);
+    }
+}
+
 int env_int(const char* name, int dflt) {
     const char* v = getenv(name);
     return (v && *v) ? atoi(v) : dflt;
+}
+
+template <typename OUT>
+void argmax_launch(const float* x, int rows, int n, OUT* out, hipStream_t s) {
+    // slices of at least kArgMinSlice tokens, enough workgroups for ~4 per CU
+    // (FT_ARG_SLICES forces a count, 1 = one workgroup per row)
+    const int cus = dev_info().cu_count;
+    int S = 1;
+    if (rows < cus)
+        S = std::min({(4 * cus + rows - 1) / rows, std::max(1, n / kArgMinSlice), kArgMaxSlices});
+    const int forced = env_int("FT_ARG_SLICES", 0);
+    if (forced > 0) S = std::min(forced, kArgMaxSlices);
+    int slen = (n + S - 1) / S;
+    slen = (slen + 3) & ~3;  // slices start on 4-token boundaries
+    S = (n + slen - 1) / slen;
+    if (S <= 1) {
+        argmax_rows<OUT><<<(unsigned)rows, kArgNT, 0, s>>>(x, n, out);
+        launch_check("argmax kernel launch");
+        return;
+    }
+    const size_t pairs = (size_t)rows * S;
+    char* buf = (char*)scratch(Scratch::Sampling, pairs * (sizeof(float) + sizeof(int)), s);
+    float* pv = (float*)buf;
+    int* pi = (int*)(buf + pairs * sizeof(float));
+    argmax_slices<<<dim3((unsigned)S, (unsigned)rows), kArgSliceNT, 0, s>>>(x, n, slen, pv, pi);
+    launch_check("argmax slice kernel launch");
+    argmax_fold<OUT><<<(unsigned)rows, 64, 0, s>>>(x, n, S, pv, pi, out);
+    launch_check("argmax fold kernel launch");
 }
 
 void sampling_check(int rows, int n, float p, float t) {
@@ -915,8 +1018,7 @@ int ft_argmax_launch(const float* x, int n, int* out, uintptr_t stream) {
     return ft::guarded([&] {
         if (n <= 0) ft::inval("argmax of empty vector");
         if (!x || !out) ft::inval("argmax: null operand");
-        ft::argmax_rows<int><<<1, ft::kArgNT, 0, ft::as_stream(stream)>>>(x, n, out);
-        ft::launch_check("argmax kernel launch");
+        ft::argmax_launch<int>(x, 1, n, out, ft::as_stream(stream));
     });
 }
 
@@ -927,8 +1029,7 @@ int ft_argmax_batched_launch(const float* x, int rows, int n, long long* out,
         if (n <= 0) ft::inval("argmax of empty vector");
         if (rows == 0) return;
         if (!x || !out) ft::inval("argmax: null operand");
-        ft::argmax_rows<long long><<<(unsigned)rows, ft::kArgNT, 0, ft::as_stream(stream)>>>(x, n, out);
-        ft::launch_check("argmax kernel launch");
+        ft::argmax_launch<long long>(x, rows, n, out, ft::as_stream(stream));
     });
 }
 

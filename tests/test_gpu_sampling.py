@@ -53,6 +53,34 @@ def test_argmax_and_batched_bit_exact():
         ft.argmax_batched(torch.zeros((2, 3), dtype=torch.float64, device=DEV))
 
 
+@pytest.mark.parametrize("slices", ["0", "1", "2", "3", "64"])
+def test_argmax_sliced_rows_bit_exact(slices, monkeypatch):
+    # rows split across workgroups (fewer rows than CUs), folded by one wave
+    # per row: ties across slice boundaries, NaN at index 0, all-NaN and
+    # all -inf rows, the maximum in the last token, misaligned rows (odd n)
+    monkeypatch.setenv("FT_ARG_SLICES", slices)
+    rng = np.random.default_rng(int(slices) + 7)
+    n = 128256
+    x = rng.integers(-1000, 1000, (8, n)).astype(np.float32)
+    x[0, 20000] = x[0, 100000] = x[0, 127000] = 5000.0
+    x[1, 0] = np.nan
+    x[1, 9] = 7000.0
+    x[2, :] = np.nan
+    x[3, :] = -np.inf
+    x[4, -1] = 9000.0
+    x[5, ::3] = np.nan
+    x[6, 64000:64004] = 3000.0
+    x[7, :] = 0.0
+    x[7, 1::2] = -0.0
+    np.testing.assert_array_equal(ft.argmax_batched(t(x)).cpu().numpy(),
+                                  oracle.argmax_batched(x))
+    for rows, m in [(5, 40001), (1, 1_000_003), (3, 4097)]:
+        y = rng.integers(-30, 30, (rows, m)).astype(np.float32)
+        np.testing.assert_array_equal(ft.argmax_batched(t(y)).cpu().numpy(),
+                                      oracle.argmax_batched(y))
+        assert ft.argmax(t(y[-1])) == int(oracle.argmax_batched(y[-1:])[0])
+
+
 @pytest.mark.parametrize("n,scale", [(100, 3.0), (2000, 2.0), (32000, 1.5), (128256, 2.0)])
 @pytest.mark.parametrize("p,temp", [(0.9, 1.0), (0.5, 0.7), (1.0, 1.3), (0.95, 0.1)])
 def test_sample_topp_matches_oracle(n, scale, p, temp):
