@@ -29,6 +29,9 @@
 //           A fragments are single 16-byte reads.
 //   bf16:   P is split into hi + lo bf16 parts (two MFMAs), so the weights
 //           carry ~16 mantissa bits; fp16 P carries 11.
+//   sums    where P is one fp16 operand, the row sums are ones . P^T on the
+//           same MFMA (the weights the PV product uses, 4 MFMAs per tile
+//           instead of 32 adds per lane); the bf16 split loop adds in lanes.
 //
 // Causal work is uneven across query tiles: the grid runs the last (most
 // keys) tiles of every head first.
@@ -205,7 +208,11 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) o[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run[2] = {-INFINITY, -INFINITY};
-    float l_run[2] = {0.f, 0.f};
+    float l_run[2] = {0.f, 0.f};  // lane partial row sums (bf16 split loop)
+    // row sums on the matrix core where P is one fp16 operand: ones . P^T
+    // puts the sum of the tile's (fp16) weights of row q in every C slot of
+    // lane (q, g); rescaled with the output
+    f32x4 osum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
     const int wrow0 = q0 + 32 * wave;  // first query row of this wave
     const float lazy_raw = kLazy / scale_log2;
 
@@ -237,6 +244,7 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
     // neither path's temporaries are live in the other.
     auto run = [&](auto f16_tag, int kt0) -> int {
         constexpr bool F16 = decltype(f16_tag)::value;
+        constexpr bool kMmaSum = F16 || !M::kSplit;
         for (int kt = kt0; kt < nkt; ++kt) {
             if (kt + 1 < nkt) load_tile(kt + 1);
             const int kv0 = kt * kPKV;
@@ -297,19 +305,26 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
                     const float alpha = __builtin_amdgcn_exp2f((m_run[qb] - m_use) * scale_log2);
                     const float nmc = -m_use * scale_log2;
                     float p[4][4];
-                    float psum = 0.f;
 #pragma unroll
                     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) {
+                        for (int i = 0; i < 4; ++i)
                             p[kb][i] = __builtin_amdgcn_exp2f(fmaf(sc[kb][qb][i], scale_log2, nmc));
-                            psum += p[kb][i];
-                        }
-                    l_run[qb] = l_run[qb] * alpha + psum;
+                    if constexpr (!kMmaSum) {
+                        float psum = 0.f;
+#pragma unroll
+                        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) psum += p[kb][i];
+                        l_run[qb] = l_run[qb] * alpha + psum;
+                    }
                     m_run[qb] = m_new;
                     if (__builtin_amdgcn_ballot_w64(upd)) {
 #pragma unroll
                         for (int db = 0; db < C::kDB; ++db) o[db][qb] *= alpha;
+                        osum[qb] *= alpha;
+                        // l_run is nonzero only in the bf16 split loop, which
+                        // rescales it above
                     }
                     // P^T fragments: dword w of step ks2 holds slots 8g + 2w, +1
 #pragma unroll
@@ -334,7 +349,18 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
                             }
                         }
                 }
-                // O^T += V^T . P^T
+                // O^T += V^T . P^T (and the row sums: ones . P^T)
+                if constexpr (kMmaSum) {
+                    const h8 ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
+                                     (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
+                                     (_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+                    for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+                        for (int qb = 0; qb < 2; ++qb)
+                            osum[qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                ones, __builtin_bit_cast(h8, ph[qb][ks2]), osum[qb], 0, 0, 0);
+                }
                 if constexpr (F16) {
 #pragma unroll
                     for (int db = 0; db < C::kDB; ++db)
@@ -388,6 +414,7 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
         float l = l_run[qb];
         l += __shfl_xor(l, 16, 64);
         l += __shfl_xor(l, 32, 64);
+        l += osum[qb][0];
         const float inv = 1.0f / l;
         const int qrow = wrow0 + 16 * qb + r16;
         if (qrow >= seq) continue;
