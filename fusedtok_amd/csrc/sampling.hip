@@ -950,6 +950,11 @@ void topp_launch(const float* x, int rows, int n, float p, float t, float pen,
     int S = 1;
     if (rows < cus && env_int("FT_SMP_SINGLE", 0) == 0)
         S = std::min({(2 * cus + rows - 1) / rows, std::max(1, n / kMinSlice), kMaxSlices});
+    // FT_SMP_SLICES forces the slice count (2 .. kMaxSlices, at most one
+    // slice per 32 tokens)
+    const int forced_s = env_int("FT_SMP_SLICES", 0);
+    if (forced_s >= 2 && env_int("FT_SMP_SINGLE", 0) == 0)
+        S = std::min({forced_s, kMaxSlices, std::max(1, n / 32)});
     if (S <= 1) {
         sample_topp_rows<<<(unsigned)rows, kSmpNT, 0, s>>>(
             x, n, p, inv_t, pen, penal ? ids : nullptr, penal ? offs : nullptr, m, seeds, seed0,

@@ -227,3 +227,26 @@ def test_sliced_pipeline_matches_single_workgroup(rows, n, monkeypatch):
                          ft.sample_topp_batched(lt, p, temperature=temp, seeds=seeds).tolist(),
                          ft.sample_topp(lt[0], p, temperature=temp, seed=seeds[0]))
         assert got["0"] == got["1"], (p, temp)
+
+
+@pytest.mark.parametrize("slices", ["2", "3", "12", "64"])
+def test_sliced_pipeline_any_slice_count(slices, monkeypatch):
+    # forced slice counts (FT_SMP_SLICES): odd splits, slices of a few
+    # hundred tokens, the maximum count; same tokens as one workgroup per row
+    rng = np.random.default_rng(int(slices) + 90)
+    rows, n = 6, 40001
+    logits = (rng.standard_normal((rows, n)) * 2).astype(np.float32)
+    logits[1] = 0.0
+    logits[2, rng.integers(0, n, 30)] = np.nan
+    logits[3, :] = -20.0
+    logits[3, n - 1] = 4.0
+    seeds = list(range(3, 3 + rows))
+    hist = [rng.integers(0, n, size=int(rng.integers(0, 40))).tolist() for _ in range(rows)]
+    lt = t(logits)
+    for p, temp in [(0.9, 0.8), (0.3, 1.2)]:
+        monkeypatch.setenv("FT_SMP_SLICES", slices)
+        a = ft.decode_step_batched(lt, hist, 1.2, p=p, temperature=temp, seeds=seeds).tolist()
+        monkeypatch.setenv("FT_SMP_SINGLE", "1")
+        b = ft.decode_step_batched(lt, hist, 1.2, p=p, temperature=temp, seeds=seeds).tolist()
+        monkeypatch.delenv("FT_SMP_SINGLE")
+        assert a == b, (p, temp)
