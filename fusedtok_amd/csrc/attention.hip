@@ -839,11 +839,6 @@ bool mfma_eligible(const T* q, const T* k, const T* v, int group, int dim) {
            ((uintptr_t)v % 16 == 0);
 }
 
-int env_int(const char* name, int dflt) {
-    const char* s = getenv(name);
-    return (s && *s) ? atoi(s) : dflt;
-}
-
 // attn_decode_stream in the row mode of the layout (paged with a power-of-2
 // page, paged with any page, contiguous).
 template <typename T, bool WIDE>

@@ -84,6 +84,10 @@ const DevInfo& dev_info();
 // True if `s` is being captured into a HIP graph.
 bool stream_capturing(hipStream_t s);
 
+// Integer value of environment variable `name` (A/B and test switches), or
+// `dflt` when it is unset or empty.
+int env_int(const char* name, int dflt);
+
 // Per-device scratch buffers, one per purpose, grown on demand and kept for
 // the process lifetime. Growth is refused during a stream capture (the
 // caller must warm the shape up once outside the capture). Returned memory

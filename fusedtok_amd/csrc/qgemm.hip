@@ -2313,11 +2313,6 @@ void qgemm_big_w16(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
 // ---------------------------------------------------------------------------
 // dispatch
 // ---------------------------------------------------------------------------
-int env_int(const char* name, int dflt) {
-    const char* s = getenv(name);
-    return (s && *s) ? atoi(s) : dflt;
-}
-
 // reference qgemm.cu:599-604 bounds m*n*k <= 2^38; this build instead bounds
 // K so the int32 accumulator provably cannot wrap (|a*b| <= 128*128), which
 // admits the large prefill shapes (4096 x 28672 x 8192).

@@ -2,6 +2,7 @@
 // properties, per-device scratch pool, device probe.
 #include "ft_common.hpp"
 
+#include <cstdlib>
 #include <mutex>
 #include <vector>
 
@@ -61,6 +62,11 @@ const DevInfo& dev_info() {
         st.info_ready = true;
     }
     return st.info;
+}
+
+int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return (v && *v) ? atoi(v) : dflt;
 }
 
 bool stream_capturing(hipStream_t s) {

@@ -891,11 +891,6 @@ __global__ __launch_bounds__(64) void argmax_fold(const float* __restrict__ x, i
     }
 }
 
-int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return (v && *v) ? atoi(v) : dflt;
-}
-
 template <typename OUT>
 void argmax_launch(const float* x, int rows, int n, OUT* out, hipStream_t s) {
     // slices of at least kArgMinSlice tokens, enough workgroups for ~4 per CU
