@@ -92,25 +92,33 @@ __device__ __forceinline__ float epi_sa(const Epi& e) {
     return e.sa_dev ? *e.sa_dev : e.sa;
 }
 
+// Store of one output given the composed scale s = f32(sa * sb_j): two f32
+// roundings (scale, then product), then one to the output type - never
+// fused: the backend would otherwise fold the product and an f16 narrowing
+// into one single-rounding mixed-precision FMA (v_fma_mixlo_f16), which can
+// land on the other side of an f16 tie. The empty asm makes the rounded f32
+// product opaque to it.
 template <int OUT>
-__device__ __forceinline__ void epi_store(const Epi& e, float sa, int n,
-                                          int row, int col, int acc) {
+__device__ __forceinline__ void epi_store_scaled(const Epi& e, int n, int row, int col,
+                                                 int acc, float s) {
     const size_t idx = (size_t)row * n + col;
     if constexpr (OUT == kOutI32) {
         static_cast<int*>(e.y)[idx] = acc;
     } else {
-        // Two f32 roundings (scale, then product), then one to the output
-        // type - never fused: the backend would otherwise fold the product
-        // and an f16 narrowing into one single-rounding mixed-precision FMA
-        // (v_fma_mixlo_f16), which can land on the other side of an f16
-        // tie. The empty asm makes the rounded f32 product opaque to it.
-        const float s = e.sb_vec ? sa * e.sb_vec[col] : sa * e.sb;
         float val = (float)acc * s;
         asm("" : "+v"(val));
         if constexpr (OUT == kOutF32) static_cast<float*>(e.y)[idx] = val;
         if constexpr (OUT == kOutBF16) static_cast<bf16*>(e.y)[idx] = (bf16)val;
         if constexpr (OUT == kOutF16) static_cast<f16*>(e.y)[idx] = (f16)val;
     }
+}
+
+template <int OUT>
+__device__ __forceinline__ void epi_store(const Epi& e, float sa, int n,
+                                          int row, int col, int acc) {
+    float s = 0.0f;
+    if constexpr (OUT != kOutI32) s = e.sb_vec ? sa * e.sb_vec[col] : sa * e.sb;
+    epi_store_scaled<OUT>(e, n, row, col, acc, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -659,17 +667,34 @@ __global__ __launch_bounds__(256) void qgemm_skinny_lds(
     }
 }
 
-// K-split fold: out[row][col] = sum over ks (in order) of part[ks][row][col]
+// K-split fold: out[row][col] = sum over ks of part[ks][row][col] (int32
+// sums: exact in any order). Up to 8 partials are loaded at once, and the
+// column scale with them, so a fold costs one memory round trip per 8
+// partials instead of one per partial.
+constexpr int kKsumBatch = 8;
+
 template <int OUT>
 __global__ __launch_bounds__(256) void qgemm_ksum(const int* __restrict__ part,
                                                   Epi e, int m, int n, int ksplit) {
     const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
     const long long mn = (long long)m * n;
     if (idx >= mn) return;
-    int s = 0;
-    for (int j = 0; j < ksplit; ++j) s += part[(size_t)j * mn + idx];
     const int row = (int)(idx / n), col = (int)(idx - (long long)row * n);
-    epi_store<OUT>(e, epi_sa(e), n, row, col, s);
+    float sa = 0.0f, sb = 0.0f;
+    if constexpr (OUT != kOutI32) {
+        sa = epi_sa(e);
+        sb = e.sb_vec ? e.sb_vec[col] : e.sb;
+    }
+    int s = 0;
+    for (int j0 = 0; j0 < ksplit; j0 += kKsumBatch) {
+        int v[kKsumBatch];
+#pragma unroll
+        for (int u = 0; u < kKsumBatch; ++u)
+            v[u] = j0 + u < ksplit ? part[(size_t)(j0 + u) * mn + idx] : 0;
+#pragma unroll
+        for (int u = 0; u < kKsumBatch; ++u) s += v[u];
+    }
+    epi_store_scaled<OUT>(e, n, row, col, s, sa * sb);
 }
 
 // ---------------------------------------------------------------------------
