@@ -394,11 +394,13 @@ def test_half_outputs_are_rounded_f32(odt, m, n):
     assert torch.equal(y.cpu(), ref)
 
 
-def test_device_scale_operand_matches_host_scale():
-    rng = np.random.default_rng(10)
-    x = rng.standard_normal((8, 1024)).astype(np.float32)
-    b = rand_q(rng, 256, 1024)
-    sb = rng.uniform(1e-3, 1e-2, 256).astype(np.float32)
+@pytest.mark.parametrize("m,n", [(8, 256), (8, 5120), (40, 700)])
+def test_device_scale_operand_matches_host_scale(m, n):
+    # decode kernel (8 x 256), its LDS-ring variant (320 column tiles), skinny
+    rng = np.random.default_rng(10 + n)
+    x = rng.standard_normal((m, 1024)).astype(np.float32)
+    b = rand_q(rng, n, 1024)
+    sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
     qx, sd = ft.quantize_int8(t(x), device_scale=True)
     y_dev = ft.qgemm_perchannel(qx, sd, t(b), t(sb))
     y_host = ft.qgemm_perchannel(qx, float(sd), t(b), t(sb))
