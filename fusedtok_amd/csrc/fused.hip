@@ -74,11 +74,14 @@ __global__ __launch_bounds__(kFNT) void rmsq_rows(
     float m = 0.0f;
     float inv;
     if (chunks <= kFNT * kRowChunks) {
-        float4 v[kRowChunks];
+        // the row and the weights in one round trip
+        float4 v[kRowChunks], wc[kRowChunks];
 #pragma unroll
         for (int j = 0; j < kRowChunks; ++j) {
             const int c = threadIdx.x + j * kFNT;
             v[j] = c < chunks ? rms_in4(x, r, base + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            wc[j] = c < chunks ? *reinterpret_cast<const float4*>(w + 4 * c)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
         }
         float acc = 0.0f;
 #pragma unroll
@@ -94,13 +97,11 @@ __global__ __launch_bounds__(kFNT) void rmsq_rows(
         inv = 1.0f / sqrtf(total / (float)cols + eps);
 #pragma unroll
         for (int j = 0; j < kRowChunks; ++j) {
-            const int c = threadIdx.x + j * kFNT;
-            if (c < chunks) {
-                const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c);
-                m = fmaxf(m, fabsf(v[j].x * inv * wv.x));
-                m = fmaxf(m, fabsf(v[j].y * inv * wv.y));
-                m = fmaxf(m, fabsf(v[j].z * inv * wv.z));
-                m = fmaxf(m, fabsf(v[j].w * inv * wv.w));
+            if ((int)threadIdx.x + j * kFNT < chunks) {
+                m = fmaxf(m, fabsf(v[j].x * inv * wc[j].x));
+                m = fmaxf(m, fabsf(v[j].y * inv * wc[j].y));
+                m = fmaxf(m, fabsf(v[j].z * inv * wc[j].z));
+                m = fmaxf(m, fabsf(v[j].w * inv * wc[j].w));
             }
         }
     } else {
