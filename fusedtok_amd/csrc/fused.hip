@@ -323,41 +323,91 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return g / (1.0f + expf(-g)) * u;
 }
 
-template <typename T>
+// VEC: cols and the row stride are multiples of 4 and g / u / q aligned to
+// 4 elements: each thread takes 4 consecutive elements of a row per load
+// (one 8-byte load per operand for half types), so a thread's few elements
+// cost one round trip instead of one per element.
+template <typename T, bool VEC>
+__device__ __forceinline__ void swq_at(const T* g, const T* u, long long c, int cols,
+                                       long long ld, float (&y)[4]) {
+    if constexpr (VEC) {
+        const int cols4 = cols >> 2;
+        const long long row = c / cols4;
+        const size_t off = (size_t)(row * ld + 4 * (c - row * cols4));
+        const float4 gv = St<T>::ld4(g + off), uv = St<T>::ld4(u + off);
+        y[0] = silu_mul(gv.x, uv.x);
+        y[1] = silu_mul(gv.y, uv.y);
+        y[2] = silu_mul(gv.z, uv.z);
+        y[3] = silu_mul(gv.w, uv.w);
+    } else {
+        const long long row = c / cols;
+        const size_t off = (size_t)(row * ld + (c - row * cols));
+        y[0] = silu_mul(St<T>::ld(g + off), St<T>::ld(u + off));
+    }
+}
+
+template <typename T, bool VEC>
 __global__ __launch_bounds__(kFNT) void swq_absmax(
     const T* __restrict__ g, const T* __restrict__ u, float* __restrict__ part,
     int rows, int cols, long long ld) {
     __shared__ float red[kFNT / 64];
-    const long long n = (long long)rows * cols;
+    constexpr int W = VEC ? 4 : 1;
+    const long long n = (long long)rows * cols / W;
     float m = 0.0f;
-    for (long long e = (long long)blockIdx.x * kFNT + threadIdx.x; e < n;
-         e += (long long)gridDim.x * kFNT) {
-        const long long row = e / cols;
-        const size_t off = (size_t)(row * ld + (e - row * cols));
-        m = fmaxf(m, fabsf(silu_mul(St<T>::ld(g + off), St<T>::ld(u + off))));
+    for (long long c = (long long)blockIdx.x * kFNT + threadIdx.x; c < n;
+         c += (long long)gridDim.x * kFNT) {
+        float y[4];
+        swq_at<T, VEC>(g, u, c, cols, ld, y);
+#pragma unroll
+        for (int k = 0; k < W; ++k) m = fmaxf(m, fabsf(y[k]));
     }
     m = block_max<kFNT>(m, red);
     if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
 
-template <typename T>
+// Fold of the partial maxima (4 loads per thread in flight), then the codes;
+// each thread's first elements are loaded before the fold.
+template <typename T, bool VEC>
 __global__ __launch_bounds__(kFNT) void swq_quant(
     const T* __restrict__ g, const T* __restrict__ u, const float* __restrict__ part,
     int nparts, signed char* __restrict__ q, float* __restrict__ scale_out, int rows,
     int cols, long long ld) {
     __shared__ float red[kFNT / 64];
+    constexpr int W = VEC ? 4 : 1;
+    const long long n = (long long)rows * cols / W;
+    const long long c0 = (long long)blockIdx.x * kFNT + threadIdx.x;
+    float y0[4] = {0.f, 0.f, 0.f, 0.f};
+    if (c0 < n) swq_at<T, VEC>(g, u, c0, cols, ld, y0);
     float m = 0.0f;
-    for (int i = threadIdx.x; i < nparts; i += kFNT) m = fmaxf(m, part[i]);
+    for (int i0 = threadIdx.x; i0 < nparts; i0 += 4 * kFNT) {
+        float pv[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) pv[k] = i0 + k * kFNT < nparts ? part[i0 + k * kFNT] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) m = fmaxf(m, pv[k]);
+    }
     m = block_max<kFNT>(m, red);
     const float scale = make_scale(m);
     const float inv_s = 1.0f / scale;
     if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
-    const long long n = (long long)rows * cols;
-    for (long long e = (long long)blockIdx.x * kFNT + threadIdx.x; e < n;
-         e += (long long)gridDim.x * kFNT) {
-        const long long row = e / cols;
-        const size_t off = (size_t)(row * ld + (e - row * cols));
-        q[e] = quant1(silu_mul(St<T>::ld(g + off), St<T>::ld(u + off)), inv_s);
+    auto put = [&](long long c, const float (&y)[4]) {
+        if constexpr (VEC) {
+            char4 o;
+            o.x = quant1(y[0], inv_s);
+            o.y = quant1(y[1], inv_s);
+            o.z = quant1(y[2], inv_s);
+            o.w = quant1(y[3], inv_s);
+            *reinterpret_cast<char4*>(q + 4 * c) = o;
+        } else {
+            q[c] = quant1(y[0], inv_s);
+        }
+    };
+    if (c0 < n) put(c0, y0);
+    for (long long c = c0 + (long long)gridDim.x * kFNT; c < n;
+         c += (long long)gridDim.x * kFNT) {
+        float y[4];
+        swq_at<T, VEC>(g, u, c, cols, ld, y);
+        put(c, y);
     }
 }
 
@@ -370,13 +420,24 @@ void swiglu_quant_run(const T* g, const T* u, signed char* q, float* scale_out,
     if (ld < cols) inval("swiglu_quant: row stride must be >= cols");
     if ((long long)rows * cols == 0) return;
     if (!g || !u || !q || !scale_out) inval("swiglu_quant: null operand");
-    const long long n = (long long)rows * cols;
+    const size_t a4 = 4 * sizeof(T);
+    const bool vec = cols % 4 == 0 && ld % 4 == 0 && (uintptr_t)g % a4 == 0 &&
+                     (uintptr_t)u % a4 == 0 && (uintptr_t)q % 4 == 0;
+    const long long n = (long long)rows * cols / (vec ? 4 : 1);
     float* part = (float*)scratch(Scratch::QuantMax, kSwqParts * sizeof(float), s);
     const unsigned g1 = grid_1d(n, kFNT, kSwqParts);
-    swq_absmax<T><<<g1, kFNT, 0, s>>>(g, u, part, rows, cols, ld);
-    launch_check("swiglu_quant absmax kernel launch");
     const unsigned g2 = grid_1d(n, kFNT, dev_info().cu_count * 4);
-    swq_quant<T><<<g2, kFNT, 0, s>>>(g, u, part, (int)g1, q, scale_out, rows, cols, ld);
+    if (vec) {
+        swq_absmax<T, true><<<g1, kFNT, 0, s>>>(g, u, part, rows, cols, ld);
+        launch_check("swiglu_quant absmax kernel launch");
+        swq_quant<T, true><<<g2, kFNT, 0, s>>>(g, u, part, (int)g1, q, scale_out, rows, cols,
+                                               ld);
+    } else {
+        swq_absmax<T, false><<<g1, kFNT, 0, s>>>(g, u, part, rows, cols, ld);
+        launch_check("swiglu_quant absmax kernel launch");
+        swq_quant<T, false><<<g2, kFNT, 0, s>>>(g, u, part, (int)g1, q, scale_out, rows,
+                                                cols, ld);
+    }
     launch_check("swiglu_quant quantize kernel launch");
 }
 

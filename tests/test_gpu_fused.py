@@ -122,7 +122,7 @@ def test_rmsnorm_quant_repeatable_over_growing_shapes():
 
 
 @pytest.mark.parametrize("dt", ALL)
-@pytest.mark.parametrize("rows,cols", [(1, 11008), (8, 14336), (64, 300), (3, 1)])
+@pytest.mark.parametrize("rows,cols", [(1, 11008), (8, 14336), (64, 300), (3, 1), (5, 301)])
 def test_swiglu_quant_halves_match_chain_and_oracle(dt, rows, cols):
     rng = np.random.default_rng(rows * 31 + cols)
     h = t((rng.standard_normal((rows, 2 * cols)) * 3).astype(np.float32), dt)
