@@ -81,6 +81,7 @@ __all__ = [
     "kv_append",
     "kv_append_paged",
     "rmsnorm_quant",
+    "rmsnorm_qgemm",
     "swiglu_quant",
     "rope_kv_append_paged",
     "argmax",
@@ -967,6 +968,68 @@ def rmsnorm_quant(x, weight, *, residual=None, eps=1e-6, device_scale=False):
                                    scale.data_ptr(), rows, cols, float(eps),
                                    _stream())
     return (q, scale) if device_scale else (q, float(scale))
+
+
+def rmsnorm_qgemm(x, weight, b_q, b_scales, *, residual=None, eps=1e-6, out_dtype=None):
+    """BASELINE config 2's chain in one call: ``q, s = rmsnorm_quant(x,
+    weight, residual=residual, eps=eps)`` then ``qgemm_perchannel(q, s, b_q,
+    b_scales, out_dtype=out_dtype)``, bit for bit. Returns ``(y, q, scale)``
+    with the scale a 1-element GPU float32 tensor (no synchronisation). One
+    row with K <= 4096 runs as one launch (every workgroup of the GEMV
+    normalises and quantises the row itself); other shapes run the two
+    ops. ``b_scales`` per-channel [N] (a float for per-tensor)."""
+    _gpu_only(x, "x")
+    _check_dtype(x, "x", _FLOAT_DTYPES)
+    _require_gpu(weight, "weight")
+    if weight.dtype is not torch.float32:
+        weight = weight.to(torch.float32)
+    if not weight.is_contiguous():
+        weight = weight.contiguous()
+    if not x.is_contiguous():
+        x = x.contiguous()
+    rows, k = _rows_cols(x.shape)
+    if weight.ndim != 1 or weight.numel() != k:
+        raise ValueError("weight must be 1-D with K entries")
+    if k % 4 != 0:
+        raise ValueError("rmsnorm_qgemm: K must be a multiple of 4")
+    _require_gpu(b_q, "b_q")
+    if b_q.dtype is not torch.int8 or b_q.ndim != 2 or b_q.shape[1] != k:
+        raise ValueError("b_q must be int8 [N, K]")
+    if not b_q.is_contiguous():
+        b_q = b_q.contiguous()
+    n = b_q.shape[0]
+    sb_vec, sb = None, 0.0
+    if _is_torch(b_scales) or isinstance(b_scales, (list, tuple, np.ndarray)):
+        if not _is_torch(b_scales):
+            b_scales = torch.as_tensor(np.asarray(b_scales, dtype=np.float32), device=x.device)
+        if b_scales.ndim != 1 or b_scales.numel() != n:
+            raise ValueError("b_scales must be 1-D with N entries")
+        b_scales = b_scales.to(device=x.device, dtype=torch.float32).contiguous()
+        sb_vec = b_scales.data_ptr()
+    else:
+        sb = float(b_scales)
+    r_ptr = None
+    if residual is not None:
+        _require_gpu(residual, "residual")
+        if residual.dtype is not x.dtype or residual.shape != x.shape:
+            raise ValueError("residual must match x in dtype and shape")
+        if not residual.is_contiguous():
+            residual = residual.contiguous()   # kept alive until the launch
+        r_ptr = residual.data_ptr()
+    odt = torch.float32 if out_dtype is None else out_dtype
+    if odt not in _OUT_CODES:
+        raise TypeError("out_dtype must be float32, bfloat16 or float16")
+    y = torch.empty((rows, n), dtype=odt, device=x.device)
+    q = torch.empty((rows, k), dtype=torch.int8, device=x.device)
+    scale = torch.empty(1, dtype=torch.float32, device=x.device)
+    if rows == 0:
+        scale.fill_(1.0)
+        return y, q, scale
+    _fusedtok.rmsnorm_qgemm_launch(x.data_ptr(), _DT_CODE[x.dtype], weight.data_ptr(), r_ptr,
+                                   float(eps), b_q.data_ptr(), sb_vec, sb, y.data_ptr(),
+                                   _OUT_CODES[odt], q.data_ptr(), scale.data_ptr(), rows, n,
+                                   k, _stream())
+    return y, q, scale
 
 
 def swiglu_quant(gate, up, *, device_scale=False):

@@ -388,6 +388,21 @@ PYBIND11_MODULE(_fusedtok, m) {
           py::arg("x"), py::arg("dtype"), py::arg("weight"), py::arg("residual"),
           py::arg("q"), py::arg("scale"), py::arg("rows"), py::arg("cols"),
           py::arg("eps"), py::arg("stream") = 0);
+    m.def("rmsnorm_qgemm_launch",
+          [](uintptr_t x, int dtype, uintptr_t w, py::object r, float eps, uintptr_t bq,
+             py::object sb_vec, float sb, uintptr_t y, int y_dtype, uintptr_t q,
+             uintptr_t scale, int rows, int n, int k, uintptr_t stream) {
+              check(ft_rmsnorm_qgemm_launch(P<const void>(x), dtype, P<const float>(w),
+                                            P<const void>(opt_ptr(r)), eps,
+                                            P<const signed char>(bq),
+                                            P<const float>(opt_ptr(sb_vec)), sb, P<void>(y),
+                                            y_dtype, P<signed char>(q), P<float>(scale),
+                                            rows, n, k, stream));
+          },
+          py::arg("x"), py::arg("dtype"), py::arg("weight"), py::arg("residual"),
+          py::arg("eps"), py::arg("b"), py::arg("sb_vec"), py::arg("sb"), py::arg("y"),
+          py::arg("y_dtype"), py::arg("q"), py::arg("scale"), py::arg("rows"),
+          py::arg("n"), py::arg("k"), py::arg("stream") = 0);
     m.def("swiglu_quant_launch",
           [](uintptr_t g, uintptr_t u, int dtype, uintptr_t q, uintptr_t scale,
              int rows, int cols, long long ld, uintptr_t stream) {

@@ -170,6 +170,17 @@ template <> struct St<f16> {
 // device: wave64 reductions (butterfly over all 64 lanes)
 // ---------------------------------------------------------------------------
 
+// Per-tensor int8 quantisation (reference quantize.cu:169-186): scale =
+// max|x| / 127 (1 when every value is 0); code = clamp(rint(x * inv), -127,
+// 127) with inv = 1 / scale.
+__device__ __forceinline__ float make_scale(float absmax) {
+    return absmax > 0.0f ? absmax / 127.0f : 1.0f;
+}
+
+__device__ __forceinline__ signed char quant1(float x, float inv) {
+    return (signed char)fmaxf(-127.0f, fminf(127.0f, rintf(x * inv)));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

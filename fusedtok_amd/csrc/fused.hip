@@ -34,14 +34,6 @@ namespace {
 
 constexpr int kFNT = 256;
 
-__device__ __forceinline__ signed char quant1(float y, float inv) {
-    return (signed char)fmaxf(-127.0f, fminf(127.0f, rintf(y * inv)));
-}
-
-__device__ __forceinline__ float make_scale(float absmax) {
-    return absmax > 0.0f ? absmax / 127.0f : 1.0f;
-}
-
 // ---------------------------------------------------------------------------
 // rmsnorm_quant
 // ---------------------------------------------------------------------------

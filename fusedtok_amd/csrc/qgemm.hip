@@ -230,6 +230,156 @@ __global__ __launch_bounds__(256) void qgemv_dot4(const i8* __restrict__ a,
 }
 
 // ---------------------------------------------------------------------------
+// RMSNorm -> per-tensor int8 quantize -> GEMV in one launch (one row,
+// K <= 4096). Every workgroup normalises and quantises the row itself (8 KB
+// of x from L2) with rmsnorm_quant's single-row arithmetic - thread t of 256
+// takes 4-element chunks t, t + 256, ..; fmaf sum of squares; wave
+// butterfly; the 4 wave totals in order; inv = 1 / sqrtf(total / K + eps);
+// y = (v * inv) * w; scale = max|y| / 127; codes rint(y * (1 / scale)) -
+// so its codes and scale are those of rmsnorm_quant bit for bit, and keeps
+// the codes in LDS for the dot products. The wave's first weight rows are
+// loaded before the normalisation, so the two overlap. Workgroup 0 also
+// writes the codes and the scale. The dot products and the epilogue are
+// qgemv_dot4's for M = 1 with sa = the computed scale.
+// ---------------------------------------------------------------------------
+template <typename T, int OUT>
+__global__ __launch_bounds__(256) void rmsq_gemv(
+    const T* __restrict__ x, const T* __restrict__ res, const float* __restrict__ wn,
+    float eps, const i8* __restrict__ b, Epi e, int n, int k, i8* __restrict__ q_out,
+    float* __restrict__ scale_out) {
+    static_assert(kGemvChunks * 1024 == 4096, "one pass covers K <= 4096");
+    __shared__ __attribute__((aligned(16))) i8 xq[kGemvChunks * 1024];
+    __shared__ float red[4], redm[4];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wv = tid >> 6;
+    const int gwave = blockIdx.x * 4 + wv;
+    const int nwaves = gridDim.x * 4;
+    const int j_first = gwave * kGemvRows;
+    const i32x4 z = {0, 0, 0, 0};
+
+    i32x4 w[kGemvChunks][kGemvRows];
+    auto load_w = [&](int j0) {
+#pragma unroll
+        for (int c = 0; c < kGemvChunks; ++c) {
+            const int kk = 1024 * c + 16 * lane;
+#pragma unroll
+            for (int r = 0; r < kGemvRows; ++r) {
+                const int row = min(j0 + r, n - 1);
+                w[c][r] = kk < k ? __builtin_nontemporal_load(
+                                       reinterpret_cast<const i32x4*>(b + (size_t)row * k + kk))
+                                 : z;
+            }
+        }
+    };
+    if (j_first < n) load_w(j_first);
+
+    // normalise and quantise the row (rmsnorm_quant's order)
+    const int chunks = k >> 2;
+    float4 v[4], wc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int c = tid + 256 * j;
+        v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        wc[j] = v[j];
+        if (c < chunks) {
+            v[j] = St<T>::ld4(x + 4 * c);
+            if (res) {
+                const float4 rv = St<T>::ld4(res + 4 * c);
+                v[j].x += rv.x; v[j].y += rv.y; v[j].z += rv.z; v[j].w += rv.w;
+            }
+            wc[j] = *reinterpret_cast<const float4*>(wn + 4 * c);
+        }
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (tid + 256 * j < chunks) {
+            acc = fmaf(v[j].x, v[j].x, acc);
+            acc = fmaf(v[j].y, v[j].y, acc);
+            acc = fmaf(v[j].z, v[j].z, acc);
+            acc = fmaf(v[j].w, v[j].w, acc);
+        }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) red[wv] = acc;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tot += red[i];
+    const float inv = 1.0f / sqrtf(tot / (float)k + eps);
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (tid + 256 * j < chunks) {
+            m = fmaxf(m, fabsf(v[j].x * inv * wc[j].x));
+            m = fmaxf(m, fabsf(v[j].y * inv * wc[j].y));
+            m = fmaxf(m, fabsf(v[j].z * inv * wc[j].z));
+            m = fmaxf(m, fabsf(v[j].w * inv * wc[j].w));
+        }
+    }
+    m = wave_max(m);
+    if (lane == 0) redm[wv] = m;
+    __syncthreads();
+    m = redm[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) m = fmaxf(m, redm[i]);
+    const float scale = make_scale(m);
+    const float inv_s = 1.0f / scale;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int c = tid + 256 * j;
+        if (c < chunks) {
+            char4 o;
+            o.x = quant1(v[j].x * inv * wc[j].x, inv_s);
+            o.y = quant1(v[j].y * inv * wc[j].y, inv_s);
+            o.z = quant1(v[j].z * inv * wc[j].z, inv_s);
+            o.w = quant1(v[j].w * inv * wc[j].w, inv_s);
+            *reinterpret_cast<char4*>(xq + 4 * c) = o;
+            if (blockIdx.x == 0 && q_out) *reinterpret_cast<char4*>(q_out + 4 * c) = o;
+        }
+    }
+    if (blockIdx.x == 0 && tid == 0 && scale_out) *scale_out = scale;
+    __syncthreads();
+
+    for (int j0 = j_first; j0 < n; j0 += nwaves * kGemvRows) {
+        if (j0 != j_first) load_w(j0);
+        int accr[kGemvRows];
+#pragma unroll
+        for (int r = 0; r < kGemvRows; ++r) accr[r] = 0;
+#pragma unroll
+        for (int c = 0; c < kGemvChunks; ++c) {
+            const int kk = 1024 * c + 16 * lane;
+            const i32x4 xv = kk < k ? *reinterpret_cast<const i32x4*>(xq + kk) : z;
+#pragma unroll
+            for (int r = 0; r < kGemvRows; ++r) {
+                int sdot = accr[r];
+                sdot = __builtin_amdgcn_sdot4(w[c][r][0], xv[0], sdot, false);
+                sdot = __builtin_amdgcn_sdot4(w[c][r][1], xv[1], sdot, false);
+                sdot = __builtin_amdgcn_sdot4(w[c][r][2], xv[2], sdot, false);
+                sdot = __builtin_amdgcn_sdot4(w[c][r][3], xv[3], sdot, false);
+                accr[r] = sdot;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kGemvRows; ++r) {
+            int t = accr[r];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+            accr[r] = t;
+        }
+#pragma unroll
+        for (int r = 0; r < kGemvRows; ++r) {
+            const int col = j0 + r;
+            if (lane == r && col < n) {
+                float s = 0.0f;
+                if constexpr (OUT != kOutI32) s = e.sb_vec ? scale * e.sb_vec[col] : scale * e.sb;
+                epi_store_scaled<OUT>(e, n, 0, col, accr[r], s);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // decode MFMA GEMM (M <= 16): a workgroup owns 16 output columns (W rows
 // n0 .. n0 + 15) over the whole of K; its KW waves split K into 512-byte
 // chunks taken round robin (wave w: chunks w, w + KW, ...), so each wave
@@ -2572,6 +2722,66 @@ int ft_qgemm_launch_ex(const signed char* aq, const signed char* bq,
         }
         ft::Epi e{y, sa, sa_dev, sb, sb_vec};
         ft::qgemm_run(aq, bq, e, out, m, n, k, ft::as_stream(stream));
+    });
+}
+
+int ft_rmsnorm_qgemm_launch(const void* x, int x_dtype, const float* w,
+                            const void* residual, float eps, const signed char* bq,
+                            const float* sb_vec, float sb, void* y, int y_dtype,
+                            signed char* q, float* scale_out, int rows, int n, int k,
+                            uintptr_t stream) {
+    return ft::guarded([&] {
+        int out;
+        switch (y_dtype) {
+        case FT_DT_F32: out = ft::kOutF32; break;
+        case FT_DT_BF16: out = ft::kOutBF16; break;
+        case FT_DT_F16: out = ft::kOutF16; break;
+        default: ft::inval("rmsnorm_qgemm: unknown output dtype code");
+        }
+        if (rows < 0 || n < 0 || k <= 0)
+            ft::inval("rmsnorm_qgemm: rows and n must be >= 0 and k > 0");
+        if (rows == 0 || n == 0) return;
+        if (!x || !w || !bq || !y || !q || !scale_out) ft::inval("rmsnorm_qgemm: null operand");
+        hipStream_t s = ft::as_stream(stream);
+        const size_t esz = x_dtype == FT_DT_F32 ? 4 : 2;
+        const bool fusable =
+            rows == 1 && k <= ft::kGemvChunks * 1024 && k % 16 == 0 &&
+            (uintptr_t)x % (4 * esz) == 0 && (!residual || (uintptr_t)residual % (4 * esz) == 0) &&
+            (uintptr_t)w % 16 == 0 && (uintptr_t)bq % 16 == 0 && (uintptr_t)q % 4 == 0 &&
+            ft::env_int("FT_RMSQ_GEMV_SPLIT", 0) == 0;
+        if (!fusable) {
+            // the two-step chain: rmsnorm_quant, then the GEMM on its codes
+            // with the device scale
+            const int rc = ft_rmsnorm_quant_launch(x, x_dtype, w, residual, q, scale_out, rows,
+                                                   k, eps, stream);
+            if (rc != FT_OK) throw ft::Error{rc, ft_last_error()};
+            ft::Epi e{y, 0.0f, scale_out, sb, sb_vec};
+            ft::qgemm_run(q, bq, e, out, rows, n, k, s);
+            return;
+        }
+        if (k % 4 != 0) ft::inval("rmsnorm_qgemm: k must be a multiple of 4");
+        ft::Epi e{y, 0.0f, scale_out, sb, sb_vec};
+        const long long waves = std::min<long long>((n + ft::kGemvRows - 1) / ft::kGemvRows,
+                                                    (long long)ft::dev_info().cu_count * 16);
+        const unsigned grid = (unsigned)((waves + 3) / 4);
+#define FT_RQG(T, O)                                                                         \
+    ft::rmsq_gemv<T, O><<<grid, 256, 0, s>>>((const T*)x, (const T*)residual, w, eps, bq, e, \
+                                             n, k, q, scale_out)
+#define FT_RQG_T(T)                                   \
+    do {                                              \
+        if (out == ft::kOutF32) FT_RQG(T, ft::kOutF32);   \
+        else if (out == ft::kOutBF16) FT_RQG(T, ft::kOutBF16); \
+        else FT_RQG(T, ft::kOutF16);                  \
+    } while (0)
+        switch (x_dtype) {
+        case FT_DT_F32: FT_RQG_T(float); break;
+        case FT_DT_BF16: FT_RQG_T(ft::bf16); break;
+        case FT_DT_F16: FT_RQG_T(ft::f16); break;
+        default: ft::inval("rmsnorm_qgemm: unknown x dtype code");
+        }
+#undef FT_RQG_T
+#undef FT_RQG
+        ft::launch_check("rmsnorm_qgemm kernel launch");
     });
 }
 

@@ -26,14 +26,6 @@ namespace {
 constexpr long long kSmallN = 1 << 16;
 constexpr int kPass1Blocks = 1024;
 
-__device__ __forceinline__ float make_scale(float absmax) {
-    return absmax > 0.0f ? absmax / 127.0f : 1.0f;
-}
-
-__device__ __forceinline__ signed char quant1(float x, float inv) {
-    return (signed char)fmaxf(-127.0f, fminf(127.0f, rintf(x * inv)));
-}
-
 // Load 4 consecutive elements widened to float (exact for every type).
 template <typename T>
 __device__ __forceinline__ float4 ld4w(const T* p) { return St<T>::ld4(p); }

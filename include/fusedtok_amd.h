@@ -322,6 +322,19 @@ int ft_rmsnorm_quant_launch(const void* x, int x_dtype, const float* w,
                             const void* residual, signed char* q,
                             float* scale_out, int rows, int cols, float eps,
                             uintptr_t stream);
+/* RMSNorm (+ optional residual) -> per-tensor int8 quantize -> W8A8
+ * GEMM (BASELINE config 2's chain): q[rows, k] and *scale_out (DEVICE
+ * float) as ft_rmsnorm_quant_launch writes them, and y[rows, n] (y_dtype
+ * FT_DT_F32 / BF16 / F16) as ft_qgemm_launch_ex with sa_dev = scale_out
+ * computes it from them (sb_vec per-channel, or per-tensor sb when NULL),
+ * bit for bit. One row with k <= 4096 (k % 16 == 0, operands aligned as
+ * for the two ops) runs as one launch; other shapes run the two ops. */
+int ft_rmsnorm_qgemm_launch(const void* x, int x_dtype, const float* w,
+                            const void* residual, float eps,
+                            const signed char* bq, const float* sb_vec,
+                            float sb, void* y, int y_dtype, signed char* q,
+                            float* scale_out, int rows, int n, int k,
+                            uintptr_t stream);
 /* SwiGLU then per-tensor int8 quantize: gate / up element (r, c) at
  * r * ld + c (so the two halves of one [rows, 2*cols] gate|up GEMM
  * output are passed as base and base + cols with ld = 2*cols); q is the

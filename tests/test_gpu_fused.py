@@ -86,6 +86,40 @@ def test_rmsnorm_quant_one_launch_matches_two_launch_path(dt, rows, cols, monkey
         assert s1 == s2
 
 
+@pytest.mark.parametrize("dt", ALL)
+@pytest.mark.parametrize("rows,n,k,res", [(1, 11008, 4096, False), (1, 777, 1024, True),
+                                          (1, 5, 48, True), (1, 300, 4112, False),
+                                          (3, 300, 512, True)])
+@pytest.mark.parametrize("odt", [torch.float16, torch.float32])
+def test_rmsnorm_qgemm_equals_the_two_ops(dt, rows, n, k, res, odt, monkeypatch):
+    # one row with K <= 4096 runs as one launch (the GEMV normalises and
+    # quantises the row in every workgroup); the codes, the scale and the
+    # output must equal rmsnorm_quant followed by qgemm_perchannel
+    rng = np.random.default_rng(rows * 31 + n + k + res)
+    x = t(rng.standard_normal((rows, k)).astype(np.float32) * 2, dt)
+    w = t(rng.uniform(0.5, 1.5, k).astype(np.float32))
+    r = t(rng.standard_normal((rows, k)).astype(np.float32), dt) if res else None
+    b = t(rng.integers(-127, 128, (n, k)).astype(np.int8))
+    sb = t(rng.uniform(1e-3, 1e-2, n).astype(np.float32))
+    y, q, s = ft.rmsnorm_qgemm(x, w, b, sb, residual=r, eps=1e-5, out_dtype=odt)
+    q2, s2 = ft.rmsnorm_quant(x, w, residual=r, eps=1e-5, device_scale=True)
+    y2 = ft.qgemm_perchannel(q2, s2, b, sb, out_dtype=odt)
+    assert torch.equal(q, q2) and torch.equal(s, s2) and torch.equal(y, y2)
+    eq, es = oracle.rmsnorm_quant(as_f32(x), w.cpu().numpy(), None if r is None else as_f32(r),
+                                  1e-5)
+    np.testing.assert_array_equal(q.cpu().numpy(), eq)
+    assert float(s) == es
+    ref = oracle.qgemm_perchannel(eq, es, b.cpu().numpy(), sb.cpu().numpy())
+    assert torch.equal(y.cpu(), torch.from_numpy(ref).to(odt))
+    # the two-op path of the same entry point, and a per-tensor weight scale
+    monkeypatch.setenv("FT_RMSQ_GEMV_SPLIT", "1")
+    y3, q3, s3 = ft.rmsnorm_qgemm(x, w, b, sb, residual=r, eps=1e-5, out_dtype=odt)
+    monkeypatch.delenv("FT_RMSQ_GEMV_SPLIT")
+    assert torch.equal(y3, y) and torch.equal(q3, q) and torch.equal(s3, s)
+    yt, _, _ = ft.rmsnorm_qgemm(x, w, b, 0.004, residual=r, eps=1e-5, out_dtype=odt)
+    assert torch.equal(yt, ft.qgemm(q2, s2, b, 0.004, out_dtype=odt))
+
+
 def test_rmsnorm_quant_device_scale_zero_rows_and_1d():
     rng = np.random.default_rng(3)
     x = t(rng.standard_normal(512).astype(np.float32), torch.bfloat16)
