@@ -187,6 +187,19 @@ def test_fused_invalid_arguments(lib):
     assert rq(None, 0, None, None, None, None, 2, 0, 1e-6, 0) == FT_EINVAL
     assert rq(None, 9, None, None, None, None, 2, 8, 1e-6, 0) == FT_EINVAL  # dtype
     assert rq(None, 1, None, None, None, None, 0, 8, 1e-6, 0) == FT_OK      # no rows
+    rg = lib.ft_rmsnorm_qgemm_launch
+    rg.argtypes = ([ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                    ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float,
+                    ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p] +
+                   [ctypes.c_int] * 3 + [ctypes.c_size_t])
+    assert rg(None, 2, None, None, 1e-5, None, None, 0.0, None, 9, None, None,
+              1, 8, 16, 0) == FT_EINVAL                                    # out dtype
+    assert rg(None, 2, None, None, 1e-5, None, None, 0.0, None, 2, None, None,
+              1, 8, 0, 0) == FT_EINVAL                                     # k == 0
+    assert rg(None, 2, None, None, 1e-5, None, None, 0.0, None, 2, None, None,
+              1, 8, 16, 0) == FT_EINVAL                                    # null operands
+    assert rg(None, 2, None, None, 1e-5, None, None, 0.0, None, 2, None, None,
+              0, 8, 16, 0) == FT_OK                                        # no rows
     sq = lib.ft_swiglu_quant_launch
     sq.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
                    ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_longlong,
