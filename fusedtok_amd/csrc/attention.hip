@@ -357,7 +357,7 @@ __device__ __forceinline__ long long stream_seg_len(long long total, int nseg, i
     return s < min_seg ? (long long)min_seg : s;
 }
 
-template <typename T, int MODE, bool WIDE>
+template <typename T, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_decode_stream(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
@@ -451,34 +451,14 @@ void attn_decode_stream(
                 }
             }
         };
-        auto kv_load = [&](int st, const int (&e)[2], V8 (&kt)[2][4], V8 (&vt)[2][4]) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int t = tok_of(st, h);
-                size_t off;
-                if constexpr (MODE == kRowsContig) {
-                    off = ((size_t)row * rows_or_page + t) * D;
-                } else {
-                    const int in_pg = MODE == kRowsPagedPow2 ? (t & (rows_or_page - 1))
-                                                             : (t % rows_or_page);
-                    off = (((size_t)e[h] * hkv + kv) * rows_or_page + in_pg) * D;
-                }
-                off += 8 * g;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    kt[h][j] = *reinterpret_cast<const V8*>(k + off + 32 * j);
-                    vt[h][j] = *reinterpret_cast<const V8*>(v + off + 32 * j);
-                }
-            }
-        };
-        // WIDE: load p (0..3) of tile h reads 4 whole rows, tile rows 4p ..
+        // Load p (0..3) of tile h reads 4 whole rows, tile rows 4p ..
         // 4p + 3: lane l takes 16-byte chunk l % 16 of tile row 4p + l / 16,
         // whose table entry is held by lane 4p + l / 16. Whole 128-byte lines
         // per instruction, non-temporal: the pages are read once per launch
         // (a read of C3's pages in this pattern runs at 6.7 TB/s, against
         // 5.6 TB/s for half lines per instruction, non-temporal, and 5.1 TB/s
         // for plain loads either way).
-        auto kv_load_wide = [&](int st, const int (&e)[2], V8 (&kt)[2][4], V8 (&vt)[2][4]) {
+        auto kv_load = [&](int st, const int (&e)[2], V8 (&kt)[2][4], V8 (&vt)[2][4]) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -500,7 +480,7 @@ void attn_decode_stream(
                 }
             }
         };
-        // WIDE staging: the wave's 32 rows x 256 B of K (then V) in its own
+        // Staging: the wave's 32 rows x 256 B of K (then V) in its own
         // s_acc slot (8448 B, written as s_acc only after the wave's last
         // step). Chunk c of row w sits at 16 (c ^ (w & 15)): the 16 lanes of
         // a write (one row) and of a fragment read (16 rows, one chunk) hit
@@ -526,16 +506,20 @@ void attn_decode_stream(
         };
         auto compute_step = [&](int st, const V8 (&kin)[2][4], const V8 (&vin)[2][4]) {
             const int tb = st << 5;
-            // WIDE: K through the staging, then V written behind K's
-            // fragment reads (one wave's LDS operations run in order), so
-            // V's load registers are free during the softmax
-            V8 kw[2][4], vw[2][4];
-            if constexpr (WIDE) {
-                stage_write(kin);
-                stage_read(kw);
-                stage_write(vin);
-            }
-            const V8 (&kt)[2][4] = WIDE ? kw : kin;
+            // K through the staging, then V written behind K's fragment
+            // reads, so V's load registers are free during the softmax. The
+            // lanes exchange data through the staging: the hardware runs one
+            // wave's LDS operations in issue order, and wave_lds_order()
+            // keeps the compiler from moving a lane's LDS access across
+            // the point where another lane's must have happened (the
+            // previous step's V reads come before this step's K writes).
+            V8 kt[2][4], vt[2][4];
+            wave_lds_order();
+            stage_write(kin);
+            wave_lds_order();
+            stage_read(kt);
+            wave_lds_order();
+            stage_write(vin);
             f32x4 s[2];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -575,8 +559,8 @@ void attn_decode_stream(
                 pb[i] = (T)p[i];
                 if (M::kSplitP) pl[i] = (T)(p[i] - (float)pb[i]);
             }
-            if constexpr (WIDE) stage_read(vw);
-            const V8 (&vt)[2][4] = WIDE ? vw : vin;
+            wave_lds_order();
+            stage_read(vt);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -603,22 +587,18 @@ void attn_decode_stream(
         if (st < nsteps) {
             V8 ka[2][4], va_[2][4], kb[2][4], vb[2][4];
             int ea[2] = {0, 0}, eb[2] = {0, 0};
-            auto kvl = [&](int s_, const int (&e)[2], V8 (&kt)[2][4], V8 (&vt)[2][4]) {
-                if constexpr (WIDE) kv_load_wide(s_, e, kt, vt);
-                else kv_load(s_, e, kt, vt);
-            };
             tbl_load(st, ea);
             tbl_load(min(st + 4, last), eb);
-            kvl(st, ea, ka, va_);
+            kv_load(st, ea, ka, va_);
             for (; st + 4 < nsteps; st += 8) {
                 tbl_load(min(st + 8, last), ea);
-                kvl(st + 4, eb, kb, vb);
+                kv_load(st + 4, eb, kb, vb);
                 // keep the prefetch ahead of the compute that follows it (the
                 // scheduler would otherwise sink the loads below the waits)
                 __builtin_amdgcn_sched_barrier(0);
                 compute_step(st, ka, va_);
                 tbl_load(min(st + 12, last), eb);
-                kvl(min(st + 8, last), ea, ka, va_);
+                kv_load(min(st + 8, last), ea, ka, va_);
                 __builtin_amdgcn_sched_barrier(0);
                 compute_step(st + 4, kb, vb);
             }
@@ -841,22 +821,22 @@ bool mfma_eligible(const T* q, const T* k, const T* v, int group, int dim) {
 
 // attn_decode_stream in the row mode of the layout (paged with a power-of-2
 // page, paged with any page, contiguous).
-template <typename T, bool WIDE>
+template <typename T>
 void launch_stream(bool paged, int page_shift, int nseg, hipStream_t s, const T* q,
                    const T* k, const T* v, const int* table, const int* lens, float* ws_ml,
                    float* ws_acc, long long* pref, T* out, int batch, int hq, int hkv,
                    int group, int rows_or_page, int tbl_width, int span, float scale_log2,
                    int min_seg) {
     if (paged && page_shift >= 0)
-        attn_decode_stream<T, kRowsPagedPow2, WIDE><<<(unsigned)nseg, 256, 0, s>>>(
+        attn_decode_stream<T, kRowsPagedPow2><<<(unsigned)nseg, 256, 0, s>>>(
             q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
             rows_or_page, page_shift, tbl_width, span, scale_log2, min_seg);
     else if (paged)
-        attn_decode_stream<T, kRowsPagedDiv, WIDE><<<(unsigned)nseg, 256, 0, s>>>(
+        attn_decode_stream<T, kRowsPagedDiv><<<(unsigned)nseg, 256, 0, s>>>(
             q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
             rows_or_page, -1, tbl_width, span, scale_log2, min_seg);
     else
-        attn_decode_stream<T, kRowsContig, WIDE><<<(unsigned)nseg, 256, 0, s>>>(
+        attn_decode_stream<T, kRowsContig><<<(unsigned)nseg, 256, 0, s>>>(
             q, k, v, nullptr, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
             rows_or_page, -1, 0, span, scale_log2, min_seg);
 }
@@ -910,17 +890,9 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
             float* ws_ml = (float*)ws;
             float* ws_acc = ws_ml + ml_floats;
             long long* pref = (long long*)(ws_acc + acc_floats);
-            // FT_ATTN_LOADS=1: the per-lane row loads straight into the MFMA
-            // layout (half a 128-byte line per instruction, plain loads)
-            if (env_int("FT_ATTN_LOADS", 0) == 1)
-                launch_stream<T, false>(paged, page_shift, nseg, s, q, k, v, table, lens, ws_ml,
-                                        ws_acc, pref, out, batch, hq, hkv, group,
-                                        rows_or_page, tbl_width, (int)span, scale_log2,
-                                        min_seg);
-            else
-                launch_stream<T, true>(paged, page_shift, nseg, s, q, k, v, table, lens, ws_ml,
-                                       ws_acc, pref, out, batch, hq, hkv, group, rows_or_page,
-                                       tbl_width, (int)span, scale_log2, min_seg);
+            launch_stream<T>(paged, page_shift, nseg, s, q, k, v, table, lens, ws_ml, ws_acc,
+                             pref, out, batch, hq, hkv, group, rows_or_page, tbl_width,
+                             (int)span, scale_log2, min_seg);
             launch_check("attention decode kernel launch");
             attn_combine_stream<T><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
                 ws_ml, ws_acc, pref, out, batch, hq, hkv, group, nseg, min_seg);

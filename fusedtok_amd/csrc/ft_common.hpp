@@ -193,6 +193,19 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Ordering point for data one wave's lanes exchange through LDS (a lane
+// reads what another lane of the same wave wrote, or overwrites what
+// another lane read). The hardware executes a wave's LDS instructions in
+// issue order, so no barrier instruction is needed; the wavefront-scope
+// release/acquire pair and the wave barrier tell the compiler that LDS
+// accesses may not move across this point, which per-lane alias analysis
+// alone would allow when it can prove one lane's addresses distinct.
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Block-wide reductions for blockDim.x == NT (multiple of 64). `red` is
 // LDS scratch of at least NT/64 floats. Every thread gets the result.
 template <int NT>

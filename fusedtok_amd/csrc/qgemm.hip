@@ -2740,9 +2740,19 @@ int ft_rmsnorm_qgemm_launch(const void* x, int x_dtype, const float* w,
         }
         if (rows < 0 || n < 0 || k <= 0)
             ft::inval("rmsnorm_qgemm: rows and n must be >= 0 and k > 0");
-        if (rows == 0 || n == 0) return;
-        if (!x || !w || !bq || !y || !q || !scale_out) ft::inval("rmsnorm_qgemm: null operand");
+        // every shape check before the first launch: no partial writes on error
+        ft::qgemm_check(rows, n, k);
+        if (rows == 0) return;
+        if (!x || !w || !q || !scale_out || (n > 0 && (!bq || !y)))
+            ft::inval("rmsnorm_qgemm: null operand");
         hipStream_t s = ft::as_stream(stream);
+        if (n == 0) {
+            // no output columns: the codes and the scale are still produced
+            const int rc = ft_rmsnorm_quant_launch(x, x_dtype, w, residual, q, scale_out, rows,
+                                                   k, eps, stream);
+            if (rc != FT_OK) throw ft::Error{rc, ft_last_error()};
+            return;
+        }
         const size_t esz = x_dtype == FT_DT_F32 ? 4 : 2;
         const bool fusable =
             rows == 1 && k <= ft::kGemvChunks * 1024 && k % 16 == 0 &&

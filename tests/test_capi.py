@@ -200,6 +200,15 @@ def test_fused_invalid_arguments(lib):
               1, 8, 16, 0) == FT_EINVAL                                    # null operands
     assert rg(None, 2, None, None, 1e-5, None, None, 0.0, None, 2, None, None,
               0, 8, 16, 0) == FT_OK                                        # no rows
+    # no output columns (b_q [0, K]) with rows: the codes and the scale are
+    # still owed, so the call proceeds to the operand checks (not FT_OK)
+    assert rg(None, 2, None, None, 1e-5, None, None, 0.0, None, 2, None, None,
+              1, 0, 16, 0) == FT_EINVAL
+    assert b"null operand" in lib.ft_last_error()
+    # the GEMM's K limit is checked before anything is launched
+    assert rg(None, 2, None, None, 1e-5, None, None, 0.0, None, 2, None, None,
+              1, 8, 131072, 0) == FT_EINVAL
+    assert b"K too large" in lib.ft_last_error()
     sq = lib.ft_swiglu_quant_launch
     sq.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
                    ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_longlong,

@@ -65,6 +65,48 @@ def test_rmsnorm_quant_matches_oracle_and_chain(dt, rows, cols, with_res):
     assert s == s2
 
 
+@pytest.mark.parametrize("rows", [1, 3])
+def test_rmsnorm_qgemm_without_output_columns_still_quantises(rows):
+    # b_q [0, K]: no GEMM output, but the codes and the scale are returned
+    # as rmsnorm_quant writes them
+    rng = np.random.default_rng(rows)
+    x = t(rng.standard_normal((rows, 256)).astype(np.float32), torch.float16)
+    w = t(rng.uniform(0.5, 1.5, 256).astype(np.float32))
+    b = torch.empty((0, 256), dtype=torch.int8, device=DEV)
+    sb = torch.empty((0,), dtype=torch.float32, device=DEV)
+    y, q, s = ft.rmsnorm_qgemm(x, w, b, sb, eps=1e-5, out_dtype=torch.float16)
+    q2, s2 = ft.rmsnorm_quant(x, w, eps=1e-5, device_scale=True)
+    assert y.shape == (rows, 0)
+    assert torch.equal(q, q2) and torch.equal(s, s2)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,cols", [(1, 4096), (16, 4096), (64, 4096), (3, 1028)])
+def test_rmsnorm_quant_vs_half_storage_chain(dt, rows, cols):
+    # The fused op quantises the float32 RMSNorm result. The unfused chain on
+    # half storage first rounds y to bf16 / fp16 (rmsnorm's output dtype),
+    # then quantises: y and the scale each move by at most one half-precision
+    # rounding (relative 2^-8 for bf16, 2^-11 for fp16), so a code of
+    # magnitude <= 127 moves by less than 127 * 2 * 2^-8 < 1 before rint, and
+    # the two codes differ by at most one step. That is the bound between the
+    # fused op and the reference's half-storage chain (rmsnorm.cu:110-130 ->
+    # quantize.cu:153-186 on the rounded y); exact agreement with that chain
+    # is not claimed.
+    rng = np.random.default_rng(rows * 13 + cols)
+    x = t(rng.standard_normal((rows, cols)).astype(np.float32) * 2, dt)
+    w = t(rng.uniform(0.5, 1.5, cols).astype(np.float32))
+    r = t(rng.standard_normal((rows, cols)).astype(np.float32), dt)
+    for res in (None, r):
+        q, s = ft.rmsnorm_quant(x, w, residual=res, eps=1e-5)
+        y_half = ft.rmsnorm(x, w, residual=res, eps=1e-5)
+        assert y_half.dtype is dt
+        q_half, s_half = ft.quantize_int8(y_half)
+        diff = np.abs(q.cpu().numpy().astype(np.int32) - q_half.cpu().numpy().astype(np.int32))
+        assert diff.max() <= 1
+        rel = 2.0 ** -8 if dt is torch.bfloat16 else 2.0 ** -11
+        assert abs(s - s_half) <= rel * s * (1 + 1e-6)
+
+
 @pytest.mark.parametrize("dt", ALL)
 @pytest.mark.parametrize("rows,cols", [(1, 4096), (2, 12), (3, 4096), (4, 4096),
                                        (4, 1000), (1, 4)])
@@ -89,8 +131,11 @@ def test_rmsnorm_quant_one_launch_matches_two_launch_path(dt, rows, cols, monkey
 @pytest.mark.parametrize("dt", ALL)
 @pytest.mark.parametrize("rows,n,k,res", [(1, 11008, 4096, False), (1, 777, 1024, True),
                                           (1, 5, 48, True), (1, 300, 4112, False),
-                                          (3, 300, 512, True)])
-@pytest.mark.parametrize("odt", [torch.float16, torch.float32])
+                                          (3, 300, 512, True),
+                                          # N > 64 * CUs: the GEMV's grid-stride
+                                          # second pass reloads its weight rows
+                                          (1, 28672, 4096, True)])
+@pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
 def test_rmsnorm_qgemm_equals_the_two_ops(dt, rows, n, k, res, odt, monkeypatch):
     # one row with K <= 4096 runs as one launch (the GEMV normalises and
     # quantises the row in every workgroup); the codes, the scale and the
