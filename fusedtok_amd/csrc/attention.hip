@@ -28,6 +28,8 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
+#include <string>
 #include <type_traits>
 
 namespace ft {
@@ -841,11 +843,29 @@ void launch_stream(bool paged, int page_shift, int nseg, hipStream_t s, const T*
             rows_or_page, -1, 0, span, scale_log2, min_seg);
 }
 
+// Device workspace of one decode call (split partials and the length
+// prefix): the library's per-device buffer, grown on demand, or a fixed
+// region of `cap` bytes that the caller owns (the no-allocation entry
+// point). A fixed region that is too small is an invalid argument, raised
+// before anything is launched.
+struct Workspace {
+    void* fixed = nullptr;
+    size_t cap = 0;
+    void* get(size_t bytes, hipStream_t s) const {
+        if (!fixed) return scratch(Scratch::AttnPartials, bytes, s);
+        if (bytes > cap)
+            inval("attention: this call needs " + std::to_string(bytes) +
+                  " bytes of split workspace; the static workspace holds " +
+                  std::to_string(cap));
+        return fixed;
+    }
+};
+
 template <typename T>
 void attention_run(const T* q, const T* k, const T* v, const int* table,
                    const int* lens, T* out, int batch, int hq, int hkv,
                    int rows_or_page, int tbl_width, int dim, bool paged,
-                   hipStream_t s) {
+                   hipStream_t s, const Workspace& wsp = Workspace{}) {
     long long span;
     if (paged) {
         span = (long long)tbl_width * rows_or_page;
@@ -884,8 +904,7 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
             const size_t nslots = ((size_t)nseg + (size_t)batch * hkv) * group;
             const size_t ml_floats = (nslots * 2 + 63) & ~(size_t)63;
             const size_t acc_floats = nslots * dim;
-            char* ws = (char*)scratch(
-                Scratch::AttnPartials,
+            char* ws = (char*)wsp.get(
                 (ml_floats + acc_floats) * sizeof(float) + (batch + 1) * sizeof(long long), s);
             float* ws_ml = (float*)ws;
             float* ws_acc = ws_ml + ml_floats;
@@ -909,8 +928,7 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
     if (units * 256 > (1LL << 31)) inval("attention problem too large for one launch");
     const size_t nslots = (size_t)units * group;
     const size_t ml_floats = (nslots * 2 + 63) & ~(size_t)63;
-    float* ws = (float*)scratch(Scratch::AttnPartials,
-                                (ml_floats + nslots * dim) * sizeof(float), s);
+    float* ws = (float*)wsp.get((ml_floats + nslots * dim) * sizeof(float), s);
     float* ws_ml = ws;
     float* ws_acc = ws + ml_floats;
     RowMap rm;
@@ -1007,7 +1025,56 @@ void kv_append_run(const T* k_new, const T* v_new, const int* table,
 using ft::bf16;
 using ft::f16;
 
+// ---------------------------------------------------------------------------
+// Static workspace of the no-allocation entry point. Each GPU holds its own
+// copy of this array for the life of the process. In host code `scratch` is
+// only a host-side stand-in for the symbol, never a device address: the
+// address of the current device's copy comes from hipGetSymbolAddress, once
+// per device, and only that pointer is handed to kernels.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[FT_NOALLOC_WORKSPACE_BYTES];
+
+namespace {
+constexpr int kMaxStaticDevices = 64;
+std::mutex g_static_ws_mutex;
+void* g_static_ws[kMaxStaticDevices];
+
+// The current device's copy of `scratch`, looked up on the first call made
+// with that device current.
+void* static_workspace() {
+    int dev = 0;
+    ft::hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxStaticDevices)
+        ft::inval("device id out of range for the static workspace");
+    std::lock_guard<std::mutex> lock(g_static_ws_mutex);
+    if (!g_static_ws[dev]) {
+        void* p = nullptr;
+        ft::hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                      "hipGetSymbolAddress(scratch)");
+        g_static_ws[dev] = p;
+    }
+    return g_static_ws[dev];
+}
+}  // namespace
+
 extern "C" {
+
+int ft_attention_decode_paged_launch_bf16_noalloc(const void* q, const void* k_pool,
+                                                  const void* v_pool, const int* table,
+                                                  const int* lens, void* out, int batch,
+                                                  int q_heads, int kv_heads, int page,
+                                                  int tbl_width, int dim,
+                                                  uintptr_t stream) {
+    return ft::guarded([&] {
+        ft::Workspace wsp;
+        wsp.fixed = static_workspace();
+        wsp.cap = FT_NOALLOC_WORKSPACE_BYTES;
+        ft::attention_run<bf16>((const bf16*)q, (const bf16*)k_pool, (const bf16*)v_pool,
+                                table, lens, (bf16*)out, batch, q_heads, kv_heads, page,
+                                tbl_width, dim, true, ft::as_stream(stream), wsp);
+    });
+}
+
 
 int ft_attention_decode_launch(const float* q, const float* k, const float* v,
                                const int* lens, float* out, int batch,

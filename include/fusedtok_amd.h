@@ -110,6 +110,30 @@ int ft_attention_decode_paged_launch_fp16(const void* q, const void* k_pool,
                                           int tbl_width, int dim,
                                           uintptr_t stream);
 
+/* No-allocation variant of ft_attention_decode_paged_launch_bf16. It   */
+/* has no counterpart in the reference: it is for callers that cannot   */
+/* allocate device memory (code under HIP graph capture, tight serving  */
+/* loops, harnesses that forbid hipMalloc). Arguments and results are   */
+/* those of ft_attention_decode_paged_launch_bf16, bit for bit; the     */
+/* split partials live in a static per-device array of                  */
+/* FT_NOALLOC_WORKSPACE_BYTES (16 MiB) instead of the library's growing */
+/* buffer, and no hipMalloc, hipFree or other allocating routine is     */
+/* called. A call whose partials do not fit returns FT_EINVAL before    */
+/* anything is launched. With D = 128 and G = q_heads / kv_heads <= 16  */
+/* the need is (2 * CUs + batch * kv_heads) * G * 520 + 8 * (batch + 1) */
+/* bytes: 1.6 MB for batch 32 with 32 / 8 heads on 256 CUs; batch 512   */
+/* at 32 / 8 heads still fits. Every call on one GPU shares that GPU's  */
+/* array, which keeps the last call's contents: calls that overlap on   */
+/* one GPU (unordered streams) race and must be serialised.             */
+#define FT_NOALLOC_WORKSPACE_BYTES (16u << 20)
+int ft_attention_decode_paged_launch_bf16_noalloc(const void* q, const void* k_pool,
+                                                  const void* v_pool,
+                                                  const int* table, const int* lens,
+                                                  void* out, int batch, int q_heads,
+                                                  int kv_heads, int page,
+                                                  int tbl_width, int dim,
+                                                  uintptr_t stream);
+
 /* ------------------------------------------------------------------ */
 /* KV append: one fresh token per sequence written at position lens[b] */
 /* k_new/v_new [B,Hkv,D]. In place. Exact copies.                      */
