@@ -110,3 +110,23 @@ def test_no_cpu_fallback_without_device():
         ft.swiglu(np.zeros(4, np.float32), np.zeros(4, np.float32))
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         ft.quantize_int8(np.ones(4, np.float32))
+
+
+def test_stub_and_marker_cover_the_public_surface():
+    # the package ships a PEP 561 marker and a stub naming every public
+    # function, with the runtime __all__ in the same order (reference
+    # tests/test_api.py:110-150 checks its own package the same way)
+    import pathlib
+    import re
+    pkg = pathlib.Path(ft.__file__).parent
+    assert (pkg / "py.typed").is_file()
+    text = (pkg / "__init__.pyi").read_text()
+    for name in ft.__all__:
+        assert f"def {name}(" in text, name
+    listed = re.findall(r'"(\w+)"', re.search(r"__all__ = \[(.*?)\]", text, re.S).group(1))
+    assert listed == list(ft.__all__)
+
+
+def test_no_public_callables_beyond_all():
+    public = {n for n, v in vars(ft).items() if not n.startswith("_") and callable(v)}
+    assert public <= set(ft.__all__), sorted(public - set(ft.__all__))
