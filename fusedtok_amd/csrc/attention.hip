@@ -886,7 +886,7 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
         inval("attention: null operand");
     const int group = hq / hkv;
     const bool fast = mfma_eligible(q, k, v, group, dim) && batch <= kStreamScanRows &&
-                      env_int("FT_ATTN_FORCE_GENERIC", 0) == 0;
+                      tune(Tune::AttnForceGeneric, 0) == 0;
     int page_shift = -1;
     if (paged && (rows_or_page & (rows_or_page - 1)) == 0) {
         int sh = 0;
@@ -898,9 +898,9 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
         if (fast && span > 0) {
             // stream split: G equal token segments, G = 2 workgroups per CU
             // (the kernel's register budget allows exactly two per CU)
-            int nseg = env_int("FT_ATTN_SEGS", 2 * dev_info().cu_count);
+            int nseg = tune(Tune::AttnSegs, 2 * dev_info().cu_count);
             nseg = std::max(1, std::min(nseg, 1 << 20));
-            const int min_seg = std::max(32, env_int("FT_ATTN_MIN_SEG", kStreamMinSeg));
+            const int min_seg = std::max(32, tune(Tune::AttnMinSeg, kStreamMinSeg));
             const size_t nslots = ((size_t)nseg + (size_t)batch * hkv) * group;
             const size_t ml_floats = (nslots * 2 + 63) & ~(size_t)63;
             const size_t acc_floats = nslots * dim;
@@ -921,7 +921,7 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
     }
     const long long target = (long long)dev_info().cu_count * 16;
     int chunk = choose_chunk(batch, hkv, span, 64, kGenMaxChunk, target);
-    const int forced = env_int("FT_ATTN_CHUNK", 0);
+    const int forced = tune(Tune::AttnChunk, 0);
     if (forced > 0) chunk = std::min(forced, kGenMaxChunk);
     const int cmax = span > 0 ? (int)((span + chunk - 1) / chunk) : 1;
     const long long units = (long long)batch * hkv * cmax;

@@ -43,6 +43,13 @@ PYBIND11_MODULE(_fusedtok, m) {
     m.def("cuda_available", []() { return ft_device_available() != 0; },
           "True if a usable HIP device is present");
     m.def("version", []() { return std::string(ft_version()); });
+    m.def("set_tuning",
+          [](const std::string& name, int value) { check(ft_set_tuning(name.c_str(), value)); },
+          py::arg("name"), py::arg("value"),
+          "override a tuning / test switch (FT_* name) for this process");
+    m.def("clear_tuning",
+          [](const std::string& name) { check(ft_clear_tuning(name.c_str())); },
+          py::arg("name"), "restore a switch to its environment value (or unset)");
 
     // ---- attention, contiguous ------------------------------------------
 #define FT_ATT(NAME, FN, T)                                                    \

@@ -84,9 +84,34 @@ const DevInfo& dev_info();
 // True if `s` is being captured into a HIP graph.
 bool stream_capturing(hipStream_t s);
 
-// Integer value of environment variable `name` (A/B and test switches), or
-// `dflt` when it is unset or empty.
-int env_int(const char* name, int dflt);
+// Tuning and test switches. Each is read once per process, on first use,
+// from the environment variable of the same name, and can be overridden at
+// run time through ft_set_tuning() / ft_clear_tuning() (tests, sweeps). The
+// defaults are the measured-fastest paths; no switch changes a result
+// beyond the op's stated tolerance (the integer paths not at all).
+enum class Tune : int {
+    AttnForceGeneric = 0,  // FT_ATTN_FORCE_GENERIC: decode on the generic kernel
+    AttnSegs,              // FT_ATTN_SEGS: stream-split segment count
+    AttnMinSeg,            // FT_ATTN_MIN_SEG: minimum tokens per segment
+    AttnChunk,             // FT_ATTN_CHUNK: generic kernel's chunk
+    QgemmKernel,           // FT_QGEMM_KERNEL: force 1 skinny .. 6 decode
+    QgemmDecKw,            // FT_QGEMM_DEC_KW: waves per decode column tile
+    QgemmDecRegs,          // FT_QGEMM_DEC_REGS: register-operand decode kernel
+    QgemmKsplit,           // FT_QGEMM_KSPLIT: skinny kernel K split
+    QgemmSkRegs,           // FT_QGEMM_SK_REGS: register-operand skinny kernel
+    QgemmBig,              // FT_QGEMM_BIG: 1 64-byte DMA slabs, 2 register-staged
+    QgemmBand,             // FT_QGEMM_BAND: big-tile band height
+    RmsqSplit,             // FT_RMSQ_SPLIT: rmsnorm_quant in two launches
+    RmsqGemvSplit,         // FT_RMSQ_GEMV_SPLIT: rmsnorm_qgemm as two ops
+    PrefillForceGeneric,   // FT_PREFILL_FORCE_GENERIC
+    ArgSlices,             // FT_ARG_SLICES: argmax_batched slices per row
+    SmpSingle,             // FT_SMP_SINGLE: sampling, one workgroup per row
+    SmpSlices,             // FT_SMP_SLICES: sampling slices per row
+    kCount
+};
+// The switch's value, or `dflt` when it is neither in the environment nor
+// set through ft_set_tuning().
+int tune(Tune which, int dflt);
 
 // Per-device scratch buffers, one per purpose, grown on demand and kept for
 // the process lifetime. Growth is refused during a stream capture (the

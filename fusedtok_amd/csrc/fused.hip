@@ -293,7 +293,7 @@ void rmsnorm_quant_run(const T* x, const float* w, const T* r, signed char* q,
     if ((uintptr_t)x % a16 || (r && (uintptr_t)r % a16) || (uintptr_t)w % 16 ||
         (uintptr_t)q % 4)
         inval("rmsnorm_quant: operands must be aligned to 4 elements");
-    if (rows <= kRmsqMaxRows && cols <= kRmsqMaxCols && env_int("FT_RMSQ_SPLIT", 0) == 0) {
+    if (rows <= kRmsqMaxRows && cols <= kRmsqMaxCols && tune(Tune::RmsqSplit, 0) == 0) {
         rmsq_small<T><<<1, (unsigned)(rows * kFNT), 0, s>>>(x, r, w, q, scale_out, rows,
                                                              cols, eps);
         launch_check("rmsnorm_quant small kernel launch");

@@ -500,7 +500,7 @@ void prefill_run(const T* q, const T* k, const T* v, T* out, int batch, int hq, 
     const float scale = 1.0f / sqrtf((float)dim);
     if constexpr (!std::is_same<T, float>::value) {
         const bool aligned = ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) % 16 == 0;
-        if ((dim == 64 || dim == 128) && aligned && !env_int("FT_PREFILL_FORCE_GENERIC", 0)) {
+        if ((dim == 64 || dim == 128) && aligned && !tune(Tune::PrefillForceGeneric, 0)) {
             const long long nqt = (seq + kPQ - 1) / kPQ;
             const long long grid = (long long)batch * hq * nqt;
             if (grid > 0x7fffffffLL) inval("attention prefill problem too large for one launch");

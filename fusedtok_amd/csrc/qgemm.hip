@@ -30,8 +30,6 @@
 //                  tiles, 8 waves (two per SIMD, 64x128 each, on
 //                  v_mfma_i32_16x16x64_i8), 128-byte K slabs DMA'd
 //                  global->LDS into two stages.
-//   qgemm_big_w8   the same on v_mfma_i32_32x32x32_i8.
-//   qgemm_big_k128 the same with 4 waves of 128x128 (one per SIMD).
 //   qgemm_big_dma  M, N >= 256, K % 64 == 0: 256x256 tiles on
 //                  v_mfma_i32_32x32x32_i8 fed by a 5-stage global->LDS DMA
 //                  ring; LDS-staged, coalesced epilogue.
@@ -1444,9 +1442,9 @@ void qgemm_big_dma(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
 }
 
 // ---------------------------------------------------------------------------
-// big, DMA-fed, 128-byte slabs (K % 128 == 0): the tiles, order and operand
-// layout of qgemm_big_dma, with each slab covering 128 bytes of K, a whole
-// cache line per row:
+// big, DMA-fed, 128-byte slabs (K % 128 == 0; qgemm_big_w16): the tiles,
+// order and operand layout of qgemm_big_dma, with each slab covering 128
+// bytes of K, a whole cache line per row:
 //  - a DMA instruction moves 8 rows x 128 B (8 full lines) instead of
 //    16 rows x 64 B (16 half lines); streaming this kernel's operand traffic
 //    alone (7.5 GB for 4096 x 8192 x 28672) runs at 18.5 TB/s L2 -> LDS this
@@ -1468,684 +1466,27 @@ void qgemm_big_dma(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
 constexpr int kK2 = 128;                     // K bytes per slab
 constexpr int kSlab2 = 2 * kBigT * kK2;      // A + B, 64 KB
 constexpr int kLoads2 = 16;                  // DMA instructions per thread per slab
-constexpr int kK2Stg = 16 * kEpiPitch;       // per-wave output staging, 16 rows
-constexpr int kK2Spare = 2 * kSlab2;         // LDS offset of the staging
-constexpr int kK2Scl = kK2Spare + 4 * kK2Stg;  // LDS offset of the 256 column scales
-constexpr int kK2Lds = kK2Scl + 4 * kBigT;   // 149,504 bytes
 
-// Epilogue of qgemm_big_k128 for the wave's 128 x 128 sub-tile at (row0,
-// col0). acc[i][j] holds C^T (lane (r32, h), register t -> row i*32 + r32,
-// column j*32 + 8(t/4) + 4h + t%4). scw: the sub-tile's 128 column scales in
-// LDS, or null (read sb_vec from global). 2-byte outputs go through this
-// wave's 16-row staging stg in 8 passes and leave as 16-byte row stores;
-// 4-byte outputs are stored from registers.
-template <int OUT>
-__device__ __forceinline__ void k128_epilogue(i32x16 (&acc)[4][4], i8* stg, const float* scw,
-                                              const Epi& e, int m, int n, int row0,
-                                              int col0, int lane, int r32, int h) {
-    const float sa = epi_sa(e);
-    auto scales4 = [&](int jc) {  // f32(sa * sb[col0 + jc .. + 3]), clamped at n
-        float4 s4;
-        if (scw) {
-            const float4 v = *reinterpret_cast<const float4*>(scw + jc);
-            s4 = make_float4(sa * v.x, sa * v.y, sa * v.z, sa * v.w);
-        } else if (e.sb_vec) {
-            const int col = col0 + jc;
-            s4.x = sa * e.sb_vec[min(col, n - 1)];
-            s4.y = sa * e.sb_vec[min(col + 1, n - 1)];
-            s4.z = sa * e.sb_vec[min(col + 2, n - 1)];
-            s4.w = sa * e.sb_vec[min(col + 3, n - 1)];
-        } else {
-            const float sc = sa * e.sb;
-            s4 = make_float4(sc, sc, sc, sc);
-        }
-        return s4;
-    };
-    if constexpr (OUT == kOutBF16 || OUT == kOutF16) {
-        typedef typename std::conditional<OUT == kOutBF16, bf16, f16>::type OT;
-        typedef OT ot4 __attribute__((ext_vector_type(4)));
-        OT* const y = static_cast<OT*>(e.y);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            ot4 v[4][4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float4 s4 = scales4(j * 32 + 8 * g + 4 * h);
-                    v[j][g][0] = (OT)epi_val(acc[i][j][4 * g + 0], s4.x);
-                    v[j][g][1] = (OT)epi_val(acc[i][j][4 * g + 1], s4.y);
-                    v[j][g][2] = (OT)epi_val(acc[i][j][4 * g + 2], s4.z);
-                    v[j][g][3] = (OT)epi_val(acc[i][j][4 * g + 3], s4.w);
-                }
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                if ((r32 >> 4) == p) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-#pragma unroll
-                        for (int g = 0; g < 4; ++g)
-                            *reinterpret_cast<ot4*>(stg + (r32 & 15) * kEpiPitch +
-                                                    (j * 32 + 8 * g + 4 * h) * 2) = v[j][g];
-                }
-                // 16 rows x 256 bytes back out: 16 lanes per row, 16 bytes each
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const int lr = rr * 4 + (lane >> 4);
-                    const int row = row0 + i * 32 + 16 * p + lr;
-                    const int cb = (lane & 15) * 8;  // first of 8 columns
-                    const i8* src = stg + lr * kEpiPitch + cb * 2;
-                    if (row >= m) continue;
-                    OT* dst = y + (size_t)row * n + col0 + cb;
-                    if ((n & 7) == 0) {
-                        if (col0 + cb < n)
-                            *reinterpret_cast<i32x4*>(dst) = *reinterpret_cast<const i32x4*>(src);
-                    } else {
-#pragma unroll
-                        for (int c = 0; c < 8; ++c)
-                            if (col0 + cb + c < n) dst[c] = reinterpret_cast<const OT*>(src)[c];
-                    }
-                }
-            }
-        }
-    } else {  // 4-byte outputs: 16-byte stores of 4 consecutive columns
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int col = col0 + j * 32 + 8 * g + 4 * h;
-                float4 s4;
-                if constexpr (OUT == kOutF32) s4 = scales4(j * 32 + 8 * g + 4 * h);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int row = row0 + i * 32 + r32;
-                    if (row >= m || col >= n) continue;
-                    i32x4 o;
-                    if constexpr (OUT == kOutI32) {
-                        o = i32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1],
-                                  acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-                    } else {
-                        o = i32x4{__float_as_int(epi_val(acc[i][j][4 * g], s4.x)),
-                                  __float_as_int(epi_val(acc[i][j][4 * g + 1], s4.y)),
-                                  __float_as_int(epi_val(acc[i][j][4 * g + 2], s4.z)),
-                                  __float_as_int(epi_val(acc[i][j][4 * g + 3], s4.w))};
-                    }
-                    int* dst = static_cast<int*>(e.y) + (size_t)row * n + col;
-                    if ((n & 3) == 0) {
-                        *reinterpret_cast<i32x4*>(dst) = o;
-                    } else {
-#pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            if (col + c < n) dst[c] = o[c];
-                    }
-                }
-            }
-    }
-}
-
-// scales_dma: the host checked that sb_vec is 16-byte aligned and n % 4 == 0,
-// so lane l's DMA of sb_vec[bn + 4 l .. + 3] (clamped to the last 4) is one
-// aligned 16-byte piece.
-template <int OUT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void qgemm_big_k128(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
-                    int m, int n, int k, int scales_dma) {
-    __shared__ __attribute__((aligned(16))) i8 lds[kK2Lds];
-
-    const int tm = (m + kBigT - 1) / kBigT, tn = (n + kBigT - 1) / kBigT;
-    const int ntiles = tm * tn;
-    // tile t -> (bm, bn) in the XCD-aware order (tile t runs on XCD t % 8
-    // because the grid is a multiple of 8)
-    auto tile_origin = [&](int t, int& bm, int& bn) {
-        int pid = t;
-        if (ntiles % 8 == 0) pid = (pid % 8) * (ntiles / 8) + pid / 8;
-        const int band = pid / (kBigBand * tn);
-        const int first_m = band * kBigBand;
-        const int band_m = min(tm - first_m, kBigBand);
-        const int in_band = pid - band * kBigBand * tn;
-        bm = (first_m + in_band % band_m) * kBigT;
-        bn = (in_band / band_m) * kBigT;
-    };
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
-    const int r32 = lane & 31, h = lane >> 5;
-    const int nk = k / kK2;
-
-    // DMA: instruction j (0..7) of this wave fills tile rows 32 j + 8 wave +
-    // lane / 8 (1 KB of LDS at row (32 j + 8 wave) * 128); lane's LDS chunk
-    // position is lane % 8, so it fetches logical chunk (lane % 8) ^ swz,
-    // where swz = (row >> 1) & 7 = (4 wave + lane / 16) & 7 for every j.
-    // Rows past M / N read a clamped (real) row; they only feed outputs that
-    // are never stored.
-    const int c16 = 16 * ((lane & 7) ^ ((4 * wave + (lane >> 4)) & 7));
-    unsigned aoff[8], boff[8];
-    const i8* abase;
-    const i8* bbase;
-    auto set_tile = [&](int bm, int bn) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int row = 32 * j + 8 * wave + (lane >> 3);
-            aoff[j] = (unsigned)(min(row, m - 1 - bm) * k + c16);
-            boff[j] = (unsigned)(min(row, n - 1 - bn) * k + c16);
-        }
-        abase = a + (size_t)bm * k;
-        bbase = b + (size_t)bn * k;
-    };
-    // instruction x (0..15) of a slab: A rows for even x, B rows for odd x
-    auto dma1 = [&](int kt, int st, int x) {
-        const int j = x >> 1;
-        i8* dst = lds + st * kSlab2 + (x & 1) * (kBigT * kK2) + (32 * j + 8 * wave) * kK2;
-        if (x & 1)
-            __builtin_amdgcn_global_load_lds(bbase + (size_t)kt * kK2 + boff[j],
-                                             (lds_void_p)dst, 16, 0, 0);
-        else
-            __builtin_amdgcn_global_load_lds(abase + (size_t)kt * kK2 + aoff[j],
-                                             (lds_void_p)dst, 16, 0, 0);
-    };
-    // slabs 0 and 1 of the tile at (bm, bn), with offsets computed here
-    // (not kept: they would stay live through the previous tile's epilogue)
-    auto first_slabs = [&](int bm, int bn) {
-        const int nsl = nk > 1 ? 2 : 1;
-        for (int sl = 0; sl < nsl; ++sl) {
-            const i8* ab = a + (size_t)bm * k + (size_t)sl * kK2;
-            const i8* bb = b + (size_t)bn * k + (size_t)sl * kK2;
-#pragma unroll
-            for (int x = 0; x < kLoads2; ++x) {
-                const int j = x >> 1;
-                const int row = 32 * j + 8 * wave + (lane >> 3);
-                i8* dst = lds + sl * kSlab2 + (x & 1) * (kBigT * kK2) + (32 * j + 8 * wave) * kK2;
-                const unsigned off = (x & 1) ? (unsigned)(min(row, n - 1 - bn) * k + c16)
-                                             : (unsigned)(min(row, m - 1 - bm) * k + c16);
-                __builtin_amdgcn_global_load_lds(((x & 1) ? bb : ab) + off, (lds_void_p)dst,
-                                                 16, 0, 0);
-            }
-        }
-    };
-
-    // fragment rows: A block i = tile row wm*128 + 32 i + r32, B block j
-    // likewise; offset of chunk c = (row << 7) | 16 (c ^ swz(row)); for
-    // sub-step s the lane's chunk is 2 s + h, so the offset is
-    // base ^ (32 s) with base = (row << 7) | 16 (h ^ swz(row)).
-    unsigned arow[4], brow[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int ra = wm * 128 + 32 * i + r32, rb = wn * 128 + 32 * i + r32;
-        arow[i] = (unsigned)((ra << 7) | (16 * (h ^ ((ra >> 1) & 7))));
-        brow[i] = (unsigned)((rb << 7) | (16 * (h ^ ((rb >> 1) & 7))));
-    }
-    const unsigned lds0 = lds_addr(lds);
-    constexpr int order[8] = {0, 4, 5, 6, 7, 1, 2, 3};  // first-use order
-    auto frag_addr = [&](int st, int s, int x) {
-        const int fi = order[x];
-        const unsigned base = lds0 + st * kSlab2;
-        return fi < 4 ? base + (arow[fi] ^ (32u * s))
-                      : base + kBigT * kK2 + (brow[fi - 4] ^ (32u * s));
-    };
-    auto read_frags = [&](int st, int s, i32x4 (&f)[8]) {
-#pragma unroll
-        for (int x = 0; x < 8; ++x) f[order[x]] = lds_read16(frag_addr(st, s, x));
-    };
-
-    i32x16 acc[4][4];  // acc[i][j] = C^T block (n block j, m block i)
-#define FT_LGKM_WAIT(N, ...)                                                    \
-    do {                                                                       \
-        __builtin_amdgcn_sched_barrier(0);                                     \
-        asm volatile("s_waitcnt lgkmcnt(" #N ")" : __VA_ARGS__);               \
-        __builtin_amdgcn_sched_barrier(0);                                     \
-    } while (0)
-    // 16 MFMAs on f (read in first-use order by the previous call and
-    // waited for piecewise: before MFMA q, floor(q/2) reads of this call
-    // are in flight too), the 8 reads of nf = (rst, rs) after the odd
-    // MFMAs, and with a DMA tag the 16 DMA instructions of slab dkt into
-    // stage dst, one after every MFMA.
-    auto step = [&](i32x4 (&f)[8], bool piecewise, int rst, int rs, i32x4 (&nf)[8],
-                    auto dma, int dkt, int dst) {
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int i = q >> 2, j = q & 3;
-            if (piecewise) {
-                if (q == 0) FT_LGKM_WAIT(6, "+v"(f[0]), "+v"(f[4]));
-                if (q == 1) FT_LGKM_WAIT(5, "+v"(f[5]));
-                if (q == 2) FT_LGKM_WAIT(5, "+v"(f[6]));
-                if (q == 3) FT_LGKM_WAIT(4, "+v"(f[7]));
-                if (q == 4) FT_LGKM_WAIT(4, "+v"(f[1]));
-                if (q == 8) FT_LGKM_WAIT(5, "+v"(f[2]));
-                if (q == 12) FT_LGKM_WAIT(6, "+v"(f[3]));
-            }
-            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[4 + j], f[i], acc[i][j], 0, 0, 0);
-            if constexpr (decltype(dma)::value) {
-                __builtin_amdgcn_sched_barrier(0);
-                dma1(dkt, dst, q);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            if (q & 1) {
-                __builtin_amdgcn_sched_barrier(0);
-                nf[order[q >> 1]] = lds_read16(frag_addr(rst, rs, q >> 1));
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-    };
-#undef FT_LGKM_WAIT
-
-    int t = blockIdx.x;
-    if (t < ntiles) {
-        int bm0, bn0;
-        tile_origin(t, bm0, bn0);
-        first_slabs(bm0, bn0);
-    }
-    for (; t < ntiles; t += gridDim.x) {
-        int bm, bn;
-        tile_origin(t, bm, bn);
-        set_tile(bm, bn);
-        // slabs 0 and 1 of this tile were issued (before the previous tile's
-        // epilogue, or just above); wait for them and for that epilogue's
-        // stores, then every wave's DMAs are visible after the barrier
-        wait_vmcnt<0>();
-        __builtin_amdgcn_s_barrier();
-        if (scales_dma && wave == 0) {
-            const int c = min(bn + 4 * lane, n - 4);
-            __builtin_amdgcn_global_load_lds(e.sb_vec + c, (lds_void_p)(lds + kK2Scl), 16, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int q = 0; q < 16; ++q) acc[i][j][q] = 0;
-
-        // Per slab kt (stage st = kt & 1), with F0 = (kt, 0) read:
-        //   sub-steps 0, 1, 2: MFMAs on (kt, s) while (kt, s + 1) is read;
-        //   wait for (kt, 3) and for slab kt+1's DMA (and the scales); barrier:
-        //   every wave is past its reads of stage st, and slab kt+1 is
-        //   visible;
-        //   sub-step 3: MFMAs on (kt, 3) while (kt+1, 0) is read from stage
-        //   st ^ 1 and stage st is refilled with slab kt + 2.
-        // (After the last slab, F0 reads a stale stage: in bounds, unused.)
-        i32x4 f0[8], f1[8];
-        read_frags(0, 0, f0);
-        auto slab = [&](int kt, auto dma) {
-            const int st = kt & 1;
-            step(f0, true, st, 1, f1, std::false_type{}, 0, 0);
-            step(f1, true, st, 2, f0, std::false_type{}, 0, 0);
-            step(f0, true, st, 3, f1, std::false_type{}, 0, 0);
-            lds_wait(f1);
-            wait_vmcnt<0>();  // slab kt+1 (the only DMA in flight) and the scales
-            __builtin_amdgcn_s_barrier();
-            step(f1, false, st ^ 1, 0, f0, dma, kt + 2, st);
-        };
-        int kt = 0;
-        for (; kt + 2 < nk; ++kt) slab(kt, std::true_type{});
-        for (; kt < nk; ++kt) slab(kt, std::false_type{});
-        lds_wait(f0);  // the last (unused) reads land before f0's registers are reused
-        wait_vmcnt<0>();  // the scales of a one-slab tile
-        // every wave is done with both stages: the next tile's first slabs
-        // may land while this tile's epilogue runs
-        __builtin_amdgcn_s_barrier();
-        const int row0 = bm + wm * 128, col0 = bn + wn * 128;
-        const int tn_ = t + gridDim.x;
-        if (tn_ < ntiles) {
-            int nbm, nbn;
-            tile_origin(tn_, nbm, nbn);
-            first_slabs(nbm, nbn);
-        }
-        k128_epilogue<OUT>(acc, lds + kK2Spare + wave * kK2Stg,
-                           scales_dma ? reinterpret_cast<const float*>(lds + kK2Scl) + wn * 128
-                                      : nullptr,
-                           e, m, n, row0, col0, lane, r32, h);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// big, 8 waves (K % 128 == 0): qgemm_big_k128's tiles, tile order, 128-byte
-// DMA slabs, LDS layout and two-stage schedule, with 512 threads = two waves
-// per SIMD. Wave w = 4 g + v owns the 64 x 128 sub-tile at rows 128 g +
-// 64 (v >> 1), columns 128 (v & 1): 2 x 4 blocks of v_mfma_i32_32x32x32_i8,
-// 128 accumulators per lane. Per 32-byte K sub-step a wave reads 6 fragments
-// (A0, B0..B3, A1 in first-use order) for 8 MFMAs. With two waves per SIMD,
-// one wave's MFMAs issue while the other waits on a fragment read, a DMA
-// issue slot or the slab barrier; and the epilogue of one wave overlaps the
-// other's. Output staging is per wave, 16 rows x 64 columns per pass (2-byte
-// outputs), so the two stages, the staging and the scales fit in 147 KB.
-// ---------------------------------------------------------------------------
+// 8 waves per workgroup, two per SIMD: one wave's MFMAs issue while the
+// other waits on a fragment read, a DMA issue slot or the slab barrier, and
+// one wave's epilogue overlaps the other's MFMAs (4 waves of 128 x 128, one
+// per SIMD, kept the matrix cores busy 60% of the cycles on 4096 x 8192 x
+// 28672 against 70% with 8). Output staging is per wave, 16 rows x 64
+// columns per pass (2-byte outputs), so the two stages, the staging and the
+// scales fit in 147 KB.
 constexpr int kW8Pitch = 144;                    // staging row pitch: 128 B + 16
 constexpr int kW8Stg = 16 * kW8Pitch;            // per-wave staging, 16 rows
 constexpr int kW8Spare = 2 * kSlab2;             // LDS offset of the staging
 constexpr int kW8Scl = kW8Spare + 8 * kW8Stg;    // LDS offset of the 256 column scales
 constexpr int kW8Lds = kW8Scl + 4 * kBigT;       // 150,528 bytes
 
-// Epilogue of qgemm_big_w8 for the wave's 64 x 128 sub-tile at (row0, col0).
-// acc[i][j] holds C^T (lane (r32, h), register t -> row i*32 + r32, column
-// j*32 + 8(t/4) + 4h + t%4). scw: the sub-tile's 128 column scales in LDS, or
-// null. 2-byte outputs go through this wave's staging stg, 16 rows x 64
-// columns per pass, and leave as 128-byte row pieces (8 lanes x 16 bytes).
-template <int OUT>
-__device__ __forceinline__ void w8_epilogue(i32x16 (&acc)[2][4], i8* stg, const float* scw,
-                                            const Epi& e, int m, int n, int row0,
-                                            int col0, int lane, int r32, int h) {
-    const float sa = epi_sa(e);
-    auto scales4 = [&](int jc) {  // f32(sa * sb[col0 + jc .. + 3]), clamped at n
-        float4 s4;
-        if (scw) {
-            const float4 v = *reinterpret_cast<const float4*>(scw + jc);
-            s4 = make_float4(sa * v.x, sa * v.y, sa * v.z, sa * v.w);
-        } else if (e.sb_vec) {
-            const int col = col0 + jc;
-            s4.x = sa * e.sb_vec[min(col, n - 1)];
-            s4.y = sa * e.sb_vec[min(col + 1, n - 1)];
-            s4.z = sa * e.sb_vec[min(col + 2, n - 1)];
-            s4.w = sa * e.sb_vec[min(col + 3, n - 1)];
-        } else {
-            const float sc = sa * e.sb;
-            s4 = make_float4(sc, sc, sc, sc);
-        }
-        return s4;
-    };
-    if constexpr (OUT == kOutBF16 || OUT == kOutF16) {
-        typedef typename std::conditional<OUT == kOutBF16, bf16, f16>::type OT;
-        typedef OT ot4 __attribute__((ext_vector_type(4)));
-        OT* const y = static_cast<OT*>(e.y);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-#pragma unroll
-            for (int jp = 0; jp < 2; ++jp) {
-                ot4 v[2][4];
-#pragma unroll
-                for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int j = 2 * jp + jj;
-                        const float4 s4 = scales4(j * 32 + 8 * g + 4 * h);
-                        v[jj][g][0] = (OT)epi_val(acc[i][j][4 * g + 0], s4.x);
-                        v[jj][g][1] = (OT)epi_val(acc[i][j][4 * g + 1], s4.y);
-                        v[jj][g][2] = (OT)epi_val(acc[i][j][4 * g + 2], s4.z);
-                        v[jj][g][3] = (OT)epi_val(acc[i][j][4 * g + 3], s4.w);
-                    }
-#pragma unroll
-                for (int p = 0; p < 2; ++p) {
-                    if ((r32 >> 4) == p) {
-#pragma unroll
-                        for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-                            for (int g = 0; g < 4; ++g)
-                                *reinterpret_cast<ot4*>(stg + (r32 & 15) * kW8Pitch +
-                                                        (jj * 32 + 8 * g + 4 * h) * 2) = v[jj][g];
-                    }
-                    // 16 rows x 128 bytes back out: 8 lanes per row, 16 bytes each
-#pragma unroll
-                    for (int rr = 0; rr < 2; ++rr) {
-                        const int lr = rr * 8 + (lane >> 3);
-                        const int row = row0 + i * 32 + 16 * p + lr;
-                        const int cb = (lane & 7) * 8;  // first of 8 columns
-                        const int col = col0 + jp * 64 + cb;
-                        const i8* src = stg + lr * kW8Pitch + cb * 2;
-                        if (row >= m) continue;
-                        OT* dst = y + (size_t)row * n + col;
-                        if ((n & 7) == 0) {
-                            if (col < n)
-                                *reinterpret_cast<i32x4*>(dst) = *reinterpret_cast<const i32x4*>(src);
-                        } else {
-#pragma unroll
-                            for (int c = 0; c < 8; ++c)
-                                if (col + c < n) dst[c] = reinterpret_cast<const OT*>(src)[c];
-                        }
-                    }
-                }
-            }
-        }
-    } else {  // 4-byte outputs: 16-byte stores of 4 consecutive columns
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int col = col0 + j * 32 + 8 * g + 4 * h;
-                float4 s4;
-                if constexpr (OUT == kOutF32) s4 = scales4(j * 32 + 8 * g + 4 * h);
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const int row = row0 + i * 32 + r32;
-                    if (row >= m || col >= n) continue;
-                    i32x4 o;
-                    if constexpr (OUT == kOutI32) {
-                        o = i32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1],
-                                  acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-                    } else {
-                        o = i32x4{__float_as_int(epi_val(acc[i][j][4 * g], s4.x)),
-                                  __float_as_int(epi_val(acc[i][j][4 * g + 1], s4.y)),
-                                  __float_as_int(epi_val(acc[i][j][4 * g + 2], s4.z)),
-                                  __float_as_int(epi_val(acc[i][j][4 * g + 3], s4.w))};
-                    }
-                    int* dst = static_cast<int*>(e.y) + (size_t)row * n + col;
-                    if ((n & 3) == 0) {
-                        *reinterpret_cast<i32x4*>(dst) = o;
-                    } else {
-#pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            if (col + c < n) dst[c] = o[c];
-                    }
-                }
-            }
-    }
-}
-
-template <int OUT>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void qgemm_big_w8(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
-                  int m, int n, int k, int scales_dma) {
-    __shared__ __attribute__((aligned(16))) i8 lds[kW8Lds];
-
-    const int tm = (m + kBigT - 1) / kBigT, tn = (n + kBigT - 1) / kBigT;
-    const int ntiles = tm * tn;
-    auto tile_origin = [&](int t, int& bm, int& bn) {  // qgemm_big_k128's order
-        int pid = t;
-        if (ntiles % 8 == 0) pid = (pid % 8) * (ntiles / 8) + pid / 8;
-        const int band = pid / (kBigBand * tn);
-        const int first_m = band * kBigBand;
-        const int band_m = min(tm - first_m, kBigBand);
-        const int in_band = pid - band * kBigBand * tn;
-        bm = (first_m + in_band % band_m) * kBigT;
-        bn = (in_band / band_m) * kBigT;
-    };
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..7
-    const int wr = 128 * (wave >> 2) + 64 * ((wave & 3) >> 1);  // sub-tile row
-    const int wc = 128 * (wave & 1);                            // sub-tile column
-    const int r32 = lane & 31, h = lane >> 5;
-    const int nk = k / kK2;
-
-    // DMA: instruction j (0..3) of this wave fills tile rows 64 j + 8 wave +
-    // lane / 8 (1 KB of LDS at row (64 j + 8 wave) * 128) of A, and the same
-    // rows of B; the lane's LDS chunk position is lane % 8, holding logical
-    // chunk (lane % 8) ^ swz with swz = (row >> 1) & 7 = (4 wave + lane / 16)
-    // & 7 for every j. Rows past M / N read a clamped (real) row.
-    const int c16 = 16 * ((lane & 7) ^ ((4 * wave + (lane >> 4)) & 7));
-    unsigned aoff[4], boff[4];
-    const i8* abase;
-    const i8* bbase;
-    auto set_tile = [&](int bm, int bn) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = 64 * j + 8 * wave + (lane >> 3);
-            aoff[j] = (unsigned)(min(row, m - 1 - bm) * k + c16);
-            boff[j] = (unsigned)(min(row, n - 1 - bn) * k + c16);
-        }
-        abase = a + (size_t)bm * k;
-        bbase = b + (size_t)bn * k;
-    };
-    // instruction x (0..7) of a slab: A rows for even x, B rows for odd x
-    auto dma1 = [&](int kt, int st, int x) {
-        const int j = x >> 1;
-        i8* dst = lds + st * kSlab2 + (x & 1) * (kBigT * kK2) + (64 * j + 8 * wave) * kK2;
-        if (x & 1)
-            __builtin_amdgcn_global_load_lds(bbase + (size_t)kt * kK2 + boff[j],
-                                             (lds_void_p)dst, 16, 0, 0);
-        else
-            __builtin_amdgcn_global_load_lds(abase + (size_t)kt * kK2 + aoff[j],
-                                             (lds_void_p)dst, 16, 0, 0);
-    };
-    auto first_slabs = [&](int bm, int bn) {
-        const int nsl = nk > 1 ? 2 : 1;
-        for (int sl = 0; sl < nsl; ++sl) {
-            const i8* ab = a + (size_t)bm * k + (size_t)sl * kK2;
-            const i8* bb = b + (size_t)bn * k + (size_t)sl * kK2;
-#pragma unroll
-            for (int x = 0; x < 8; ++x) {
-                const int j = x >> 1;
-                const int row = 64 * j + 8 * wave + (lane >> 3);
-                i8* dst = lds + sl * kSlab2 + (x & 1) * (kBigT * kK2) + (64 * j + 8 * wave) * kK2;
-                const unsigned off = (x & 1) ? (unsigned)(min(row, n - 1 - bn) * k + c16)
-                                             : (unsigned)(min(row, m - 1 - bm) * k + c16);
-                __builtin_amdgcn_global_load_lds(((x & 1) ? bb : ab) + off, (lds_void_p)dst,
-                                                 16, 0, 0);
-            }
-        }
-    };
-
-    // fragment f[0..1] = A blocks (rows wr + 32 i + r32), f[2..5] = B blocks
-    // (rows wc + 32 j + r32); offset of chunk c = (row << 7) | 16 (c ^
-    // swz(row)); sub-step s reads chunk 2 s + h: base ^ (32 s).
-    unsigned arow[2], brow[4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int ra = wr + 32 * i + r32;
-        arow[i] = (unsigned)((ra << 7) | (16 * (h ^ ((ra >> 1) & 7))));
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int rb = wc + 32 * j + r32;
-        brow[j] = (unsigned)((rb << 7) | (16 * (h ^ ((rb >> 1) & 7))));
-    }
-    const unsigned lds0 = lds_addr(lds);
-    constexpr int order[6] = {0, 2, 3, 4, 5, 1};  // first-use order: A0 B0 B1 B2 B3 A1
-    auto frag_addr = [&](int st, int s, int x) {
-        const int fi = order[x];
-        const unsigned base = lds0 + st * kSlab2;
-        return fi < 2 ? base + (arow[fi] ^ (32u * s))
-                      : base + kBigT * kK2 + (brow[fi - 2] ^ (32u * s));
-    };
-    auto read_frags = [&](int st, int s, i32x4 (&f)[6]) {
-#pragma unroll
-        for (int x = 0; x < 6; ++x) f[order[x]] = lds_read16(frag_addr(st, s, x));
-    };
-    auto frags_wait = [&](i32x4 (&f)[6]) {
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]));
-    };
-
-    i32x16 acc[2][4];  // acc[i][j] = C^T block (n block j, m block i)
-#define FT_LGKM_WAIT(N, ...)                                                    \
-    do {                                                                       \
-        __builtin_amdgcn_sched_barrier(0);                                     \
-        asm volatile("s_waitcnt lgkmcnt(" #N ")" : __VA_ARGS__);               \
-        __builtin_amdgcn_sched_barrier(0);                                     \
-    } while (0)
-    // 8 MFMAs on f (read in first-use order by the previous call); read r of
-    // nf goes out after MFMA r (r < 6), so before MFMA q, q reads of this
-    // call are in flight and "read r of f landed" is lgkmcnt(5 - r + q):
-    // lgkmcnt(4) before each of MFMAs 0..4 (they need reads 1, 2, 3, 4, 5).
-    // With a DMA tag, the 8 DMA instructions of slab dkt into stage dst go
-    // out one after every MFMA.
-    auto step = [&](i32x4 (&f)[6], bool piecewise, int rst, int rs, i32x4 (&nf)[6],
-                    auto dma, int dkt, int dst) {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int i = q >> 2, j = q & 3;
-            if (piecewise) {
-                if (q == 0) FT_LGKM_WAIT(4, "+v"(f[0]), "+v"(f[2]));
-                if (q == 1) FT_LGKM_WAIT(4, "+v"(f[3]));
-                if (q == 2) FT_LGKM_WAIT(4, "+v"(f[4]));
-                if (q == 3) FT_LGKM_WAIT(4, "+v"(f[5]));
-                if (q == 4) FT_LGKM_WAIT(4, "+v"(f[1]));
-            }
-            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[2 + j], f[i], acc[i][j], 0, 0, 0);
-            if constexpr (decltype(dma)::value) {
-                __builtin_amdgcn_sched_barrier(0);
-                dma1(dkt, dst, q);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            if (q < 6) {
-                __builtin_amdgcn_sched_barrier(0);
-                nf[order[q]] = lds_read16(frag_addr(rst, rs, q));
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-    };
-#undef FT_LGKM_WAIT
-
-    int t = blockIdx.x;
-    if (t < ntiles) {
-        int bm0, bn0;
-        tile_origin(t, bm0, bn0);
-        first_slabs(bm0, bn0);
-    }
-    for (; t < ntiles; t += gridDim.x) {
-        int bm, bn;
-        tile_origin(t, bm, bn);
-        set_tile(bm, bn);
-        // slabs 0 and 1 of this tile are in flight (issued before the
-        // previous tile's epilogue, or just above): wait for them and for
-        // that epilogue's stores; after the barrier every wave's DMAs are
-        // visible
-        wait_vmcnt<0>();
-        __builtin_amdgcn_s_barrier();
-        if (scales_dma && wave == 0) {
-            const int c = min(bn + 4 * lane, n - 4);
-            __builtin_amdgcn_global_load_lds(e.sb_vec + c, (lds_void_p)(lds + kW8Scl), 16, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int q = 0; q < 16; ++q) acc[i][j][q] = 0;
-
-        // Per slab kt (stage st = kt & 1), with F0 = (kt, 0) read: sub-steps
-        // 0..2 multiply (kt, s) while (kt, s + 1) is read; wait for (kt, 3)
-        // and slab kt+1's DMA; barrier (every wave is past its reads of
-        // stage st; slab kt+1 is visible); sub-step 3 multiplies (kt, 3)
-        // while (kt+1, 0) is read from stage st ^ 1 and stage st is refilled
-        // with slab kt + 2. After the last slab, F0 reads a stale stage: in
-        // bounds, unused.
-        i32x4 f0[6], f1[6];
-        read_frags(0, 0, f0);
-        auto slab = [&](int kt, auto dma) {
-            const int st = kt & 1;
-            step(f0, true, st, 1, f1, std::false_type{}, 0, 0);
-            step(f1, true, st, 2, f0, std::false_type{}, 0, 0);
-            step(f0, true, st, 3, f1, std::false_type{}, 0, 0);
-            frags_wait(f1);
-            wait_vmcnt<0>();  // slab kt+1 (the only DMA in flight) and the scales
-            __builtin_amdgcn_s_barrier();
-            step(f1, false, st ^ 1, 0, f0, dma, kt + 2, st);
-        };
-        int kt = 0;
-        for (; kt + 2 < nk; ++kt) slab(kt, std::true_type{});
-        for (; kt < nk; ++kt) slab(kt, std::false_type{});
-        frags_wait(f0);   // the last (unused) reads land before f0's registers are reused
-        wait_vmcnt<0>();  // the scales of a one-slab tile
-        __builtin_amdgcn_s_barrier();
-        const int tn_ = t + gridDim.x;
-        if (tn_ < ntiles) {
-            int nbm, nbn;
-            tile_origin(tn_, nbm, nbn);
-            first_slabs(nbm, nbn);
-        }
-        w8_epilogue<OUT>(acc, lds + kW8Spare + wave * kW8Stg,
-                         scales_dma ? reinterpret_cast<const float*>(lds + kW8Scl) + wc : nullptr,
-                         e, m, n, bm + wr, bn + wc, lane, r32, h);
-    }
-}
-
 // ---------------------------------------------------------------------------
-// big, 8 waves, 16x16x64 MFMAs: qgemm_big_w8's tiles, tile order, DMA slabs,
-// LDS layout and barriers, with each wave's 64 x 128 sub-tile computed as
-// 4 x 8 blocks of v_mfma_i32_16x16x64_i8 (128 accumulators per lane, as
-// before). The fragment bytes per MAC are the same as with 32x32x32; what
-// changes is the instruction: under the board power limit of random int8
+// big, 8 waves, 16x16x64 MFMAs (qgemm_big_w16): 256 x 256 tiles in the
+// XCD-aware order, 128-byte DMA slabs in two stages. Wave w = 4 g + v owns
+// the 64 x 128 sub-tile at rows 128 g + 64 (v >> 1), columns 128 (v & 1),
+// computed as 4 x 8 blocks of v_mfma_i32_16x16x64_i8 (128 accumulators per
+// lane). The fragment bytes per MAC equal those of 32x32x32 blocks; what
+// differs is the instruction: under the board power limit of random int8
 // operands the 16x16x64 form sustains more operations per second (all CUs,
 // operands cycling through 8 random register sets: 3.24 vs 2.91 POP/s).
 // Lane (r16, q4) = (lane % 16, lane / 16) holds 16 bytes (chunk 4 s + q4 of
@@ -2184,8 +1525,10 @@ constexpr int kW16Wait[32] = {10, 9, 8, 7, 7, -1, -1, -1, 10, -1, -1, -1, 10, -1
                               10, -1, -1, -1, 10, -1, -1, -1, 10, -1, -1, -1, 10, -1, -1, -1};
 
 // Epilogue of qgemm_big_w16: the wave's 64 x 128 sub-tile at (row0, col0),
-// acc[i][j] as above; scw and the staging as in w8_epilogue (16 rows x 64
-// columns per pass, 128-byte row pieces out).
+// acc[i][j] as above. scw: the sub-tile's 128 column scales in LDS, or null
+// (read sb_vec from global). 2-byte outputs go through the wave's staging
+// stg, 16 rows x 64 columns per pass, and leave as 128-byte row pieces (8
+// lanes x 16 bytes); 4-byte outputs are stored from registers.
 template <int OUT>
 __device__ __forceinline__ void w16_epilogue(i32x4 (&acc)[4][8], i8* stg, const float* scw,
                                              const Epi& e, int m, int n, int row0,
@@ -2301,7 +1644,9 @@ void qgemm_big_w16(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
 
     const int tm = (m + kBigT - 1) / kBigT, tn = (n + kBigT - 1) / kBigT;
     const int ntiles = tm * tn;
-    // qgemm_big_k128's order with `band` tile rows per band
+    // tile t -> (bm, bn): tile t runs on XCD t % 8 (the grid is a multiple
+    // of 8), and the tiles one XCD holds at once form a block of `band` tile
+    // rows, so they share A and B panels in that XCD's L2
     auto tile_origin = [&](int t, int& bm, int& bn) {
         int pid = t;
         if (ntiles % 8 == 0) pid = (pid % 8) * (ntiles / 8) + pid / 8;
@@ -2321,7 +1666,7 @@ void qgemm_big_w16(const i8* __restrict__ a, const i8* __restrict__ b, Epi e,
     const int r16 = lane & 15, q4 = lane >> 4;
     const int nk = k / kK2;
 
-    // DMA exactly as qgemm_big_w8: instruction j (0..3) of this wave fills
+    // DMA: instruction j (0..3) of this wave fills
     // tile rows 64 j + 8 wave + lane / 8 of A and of B; the lane's LDS chunk
     // position lane % 8 holds logical chunk (lane % 8) ^ swz, swz = (row >> 1)
     // & 7. Rows past M / N read a clamped (real) row.
@@ -2506,7 +1851,7 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
     const bool aligned = (k % 16 == 0) && ((uintptr_t)a % 16 == 0) &&
                          ((uintptr_t)b % 16 == 0);
     // FT_QGEMM_KERNEL: 1 skinny, 2 tiled, 3 scalar, 4 big, 5 gemv, 6 decode
-    const int force = env_int("FT_QGEMM_KERNEL", 0);
+    const int force = tune(Tune::QgemmKernel, 0);
     if (!aligned || force == 3) {
         const long long total = (long long)m * n;
         qgemm_scalar<OUT><<<grid_1d(total, 256, 1 << 30), 256, 0, s>>>(a, b, e, m, n, k);
@@ -2546,19 +1891,14 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         // (N=6144: 1 wave per tile 8.3 us vs 9.3 us; N=4096 K=14336: 2 waves
         // 13.4 us vs 18.9 us)
         int kw = tiles >= 320 ? 1 : tiles >= 128 ? 2 : 4;
-        const int kw_env = env_int("FT_QGEMM_DEC_KW", 0);
-        if (kw_env == 1 || kw_env == 2 || kw_env == 4) kw = kw_env;
-        // W and A through an LDS ring in whole lines, W non-temporal (C2 chain,
-        // M = 8 / 16: 21.1 / 23.3 us with register operands, 16.5 / 17.4 us
-        // with 2 stages; 3 stages the same, 4 stages slower: 64 KB per wave
-        // leaves 2 waves per CU; plain W loads 19.1 / 19.4 us)
-        const int lds_stages = env_int("FT_QGEMM_DEC_LDS", 2);
-        if (kw == 1 && k % kDwChunk == 0 && (lds_stages == 2 || lds_stages == 3)) {
-            const bool nt = env_int("FT_QGEMM_DEC_NT", 1) != 0;
-#define FT_DEC_LDS(S, C) qgemm_dec_lds<S, C, OUT><<<grid, 64, 0, s>>>(a, b, e, m, n, k)
-            if (lds_stages == 2) { if (nt) FT_DEC_LDS(2, 2); else FT_DEC_LDS(2, 0); }
-            else { if (nt) FT_DEC_LDS(3, 2); else FT_DEC_LDS(3, 0); }
-#undef FT_DEC_LDS
+        const int kw_forced = tune(Tune::QgemmDecKw, 0);
+        if (kw_forced == 1 || kw_forced == 2 || kw_forced == 4) kw = kw_forced;
+        // W and A through a 2-stage LDS ring in whole lines, W non-temporal
+        // (C2 chain, M = 8 / 16: 21.1 / 23.3 us with register operands,
+        // 16.5 / 17.4 us with the ring; 3 stages the same, 4 stages slower:
+        // 64 KB per wave leaves 2 waves per CU; plain W loads 19.1 / 19.4 us)
+        if (kw == 1 && k % kDwChunk == 0 && tune(Tune::QgemmDecRegs, 0) == 0) {
+            qgemm_dec_lds<2, 2, OUT><<<grid, 64, 0, s>>>(a, b, e, m, n, k);
             launch_check("qgemm decode lds kernel launch");
             return;
         }
@@ -2582,7 +1922,7 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         int ksplit = col_wgs >= cus
                          ? 1
                          : std::max(1, std::min((2 * cus + col_wgs - 1) / col_wgs, chunks));
-        const int forced_split = env_int("FT_QGEMM_KSPLIT", 0);
+        const int forced_split = tune(Tune::QgemmKsplit, 0);
         if (forced_split > 0) ksplit = std::min(forced_split, chunks);
         if (ksplit > 65535) ksplit = 65535;
         const int mt = (m + 15) / 16;
@@ -2594,19 +1934,12 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         // operands through a 2-stage LDS ring in whole lines (C4 layer: 462 us
         // against 477 us with register W operands; 3 stages 470 us: 96 KB of
         // LDS leaves one workgroup per CU)
-        const int sk_stages = env_int("FT_QGEMM_SK_LDS", 2);
-        if (k % kSlChunk == 0 && (sk_stages == 2 || sk_stages == 3)) {
-#define FT_SK_LDS(MT, S) \
-    qgemm_skinny_lds<MT, S, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part)
-            if (sk_stages == 2) {
-                if (mt <= 1) FT_SK_LDS(1, 2);
-                else if (mt <= 2) FT_SK_LDS(2, 2);
-                else FT_SK_LDS(4, 2);
-            } else {
-                if (mt <= 1) FT_SK_LDS(1, 3);
-                else if (mt <= 2) FT_SK_LDS(2, 3);
-                else FT_SK_LDS(4, 3);
-            }
+        if (k % kSlChunk == 0 && tune(Tune::QgemmSkRegs, 0) == 0) {
+#define FT_SK_LDS(MT) \
+    qgemm_skinny_lds<MT, 2, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part)
+            if (mt <= 1) FT_SK_LDS(1);
+            else if (mt <= 2) FT_SK_LDS(2);
+            else FT_SK_LDS(4);
 #undef FT_SK_LDS
         } else if (mt <= 1)
             qgemm_skinny<1, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part);
@@ -2625,10 +1958,10 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
     if ((m >= kBigT && n >= kBigT && force != 2) || force == 4) {
         const long long tiles = (long long)((m + kBigT - 1) / kBigT) * ((n + kBigT - 1) / kBigT);
         if (tiles > (1LL << 30)) inval("qgemm problem too large for one launch");
-        // FT_QGEMM_BIG: 1: 64-byte slabs, 2: register-staged, 3: 128-byte
-        // slabs with 4 waves (one per SIMD), 4: 8 waves on 32x32x32 MFMAs
-        const int big = env_int("FT_QGEMM_BIG", 0);
-        if (k % kK2 == 0 && (big == 0 || big == 3 || big == 4)) {
+        // FT_QGEMM_BIG (tests): 1 the 64-byte-slab kernel, 2 the
+        // register-staged one, on shapes that would take the default
+        const int big = tune(Tune::QgemmBig, 0);
+        if (k % kK2 == 0 && big == 0) {
             // persistent: a multiple of 8 workgroups (XCD-aware order), at
             // most one per CU. 8 waves by default: on C5a (4096 x 8192 x
             // 28672, random int8) the MFMA pipes are busy 70% of the cycles
@@ -2638,19 +1971,13 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
             const long long cus = dev_info().cu_count;
             long long grid = std::min<long long>(tiles, cus);
             if (grid >= 8) grid -= grid % 8;
-            if (env_int("FT_QGEMM_ONE_TILE", 0)) grid = tiles;  // A/B: no persistence
-            const int band = std::max(1, env_int("FT_QGEMM_BAND", kBigBand));
+            const int band = std::max(1, tune(Tune::QgemmBand, kBigBand));
             const int scales_dma = e.sb_vec && (n % 4 == 0) &&
                                    ((uintptr_t)e.sb_vec % 16 == 0);
-            if (big == 3)
-                qgemm_big_k128<OUT><<<(unsigned)grid, 256, 0, s>>>(a, b, e, m, n, k, scales_dma);
-            else if (big == 4)
-                qgemm_big_w8<OUT><<<(unsigned)grid, 512, 0, s>>>(a, b, e, m, n, k, scales_dma);
-            else
-                qgemm_big_w16<OUT><<<(unsigned)grid, 512, 0, s>>>(a, b, e, m, n, k, scales_dma,
-                                                                  band);
+            qgemm_big_w16<OUT><<<(unsigned)grid, 512, 0, s>>>(a, b, e, m, n, k, scales_dma,
+                                                              band);
         }
-        else if (k % kBigK == 0 && big != 2 && env_int("FT_QGEMM_NO_DMA", 0) == 0)
+        else if (k % kBigK == 0 && big != 2)
             qgemm_big_dma<OUT><<<(unsigned)tiles, 256, 0, s>>>(a, b, e, m, n, k);
         else
             qgemm_big<OUT><<<(unsigned)tiles, 256, 0, s>>>(a, b, e, m, n, k);
@@ -2758,7 +2085,7 @@ int ft_rmsnorm_qgemm_launch(const void* x, int x_dtype, const float* w,
             rows == 1 && k <= ft::kGemvChunks * 1024 && k % 16 == 0 &&
             (uintptr_t)x % (4 * esz) == 0 && (!residual || (uintptr_t)residual % (4 * esz) == 0) &&
             (uintptr_t)w % 16 == 0 && (uintptr_t)bq % 16 == 0 && (uintptr_t)q % 4 == 0 &&
-            ft::env_int("FT_RMSQ_GEMV_SPLIT", 0) == 0;
+            ft::tune(ft::Tune::RmsqGemvSplit, 0) == 0;
         if (!fusable) {
             // the two-step chain: rmsnorm_quant, then the GEMM on its codes
             // with the device scale

@@ -2,7 +2,9 @@
 // properties, per-device scratch pool, device probe.
 #include "ft_common.hpp"
 
+#include <atomic>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <vector>
 
@@ -64,9 +66,52 @@ const DevInfo& dev_info() {
     return st.info;
 }
 
-int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return (v && *v) ? atoi(v) : dflt;
+namespace {
+constexpr const char* kTuneNames[(int)Tune::kCount] = {
+    "FT_ATTN_FORCE_GENERIC", "FT_ATTN_SEGS",       "FT_ATTN_MIN_SEG",
+    "FT_ATTN_CHUNK",         "FT_QGEMM_KERNEL",    "FT_QGEMM_DEC_KW",
+    "FT_QGEMM_DEC_REGS",     "FT_QGEMM_KSPLIT",    "FT_QGEMM_SK_REGS",
+    "FT_QGEMM_BIG",          "FT_QGEMM_BAND",      "FT_RMSQ_SPLIT",
+    "FT_RMSQ_GEMV_SPLIT",    "FT_PREFILL_FORCE_GENERIC", "FT_ARG_SLICES",
+    "FT_SMP_SINGLE",         "FT_SMP_SLICES"};
+
+// value and presence per switch: the environment's (read once), then the
+// run-time override, which wins while set
+struct TuneState {
+    int env_val[(int)Tune::kCount] = {};
+    bool env_set[(int)Tune::kCount] = {};
+    std::atomic<int> val[(int)Tune::kCount];
+    std::atomic<bool> set[(int)Tune::kCount];
+};
+
+TuneState& tune_state() {
+    static TuneState st;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        for (int i = 0; i < (int)Tune::kCount; ++i) {
+            const char* v = getenv(kTuneNames[i]);
+            st.env_set[i] = v && *v;
+            st.env_val[i] = st.env_set[i] ? atoi(v) : 0;
+            st.val[i].store(st.env_val[i]);
+            st.set[i].store(st.env_set[i]);
+        }
+    });
+    return st;
+}
+
+int tune_index(const char* name) {
+    if (!name) return -1;
+    for (int i = 0; i < (int)Tune::kCount; ++i)
+        if (strcmp(name, kTuneNames[i]) == 0) return i;
+    return -1;
+}
+}  // namespace
+
+int tune(Tune which, int dflt) {
+    TuneState& st = tune_state();
+    const int i = (int)which;
+    return st.set[i].load(std::memory_order_relaxed) ? st.val[i].load(std::memory_order_relaxed)
+                                                     : dflt;
 }
 
 bool stream_capturing(hipStream_t s) {
@@ -134,5 +179,25 @@ int ft_device_available(void) {
 }
 
 const char* ft_version(void) { return "0.1.0"; }
+
+int ft_set_tuning(const char* name, int value) {
+    return ft::guarded([&] {
+        const int i = ft::tune_index(name);
+        if (i < 0) ft::inval(std::string("unknown tuning switch: ") + (name ? name : "(null)"));
+        ft::TuneState& st = ft::tune_state();
+        st.val[i].store(value);
+        st.set[i].store(true);
+    });
+}
+
+int ft_clear_tuning(const char* name) {
+    return ft::guarded([&] {
+        const int i = ft::tune_index(name);
+        if (i < 0) ft::inval(std::string("unknown tuning switch: ") + (name ? name : "(null)"));
+        ft::TuneState& st = ft::tune_state();
+        st.val[i].store(st.env_val[i]);
+        st.set[i].store(st.env_set[i]);
+    });
+}
 
 }  // extern "C"

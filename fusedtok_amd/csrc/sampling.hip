@@ -899,7 +899,7 @@ void argmax_launch(const float* x, int rows, int n, OUT* out, hipStream_t s) {
     int S = 1;
     if (rows < cus)
         S = std::min({(4 * cus + rows - 1) / rows, std::max(1, n / kArgMinSlice), kArgMaxSlices});
-    const int forced = env_int("FT_ARG_SLICES", 0);
+    const int forced = tune(Tune::ArgSlices, 0);
     if (forced > 0) S = std::min(forced, kArgMaxSlices);
     int slen = (n + S - 1) / S;
     slen = (slen + 3) & ~3;  // slices start on 4-token boundaries
@@ -943,12 +943,12 @@ void topp_launch(const float* x, int rows, int n, float p, float t, float pen,
     // kMinSlice tokens each; FT_SMP_SINGLE=1 keeps one workgroup per row
     const int cus = dev_info().cu_count;
     int S = 1;
-    if (rows < cus && env_int("FT_SMP_SINGLE", 0) == 0)
+    if (rows < cus && tune(Tune::SmpSingle, 0) == 0)
         S = std::min({(2 * cus + rows - 1) / rows, std::max(1, n / kMinSlice), kMaxSlices});
     // FT_SMP_SLICES forces the slice count (2 .. kMaxSlices, at most one
     // slice per 32 tokens)
-    const int forced_s = env_int("FT_SMP_SLICES", 0);
-    if (forced_s >= 2 && env_int("FT_SMP_SINGLE", 0) == 0)
+    const int forced_s = tune(Tune::SmpSlices, 0);
+    if (forced_s >= 2 && tune(Tune::SmpSingle, 0) == 0)
         S = std::min({forced_s, kMaxSlices, std::max(1, n / 32)});
     if (S <= 1) {
         sample_topp_rows<<<(unsigned)rows, kSmpNT, 0, s>>>(

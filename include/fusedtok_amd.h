@@ -60,6 +60,16 @@ int ft_device_available(void);
 /* Library version string. */
 const char* ft_version(void);
 
+/* Build addition (tests and measurement sweeps; no reference counterpart):
+ * tuning switches. Each FT_* switch (FT_ATTN_SEGS, FT_QGEMM_KERNEL, ...) is
+ * read from the environment once per process, on first use;
+ * ft_set_tuning overrides its value for the rest of the process and
+ * ft_clear_tuning restores the environment's value (or unset). An unknown
+ * name is FT_EINVAL. No switch changes a result beyond the op's stated
+ * tolerance (integer results not at all). */
+int ft_set_tuning(const char* name, int value);
+int ft_clear_tuning(const char* name);
+
 /* ------------------------------------------------------------------ */
 /* Attention, decode step, contiguous cache                            */
 /* out[b,h] = softmax(q[b,h] . K[b,h/G]^T / sqrt(D)) . V[b,h/G]         */

@@ -31,3 +31,21 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture
+def tuning():
+    """Set the library's FT_* tuning switches for one test through the
+    binding (ft_set_tuning); every switch set is restored afterwards.
+    ``tuning(name, value)`` sets, ``tuning.clear(name)`` restores one now."""
+    import fusedtok_amd as ft
+    touched = set()
+
+    def set_switch(name, value):
+        ft._fusedtok.set_tuning(name, int(value))
+        touched.add(name)
+
+    set_switch.clear = ft._fusedtok.clear_tuning
+    yield set_switch
+    for name in touched:
+        ft._fusedtok.clear_tuning(name)

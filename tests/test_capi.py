@@ -231,3 +231,15 @@ def test_fused_invalid_arguments(lib):
     assert call(off=-1) == FT_EINVAL
     assert call(batch=0) == FT_OK
     assert call(**ok) == FT_EINVAL               # null operands
+
+
+def test_tuning_switches_by_name(lib):
+    # the FT_* switches are read once per process; the ABI overrides them
+    # by name and restores them (no device involved)
+    lib.ft_set_tuning.argtypes = [ctypes.c_char_p, ctypes.c_int]
+    lib.ft_clear_tuning.argtypes = [ctypes.c_char_p]
+    assert lib.ft_set_tuning(b"FT_QGEMM_BAND", 8) == FT_OK
+    assert lib.ft_clear_tuning(b"FT_QGEMM_BAND") == FT_OK
+    assert lib.ft_set_tuning(b"FT_NO_SUCH_SWITCH", 1) == FT_EINVAL
+    assert b"unknown tuning switch" in lib.ft_last_error()
+    assert lib.ft_clear_tuning(None) == FT_EINVAL

@@ -102,8 +102,8 @@ def test_decode_f32_split_every_group(group):
 
 
 @pytest.mark.parametrize("dt", HALF)
-def test_generic_kernel_on_half_storage(dt, monkeypatch):
-    monkeypatch.setenv("FT_ATTN_FORCE_GENERIC", "1")
+def test_generic_kernel_on_half_storage(dt, tuning):
+    tuning("FT_ATTN_FORCE_GENERIC", 1)
     rng = np.random.default_rng(5)
     q, k, v, lens = make_case(rng, 3, 16, 4, 700, 128, True)
     y = ft.attention_decode(t(q, dt), t(k, dt), t(v, dt), t(lens))

@@ -110,7 +110,7 @@ def test_rmsnorm_quant_vs_half_storage_chain(dt, rows, cols):
 @pytest.mark.parametrize("dt", ALL)
 @pytest.mark.parametrize("rows,cols", [(1, 4096), (2, 12), (3, 4096), (4, 4096),
                                        (4, 1000), (1, 4)])
-def test_rmsnorm_quant_one_launch_matches_two_launch_path(dt, rows, cols, monkeypatch):
+def test_rmsnorm_quant_one_launch_matches_two_launch_path(dt, rows, cols, tuning):
     # up to 4 rows of up to 4096 columns run as one workgroup; FT_RMSQ_SPLIT=1
     # forces the per-row + fold/quantize kernels. Both must agree bit for bit.
     rng = np.random.default_rng(rows * 131 + cols)
@@ -121,9 +121,9 @@ def test_rmsnorm_quant_one_launch_matches_two_launch_path(dt, rows, cols, monkey
     r = t(rng.standard_normal((rows, cols)).astype(np.float32), dt)
     for res in (None, r):
         q1, s1 = ft.rmsnorm_quant(x, w, residual=res, eps=1e-5)
-        monkeypatch.setenv("FT_RMSQ_SPLIT", "1")
+        tuning("FT_RMSQ_SPLIT", 1)
         q2, s2 = ft.rmsnorm_quant(x, w, residual=res, eps=1e-5)
-        monkeypatch.delenv("FT_RMSQ_SPLIT")
+        tuning.clear("FT_RMSQ_SPLIT")
         np.testing.assert_array_equal(q1.cpu().numpy(), q2.cpu().numpy())
         assert s1 == s2
 
@@ -136,7 +136,7 @@ def test_rmsnorm_quant_one_launch_matches_two_launch_path(dt, rows, cols, monkey
                                           # second pass reloads its weight rows
                                           (1, 28672, 4096, True)])
 @pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
-def test_rmsnorm_qgemm_equals_the_two_ops(dt, rows, n, k, res, odt, monkeypatch):
+def test_rmsnorm_qgemm_equals_the_two_ops(dt, rows, n, k, res, odt, tuning):
     # one row with K <= 4096 runs as one launch (the GEMV normalises and
     # quantises the row in every workgroup); the codes, the scale and the
     # output must equal rmsnorm_quant followed by qgemm_perchannel
@@ -157,9 +157,9 @@ def test_rmsnorm_qgemm_equals_the_two_ops(dt, rows, n, k, res, odt, monkeypatch)
     ref = oracle.qgemm_perchannel(eq, es, b.cpu().numpy(), sb.cpu().numpy())
     assert torch.equal(y.cpu(), torch.from_numpy(ref).to(odt))
     # the two-op path of the same entry point, and a per-tensor weight scale
-    monkeypatch.setenv("FT_RMSQ_GEMV_SPLIT", "1")
+    tuning("FT_RMSQ_GEMV_SPLIT", 1)
     y3, q3, s3 = ft.rmsnorm_qgemm(x, w, b, sb, residual=r, eps=1e-5, out_dtype=odt)
-    monkeypatch.delenv("FT_RMSQ_GEMV_SPLIT")
+    tuning.clear("FT_RMSQ_GEMV_SPLIT")
     assert torch.equal(y3, y) and torch.equal(q3, q) and torch.equal(s3, s)
     yt, _, _ = ft.rmsnorm_qgemm(x, w, b, 0.004, residual=r, eps=1e-5, out_dtype=odt)
     assert torch.equal(yt, ft.qgemm(q2, s2, b, 0.004, out_dtype=odt))

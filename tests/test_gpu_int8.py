@@ -192,15 +192,17 @@ GEMM_SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("big", ["0", "3", "4"])
-def test_big_persistent_tiles_bit_exact(big, monkeypatch):
+@pytest.mark.parametrize("band", [0, 1, 3])
+def test_big_persistent_tiles_bit_exact(band, tuning):
     # 9 x 33 = 297 tiles of 256 x 256 > one workgroup per CU: the persistent
-    # 128-byte-slab kernels (8 waves with 16x16x64 MFMAs, default, or
-    # 32x32x32, and 4 waves) walk several tiles per
-    # workgroup, with the next tile's first slabs loading during the
-    # previous tile's epilogue. Rows from every 256-row band are checked
-    # against the oracle over all columns, so every tile is covered.
-    monkeypatch.setenv("FT_QGEMM_BIG", big)
+    # 128-byte-slab kernel (8 waves with 16x16x64 MFMAs) walks several tiles
+    # per workgroup, with the next tile's first slabs loading during the
+    # previous tile's epilogue; the default tile order and two other band
+    # heights (a band of 3 leaves a ragged last band). Rows from every
+    # 256-row band are checked against the oracle over all columns, so every
+    # tile is covered.
+    if band:
+        tuning("FT_QGEMM_BAND", band)
     rng = np.random.default_rng(77)
     m, n, k = 2304, 8448, 384
     a, b = rand_q(rng, m, k), rand_q(rng, n, k)
@@ -215,15 +217,15 @@ def test_big_persistent_tiles_bit_exact(big, monkeypatch):
     assert torch.equal(y[rows], ref)
 
 
-@pytest.mark.parametrize("big", ["0", "1", "2", "3", "4"])
-def test_big_kernels_bit_exact(big, monkeypatch):
-    # the five big-tile kernels on one K % 128 == 0 shape with ragged edges:
-    # 128-byte DMA slabs with 8 waves on 16x16x64 MFMAs (default), 64-byte
-    # DMA slabs, register-staged, 128-byte DMA slabs with 4 waves, 8 waves on
-    # 32x32x32 MFMAs; every output type (i32, f32 per-tensor and per-channel,
-    # bf16, f16)
-    monkeypatch.setenv("FT_QGEMM_BIG", big)
-    rng = np.random.default_rng(400 + int(big))
+@pytest.mark.parametrize("big", [0, 1, 2])
+def test_big_kernels_bit_exact(big, tuning):
+    # the three big-tile kernels on one K % 128 == 0 shape with ragged
+    # edges: 128-byte DMA slabs with 8 waves on 16x16x64 MFMAs (default),
+    # 64-byte DMA slabs (K % 64 == 0 shapes), register-staged (any K); every
+    # output type (i32, f32 per-tensor and per-channel, bf16, f16)
+    if big:
+        tuning("FT_QGEMM_BIG", big)
+    rng = np.random.default_rng(400 + big)
     m, n, k = 520, 777, 1280
     a, b = rand_q(rng, m, k), rand_q(rng, n, k)
     sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
@@ -267,12 +269,12 @@ def test_qgemm_bit_exact(m, n, k):
     (17, 64, 16, 0),        # a single 16-byte K piece
     (64, 16448, 512, 0),    # 257 column workgroups: no K split
 ])
-def test_skinny_kernel_bit_exact(m, n, k, split, monkeypatch):
+def test_skinny_kernel_bit_exact(m, n, k, split, tuning):
     # 16 < M <= 64 (qgemm_skinny), with and without K splits (int32 partials
     # folded by a second launch), including a split that leaves a workgroup
     # an empty K range
     if split:
-        monkeypatch.setenv("FT_QGEMM_KSPLIT", str(split))
+        tuning("FT_QGEMM_KSPLIT", split)
     rng = np.random.default_rng(m * 7 + n + k + split)
     a, b = rand_q(rng, m, k), rand_q(rng, n, k)
     sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
@@ -284,7 +286,7 @@ def test_skinny_kernel_bit_exact(m, n, k, split, monkeypatch):
     assert torch.equal(y.cpu(), ref)
 
 
-@pytest.mark.parametrize("stages", ["0", "2", "3"])
+@pytest.mark.parametrize("regs", [0, 1])
 @pytest.mark.parametrize("m,n,k,split", [
     (17, 200, 256, 0),      # one chunk, one 16-row tile
     (33, 300, 1280, 0),     # three tiles (MT = 4 with one row past M), ragged N
@@ -292,12 +294,13 @@ def test_skinny_kernel_bit_exact(m, n, k, split, monkeypatch):
     (20, 70, 2304, 2),      # split into 5 + 4 chunks; ragged N (dead waves)
     (64, 16448, 512, 0),    # 257 column workgroups, no split
 ])
-def test_skinny_lds_ring_bit_exact(stages, m, n, k, split, monkeypatch):
-    # the LDS-ring skinny kernel (K % 256 == 0) against the oracle, for both
-    # ring depths and the register-operand kernel (FT_QGEMM_SK_LDS=0)
-    monkeypatch.setenv("FT_QGEMM_SK_LDS", stages)
+def test_skinny_lds_ring_bit_exact(regs, m, n, k, split, tuning):
+    # the LDS-ring skinny kernel (K % 256 == 0) against the oracle, and the
+    # register-operand kernel on the same shapes (FT_QGEMM_SK_REGS=1)
+    if regs:
+        tuning("FT_QGEMM_SK_REGS", 1)
     if split:
-        monkeypatch.setenv("FT_QGEMM_KSPLIT", str(split))
+        tuning("FT_QGEMM_KSPLIT", split)
     rng = np.random.default_rng(m * 3 + n + k + split)
     a, b = rand_q(rng, m, k), rand_q(rng, n, k)
     sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
@@ -309,11 +312,11 @@ def test_skinny_lds_ring_bit_exact(stages, m, n, k, split, monkeypatch):
     assert torch.equal(y.cpu(), ref)
 
 
-@pytest.mark.parametrize("kernel", ["1", "2", "3", "4", "5", "6"])
-def test_every_gemm_kernel_bit_exact(kernel, monkeypatch):
-    monkeypatch.setenv("FT_QGEMM_KERNEL", kernel)
-    rng = np.random.default_rng(int(kernel))
-    m = {"1": 48, "5": 7, "6": 13}.get(kernel, 80)
+@pytest.mark.parametrize("kernel", [1, 2, 3, 4, 5, 6])
+def test_every_gemm_kernel_bit_exact(kernel, tuning):
+    tuning("FT_QGEMM_KERNEL", kernel)
+    rng = np.random.default_rng(kernel)
+    m = {1: 48, 5: 7, 6: 13}.get(kernel, 80)
     a, b = rand_q(rng, m, 640), rand_q(rng, 200, 640)
     sb = rng.uniform(1e-3, 1e-2, 200).astype(np.float32)
     y = ft.qgemm_perchannel(t(a), 0.5, t(b), t(sb))
@@ -321,15 +324,15 @@ def test_every_gemm_kernel_bit_exact(kernel, monkeypatch):
     np.testing.assert_array_equal(y.cpu().numpy(), oracle.qgemm_perchannel(a, 0.5, b, sb))
 
 
-@pytest.mark.parametrize("kw", ["1", "2", "4"])
+@pytest.mark.parametrize("kw", [1, 2, 4])
 @pytest.mark.parametrize("m,n,k", [(1, 200, 640), (5, 33, 4096), (16, 200, 640),
                                    (3, 16, 80), (16, 40, 16), (8, 1000, 14336)])
-def test_decode_gemm_kernel_bit_exact(kw, m, n, k, monkeypatch):
+def test_decode_gemm_kernel_bit_exact(kw, m, n, k, tuning):
     # the K-split-in-workgroup decode kernel: ragged chunks (K % 512 != 0),
     # K below one MFMA step, waves with no chunk, N % 16 != 0
-    monkeypatch.setenv("FT_QGEMM_KERNEL", "6")
-    monkeypatch.setenv("FT_QGEMM_DEC_KW", kw)
-    rng = np.random.default_rng(m * 100 + n + k + int(kw))
+    tuning("FT_QGEMM_KERNEL", 6)
+    tuning("FT_QGEMM_DEC_KW", kw)
+    rng = np.random.default_rng(m * 100 + n + k + kw)
     a, b = rand_q(rng, m, k), rand_q(rng, n, k)
     sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
     acc = ft.qgemm_i32(t(a), t(b))
@@ -340,16 +343,13 @@ def test_decode_gemm_kernel_bit_exact(kw, m, n, k, monkeypatch):
     assert torch.equal(y.cpu(), ref)
 
 
-@pytest.mark.parametrize("stages,nt", [("2", "0"), ("2", "1"), ("3", "1")])
-def test_decode_gemm_lds_ring_bit_exact(stages, nt, monkeypatch):
+def test_decode_gemm_lds_ring_bit_exact(tuning):
     # the LDS-staged decode kernel (K % 512 == 0, one wave per 16 columns):
     # one chunk, fewer chunks than ring stages, ragged N, odd M; the C2 shape
-    # against the register-operand kernel (FT_QGEMM_DEC_LDS=0)
-    monkeypatch.setenv("FT_QGEMM_KERNEL", "6")
-    monkeypatch.setenv("FT_QGEMM_DEC_KW", "1")
-    monkeypatch.setenv("FT_QGEMM_DEC_NT", nt)
+    # against the register-operand kernel (FT_QGEMM_DEC_REGS=1)
+    tuning("FT_QGEMM_KERNEL", 6)
+    tuning("FT_QGEMM_DEC_KW", 1)
     for m, n, k in [(2, 40, 512), (7, 1000, 1024), (16, 333, 2560), (9, 17, 4608)]:
-        monkeypatch.setenv("FT_QGEMM_DEC_LDS", stages)
         rng = np.random.default_rng(m * 10 + n + k)
         a, b = rand_q(rng, m, k), rand_q(rng, n, k)
         sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
@@ -362,19 +362,21 @@ def test_decode_gemm_lds_ring_bit_exact(stages, nt, monkeypatch):
     for m, n, k in [(16, 11008, 4096), (13, 5000, 14336)]:
         rng = np.random.default_rng(m + n + k)
         at, bt = t(rand_q(rng, m, k)), t(rand_q(rng, n, k))
-        monkeypatch.setenv("FT_QGEMM_DEC_LDS", stages)
         acc = ft.qgemm_i32(at, bt)
-        monkeypatch.setenv("FT_QGEMM_DEC_LDS", "0")
+        tuning("FT_QGEMM_DEC_REGS", 1)
         acc0 = ft.qgemm_i32(at, bt)
+        tuning.clear("FT_QGEMM_DEC_REGS")
         assert torch.equal(acc, acc0)
 
 
-@pytest.mark.parametrize("ksplit", ["1", "2", "4", "7"])
-def test_skinny_k_split_bit_exact_and_counters_reset(ksplit, monkeypatch):
-    monkeypatch.setenv("FT_QGEMM_KSPLIT", ksplit)
-    rng = np.random.default_rng(int(ksplit) + 50)
-    a, b = rand_q(rng, 16, 4096), rand_q(rng, 700, 4096)
-    for rep in range(3):   # repeats reuse the arrival counters
+@pytest.mark.parametrize("ksplit", [1, 2, 4, 7])
+def test_skinny_k_split_bit_exact_on_repeats(ksplit, tuning):
+    # forced K splits of the skinny kernel; repeated calls reuse the partials
+    # buffer, whose previous contents must not leak into the fold
+    tuning("FT_QGEMM_KSPLIT", ksplit)
+    rng = np.random.default_rng(ksplit + 50)
+    a, b = rand_q(rng, 48, 4096), rand_q(rng, 700, 4096)
+    for rep in range(3):
         acc = ft.qgemm_i32(t(a), t(b))
         torch.cuda.synchronize()
         np.testing.assert_array_equal(acc.cpu().numpy(), oracle.qgemm_i32(a, b))

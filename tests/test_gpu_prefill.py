@@ -135,11 +135,11 @@ def test_prefill_half_generic_dims(dt, d):
 
 
 @pytest.mark.parametrize("dt", HALF)
-def test_prefill_mfma_and_generic_agree(dt, monkeypatch):
+def test_prefill_mfma_and_generic_agree(dt, tuning):
     rng = np.random.default_rng(9)
     q, k, v = _inputs(rng, 1, 4, 2, 150, 128, dt)
     a = ft.attention_prefill(q, k, v).float()
-    monkeypatch.setenv("FT_PREFILL_FORCE_GENERIC", "1")
+    tuning("FT_PREFILL_FORCE_GENERIC", 1)
     g = ft.attention_prefill(q, k, v).float()
     _check_half(g.to(dt), q, k, v, True)
     assert (a - g).abs().max().item() <= 2e-3 + 1e-2 * g.abs().max().item()

@@ -53,13 +53,13 @@ def test_argmax_and_batched_bit_exact():
         ft.argmax_batched(torch.zeros((2, 3), dtype=torch.float64, device=DEV))
 
 
-@pytest.mark.parametrize("slices", ["0", "1", "2", "3", "64"])
-def test_argmax_sliced_rows_bit_exact(slices, monkeypatch):
+@pytest.mark.parametrize("slices", [0, 1, 2, 3, 64])
+def test_argmax_sliced_rows_bit_exact(slices, tuning):
     # rows split across workgroups (fewer rows than CUs), folded by one wave
     # per row: ties across slice boundaries, NaN at index 0, all-NaN and
     # all -inf rows, the maximum in the last token, misaligned rows (odd n)
-    monkeypatch.setenv("FT_ARG_SLICES", slices)
-    rng = np.random.default_rng(int(slices) + 7)
+    tuning("FT_ARG_SLICES", slices)
+    rng = np.random.default_rng(slices + 7)
     n = 128256
     x = rng.integers(-1000, 1000, (8, n)).astype(np.float32)
     x[0, 20000] = x[0, 100000] = x[0, 127000] = 5000.0
@@ -200,7 +200,7 @@ def test_sampling_contract():
 
 @pytest.mark.parametrize("rows,n", [(1, 128256), (3, 50000), (16, 32000), (64, 128256),
                                     (2, 16417), (5, 20000)])
-def test_sliced_pipeline_matches_single_workgroup(rows, n, monkeypatch):
+def test_sliced_pipeline_matches_single_workgroup(rows, n, tuning):
     # Fewer rows than CUs: each row is split over several workgroups (slice
     # maxima, slice histograms, a per-row plan, a gather of the bins the two
     # queries can cross, the exact select). Masses are integers, so the
@@ -220,20 +220,20 @@ def test_sliced_pipeline_matches_single_workgroup(rows, n, monkeypatch):
     lt = t(logits)
     for p, temp in [(0.9, 0.8), (0.5, 1.3), (1.0, 1.0), (0.05, 0.3)]:
         got = {}
-        for mode in ("0", "1"):
-            monkeypatch.setenv("FT_SMP_SINGLE", mode)
+        for mode in (0, 1):
+            tuning("FT_SMP_SINGLE", mode)
             got[mode] = (ft.decode_step_batched(lt, hist, 1.3, p=p, temperature=temp,
                                                 seeds=seeds).tolist(),
                          ft.sample_topp_batched(lt, p, temperature=temp, seeds=seeds).tolist(),
                          ft.sample_topp(lt[0], p, temperature=temp, seed=seeds[0]))
-        assert got["0"] == got["1"], (p, temp)
+        assert got[0] == got[1], (p, temp)
 
 
-@pytest.mark.parametrize("slices", ["2", "3", "12", "64"])
-def test_sliced_pipeline_any_slice_count(slices, monkeypatch):
+@pytest.mark.parametrize("slices", [2, 3, 12, 64])
+def test_sliced_pipeline_any_slice_count(slices, tuning):
     # forced slice counts (FT_SMP_SLICES): odd splits, slices of a few
     # hundred tokens, the maximum count; same tokens as one workgroup per row
-    rng = np.random.default_rng(int(slices) + 90)
+    rng = np.random.default_rng(slices + 90)
     rows, n = 6, 40001
     logits = (rng.standard_normal((rows, n)) * 2).astype(np.float32)
     logits[1] = 0.0
@@ -244,9 +244,9 @@ def test_sliced_pipeline_any_slice_count(slices, monkeypatch):
     hist = [rng.integers(0, n, size=int(rng.integers(0, 40))).tolist() for _ in range(rows)]
     lt = t(logits)
     for p, temp in [(0.9, 0.8), (0.3, 1.2)]:
-        monkeypatch.setenv("FT_SMP_SLICES", slices)
+        tuning("FT_SMP_SLICES", slices)
         a = ft.decode_step_batched(lt, hist, 1.2, p=p, temperature=temp, seeds=seeds).tolist()
-        monkeypatch.setenv("FT_SMP_SINGLE", "1")
+        tuning("FT_SMP_SINGLE", 1)
         b = ft.decode_step_batched(lt, hist, 1.2, p=p, temperature=temp, seeds=seeds).tolist()
-        monkeypatch.delenv("FT_SMP_SINGLE")
+        tuning.clear("FT_SMP_SINGLE")
         assert a == b, (p, temp)
