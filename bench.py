@@ -89,7 +89,7 @@ def parse():
     p.add_argument("--no-chains", action="store_true",
                    help="skip the config 2 / config 4 chain measurements")
     p.add_argument("--only", choices=["decode", "gemm", "copy", "c1", "c2", "c4", "c5b",
-                            "int8", "prefill", "sampling"],
+                            "int8", "prefill", "sampling", "cpu"],
                    default=None,
                    help="run one workload only (profiling runs); 'copy' is "
                         "the HBM-counter calibration: a plain 1 GiB "
@@ -552,9 +552,50 @@ def bench_sampling(torch, ft, dev):
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the oracle on a bounded sample of config 3's rows
+# CPU baselines, timed on this host after the GPU legs. The reference CPU
+# path (its single-threaded *_cpu functions, unbuildable here) runs as the
+# oracle's C++ restatement on ONE pinned core ("port"); a torch-CPU float32
+# composite of the same math runs on every core the process may use.
+# Bounded samples, stated in each entry; about 20-30 s of CPU work in all.
 # ---------------------------------------------------------------------------
-def cpu_baseline_c3(torch, np, w, budget_s=12.0):
+def host_facts():
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0))}
+
+
+class one_core:
+    """Pin this process to one of its allowed cores for the block (the
+    oracle is single-threaded; this keeps it from migrating)."""
+    def __enter__(self):
+        self.saved = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {min(self.saved)})
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.saved)
+
+
+def timed(fn, reps=3):
+    """Median wall time of `reps` runs of fn()."""
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def cpu_baseline_c3(torch, np, w, budget_s=8.0):
+    """Oracle on config 3 rows (kv_append_paged + attention_decode_paged),
+    one core, rows taken in order until the budget is spent."""
     import oracle
     c = C3
     page, hkv, d = c["page"], c["hkv"], c["dim"]
@@ -572,22 +613,111 @@ def cpu_baseline_c3(torch, np, w, budget_s=12.0):
         vn = w["vn"][i:i + 1].float().cpu().numpy()
         sub = np.arange(npg, dtype=np.int32)[None, :]
         ln = lens[i:i + 1].astype(np.int32)
-        t0 = time.perf_counter()
-        oracle.kv_append_paged(kp, vp, sub, kn, vn, ln)
-        oracle.attention_decode_paged(q, kp, vp, sub, ln + 1)
-        spent += time.perf_counter() - t0
+        with one_core():
+            t0 = time.perf_counter()
+            oracle.kv_append_paged(kp, vp, sub, kn, vn, ln)
+            oracle.attention_decode_paged(q, kp, vp, sub, ln + 1)
+            spent += time.perf_counter() - t0
         done_rows += 1
         done_bytes += ((int(lens[i]) + 1) * hkv * d * 2 * 2 + 2 * c["hq"] * d * 2
                        + npg * 4 + 4 + 2 * 2 * hkv * d * 2)
         if spent >= budget_s:
             break
     gbs = done_bytes / spent / 1e9
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+    return {"config": "C3", "value": round(gbs, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port",
             "sample": f"{done_rows} of {len(lens)} config-3 rows "
                       f"(kv_append_paged + attention_decode_paged, "
                       f"{int(lens[:done_rows].sum()) + done_rows} tokens), "
                       f"oracle/oracle.cpp restatement of the reference *_cpu "
-                      f"functions, g++ -O2, single thread, {spent:.2f} s"}
+                      f"functions, g++ -O2, one pinned core, {spent:.2f} s; "
+                      f"bytes counted as on the GPU (bf16 K/V)"}
+
+
+def cpu_baselines_more(torch, np):
+    """C1, C2 and C5a on the oracle (one core), and a torch-CPU f32
+    composite of C1, C3-like rows and C5a on all allowed cores."""
+    import oracle
+    rng = np.random.default_rng(17)
+    out = []
+    # C1: contiguous decode, B=1, Hq=Hkv=32, T=4096 (fp16 bytes counted)
+    c = C1
+    q = rng.standard_normal((1, c["hq"], c["dim"])).astype(np.float32)
+    k = rng.standard_normal((1, c["hkv"], c["t"], c["dim"])).astype(np.float32)
+    v = rng.standard_normal((1, c["hkv"], c["t"], c["dim"])).astype(np.float32)
+    c1_bytes = 2 * c["hkv"] * c["t"] * c["dim"] * 2 + 2 * c["hq"] * c["dim"] * 2
+    with one_core():
+        t = timed(lambda: oracle.attention_decode(q, k, v))
+    out.append({"config": "C1", "value": round(c1_bytes / t / 1e9, 4), "unit": "GB/s",
+                "cores": 1, "kind": "port", "sample": f"the whole call, median of 3: "
+                f"{t * 1e3:.2f} ms (fp16 bytes counted)"})
+    qt, kt, vt = (torch.from_numpy(a) for a in (q, k, v))
+
+    def torch_attn():
+        s = torch.matmul(kt[0], qt[0].unsqueeze(-1)).squeeze(-1) / c["dim"] ** 0.5
+        return torch.matmul(torch.softmax(s, -1).unsqueeze(1), vt[0])
+    t = timed(torch_attn)
+    out.append({"config": "C1", "value": round(c1_bytes / t / 1e9, 4), "unit": "GB/s",
+                "cores": torch.get_num_threads(), "kind": "torch-cpu",
+                "sample": f"float32 softmax(qK^T/sqrt(D))V, whole call, median of 3: "
+                          f"{t * 1e3:.2f} ms"})
+    # C2: RMSNorm -> quantize -> W8A8 GEMM, N=11008, K=4096, per M
+    c = C2
+    wt = rng.integers(-127, 128, (c["n"], c["k"])).astype(np.int8)
+    sb = rng.uniform(1e-3, 1e-2, c["n"]).astype(np.float32)
+    wn = (rng.random(c["k"]) + 0.5).astype(np.float32)
+    res = []
+    for m in c["ms"]:
+        x = rng.standard_normal((m, c["k"])).astype(np.float32)
+
+        def chain():
+            qx, sx = oracle.quantize_int8(oracle.rmsnorm(x, wn, eps=1e-5))
+            return oracle.qgemm_perchannel(qx, sx, wt, sb)
+        with one_core():
+            t = timed(chain)
+        res.append({"m": m, "us_per_chain": round(t * 1e6, 1)})
+    out.append({"config": "C2", "value": res, "unit": "us per chain", "cores": 1,
+                "kind": "port", "sample": "rmsnorm -> quantize_int8 -> qgemm_perchannel "
+                "(oracle), each M, median of 3"})
+    # C5a: 4096 x 8192 x 28672 on a 64-row subset, extrapolated linearly
+    c = C5A
+    rows = 64
+    a = rng.integers(-127, 128, (rows, c["k"])).astype(np.int8)
+    b = rng.integers(-127, 128, (c["n"], c["k"])).astype(np.int8)
+    sb = rng.uniform(1e-3, 1e-2, c["n"]).astype(np.float32)
+    with one_core():
+        t0 = time.perf_counter()
+        oracle.qgemm_perchannel(a, 0.01, b, sb)
+        t = time.perf_counter() - t0
+    full = t * c["m"] / rows
+    out.append({"config": "C5a", "value": round(2.0 * c["m"] * c["n"] * c["k"] / full / 1e12, 5),
+                "unit": "TOPS", "cores": 1, "kind": "port",
+                "sample": f"{rows} of {c['m']} rows ({t:.2f} s), extrapolated linearly "
+                          f"to {full:.0f} s for the whole GEMM"})
+    af, bf_ = torch.from_numpy(a.astype(np.float32)), torch.from_numpy(b.astype(np.float32))
+    t = timed(lambda: torch.matmul(af, bf_.t()))
+    full = t * c["m"] / rows
+    out.append({"config": "C5a", "value": round(2.0 * c["m"] * c["n"] * c["k"] / full / 1e12, 4),
+                "unit": "TOPS", "cores": torch.get_num_threads(), "kind": "torch-cpu",
+                "sample": f"float32 matmul of the int8 values (not bit-exact past 2^24), "
+                          f"{rows} rows, median of 3 ({t * 1e3:.1f} ms), extrapolated to "
+                          f"{c['m']} rows"})
+    # C3-like rows on torch-CPU: 4 sequences of 8192 tokens, 32/8 heads
+    b4, hq, hkv, d, tt = 4, C3["hq"], C3["hkv"], C3["dim"], 8192
+    qq = torch.randn(b4, hkv, hq // hkv, d)
+    kk = torch.randn(b4, hkv, tt, d)
+    vv = torch.randn(b4, hkv, tt, d)
+
+    def torch_gqa():
+        s = torch.matmul(qq, kk.transpose(-1, -2)) / d ** 0.5
+        return torch.matmul(torch.softmax(s, -1), vv)
+    t = timed(torch_gqa)
+    c3b = 2 * b4 * hkv * tt * d * 2 + 2 * b4 * hq * d * 2
+    out.append({"config": "C3", "value": round(c3b / t / 1e9, 4), "unit": "GB/s",
+                "cores": torch.get_num_threads(), "kind": "torch-cpu",
+                "sample": f"float32 GQA decode over 4 rows of 8192 tokens (bf16 bytes "
+                          f"counted), median of 3: {t * 1e3:.2f} ms"})
+    return out
 
 
 def traffic_for(key):
@@ -727,10 +857,20 @@ def main():
         torch.cuda.empty_cache()
 
     cpu = None
-    if not args.no_cpu and args.only is None:
+    if not args.no_cpu and args.only in (None, "cpu"):
         w2 = make_c3(torch, np, dev)  # pools were released for the GEMM leg
-        cpu = cpu_baseline_c3(torch, np, w2)
-        log(f"cpu baseline: {cpu['value']} GB/s over {cpu['sample']}")
+        c3 = cpu_baseline_c3(torch, np, w2)
+        del w2
+        torch.cuda.empty_cache()
+        log(f"cpu baseline: {c3['value']} GB/s over {c3['sample']}")
+        torch.set_num_threads(len(os.sched_getaffinity(0)))
+        more = cpu_baselines_more(torch, np)
+        for e in more:
+            log(f"cpu {e['config']} {e['kind']}: {e['value']} {e['unit']} ({e['cores']} cores)")
+        cpu = dict(c3)
+        cpu.pop("config")
+        cpu["host"] = dict(host_facts(), torch_threads=torch.get_num_threads())
+        cpu["configs"] = [c3] + more
 
     line = {
         "metric": "flash-decode KV GB/s (% HBM peak); W8A8 GEMM TOPS (% int8 MFMA peak)",

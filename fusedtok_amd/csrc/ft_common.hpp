@@ -99,6 +99,8 @@ enum class Tune : int {
     QgemmDecRegs,          // FT_QGEMM_DEC_REGS: register-operand decode kernel
     QgemmKsplit,           // FT_QGEMM_KSPLIT: skinny kernel K split
     QgemmSkRegs,           // FT_QGEMM_SK_REGS: register-operand skinny kernel
+    QgemmSkWaves,          // FT_QGEMM_SK_WAVES: 4 or 8 waves (64 / 128 columns)
+    QgemmSkStages,         // FT_QGEMM_SK_STAGES: LDS ring depth, 2 or 3
     QgemmBig,              // FT_QGEMM_BIG: 1 64-byte DMA slabs, 2 register-staged
     QgemmBand,             // FT_QGEMM_BAND: big-tile band height
     RmsqSplit,             // FT_RMSQ_SPLIT: rmsnorm_quant in two launches

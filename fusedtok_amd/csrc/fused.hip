@@ -52,11 +52,23 @@ __device__ __forceinline__ float4 rms_in4(const T* x, const T* r, size_t off) {
     return v;
 }
 
+// x + r for kernels instantiated with (RES) and without a residual: the
+// loads of a row are issued together, with no branch between them (a
+// runtime residual test between loads made the compiler wait after each
+// chunk, one memory round trip per chunk instead of one per row).
+template <bool RES>
+__device__ __forceinline__ float4 rms_add4(float4 xv, float4 rv) {
+    if constexpr (RES)
+        return make_float4(xv.x + rv.x, xv.y + rv.y, xv.z + rv.z, xv.w + rv.w);
+    else
+        return xv;
+}
+
 constexpr int kRowChunks = 4;  // 4-element chunks per thread held in registers
 
 // One workgroup per row: sum of squares -> inv, then the row's max |y|. A row
 // of up to 4096 columns stays in registers between the two passes.
-template <typename T>
+template <typename T, bool RES>
 __global__ __launch_bounds__(kFNT) void rmsq_rows(
     const T* __restrict__ x, const T* __restrict__ r, const float* __restrict__ w,
     RowStat* __restrict__ stat, int cols, float eps) {
@@ -66,15 +78,18 @@ __global__ __launch_bounds__(kFNT) void rmsq_rows(
     float m = 0.0f;
     float inv;
     if (chunks <= kFNT * kRowChunks) {
-        // the row and the weights in one round trip
-        float4 v[kRowChunks], wc[kRowChunks];
+        // the row, its residual and the weights in one round trip (indices
+        // clamped to a real chunk; chunks past the row are not used below)
+        float4 v[kRowChunks], rv[kRowChunks], wc[kRowChunks];
 #pragma unroll
         for (int j = 0; j < kRowChunks; ++j) {
-            const int c = threadIdx.x + j * kFNT;
-            v[j] = c < chunks ? rms_in4(x, r, base + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
-            wc[j] = c < chunks ? *reinterpret_cast<const float4*>(w + 4 * c)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int c = min((int)threadIdx.x + j * kFNT, chunks - 1);
+            v[j] = St<T>::ld4(x + base + 4 * c);
+            if constexpr (RES) rv[j] = St<T>::ld4(r + base + 4 * c);
+            wc[j] = *reinterpret_cast<const float4*>(w + 4 * c);
         }
+#pragma unroll
+        for (int j = 0; j < kRowChunks; ++j) v[j] = rms_add4<RES>(v[j], rv[j]);
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < kRowChunks; ++j) {
@@ -123,7 +138,7 @@ __global__ __launch_bounds__(kFNT) void rmsq_rows(
 // Fold of the row maxima -> scale, then the codes. Each thread's first
 // element (x, r, w and its row's inv) is loaded before the fold, so the fold's
 // reads and the data reads share one round trip.
-template <typename T>
+template <typename T, bool RES>
 __global__ __launch_bounds__(kFNT) void rmsq_quant(
     const T* __restrict__ x, const T* __restrict__ r, const float* __restrict__ w,
     const RowStat* __restrict__ stat, signed char* __restrict__ q,
@@ -132,15 +147,17 @@ __global__ __launch_bounds__(kFNT) void rmsq_quant(
     const long long n4 = (long long)rows * cols / 4;
     const int cols4 = cols >> 2;
     const long long e0 = (long long)blockIdx.x * kFNT + threadIdx.x;
-    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), w0 = v0;
-    float inv0 = 0.0f;
-    if (e0 < n4) {
-        const int row = (int)(e0 / cols4);
-        const int c = (int)(e0 - (long long)row * cols4) * 4;
-        v0 = rms_in4(x, r, (size_t)row * cols + c);
-        w0 = *reinterpret_cast<const float4*>(w + c);
-        inv0 = stat[row].inv;
-    }
+    // this thread's first element (clamped to a real one) with its row's
+    // inv, loaded without branches so they share the fold's round trip
+    const long long ec = e0 < n4 ? e0 : n4 - 1;
+    const int row0 = (int)(ec / cols4);
+    const int c0 = (int)(ec - (long long)row0 * cols4) * 4;
+    float4 v0 = St<T>::ld4(x + (size_t)row0 * cols + c0);
+    float4 rv0;
+    if constexpr (RES) rv0 = St<T>::ld4(r + (size_t)row0 * cols + c0);
+    const float4 w0 = *reinterpret_cast<const float4*>(w + c0);
+    const float inv0 = stat[row0].inv;
+    v0 = rms_add4<RES>(v0, rv0);
     float m = 0.0f;
     for (int i = threadIdx.x; i < rows; i += kFNT) m = fmaxf(m, stat[i].absmax);
     m = block_max<kFNT>(m, red);
@@ -185,7 +202,7 @@ constexpr int kRmsqRows = 1;    // rows per lane
 constexpr int kRmsqMaxRows = 4 * kRmsqRows;
 constexpr int kRmsqMaxCols = 4 * kFNT * kRowChunks;
 
-template <typename T>
+template <typename T, bool RES>
 __global__ __launch_bounds__(4 * kFNT) void rmsq_small(
     const T* __restrict__ x, const T* __restrict__ r, const float* __restrict__ w,
     signed char* __restrict__ q, float* __restrict__ scale_out, int rows, int cols,
@@ -201,22 +218,23 @@ __global__ __launch_bounds__(4 * kFNT) void rmsq_small(
     float4 v[kRmsqRows][kRowChunks];
     float4 wc[kRowChunks];
 #pragma unroll
-    for (int j = 0; j < kRowChunks; ++j) {
-        const int c = t + j * kFNT;
-        wc[j] = c < chunks ? *reinterpret_cast<const float4*>(w + 4 * c)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    for (int j = 0; j < kRowChunks; ++j)
+        wc[j] = *reinterpret_cast<const float4*>(w + 4 * min(t + j * kFNT, chunks - 1));
+    float4 rv[kRmsqRows][kRowChunks];
 #pragma unroll
     for (int i = 0; i < kRmsqRows; ++i) {
-        const int row = lane_g + i * G;
+        const int row = min(lane_g + i * G, rows - 1);
 #pragma unroll
         for (int j = 0; j < kRowChunks; ++j) {
-            const int c = t + j * kFNT;
-            v[i][j] = (row < rows && c < chunks)
-                          ? rms_in4(x, r, (size_t)row * cols + 4 * c)
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int c = min(t + j * kFNT, chunks - 1);  // clamped; unused past the row
+            v[i][j] = St<T>::ld4(x + (size_t)row * cols + 4 * c);
+            if constexpr (RES) rv[i][j] = St<T>::ld4(r + (size_t)row * cols + 4 * c);
         }
     }
+#pragma unroll
+    for (int i = 0; i < kRmsqRows; ++i)
+#pragma unroll
+        for (int j = 0; j < kRowChunks; ++j) v[i][j] = rms_add4<RES>(v[i][j], rv[i][j]);
 #pragma unroll
     for (int i = 0; i < kRmsqRows; ++i) {
         float acc = 0.0f;
@@ -294,17 +312,27 @@ void rmsnorm_quant_run(const T* x, const float* w, const T* r, signed char* q,
         (uintptr_t)q % 4)
         inval("rmsnorm_quant: operands must be aligned to 4 elements");
     if (rows <= kRmsqMaxRows && cols <= kRmsqMaxCols && tune(Tune::RmsqSplit, 0) == 0) {
-        rmsq_small<T><<<1, (unsigned)(rows * kFNT), 0, s>>>(x, r, w, q, scale_out, rows,
-                                                             cols, eps);
+        if (r)
+            rmsq_small<T, true><<<1, (unsigned)(rows * kFNT), 0, s>>>(x, r, w, q, scale_out,
+                                                                       rows, cols, eps);
+        else
+            rmsq_small<T, false><<<1, (unsigned)(rows * kFNT), 0, s>>>(x, r, w, q, scale_out,
+                                                                        rows, cols, eps);
         launch_check("rmsnorm_quant small kernel launch");
         return;
     }
     RowStat* stat = (RowStat*)scratch(Scratch::QuantMax, (size_t)rows * sizeof(RowStat), s);
-    rmsq_rows<T><<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps);
+    if (r)
+        rmsq_rows<T, true><<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps);
+    else
+        rmsq_rows<T, false><<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps);
     launch_check("rmsnorm_quant row kernel launch");
     const long long n4 = (long long)rows * cols / 4;
     const unsigned grid = grid_1d(n4, kFNT, dev_info().cu_count * 4);
-    rmsq_quant<T><<<grid, kFNT, 0, s>>>(x, r, w, stat, q, scale_out, rows, cols);
+    if (r)
+        rmsq_quant<T, true><<<grid, kFNT, 0, s>>>(x, r, w, stat, q, scale_out, rows, cols);
+    else
+        rmsq_quant<T, false><<<grid, kFNT, 0, s>>>(x, r, w, stat, q, scale_out, rows, cols);
     launch_check("rmsnorm_quant quantize kernel launch");
 }
 

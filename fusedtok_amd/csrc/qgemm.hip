@@ -240,7 +240,7 @@ __global__ __launch_bounds__(256) void qgemv_dot4(const i8* __restrict__ a,
 // writes the codes and the scale. The dot products and the epilogue are
 // qgemv_dot4's for M = 1 with sa = the computed scale.
 // ---------------------------------------------------------------------------
-template <typename T, int OUT>
+template <typename T, bool RES, int OUT>
 __global__ __launch_bounds__(256) void rmsq_gemv(
     const T* __restrict__ x, const T* __restrict__ res, const float* __restrict__ wn,
     float eps, const i8* __restrict__ b, Epi e, int n, int k, i8* __restrict__ q_out,
@@ -256,6 +256,9 @@ __global__ __launch_bounds__(256) void rmsq_gemv(
     const i32x4 z = {0, 0, 0, 0};
 
     i32x4 w[kGemvChunks][kGemvRows];
+    // every load is issued, rows and K pieces clamped to real ones, so no
+    // branch separates the loads and the compiler's wait counts stay exact;
+    // a piece past K meets a zero activation piece below
     auto load_w = [&](int j0) {
 #pragma unroll
         for (int c = 0; c < kGemvChunks; ++c) {
@@ -263,31 +266,35 @@ __global__ __launch_bounds__(256) void rmsq_gemv(
 #pragma unroll
             for (int r = 0; r < kGemvRows; ++r) {
                 const int row = min(j0 + r, n - 1);
-                w[c][r] = kk < k ? __builtin_nontemporal_load(
-                                       reinterpret_cast<const i32x4*>(b + (size_t)row * k + kk))
-                                 : z;
+                w[c][r] = __builtin_nontemporal_load(
+                    reinterpret_cast<const i32x4*>(b + (size_t)row * k + min(kk, k - 16)));
             }
         }
     };
-    if (j_first < n) load_w(j_first);
-
-    // normalise and quantise the row (rmsnorm_quant's order)
+    // the row, its residual and the norm weights first, then this wave's
+    // weight rows: loads complete in issue order, so the normalisation
+    // below waits only for the row and runs while the weights stream in
     const int chunks = k >> 2;
-    float4 v[4], wc[4];
+    float4 v[4], rv[4], wc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int c = tid + 256 * j;
-        v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-        wc[j] = v[j];
-        if (c < chunks) {
-            v[j] = St<T>::ld4(x + 4 * c);
-            if (res) {
-                const float4 rv = St<T>::ld4(res + 4 * c);
-                v[j].x += rv.x; v[j].y += rv.y; v[j].z += rv.z; v[j].w += rv.w;
-            }
-            wc[j] = *reinterpret_cast<const float4*>(wn + 4 * c);
+        const int c = min(tid + 256 * j, chunks - 1);  // clamped: a real chunk
+        v[j] = St<T>::ld4(x + 4 * c);
+        if constexpr (RES) rv[j] = St<T>::ld4(res + 4 * c);
+        wc[j] = *reinterpret_cast<const float4*>(wn + 4 * c);
+    }
+    // a wave past the last column tile loads clamped real rows it never uses
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(j_first);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (RES) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[j].x += rv[j].x; v[j].y += rv[j].y; v[j].z += rv[j].z; v[j].w += rv[j].w;
         }
     }
+
+    // normalise and quantise the row (rmsnorm_quant's order)
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -690,8 +697,9 @@ constexpr int kSlChunk = 256;
 constexpr int kSlSteps = kSlChunk / 64;
 
 // one chunk of qgemm_skinny_lds: this wave's 4 W instructions (non-temporal)
-// and its share of the A instructions, into the stage at dst
-template <int MT>
+// and its share of the 4 MT A instructions (instruction j = wave + NW i
+// covers A rows 4 j .. 4 j + 3), into the stage at dst
+template <int MT, int NW>
 __device__ __forceinline__ void sl_issue(const i8* a, const i8* b, const size_t* aoff,
                                          const size_t* boff, char* dst, size_t kc, int wave) {
     constexpr int kArows = 16 * MT;
@@ -701,25 +709,26 @@ __device__ __forceinline__ void sl_issue(const i8* a, const i8* b, const size_t*
             b + boff[i] + kc, (lds_void_p)(dst + (kArows + 16 * wave + 4 * i) * kSlChunk), 16,
             0, 2);
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+    for (int i = 0; i < 4 * MT / NW; ++i)
         __builtin_amdgcn_global_load_lds(a + aoff[i] + kc,
-                                         (lds_void_p)(dst + 4 * (wave + 4 * i) * kSlChunk), 16,
+                                         (lds_void_p)(dst + 4 * (wave + NW * i) * kSlChunk), 16,
                                          0, 0);
 }
 
-template <int MT, int NSTAGE, int OUT>
-__global__ __launch_bounds__(256) void qgemm_skinny_lds(
+template <int MT, int NSTAGE, int NW, int OUT>
+__global__ __launch_bounds__(64 * NW) void qgemm_skinny_lds(
     const i8* __restrict__ a, const i8* __restrict__ b, Epi e, int m, int n,
     int k, int ksplit, int* __restrict__ part) {
     constexpr int kArows = 16 * MT;
-    constexpr int kStage = (kArows + 64) * kSlChunk;
-    constexpr int kAIns = kArows / 4 / 4;  // A DMA instructions per wave per chunk
+    constexpr int kStage = (kArows + 16 * NW) * kSlChunk;
+    constexpr int kAIns = kArows / 4 / NW;  // A DMA instructions per wave per chunk
     static_assert(NSTAGE == 2 || NSTAGE == 3, "stage count");
+    static_assert(kAIns * NW * 4 == kArows, "A rows split evenly over the waves");
     __shared__ __attribute__((aligned(16))) char lds[NSTAGE * kStage];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
-    const int n0 = (blockIdx.x * 4 + wave) * 16;
+    const int n0 = (blockIdx.x * NW + wave) * 16;
     const bool live = n0 < n;
     const int ks = blockIdx.y;
     const int chunks = k / kSlChunk;
@@ -731,7 +740,7 @@ __global__ __launch_bounds__(256) void qgemm_skinny_lds(
     size_t aoff[kAIns], boff[4];
 #pragma unroll
     for (int i = 0; i < kAIns; ++i) {
-        const int row = 4 * (wave + 4 * i) + drow;  // A row staged by this lane
+        const int row = 4 * (wave + NW * i) + drow;  // A row staged by this lane
         aoff[i] = (size_t)min(row, m - 1) * k + 16 * ((lane & 15) ^ (row & 15));
     }
 #pragma unroll
@@ -752,7 +761,8 @@ __global__ __launch_bounds__(256) void qgemm_skinny_lds(
 #pragma unroll
     for (int j = 0; j < NSTAGE - 1; ++j)
         if (c0 + j < c1)
-            sl_issue<MT>(a, b, aoff, boff, lds + j * kStage, (size_t)(c0 + j) * kSlChunk, wave);
+            sl_issue<MT, NW>(a, b, aoff, boff, lds + j * kStage, (size_t)(c0 + j) * kSlChunk,
+                             wave);
     int st = 0;
     for (int c = c0; c < c1; ++c) {
         // this wave's copies of chunk c landed (the later chunks may still fly)
@@ -768,7 +778,7 @@ __global__ __launch_bounds__(256) void qgemm_skinny_lds(
         __builtin_amdgcn_sched_barrier(0);
         const int nxt = c + NSTAGE - 1;
         if (nxt < c1)
-            sl_issue<MT>(a, b, aoff, boff, lds + ((st + NSTAGE - 1) % NSTAGE) * kStage,
+            sl_issue<MT, NW>(a, b, aoff, boff, lds + ((st + NSTAGE - 1) % NSTAGE) * kStage,
                          (size_t)nxt * kSlChunk, wave);
         const unsigned base = lds0 + st * kStage;
         i32x4 fw[kSlSteps], fa[MT][kSlSteps];
@@ -1913,33 +1923,46 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
     }
     if ((m <= 64 && force != 2 && force != 4) || force == 1) {
         if (m > 64) inval("skinny qgemm supports m <= 64");
-        const int col_wgs = (n + 63) / 64;
-        const int chunks = (k + kSkChunk - 1) / kSkChunk;  // 1 KB K chunks
         const int cus = dev_info().cu_count;
-        // no K split once the column workgroups alone cover every CU (M=64,
-        // N=28672, K=4096: 38.9 us against 45.0 us split in two, which also
-        // needs the fold launch); below that, enough workgroups for 2 per CU
-        int ksplit = col_wgs >= cus
+        const int mt = (m + 15) / 16;
+        const bool ring = k % kSlChunk == 0 && tune(Tune::QgemmSkRegs, 0) == 0;
+        // LDS ring: NW waves of 16 columns each; the ring holds the A rows
+        // and the NW * 16 W rows of `stages` 256-byte K chunks
+        const int nw = ring && mt >= 2 && tune(Tune::QgemmSkWaves, 4) == 8 ? 8 : 4;
+        const int stages = ring && tune(Tune::QgemmSkStages, 2) == 3 ? 3 : 2;
+        const int lds_bytes = (16 * (mt <= 1 ? 1 : mt <= 2 ? 2 : 4) + 16 * nw) * kSlChunk * stages;
+        const int per_cu = ring ? std::max(1, (160 << 10) / lds_bytes) : 2;
+        const int col_wgs = (n + 16 * nw - 1) / (16 * nw);
+        // K chunks the split divides: 256-byte ring chunks, 1 KB register chunks
+        const int chunks = ring ? k / kSlChunk : (k + kSkChunk - 1) / kSkChunk;
+        // no K split once the column workgroups alone fill 3/4 of the
+        // resident slots (M=64, N=28672, K=4096: 38.9 us against 45.0 us
+        // split in two, which also needs the fold launch); below that,
+        // enough workgroups to fill them
+        const int slots = per_cu * cus;
+        int ksplit = 4 * col_wgs >= 3 * slots
                          ? 1
-                         : std::max(1, std::min((2 * cus + col_wgs - 1) / col_wgs, chunks));
+                         : std::max(1, std::min((slots + col_wgs - 1) / col_wgs, chunks));
         const int forced_split = tune(Tune::QgemmKsplit, 0);
         if (forced_split > 0) ksplit = std::min(forced_split, chunks);
         if (ksplit > 65535) ksplit = 65535;
-        const int mt = (m + 15) / 16;
         int* part = nullptr;
         if (ksplit > 1)
             part = (int*)scratch(Scratch::GemmPartials,
                                  (size_t)ksplit * m * n * sizeof(int), s);
         dim3 grid(col_wgs, ksplit);
-        // operands through a 2-stage LDS ring in whole lines (C4 layer: 462 us
-        // against 477 us with register W operands; 3 stages 470 us: 96 KB of
-        // LDS leaves one workgroup per CU)
-        if (k % kSlChunk == 0 && tune(Tune::QgemmSkRegs, 0) == 0) {
-#define FT_SK_LDS(MT) \
-    qgemm_skinny_lds<MT, 2, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part)
-            if (mt <= 1) FT_SK_LDS(1);
-            else if (mt <= 2) FT_SK_LDS(2);
-            else FT_SK_LDS(4);
+        if (ring) {
+#define FT_SK_LDS(MT, S, NW) \
+    qgemm_skinny_lds<MT, S, NW, OUT><<<grid, 64 * NW, 0, s>>>(a, b, e, m, n, k, ksplit, part)
+            if (mt <= 1) {
+                if (stages == 3) FT_SK_LDS(1, 3, 4); else FT_SK_LDS(1, 2, 4);
+            } else if (mt <= 2) {
+                if (nw == 8) { if (stages == 3) FT_SK_LDS(2, 3, 8); else FT_SK_LDS(2, 2, 8); }
+                else { if (stages == 3) FT_SK_LDS(2, 3, 4); else FT_SK_LDS(2, 2, 4); }
+            } else {
+                if (nw == 8) { if (stages == 3) FT_SK_LDS(4, 3, 8); else FT_SK_LDS(4, 2, 8); }
+                else { if (stages == 3) FT_SK_LDS(4, 3, 4); else FT_SK_LDS(4, 2, 4); }
+            }
 #undef FT_SK_LDS
         } else if (mt <= 1)
             qgemm_skinny<1, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part);
@@ -2101,9 +2124,16 @@ int ft_rmsnorm_qgemm_launch(const void* x, int x_dtype, const float* w,
         const long long waves = std::min<long long>((n + ft::kGemvRows - 1) / ft::kGemvRows,
                                                     (long long)ft::dev_info().cu_count * 16);
         const unsigned grid = (unsigned)((waves + 3) / 4);
-#define FT_RQG(T, O)                                                                         \
-    ft::rmsq_gemv<T, O><<<grid, 256, 0, s>>>((const T*)x, (const T*)residual, w, eps, bq, e, \
-                                             n, k, q, scale_out)
+#define FT_RQG(T, O)                                                                       \
+    do {                                                                                   \
+        if (residual)                                                                      \
+            ft::rmsq_gemv<T, true, O><<<grid, 256, 0, s>>>((const T*)x, (const T*)residual, \
+                                                           w, eps, bq, e, n, k, q,         \
+                                                           scale_out);                     \
+        else                                                                               \
+            ft::rmsq_gemv<T, false, O><<<grid, 256, 0, s>>>((const T*)x, nullptr, w, eps,   \
+                                                            bq, e, n, k, q, scale_out);    \
+    } while (0)
 #define FT_RQG_T(T)                                   \
     do {                                              \
         if (out == ft::kOutF32) FT_RQG(T, ft::kOutF32);   \

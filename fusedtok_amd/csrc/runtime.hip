@@ -71,6 +71,7 @@ constexpr const char* kTuneNames[(int)Tune::kCount] = {
     "FT_ATTN_FORCE_GENERIC", "FT_ATTN_SEGS",       "FT_ATTN_MIN_SEG",
     "FT_ATTN_CHUNK",         "FT_QGEMM_KERNEL",    "FT_QGEMM_DEC_KW",
     "FT_QGEMM_DEC_REGS",     "FT_QGEMM_KSPLIT",    "FT_QGEMM_SK_REGS",
+    "FT_QGEMM_SK_WAVES",     "FT_QGEMM_SK_STAGES",
     "FT_QGEMM_BIG",          "FT_QGEMM_BAND",      "FT_RMSQ_SPLIT",
     "FT_RMSQ_GEMV_SPLIT",    "FT_PREFILL_FORCE_GENERIC", "FT_ARG_SLICES",
     "FT_SMP_SINGLE",         "FT_SMP_SLICES"};
