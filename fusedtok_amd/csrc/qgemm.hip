@@ -801,10 +801,10 @@ __global__ __launch_bounds__(64 * NW) void qgemm_skinny_lds(
                 acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[t][u], fw[u], acc[t], 0, 0, 0);
         st = st + 1 == NSTAGE ? 0 : st + 1;
     }
-    if (!live) return;
     const int col = n0 + r;
-    if (col >= n) return;
+    const bool own = live && col < n;
     if (ksplit == 1) {
+        if (!own) return;
         const float sa = epi_sa(e);
 #pragma unroll
         for (int t = 0; t < MT; ++t)
@@ -813,8 +813,10 @@ __global__ __launch_bounds__(64 * NW) void qgemm_skinny_lds(
                 const int row = 16 * t + 4 * g + i;
                 if (row < m) epi_store<OUT>(e, sa, n, row, col, acc[t][i]);
             }
-    } else {
-        int* mine = part + (size_t)ks * m * n;
+        return;
+    }
+    int* mine = part + (size_t)ks * m * n;
+    if (own) {
 #pragma unroll
         for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -1928,8 +1930,16 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         const bool ring = k % kSlChunk == 0 && tune(Tune::QgemmSkRegs, 0) == 0;
         // LDS ring: NW waves of 16 columns each; the ring holds the A rows
         // and the NW * 16 W rows of `stages` 256-byte K chunks
-        const int nw = ring && mt >= 2 && tune(Tune::QgemmSkWaves, 4) == 8 ? 8 : 4;
-        const int stages = ring && tune(Tune::QgemmSkStages, 2) == 3 ? 3 : 2;
+        // 3 ring stages (two chunks in flight; one workgroup per CU). 8 waves
+        // (128 columns) when the column workgroups alone cover 3/4 of the CUs:
+        // M = 64, graph replays, weights cycled past the last-level cache:
+        // N=28672 K=4096 28.5 us against 30.2 with 4 waves and 2 stages;
+        // N=4096 K=4096 9.9 vs 10.8; N=4096 K=14336 17.3 vs 19.6;
+        // N=6144 K=4096 12.3 vs 13.9 (K split 2)
+        const int stages = ring ? (tune(Tune::QgemmSkStages, 3) == 2 ? 2 : 3) : 2;
+        const int wide = (n + 127) / 128;
+        const int nw_pick = 4 * wide >= 3 * cus ? 8 : 4;
+        const int nw = ring && mt >= 2 && tune(Tune::QgemmSkWaves, nw_pick) == 8 ? 8 : 4;
         const int lds_bytes = (16 * (mt <= 1 ? 1 : mt <= 2 ? 2 : 4) + 16 * nw) * kSlChunk * stages;
         const int per_cu = ring ? std::max(1, (160 << 10) / lds_bytes) : 2;
         const int col_wgs = (n + 16 * nw - 1) / (16 * nw);
@@ -1937,15 +1947,21 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         const int chunks = ring ? k / kSlChunk : (k + kSkChunk - 1) / kSkChunk;
         // no K split once the column workgroups alone fill 3/4 of the
         // resident slots (M=64, N=28672, K=4096: 38.9 us against 45.0 us
-        // split in two, which also needs the fold launch); below that,
-        // enough workgroups to fill them
+        // split in two, which also needs the fold launch); below that, as
+        // many splits as fit in one round of resident workgroups (a partial
+        // second round costs a whole extra round: N=6144, split 3 on 256
+        // slots, 14.2 us against 12.3 with split 2)
         const int slots = per_cu * cus;
         int ksplit = 4 * col_wgs >= 3 * slots
                          ? 1
-                         : std::max(1, std::min((slots + col_wgs - 1) / col_wgs, chunks));
+                         : std::max(1, std::min(slots / col_wgs, chunks));
         const int forced_split = tune(Tune::QgemmKsplit, 0);
         if (forced_split > 0) ksplit = std::min(forced_split, chunks);
         if (ksplit > 65535) ksplit = 65535;
+        // the K split's int32 partials are folded by a second launch: a fold
+        // by the last workgroup of each column tile (device-scope release /
+        // acquire fences around a counter) measured 3-4x slower on every
+        // split shape (N=6144 K=4096: 37.0 against 12.0 us)
         int* part = nullptr;
         if (ksplit > 1)
             part = (int*)scratch(Scratch::GemmPartials,

@@ -286,19 +286,26 @@ def test_skinny_kernel_bit_exact(m, n, k, split, tuning):
     assert torch.equal(y.cpu(), ref)
 
 
-@pytest.mark.parametrize("regs", [0, 1])
+@pytest.mark.parametrize("variant", ["regs", "w4s2", "w4s3", "w8s2", "w8s3"])
 @pytest.mark.parametrize("m,n,k,split", [
     (17, 200, 256, 0),      # one chunk, one 16-row tile
     (33, 300, 1280, 0),     # three tiles (MT = 4 with one row past M), ragged N
     (64, 1000, 3072, 3),    # forced split in three
     (20, 70, 2304, 2),      # split into 5 + 4 chunks; ragged N (dead waves)
     (64, 16448, 512, 0),    # 257 column workgroups, no split
+    (40, 28672, 1024, 0),   # MT = 3 rows of tiles, 8 waves by default (wide N)
+    (64, 6144, 4096, 2),    # C4's QKV shape with its default split
 ])
-def test_skinny_lds_ring_bit_exact(regs, m, n, k, split, tuning):
-    # the LDS-ring skinny kernel (K % 256 == 0) against the oracle, and the
-    # register-operand kernel on the same shapes (FT_QGEMM_SK_REGS=1)
-    if regs:
+def test_skinny_lds_ring_bit_exact(variant, m, n, k, split, tuning):
+    # the LDS-ring skinny kernel (K % 256 == 0) against the oracle in each
+    # shape of workgroup (4 waves / 64 columns or 8 waves / 128 columns) and
+    # ring depth (2 or 3 stages), and the register-operand kernel on the
+    # same shapes (FT_QGEMM_SK_REGS=1)
+    if variant == "regs":
         tuning("FT_QGEMM_SK_REGS", 1)
+    else:
+        tuning("FT_QGEMM_SK_WAVES", int(variant[1]))
+        tuning("FT_QGEMM_SK_STAGES", int(variant[3]))
     if split:
         tuning("FT_QGEMM_KSPLIT", split)
     rng = np.random.default_rng(m * 3 + n + k + split)
