@@ -85,6 +85,7 @@ __all__ = [
     "qgemm_i32",
     "attention_decode",
     "attention_decode_paged",
+    "attention_decode_paged_quant",
     "attention_prefill",
     "kv_append",
     "kv_append_paged",
@@ -372,6 +373,34 @@ def attention_decode_paged(q, k_pool, v_pool, block_table, lens=None, *,
             c.ptr("q"), c.ptr("k_pool"), c.ptr("v_pool"), c.ptr("block_table"),
             c.ptr("lens"), out.data_ptr(), c.B, c.Hq, c.Hkv, c.P, c.S, c.D, _stream())
     return out
+
+
+def attention_decode_paged_quant(q, k_pool, v_pool, block_table, lens=None, *,
+                                 device_scale=False):
+    """``out = attention_decode_paged(q, k_pool, v_pool, block_table, lens)``
+    and ``quantize_int8(out)`` in one call, bit for bit: returns ``(out,
+    codes, scale)`` with codes int8 of out's shape (the o_proj GEMM's input).
+    On the split-stream attention path the attention kernels also keep the
+    max |out| of each (sequence, head), so the quantize is a single launch.
+    GPU tensors only; ``device_scale=True`` returns the scale as a 1-element
+    GPU float32 tensor without synchronising. Build addition: the reference
+    runs the two launches one after the other."""
+    c = _DECODE_PAGED.bind(q=q, k_pool=k_pool, v_pool=v_pool, block_table=block_table,
+                           lens=lens)
+    if not c.on_gpu:
+        raise TypeError("attention_decode_paged_quant takes GPU tensors (fused ops have no "
+                        "host path)")
+    out = torch.empty((c.B, c.Hq, c.D), dtype=c.q.dtype, device=c.device)
+    codes = torch.empty((c.B, c.Hq, c.D), dtype=torch.int8, device=c.device)
+    scale = torch.empty(1, dtype=torch.float32, device=c.device)
+    if c.B * c.Hq == 0:
+        scale.fill_(1.0)   # no values: the all-zero scale
+    else:
+        _fusedtok.attention_decode_paged_quant_launch(
+            c.ptr("q"), c.ptr("k_pool"), c.ptr("v_pool"), c.ptr("block_table"),
+            c.ptr("lens"), out.data_ptr(), _CODE[c.q.dtype], codes.data_ptr(),
+            scale.data_ptr(), c.B, c.Hq, c.Hkv, c.P, c.S, c.D, _stream())
+    return (out, codes, scale) if device_scale else (out, codes, float(scale))
 
 
 # ---------------------------------------------------------------------------

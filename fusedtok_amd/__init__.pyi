@@ -28,6 +28,7 @@ __all__ = [
     "qgemm_i32",
     "attention_decode",
     "attention_decode_paged",
+    "attention_decode_paged_quant",
     "attention_prefill",
     "kv_append",
     "kv_append_paged",
@@ -60,6 +61,11 @@ def attention_decode(q: Array, k_cache: Array, v_cache: Array,
 def attention_decode_paged(q: Array, k_pool: Array, v_pool: Array,
                            block_table: IntArray, lens: Optional[IntArray] = ..., *,
                            cuda: bool = ...) -> Array: ...
+def attention_decode_paged_quant(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                                 block_table: torch.Tensor,
+                                 lens: Optional[torch.Tensor] = ..., *,
+                                 device_scale: bool = ...
+                                 ) -> Tuple[torch.Tensor, torch.Tensor, Scale]: ...
 def attention_prefill(q: Array, k: Array, v: Array, causal: bool = ..., *,
                       cuda: bool = ...) -> Array: ...
 def kv_append(k_cache: Array, v_cache: Array, k_new: Array, v_new: Array,

@@ -365,8 +365,8 @@ void attn_decode_stream(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int* __restrict__ table, const int* __restrict__ lens,
     float* __restrict__ ws_ml, float* __restrict__ ws_acc,
-    long long* __restrict__ pref_out, T* __restrict__ out, int batch, int hq,
-    int hkv, int group, int rows_or_page, int page_shift, int tbl_width,
+    long long* __restrict__ pref_out, T* __restrict__ out, float* __restrict__ amax,
+    int batch, int hq, int hkv, int group, int rows_or_page, int page_shift, int tbl_width,
     int span, float scale_log2, int min_seg) {
     using M = Mfma<T>;
     using V8 = typename M::v8;
@@ -640,8 +640,16 @@ void attn_decode_stream(
             }
             if (whole) {
                 const float inv = 1.0f / lsum;
-                St<T>::st4(orow + (size_t)hh * D + 4 * d4,
-                           make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv));
+                const float4 ov = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+                St<T>::st4(orow + (size_t)hh * D + 4 * d4, ov);
+                if (amax) {
+                    // max |stored value| of this head: its D / 4 = 32 chunks
+                    // sit in 32 consecutive lanes (a half wave)
+                    float m = stored_absmax4<T>(ov);
+#pragma unroll
+                    for (int o2 = 16; o2 > 0; o2 >>= 1) m = fmaxf(m, __shfl_xor(m, o2, 64));
+                    if (d4 == 0) amax[(size_t)b * hq + (size_t)kv * group + hh] = m;
+                }
             } else {
                 *reinterpret_cast<float4*>(ws_acc + (slot0 + hh) * D + 4 * d4) = o;
                 if (d4 == 0) {
@@ -666,8 +674,8 @@ void attn_decode_stream(
 template <typename T>
 __global__ __launch_bounds__(64) void attn_combine_stream(
     const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
-    const long long* __restrict__ pref, T* __restrict__ out, int batch, int hq,
-    int hkv, int group, int nseg, int min_seg) {
+    const long long* __restrict__ pref, T* __restrict__ out, float* __restrict__ amax,
+    int batch, int hq, int hkv, int group, int nseg, int min_seg) {
     constexpr int D = kMfmaDim;
     const int b = blockIdx.x / hq;
     const int h = blockIdx.x - b * hq;
@@ -677,6 +685,7 @@ __global__ __launch_bounds__(64) void attn_combine_stream(
     const int len = (int)(pref[b + 1] - pref[b]);
     if (len == 0) {
         if (lane < D / 4) St<T>::st4(o + 4 * lane, make_float4(0.f, 0.f, 0.f, 0.f));
+        if (amax && lane == 0) amax[blockIdx.x] = 0.0f;
         return;
     }
     const long long S = stream_seg_len(pref[batch] * hkv, nseg, min_seg);
@@ -708,7 +717,14 @@ __global__ __launch_bounds__(64) void attn_combine_stream(
     a.w += __shfl_xor(a.w, 32, 64);
     if (grp != 0) return;
     const float inv = 1.0f / lsum;
-    St<T>::st4(o + 4 * d4, make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv));
+    const float4 ov = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
+    St<T>::st4(o + 4 * d4, ov);
+    if (amax) {
+        float m = stored_absmax4<T>(ov);
+#pragma unroll
+        for (int o2 = 16; o2 > 0; o2 >>= 1) m = fmaxf(m, __shfl_xor(m, o2, 64));
+        if (lane == 0) amax[blockIdx.x] = m;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -826,20 +842,20 @@ bool mfma_eligible(const T* q, const T* k, const T* v, int group, int dim) {
 template <typename T>
 void launch_stream(bool paged, int page_shift, int nseg, hipStream_t s, const T* q,
                    const T* k, const T* v, const int* table, const int* lens, float* ws_ml,
-                   float* ws_acc, long long* pref, T* out, int batch, int hq, int hkv,
-                   int group, int rows_or_page, int tbl_width, int span, float scale_log2,
-                   int min_seg) {
+                   float* ws_acc, long long* pref, T* out, float* amax, int batch, int hq,
+                   int hkv, int group, int rows_or_page, int tbl_width, int span,
+                   float scale_log2, int min_seg) {
     if (paged && page_shift >= 0)
         attn_decode_stream<T, kRowsPagedPow2><<<(unsigned)nseg, 256, 0, s>>>(
-            q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
+            q, k, v, table, lens, ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group,
             rows_or_page, page_shift, tbl_width, span, scale_log2, min_seg);
     else if (paged)
         attn_decode_stream<T, kRowsPagedDiv><<<(unsigned)nseg, 256, 0, s>>>(
-            q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
+            q, k, v, table, lens, ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group,
             rows_or_page, -1, tbl_width, span, scale_log2, min_seg);
     else
         attn_decode_stream<T, kRowsContig><<<(unsigned)nseg, 256, 0, s>>>(
-            q, k, v, nullptr, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
+            q, k, v, nullptr, lens, ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group,
             rows_or_page, -1, 0, span, scale_log2, min_seg);
 }
 
@@ -862,10 +878,11 @@ struct Workspace {
 };
 
 template <typename T>
-void attention_run(const T* q, const T* k, const T* v, const int* table,
+bool attention_run(const T* q, const T* k, const T* v, const int* table,
                    const int* lens, T* out, int batch, int hq, int hkv,
                    int rows_or_page, int tbl_width, int dim, bool paged,
-                   hipStream_t s, const Workspace& wsp = Workspace{}) {
+                   hipStream_t s, const Workspace& wsp = Workspace{},
+                   float* amax = nullptr) {
     long long span;
     if (paged) {
         span = (long long)tbl_width * rows_or_page;
@@ -881,7 +898,7 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
         span = rows_or_page;
         attention_check(batch, hq, hkv, span, dim);
     }
-    if (batch == 0) return;
+    if (batch == 0) return false;
     if (!q || !out || (span > 0 && (!k || !v)) || (paged && span > 0 && !table))
         inval("attention: null operand");
     const int group = hq / hkv;
@@ -910,13 +927,13 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
             float* ws_acc = ws_ml + ml_floats;
             long long* pref = (long long*)(ws_acc + acc_floats);
             launch_stream<T>(paged, page_shift, nseg, s, q, k, v, table, lens, ws_ml, ws_acc,
-                             pref, out, batch, hq, hkv, group, rows_or_page, tbl_width,
+                             pref, out, amax, batch, hq, hkv, group, rows_or_page, tbl_width,
                              (int)span, scale_log2, min_seg);
             launch_check("attention decode kernel launch");
             attn_combine_stream<T><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
-                ws_ml, ws_acc, pref, out, batch, hq, hkv, group, nseg, min_seg);
+                ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group, nseg, min_seg);
             launch_check("attention combine kernel launch");
-            return;
+            return true;  // the stream kernels wrote amax when asked
         }
     }
     const long long target = (long long)dev_info().cu_count * 16;
@@ -952,6 +969,7 @@ void attention_run(const T* q, const T* k, const T* v, const int* table,
     // (also the zero fill of every row when the cache holds no rows at all)
     launch_combine<T>(ws_ml, ws_acc, span > 0 ? lens : nullptr, out, batch, hq,
                       hkv, group, dim, (int)span, chunk, cmax, false, s);
+    return false;  // no per-head maxima on this path
 }
 
 // ---------------------------------------------------------------------------
@@ -1025,6 +1043,34 @@ void kv_append_run(const T* k_new, const T* v_new, const int* table,
 using ft::bf16;
 using ft::f16;
 
+namespace ft {
+namespace {
+// Paged decode followed by the per-tensor int8 quantize of its output. On
+// the stream kernels' path the decode and combine kernels also write the max
+// |stored output| of every (sequence, q head), so the quantize is one launch
+// over those B * Hq maxima; other paths quantize the output in full.
+template <typename T>
+void attention_paged_quant_run(const T* q, const T* k_pool, const T* v_pool, const int* table,
+                               const int* lens, T* out, signed char* codes, float* scale_out,
+                               int batch, int hq, int hkv, int page, int tbl_width, int dim,
+                               hipStream_t s) {
+    if (batch < 0 || hq < 1) inval("attention shapes must satisfy batch>=0, heads>=1, rows>=0, dim>=1");
+    if (batch > 0 && (!codes || !scale_out)) inval("attention quantize: null operand");
+    const long long rows = (long long)batch * hq;
+    float* amax = rows > 0 ? (float*)scratch(Scratch::QuantMax, (size_t)rows * sizeof(float), s)
+                           : nullptr;
+    const bool have_max = attention_run<T>(q, k_pool, v_pool, table, lens, out, batch, hq, hkv,
+                                           page, tbl_width, dim, true, s, Workspace{}, amax);
+    if (batch == 0) return;
+    const long long n = rows * dim;
+    if (have_max)
+        quantize_from_partials<T>(out, codes, amax, (int)rows, scale_out, n, s);
+    else
+        quantize_tensor<T>(out, codes, scale_out, n, s);
+}
+}  // namespace
+}  // namespace ft
+
 // ---------------------------------------------------------------------------
 // Static workspace of the no-allocation entry point. Each GPU holds its own
 // copy of this array for the life of the process. In host code `scratch` is
@@ -1058,6 +1104,39 @@ void* static_workspace() {
 }  // namespace
 
 extern "C" {
+
+int ft_attention_decode_paged_quant_launch(const void* q, const void* k_pool,
+                                           const void* v_pool, const int* table,
+                                           const int* lens, void* out, int dtype,
+                                           signed char* codes, float* scale_out, int batch,
+                                           int q_heads, int kv_heads, int page,
+                                           int tbl_width, int dim, uintptr_t stream) {
+    return ft::guarded([&] {
+        hipStream_t s = ft::as_stream(stream);
+        switch (dtype) {
+        case FT_DT_F32:
+            ft::attention_paged_quant_run<float>((const float*)q, (const float*)k_pool,
+                                                 (const float*)v_pool, table, lens, (float*)out,
+                                                 codes, scale_out, batch, q_heads, kv_heads,
+                                                 page, tbl_width, dim, s);
+            break;
+        case FT_DT_BF16:
+            ft::attention_paged_quant_run<bf16>((const bf16*)q, (const bf16*)k_pool,
+                                                (const bf16*)v_pool, table, lens, (bf16*)out,
+                                                codes, scale_out, batch, q_heads, kv_heads,
+                                                page, tbl_width, dim, s);
+            break;
+        case FT_DT_F16:
+            ft::attention_paged_quant_run<f16>((const f16*)q, (const f16*)k_pool,
+                                               (const f16*)v_pool, table, lens, (f16*)out,
+                                               codes, scale_out, batch, q_heads, kv_heads,
+                                               page, tbl_width, dim, s);
+            break;
+        default:
+            ft::inval("attention quantize: unknown dtype code");
+        }
+    });
+}
 
 int ft_attention_decode_paged_launch_bf16_noalloc(const void* q, const void* k_pool,
                                                   const void* v_pool, const int* table,

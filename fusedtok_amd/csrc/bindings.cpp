@@ -109,6 +109,20 @@ PYBIND11_MODULE(_fusedtok, m) {
     FT_ATTP("attention_decode_paged_launch_fp16",
             ft_attention_decode_paged_launch_fp16, void);
 #undef FT_ATTP
+    m.def("attention_decode_paged_quant_launch",
+          [](uintptr_t q, uintptr_t kp, uintptr_t vp, uintptr_t table, py::object lens,
+             uintptr_t out, int dtype, uintptr_t codes, uintptr_t scale, int batch, int hq,
+             int hkv, int page, int tbl_width, int dim, uintptr_t stream) {
+              check(ft_attention_decode_paged_quant_launch(
+                  P<const void>(q), P<const void>(kp), P<const void>(vp),
+                  P<const int>(table), P<const int>(opt_ptr(lens)), P<void>(out), dtype,
+                  P<signed char>(codes), P<float>(scale), batch, hq, hkv, page, tbl_width,
+                  dim, stream));
+          },
+          py::arg("q"), py::arg("k_pool"), py::arg("v_pool"), py::arg("table"),
+          py::arg("lens"), py::arg("out"), py::arg("dtype"), py::arg("codes"),
+          py::arg("scale"), py::arg("batch"), py::arg("q_heads"), py::arg("kv_heads"),
+          py::arg("page"), py::arg("tbl_width"), py::arg("dim"), py::arg("stream") = 0);
 
     // ---- kv append --------------------------------------------------------
 #define FT_KVP(NAME, FN, T)                                                    \

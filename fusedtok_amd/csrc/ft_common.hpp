@@ -131,6 +131,18 @@ void* scratch(Scratch which, size_t bytes, hipStream_t s);
 // that use it must leave it zero when they finish (e.g. arrival counters).
 void* scratch_zeroed(Scratch which, size_t bytes, hipStream_t s);
 
+// Per-tensor int8 quantize of x[0, n) (T = float, bf16, f16) when its max |x|
+// is already known as the max of nparts partial maxima (written by the
+// producer of x): one launch, codes and *scale_out (device) as quantize_int8
+// computes them. quantize.hip.
+template <typename T>
+void quantize_from_partials(const T* x, signed char* q, const float* partial, int nparts,
+                            float* scale_out, long long n, hipStream_t s);
+// The whole quantize_int8 (two launches above 64K elements). quantize.hip.
+template <typename T>
+void quantize_tensor(const T* x, signed char* q, float* scale_out, long long n,
+                     hipStream_t s);
+
 // ---------------------------------------------------------------------------
 // device: storage traits
 // ---------------------------------------------------------------------------
@@ -202,6 +214,14 @@ template <> struct St<f16> {
 // 127) with inv = 1 / scale.
 __device__ __forceinline__ float make_scale(float absmax) {
     return absmax > 0.0f ? absmax / 127.0f : 1.0f;
+}
+
+// max |v| of 4 values as they are stored in T (rounded to nearest-even):
+// the quantity a later per-tensor quantize of the stored tensor folds
+template <typename T>
+__device__ __forceinline__ float stored_absmax4(float4 v) {
+    return fmaxf(fmaxf(fabsf((float)(T)v.x), fabsf((float)(T)v.y)),
+                 fmaxf(fabsf((float)(T)v.z), fabsf((float)(T)v.w)));
 }
 
 __device__ __forceinline__ signed char quant1(float x, float inv) {

@@ -149,6 +149,41 @@ void quantize_run(const T* x, signed char* q, float* scale_out, long long n,
     launch_check("quantize kernel launch");
 }
 
+}  // namespace
+
+template <typename T>
+void quantize_from_partials(const T* x, signed char* q, const float* partial, int nparts,
+                            float* scale_out, long long n, hipStream_t s) {
+    if (n <= 0) return;
+    if (!x || !q || !partial || !scale_out || nparts < 1) inval("quantize: null operand");
+    const unsigned g2 = grid_1d((n + 3) / 4, 256, dev_info().cu_count * 8);
+    if (((uintptr_t)x % (4 * sizeof(T)) == 0) && ((uintptr_t)q % 4 == 0))
+        quantize_fold_kernel<T, true><<<g2, 256, 0, s>>>(x, q, partial, nparts, scale_out, n);
+    else
+        quantize_fold_kernel<T, false><<<g2, 256, 0, s>>>(x, q, partial, nparts, scale_out, n);
+    launch_check("quantize kernel launch");
+}
+
+template <typename T>
+void quantize_tensor(const T* x, signed char* q, float* scale_out, long long n,
+                     hipStream_t s) {
+    quantize_run<T>(x, q, scale_out, n, s);
+}
+
+template void quantize_from_partials<float>(const float*, signed char*, const float*, int,
+                                            float*, long long, hipStream_t);
+template void quantize_from_partials<bf16>(const bf16*, signed char*, const float*, int,
+                                           float*, long long, hipStream_t);
+template void quantize_from_partials<f16>(const f16*, signed char*, const float*, int,
+                                          float*, long long, hipStream_t);
+template void quantize_tensor<float>(const float*, signed char*, float*, long long,
+                                     hipStream_t);
+template void quantize_tensor<bf16>(const bf16*, signed char*, float*, long long,
+                                    hipStream_t);
+template void quantize_tensor<f16>(const f16*, signed char*, float*, long long, hipStream_t);
+
+namespace {
+
 // ---------------------------------------------------------------------------
 // dequantize: x = (float)q * scale (reference quantize.cu:101-108), one
 // rounding; 2-byte outputs are that f32 value rounded to nearest-even.

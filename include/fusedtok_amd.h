@@ -393,6 +393,21 @@ int ft_rope_kv_append_paged_launch(const void* qkv, int dtype, long long ld,
                                    int dim, int page, int tbl_width,
                                    float theta, int pos_offset, int neox,
                                    uintptr_t stream);
+/* Paged decode attention then per-tensor int8 quantize of its output:
+ * out [batch, q_heads, dim] as ft_attention_decode_paged_launch* writes it
+ * (arguments as there; dtype FT_DT_*), and codes [batch, q_heads, dim]
+ * int8 plus *scale_out (DEVICE float) bit-identical to quantizing that
+ * stored out (ft_quantize_int8_launch for float32, its bf16 / fp16 form
+ * otherwise) -- the decode layer's o_proj input. On the split-stream
+ * attention path the attention kernels also write the max |out| of each
+ * (sequence, q head) and the quantize is one launch over those maxima. */
+int ft_attention_decode_paged_quant_launch(const void* q, const void* k_pool,
+                                           const void* v_pool, const int* table,
+                                           const int* lens, void* out, int dtype,
+                                           signed char* codes, float* scale_out,
+                                           int batch, int q_heads, int kv_heads,
+                                           int page, int tbl_width, int dim,
+                                           uintptr_t stream);
 
 /* ------------------------------------------------------------------ */
 /* Post-logits sampling                                                */

@@ -1,12 +1,13 @@
 """GPU parity of the fused decode-chain steps (rmsnorm_quant, swiglu_quant,
-rope_kv_append_paged):
+rope_kv_append_paged, attention_decode_paged_quant):
   - against the CPU oracle on the same seeded inputs: int8 codes and the
     scale bit-exact for rmsnorm_quant (the oracle follows the kernel's
     summation order); within one code step for swiglu_quant (device expf vs
     the host's); RoPE within 1e-6 (f32) / one storage ulp (bf16, fp16);
   - against this library's unfused GPU chain (rmsnorm -> quantize_int8,
-    swiglu -> quantize_int8, rope(positions=lens) -> kv_append_paged):
-    bit-exact, which is the fused ops' contract."""
+    swiglu -> quantize_int8, rope(positions=lens) -> kv_append_paged,
+    attention_decode_paged -> quantize_int8): bit-exact, which is the fused
+    ops' contract."""
 
 import numpy as np
 import pytest
@@ -317,6 +318,67 @@ def test_rope_kv_append_strided_rows_and_errors():
 # replay must equal the eager layer bit for bit (all kernels here are
 # deterministic: fixed reduction orders, integer GEMM sums)
 # ---------------------------------------------------------------------------
+
+
+# ---------------------------------------------------------------------------
+# attention_decode_paged_quant
+# ---------------------------------------------------------------------------
+
+# (b, hq, hkv, d, page, lens): C4's decode batch; one long row split over many
+# segments (the combine kernel writes the maxima); ragged rows with empty
+# ones; group 1 at D = 64 (the generic kernel, quantised in full)
+ATTN_Q_CASES = {
+    "c4": (32, 32, 8, 128, 16, None),
+    "long": (1, 32, 8, 128, 16, [4133]),
+    "ragged": (5, 16, 2, 128, 32, [0, 1, 33, 0, 900]),
+    "d64": (3, 8, 8, 64, 16, [10, 200, 3]),
+}
+
+
+@pytest.mark.parametrize("dt", ALL)
+@pytest.mark.parametrize("case", list(ATTN_Q_CASES))
+@pytest.mark.parametrize("generic", [False, True])
+def test_attention_decode_paged_quant_equals_the_two_ops(dt, case, generic, tuning):
+    if generic:
+        tuning("FT_ATTN_FORCE_GENERIC", 1)
+    rng = np.random.default_rng(sorted(ATTN_Q_CASES).index(case) + 7 * generic)
+    b, hq, hkv, d, page, lens = ATTN_Q_CASES[case]
+    if lens is None:
+        lens = rng.integers(1, 700, b).tolist()
+    width = max(1, max((n + page - 1) // page for n in lens))
+    nb = b * width + 2
+    q = t(rng.standard_normal((b, hq, d)).astype(np.float32), dt)
+    kp = t(rng.standard_normal((nb, hkv, page, d)).astype(np.float32), dt)
+    vp = t(rng.standard_normal((nb, hkv, page, d)).astype(np.float32), dt)
+    tbl = t(rng.permutation(nb)[: b * width].reshape(b, width).astype(np.int32))
+    ln = t(np.array(lens, np.int32))
+    out_ref = ft.attention_decode_paged(q, kp, vp, tbl, ln)
+    codes_ref, scale_ref = ft.quantize_int8(out_ref, device_scale=True)
+    for rep in range(2):  # the second call reuses the maxima scratch
+        out, codes, scale = ft.attention_decode_paged_quant(q, kp, vp, tbl, ln,
+                                                            device_scale=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(raw(out), raw(out_ref)), f"{case} rep {rep}: out differs"
+        assert torch.equal(codes, codes_ref), f"{case} rep {rep}: codes differ"
+        assert scale.item() == scale_ref.item(), (scale.item(), scale_ref.item())
+    empty = torch.tensor([n == 0 for n in lens], device=DEV)
+    assert not codes[empty].any()  # empty rows are zero and quantise to 0
+    # the scale is max |stored output| / 127 in float32
+    expect = np.float32(out_ref.float().abs().max().item()) / np.float32(127.0)
+    assert scale.item() == expect
+
+
+def test_attention_decode_paged_quant_empty_and_errors():
+    q = torch.zeros((0, 4, 128), dtype=torch.bfloat16, device=DEV)
+    kp = torch.zeros((2, 2, 16, 128), dtype=torch.bfloat16, device=DEV)
+    out, codes, scale = ft.attention_decode_paged_quant(
+        q, kp, kp, torch.zeros((0, 1), dtype=torch.int32, device=DEV))
+    assert out.shape == (0, 4, 128) and codes.shape == (0, 4, 128) and scale == 1.0
+    with pytest.raises(TypeError, match="GPU tensors"):
+        ft.attention_decode_paged_quant(np.zeros((1, 4, 8), np.float32),
+                                        np.zeros((2, 2, 4, 8), np.float32),
+                                        np.zeros((2, 2, 4, 8), np.float32),
+                                        np.zeros((1, 1), np.int32))
 
 
 def test_decode_layer_graph_replays_equal_eager():
