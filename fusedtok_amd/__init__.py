@@ -93,6 +93,8 @@ __all__ = [
     "rmsnorm_qgemm",
     "swiglu_quant",
     "rope_kv_append_paged",
+    "qgemm_rope_kv_append_paged",
+    "qgemm_rmsnorm_quant",
     "argmax",
     "argmax_batched",
     "sample_topp",
@@ -830,6 +832,94 @@ def rope_kv_append_paged(qkv, q_heads, kv_heads, k_pool, v_pool, block_table,
         c.ptr("v_pool"), c.B, q_heads, kv_heads, c.D, c.P, c.S, float(theta),
         int(pos_offset), bool(neox), _stream())
     return q_out
+
+
+def _device_scale(a_scale, device):
+    """The GEMM's activation scale as a 1-element GPU float32 tensor."""
+    _, ptr = _scale_operand(a_scale, "a_scale")
+    if ptr is not None:
+        return a_scale
+    return torch.tensor([float(a_scale.item() if torch.is_tensor(a_scale) else a_scale)],
+                        dtype=torch.float32, device=device)
+
+
+def _fused_gemm_operands(a_q, w_q, w_scales, name):
+    if not all(torch.is_tensor(t) and t.is_cuda for t in (a_q, w_q)):
+        raise TypeError(f"{name}: a_q and w_q must be GPU tensors (fused ops have no host path)")
+    if not torch.is_tensor(w_scales):
+        w_scales = torch.as_tensor(np.asarray(w_scales, dtype=np.float32), device=a_q.device)
+    return _GEMM_PC.bind(a_q=a_q, b_q=w_q, b_scales=w_scales.to(a_q.device))
+
+
+def qgemm_rope_kv_append_paged(a_q, a_scale, w_q, w_scales, q_heads, kv_heads, k_pool,
+                               v_pool, block_table, lens, *, theta=10000.0, pos_offset=0,
+                               neox=False):
+    """The QKV projection and the decode token's RoPE + paged KV append:
+    ``qkv = qgemm_perchannel(a_q, a_scale, w_q, w_scales, out_dtype=pool
+    dtype)`` then ``rope_kv_append_paged(qkv, ...)``, bit for bit. Returns
+    ``(q_rot, qkv)``. A K-split GEMM's partial sums are folded by the RoPE
+    kernel itself, so the chain is two launches."""
+    g = _fused_gemm_operands(a_q, w_q, w_scales, "qgemm_rope_kv_append_paged")
+    if not (torch.is_tensor(k_pool) and k_pool.is_cuda and k_pool.dtype in _FLOATS):
+        raise TypeError("k_pool must be a float32, bfloat16 or float16 GPU tensor")
+    q_heads, kv_heads = int(q_heads), int(kv_heads)
+    if q_heads < 1 or kv_heads < 1 or q_heads % kv_heads:
+        raise ValueError("q_heads and kv_heads must be >= 1, q_heads a multiple of kv_heads")
+    if int(pos_offset) < 0:
+        raise ValueError("pos_offset must be >= 0")
+    c = _ROPE_KV.bind(k_pool=k_pool, v_pool=v_pool, block_table=block_table, lens=lens)
+    if c.Hkv != kv_heads:
+        raise ValueError("kv_heads must equal the pools' head count")
+    if g.N != (q_heads + 2 * kv_heads) * c.D or g.M != c.B:
+        raise ValueError("w_q must be [(q_heads + 2 * kv_heads) * D, K] and a_q [B, K]")
+    if c.D % 2:
+        raise ValueError("dim must be even (RoPE pairs elements)")
+    dt = k_pool.dtype
+    qkv = torch.empty((c.B, g.N), dtype=dt, device=k_pool.device)
+    q_out = torch.empty((c.B, q_heads, c.D), dtype=dt, device=k_pool.device)
+    if c.B:
+        sa = _device_scale(a_scale, k_pool.device)
+        _fusedtok.qgemm_rope_kv_append_paged_launch(
+            g.ptr("a_q"), sa.data_ptr(), g.ptr("b_q"), g.ptr("b_scales"), g.K, _CODE[dt],
+            qkv.data_ptr(), c.ptr("lens"), c.ptr("block_table"), q_out.data_ptr(),
+            c.ptr("k_pool"), c.ptr("v_pool"), c.B, q_heads, kv_heads, c.D, c.P, c.S,
+            float(theta), int(pos_offset), bool(neox), _stream())
+    return q_out, qkv
+
+
+def qgemm_rmsnorm_quant(a_q, a_scale, w_q, w_scales, weight, *, residual=None, eps=1e-6,
+                        out_dtype=None, device_scale=False):
+    """A projection followed by the next RMSNorm's quantize: ``y =
+    qgemm_perchannel(a_q, a_scale, w_q, w_scales, out_dtype=out_dtype)`` then
+    ``q, s = rmsnorm_quant(y, weight, residual=residual, eps=eps)``, bit for
+    bit. Returns ``(y, q, scale)``. A K-split GEMM's partial sums are folded
+    by the RMSNorm row pass (which stores y), so the chain is three launches
+    instead of four. ``device_scale=True`` returns the scale as a 1-element
+    GPU float32 tensor without synchronising."""
+    g = _fused_gemm_operands(a_q, w_q, w_scales, "qgemm_rmsnorm_quant")
+    dt = _out_dtype(out_dtype)
+    if g.N % 4:
+        raise ValueError("qgemm_rmsnorm_quant: N must be a multiple of 4")
+    w = torch.as_tensor(weight).to(device=a_q.device, dtype=torch.float32).contiguous()
+    if w.shape != (g.N,):
+        raise ValueError("weight must be 1-D with N entries")
+    if residual is not None:
+        if not (torch.is_tensor(residual) and residual.is_cuda and residual.dtype is dt
+                and residual.shape == (g.M, g.N)):
+            raise ValueError("residual must be a GPU tensor of y's dtype and shape [M, N]")
+        residual = residual.contiguous()
+    y = torch.empty((g.M, g.N), dtype=dt, device=a_q.device)
+    q = torch.empty((g.M, g.N), dtype=torch.int8, device=a_q.device)
+    scale = torch.empty(1, dtype=torch.float32, device=a_q.device)
+    if g.M == 0 or g.N == 0:
+        scale.fill_(1.0)
+    else:
+        sa = _device_scale(a_scale, a_q.device)
+        _fusedtok.qgemm_rmsnorm_quant_launch(
+            g.ptr("a_q"), sa.data_ptr(), g.ptr("b_q"), g.ptr("b_scales"), _CODE[dt],
+            y.data_ptr(), None if residual is None else residual.data_ptr(), w.data_ptr(),
+            float(eps), q.data_ptr(), scale.data_ptr(), g.M, g.N, g.K, _stream())
+    return (y, q, scale) if device_scale else (y, q, float(scale))
 
 
 # ---------------------------------------------------------------------------

@@ -36,6 +36,8 @@ __all__ = [
     "rmsnorm_qgemm",
     "swiglu_quant",
     "rope_kv_append_paged",
+    "qgemm_rope_kv_append_paged",
+    "qgemm_rmsnorm_quant",
     "argmax",
     "argmax_batched",
     "sample_topp",
@@ -105,6 +107,17 @@ def rope_kv_append_paged(qkv: torch.Tensor, q_heads: int, kv_heads: int,
                          k_pool: torch.Tensor, v_pool: torch.Tensor,
                          block_table: IntArray, lens: IntArray, *,
                          theta: float = ..., pos_offset: int = ...,
+def qgemm_rope_kv_append_paged(a_q: torch.Tensor, a_scale: Scale, w_q: torch.Tensor,
+                               w_scales: Union[torch.Tensor, Sequence[float]], q_heads: int,
+                               kv_heads: int, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                               block_table: IntArray, lens: IntArray, *, theta: float = ...,
+                               pos_offset: int = ..., neox: bool = ...
+                               ) -> Tuple[torch.Tensor, torch.Tensor]: ...
+def qgemm_rmsnorm_quant(a_q: torch.Tensor, a_scale: Scale, w_q: torch.Tensor,
+                        w_scales: Union[torch.Tensor, Sequence[float]], weight: Array, *,
+                        residual: Optional[torch.Tensor] = ..., eps: float = ...,
+                        out_dtype: Optional[torch.dtype] = ..., device_scale: bool = ...
+                        ) -> Tuple[torch.Tensor, torch.Tensor, Scale]: ...
                          neox: bool = ...) -> torch.Tensor: ...
 
 # -- post-logits sampling -------------------------------------------------------

@@ -434,6 +434,37 @@ PYBIND11_MODULE(_fusedtok, m) {
           py::arg("gate"), py::arg("up"), py::arg("dtype"), py::arg("q"),
           py::arg("scale"), py::arg("rows"), py::arg("cols"), py::arg("ld"),
           py::arg("stream") = 0);
+    m.def("qgemm_rope_kv_append_paged_launch",
+          [](uintptr_t a, uintptr_t sa, uintptr_t w, uintptr_t ws, int k, int dtype,
+             uintptr_t qkv, uintptr_t lens, uintptr_t table, uintptr_t q_out, uintptr_t kp,
+             uintptr_t vp, int batch, int hq, int hkv, int dim, int page, int tbl_width,
+             float theta, int pos_offset, bool neox, uintptr_t stream) {
+              check(ft_qgemm_rope_kv_append_paged_launch(
+                  P<const signed char>(a), P<const float>(sa), P<const signed char>(w),
+                  P<const float>(ws), k, dtype, P<void>(qkv), P<const int>(lens),
+                  P<const int>(table), P<void>(q_out), P<void>(kp), P<void>(vp), batch, hq,
+                  hkv, dim, page, tbl_width, theta, pos_offset, neox ? 1 : 0, stream));
+          },
+          py::arg("a_q"), py::arg("sa_dev"), py::arg("w_q"), py::arg("w_scales"),
+          py::arg("k"), py::arg("dtype"), py::arg("qkv"), py::arg("lens"), py::arg("table"),
+          py::arg("q_out"), py::arg("k_pool"), py::arg("v_pool"), py::arg("batch"),
+          py::arg("q_heads"), py::arg("kv_heads"), py::arg("dim"), py::arg("page"),
+          py::arg("tbl_width"), py::arg("theta"), py::arg("pos_offset"), py::arg("neox"),
+          py::arg("stream") = 0);
+    m.def("qgemm_rmsnorm_quant_launch",
+          [](uintptr_t a, uintptr_t sa, uintptr_t w, uintptr_t ws, int dtype, uintptr_t y,
+             py::object r, uintptr_t nw, float eps, uintptr_t q, uintptr_t scale, int rows,
+             int n, int k, uintptr_t stream) {
+              check(ft_qgemm_rmsnorm_quant_launch(
+                  P<const signed char>(a), P<const float>(sa), P<const signed char>(w),
+                  P<const float>(ws), dtype, P<void>(y), P<const void>(opt_ptr(r)),
+                  P<const float>(nw), eps, P<signed char>(q), P<float>(scale), rows, n, k,
+                  stream));
+          },
+          py::arg("a_q"), py::arg("sa_dev"), py::arg("w_q"), py::arg("w_scales"),
+          py::arg("dtype"), py::arg("y"), py::arg("residual"), py::arg("weight"),
+          py::arg("eps"), py::arg("q"), py::arg("scale"), py::arg("rows"), py::arg("n"),
+          py::arg("k"), py::arg("stream") = 0);
     m.def("rope_kv_append_paged_launch",
           [](uintptr_t qkv, int dtype, long long ld, uintptr_t lens, uintptr_t table,
              uintptr_t q_out, uintptr_t k_pool, uintptr_t v_pool, int batch,

@@ -26,6 +26,7 @@
 //   SwiGLU: g / (1 + expf(-g)) * u (reference activations.cu:68-72, 501-511).
 //   RoPE: angle, cos/sin and rotation in float64 as the rope kernel.
 #include "ft_common.hpp"
+#include "kfold.hpp"
 
 #include <cmath>
 
@@ -68,13 +69,29 @@ constexpr int kRowChunks = 4;  // 4-element chunks per thread held in registers
 
 // One workgroup per row: sum of squares -> inv, then the row's max |y|. A row
 // of up to 4096 columns stays in registers between the two passes.
-template <typename T, bool RES>
+// FOLD: x is the output of a K-split GEMM, folded here from its partials
+// (and stored into x_out, as the GEMM would have stored it).
+template <typename T, bool RES, bool FOLD>
 __global__ __launch_bounds__(kFNT) void rmsq_rows(
     const T* __restrict__ x, const T* __restrict__ r, const float* __restrict__ w,
-    RowStat* __restrict__ stat, int cols, float eps) {
+    RowStat* __restrict__ stat, int cols, float eps, KFold fold, T* __restrict__ x_out) {
     __shared__ float red[kFNT / 64];
     const size_t base = (size_t)blockIdx.x * cols;
     const int chunks = cols >> 2;
+    float sa = 0.0f;
+    if constexpr (FOLD) sa = kfold_sa(fold);
+    // chunk c of the row as stored in T, widened to f32
+    auto load_x4 = [&](int c) -> float4 {
+        if constexpr (FOLD) {
+            const int4 a = kfold_sum4(fold, base + 4 * c);
+            return make_float4(kfold_value<T>(a.x, kfold_scale(fold, sa, 4 * c)),
+                               kfold_value<T>(a.y, kfold_scale(fold, sa, 4 * c + 1)),
+                               kfold_value<T>(a.z, kfold_scale(fold, sa, 4 * c + 2)),
+                               kfold_value<T>(a.w, kfold_scale(fold, sa, 4 * c + 3)));
+        } else {
+            return St<T>::ld4(x + base + 4 * c);
+        }
+    };
     float m = 0.0f;
     float inv;
     if (chunks <= kFNT * kRowChunks) {
@@ -84,9 +101,15 @@ __global__ __launch_bounds__(kFNT) void rmsq_rows(
 #pragma unroll
         for (int j = 0; j < kRowChunks; ++j) {
             const int c = min((int)threadIdx.x + j * kFNT, chunks - 1);
-            v[j] = St<T>::ld4(x + base + 4 * c);
+            v[j] = load_x4(c);
             if constexpr (RES) rv[j] = St<T>::ld4(r + base + 4 * c);
             wc[j] = *reinterpret_cast<const float4*>(w + 4 * c);
+        }
+        if constexpr (FOLD) {
+#pragma unroll
+            for (int j = 0; j < kRowChunks; ++j)
+                if ((int)threadIdx.x + j * kFNT < chunks)
+                    St<T>::st4(x_out + base + 4 * ((int)threadIdx.x + j * kFNT), v[j]);
         }
 #pragma unroll
         for (int j = 0; j < kRowChunks; ++j) v[j] = rms_add4<RES>(v[j], rv[j]);
@@ -114,7 +137,9 @@ __global__ __launch_bounds__(kFNT) void rmsq_rows(
     } else {
         float acc = 0.0f;
         for (int c = threadIdx.x; c < chunks; c += kFNT) {
-            const float4 v = rms_in4(x, r, base + 4 * c);
+            float4 v = load_x4(c);
+            if constexpr (FOLD) St<T>::st4(x_out + base + 4 * c, v);
+            if constexpr (RES) v = rms_add4<true>(v, St<T>::ld4(r + base + 4 * c));
             acc = fmaf(v.x, v.x, acc);
             acc = fmaf(v.y, v.y, acc);
             acc = fmaf(v.z, v.z, acc);
@@ -123,7 +148,8 @@ __global__ __launch_bounds__(kFNT) void rmsq_rows(
         const float total = block_sum<kFNT>(acc, red);
         inv = 1.0f / sqrtf(total / (float)cols + eps);
         for (int c = threadIdx.x; c < chunks; c += kFNT) {
-            const float4 v = rms_in4(x, r, base + 4 * c);
+            float4 v = load_x4(c);
+            if constexpr (RES) v = rms_add4<true>(v, St<T>::ld4(r + base + 4 * c));
             const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c);
             m = fmaxf(m, fabsf(v.x * inv * wv.x));
             m = fmaxf(m, fabsf(v.y * inv * wv.y));
@@ -300,9 +326,8 @@ __global__ __launch_bounds__(4 * kFNT) void rmsq_small(
 }
 
 template <typename T>
-void rmsnorm_quant_run(const T* x, const float* w, const T* r, signed char* q,
-                       float* scale_out, int rows, int cols, float eps,
-                       hipStream_t s) {
+void rmsq_check(const T* x, const float* w, const T* r, const signed char* q,
+                const float* scale_out, int rows, int cols) {
     if (rows < 0 || cols <= 0) inval("rows must be >= 0 and cols must be > 0");
     if (cols % 4 != 0) inval("rmsnorm_quant: cols must be a multiple of 4");
     if (rows == 0) return;
@@ -311,6 +336,38 @@ void rmsnorm_quant_run(const T* x, const float* w, const T* r, signed char* q,
     if ((uintptr_t)x % a16 || (r && (uintptr_t)r % a16) || (uintptr_t)w % 16 ||
         (uintptr_t)q % 4)
         inval("rmsnorm_quant: operands must be aligned to 4 elements");
+}
+
+// the row pass (FOLD: folding a K-split GEMM's partials into x_out first),
+// then the fold of the row maxima and the codes
+template <typename T, bool FOLD>
+void rmsq_two_pass(const T* x, const KFold& fold, T* x_out, const float* w, const T* r,
+                   signed char* q, float* scale_out, int rows, int cols, float eps,
+                   hipStream_t s) {
+    RowStat* stat = (RowStat*)scratch(Scratch::QuantMax, (size_t)rows * sizeof(RowStat), s);
+    if (r)
+        rmsq_rows<T, true, FOLD><<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps,
+                                                                 fold, x_out);
+    else
+        rmsq_rows<T, false, FOLD><<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps,
+                                                                  fold, x_out);
+    launch_check("rmsnorm_quant row kernel launch");
+    if constexpr (FOLD) x = x_out;
+    const long long n4 = (long long)rows * cols / 4;
+    const unsigned grid = grid_1d(n4, kFNT, dev_info().cu_count * 4);
+    if (r)
+        rmsq_quant<T, true><<<grid, kFNT, 0, s>>>(x, r, w, stat, q, scale_out, rows, cols);
+    else
+        rmsq_quant<T, false><<<grid, kFNT, 0, s>>>(x, r, w, stat, q, scale_out, rows, cols);
+    launch_check("rmsnorm_quant quantize kernel launch");
+}
+
+template <typename T>
+void rmsnorm_quant_run(const T* x, const float* w, const T* r, signed char* q,
+                       float* scale_out, int rows, int cols, float eps,
+                       hipStream_t s) {
+    rmsq_check(x, w, r, q, scale_out, rows, cols);
+    if (rows == 0) return;
     if (rows <= kRmsqMaxRows && cols <= kRmsqMaxCols && tune(Tune::RmsqSplit, 0) == 0) {
         if (r)
             rmsq_small<T, true><<<1, (unsigned)(rows * kFNT), 0, s>>>(x, r, w, q, scale_out,
@@ -321,19 +378,27 @@ void rmsnorm_quant_run(const T* x, const float* w, const T* r, signed char* q,
         launch_check("rmsnorm_quant small kernel launch");
         return;
     }
-    RowStat* stat = (RowStat*)scratch(Scratch::QuantMax, (size_t)rows * sizeof(RowStat), s);
-    if (r)
-        rmsq_rows<T, true><<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps);
+    rmsq_two_pass<T, false>(x, KFold{}, nullptr, w, r, q, scale_out, rows, cols, eps, s);
+}
+
+
+// o_proj-style GEMM (a_q codes with the device scale *sa_dev, w_q [n, k],
+// per-channel w_scales) -> y [rows, n] in T, then rmsnorm_quant(y [+ r]).
+// A K-split GEMM's partials are folded by the row pass, which stores y.
+template <typename T>
+void qgemm_rmsq_run(const signed char* a_q, const float* sa_dev, const signed char* w_q,
+                    const float* w_scales, T* y, const T* r, const float* w, float eps,
+                    signed char* q, float* scale_out, int rows, int n, int k, int dtype,
+                    hipStream_t s) {
+    if (k < 1) inval("qgemm_rmsnorm_quant: k must be >= 1");
+    rmsq_check(y, w, r, q, scale_out, rows, n);
+    if (rows == 0) return;
+    if (!a_q || !sa_dev || !w_q || !w_scales) inval("qgemm_rmsnorm_quant: null operand");
+    KFold fold;
+    if (qgemm_deferred(a_q, w_q, 0.0f, sa_dev, 0.0f, w_scales, y, dtype, rows, n, k, s, fold))
+        rmsq_two_pass<T, true>(nullptr, fold, y, w, r, q, scale_out, rows, n, eps, s);
     else
-        rmsq_rows<T, false><<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps);
-    launch_check("rmsnorm_quant row kernel launch");
-    const long long n4 = (long long)rows * cols / 4;
-    const unsigned grid = grid_1d(n4, kFNT, dev_info().cu_count * 4);
-    if (r)
-        rmsq_quant<T, true><<<grid, kFNT, 0, s>>>(x, r, w, stat, q, scale_out, rows, cols);
-    else
-        rmsq_quant<T, false><<<grid, kFNT, 0, s>>>(x, r, w, stat, q, scale_out, rows, cols);
-    launch_check("rmsnorm_quant quantize kernel launch");
+        rmsnorm_quant_run<T>(y, w, r, q, scale_out, rows, n, eps, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -466,12 +531,12 @@ void swiglu_quant_run(const T* g, const T* u, signed char* q, float* scale_out,
 // Hq + Hkv rotated heads, plus one per (b, v head, pair) copied. The QKV row
 // of sequence b is qkv[b * ld + (head * D ..)], heads ordered q | k | v.
 // ---------------------------------------------------------------------------
-template <typename T, bool NEOX>
+template <typename T, bool NEOX, bool FOLD>
 __global__ __launch_bounds__(256) void rope_kv_kernel(
-    const T* __restrict__ qkv, long long ld, const int* __restrict__ lens,
-    const int* __restrict__ table, T* __restrict__ q_out, T* __restrict__ k_pool,
-    T* __restrict__ v_pool, int batch, int hq, int hkv, int dim, int page,
-    int tbl_width, double theta, int pos_offset) {
+    const T* __restrict__ qkv, long long ld, KFold fold, T* __restrict__ qkv_out,
+    const int* __restrict__ lens, const int* __restrict__ table, T* __restrict__ q_out,
+    T* __restrict__ k_pool, T* __restrict__ v_pool, int batch, int hq, int hkv, int dim,
+    int page, int tbl_width, double theta, int pos_offset) {
     const int half = dim >> 1;
     const int heads = hq + 2 * hkv;
     const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -480,9 +545,24 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     const int rem = (int)(p - (long long)b * heads * half);
     const int h = rem / half, j = rem - (rem / half) * half;
     const int slot = lens[b];
-    const T* src = qkv + (size_t)b * ld + (size_t)h * dim;
+    const size_t row0 = (size_t)b * ld + (size_t)h * dim;
     const int i1 = NEOX ? j : 2 * j;
     const int i2 = NEOX ? j + half : 2 * j + 1;
+    // the two inputs: the GEMM output as stored in T, read back or folded
+    // from the K-split partials (and then also stored, as the GEMM would)
+    float x1, x2;
+    if constexpr (FOLD) {
+        const float sa = kfold_sa(fold);
+        const int c1 = h * dim + i1, c2 = h * dim + i2;
+        const int a1 = kfold_sum(fold, row0 + i1), a2 = kfold_sum(fold, row0 + i2);
+        x1 = kfold_value<T>(a1, kfold_scale(fold, sa, c1));
+        x2 = kfold_value<T>(a2, kfold_scale(fold, sa, c2));
+        St<T>::st(qkv_out + row0 + i1, x1);
+        St<T>::st(qkv_out + row0 + i2, x2);
+    } else {
+        x1 = St<T>::ld(qkv + row0 + i1);
+        x2 = St<T>::ld(qkv + row0 + i2);
+    }
     // destination row of a K / V head: skipped if the slot is outside the
     // table's capacity (the device lengths are trusted, never read back)
     auto cache_row = [&](T* pool, int kv) -> T* {
@@ -493,8 +573,13 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     if (h >= hq + hkv) {  // v head: copy two elements
         T* dst = cache_row(v_pool, h - hq - hkv);
         if (dst) {
-            dst[i1] = src[i1];
-            dst[i2] = src[i2];
+            if constexpr (FOLD) {
+                St<T>::st(dst + i1, x1);
+                St<T>::st(dst + i2, x2);
+            } else {  // the stored bits, NaN payloads included
+                dst[i1] = qkv[row0 + i1];
+                dst[i2] = qkv[row0 + i2];
+            }
         }
         return;
     }
@@ -502,7 +587,6 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     const double angle = (double)m * pow(theta, -2.0 * j / dim);
     double sn, cs;
     sincos(angle, &sn, &cs);
-    const float x1 = St<T>::ld(src + i1), x2 = St<T>::ld(src + i2);
     const float y1 = (float)(x1 * cs - x2 * sn);
     const float y2 = (float)(x1 * sn + x2 * cs);
     T* dst = h < hq ? q_out + ((size_t)b * hq + h) * dim : cache_row(k_pool, h - hq);
@@ -512,32 +596,81 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     }
 }
 
-template <typename T>
-void rope_kv_run(const T* qkv, long long ld, const int* lens, const int* table,
-                 T* q_out, T* k_pool, T* v_pool, int batch, int hq, int hkv,
-                 int dim, int page, int tbl_width, float theta, int pos_offset,
-                 bool neox, hipStream_t s) {
+void rope_kv_check(long long ld, const int* lens, const int* table, const void* q_out,
+                   const void* k_pool, const void* v_pool, int batch, int hq, int hkv, int dim,
+                   int page, int tbl_width, int pos_offset) {
     if (batch < 0 || hq < 1 || hkv < 1 || dim < 2 || dim % 2 != 0)
         inval("rope_kv_append: batch >= 0, heads >= 1 and an even dim >= 2 are required");
     if (page < 1 || tbl_width < 0) inval("rope_kv_append: page >= 1, table width >= 0");
     if (ld < (long long)(hq + 2 * hkv) * dim) inval("rope_kv_append: qkv row stride too small");
     if (pos_offset < 0) inval("pos_offset must be >= 0");
     if ((long long)tbl_width * page > (1LL << 30)) inval("table capacity too large");
-    if (batch == 0) return;
-    if (!qkv || !lens || !table || !q_out || !k_pool || !v_pool)
+    if (batch > 0 && (!lens || !table || !q_out || !k_pool || !v_pool))
         inval("rope_kv_append: null operand");
+    if ((long long)batch * (hq + 2 * hkv) * (dim / 2) > (1LL << 40))
+        inval("rope_kv_append: problem too large");
+}
+
+// FOLD: the input row is the K-split GEMM's partials `fold` (ld = its n),
+// folded in the kernel and also stored into qkv_out
+template <typename T, bool FOLD>
+void rope_kv_launch(const T* qkv, long long ld, const KFold& fold, T* qkv_out, const int* lens,
+                    const int* table, T* q_out, T* k_pool, T* v_pool, int batch, int hq,
+                    int hkv, int dim, int page, int tbl_width, float theta, int pos_offset,
+                    bool neox, hipStream_t s) {
+    if (batch == 0) return;
     const long long threads = (long long)batch * (hq + 2 * hkv) * (dim / 2);
-    if (threads > (1LL << 40)) inval("rope_kv_append: problem too large");
     const unsigned grid = (unsigned)((threads + 255) / 256);
     if (neox)
-        rope_kv_kernel<T, true><<<grid, 256, 0, s>>>(qkv, ld, lens, table, q_out, k_pool,
-                                                     v_pool, batch, hq, hkv, dim, page,
-                                                     tbl_width, (double)theta, pos_offset);
+        rope_kv_kernel<T, true, FOLD><<<grid, 256, 0, s>>>(
+            qkv, ld, fold, qkv_out, lens, table, q_out, k_pool, v_pool, batch, hq, hkv, dim,
+            page, tbl_width, (double)theta, pos_offset);
     else
-        rope_kv_kernel<T, false><<<grid, 256, 0, s>>>(qkv, ld, lens, table, q_out, k_pool,
-                                                      v_pool, batch, hq, hkv, dim, page,
-                                                      tbl_width, (double)theta, pos_offset);
+        rope_kv_kernel<T, false, FOLD><<<grid, 256, 0, s>>>(
+            qkv, ld, fold, qkv_out, lens, table, q_out, k_pool, v_pool, batch, hq, hkv, dim,
+            page, tbl_width, (double)theta, pos_offset);
     launch_check("rope_kv_append kernel launch");
+}
+
+template <typename T>
+void rope_kv_run(const T* qkv, long long ld, const int* lens, const int* table,
+                 T* q_out, T* k_pool, T* v_pool, int batch, int hq, int hkv,
+                 int dim, int page, int tbl_width, float theta, int pos_offset,
+                 bool neox, hipStream_t s) {
+    rope_kv_check(ld, lens, table, q_out, k_pool, v_pool, batch, hq, hkv, dim, page, tbl_width,
+                  pos_offset);
+    if (batch > 0 && !qkv) inval("rope_kv_append: null operand");
+    rope_kv_launch<T, false>(qkv, ld, KFold{}, nullptr, lens, table, q_out, k_pool, v_pool,
+                             batch, hq, hkv, dim, page, tbl_width, theta, pos_offset, neox, s);
+}
+
+// QKV GEMM (a_q [batch, k] codes with the device scale *sa_dev, w_q [n, k],
+// per-channel w_scales) -> qkv [batch, n] in T, then rope_kv_run on it. A
+// K-split GEMM's partials are folded by the RoPE kernel itself.
+template <typename T>
+void qgemm_rope_kv_run(const signed char* a_q, const float* sa_dev, const signed char* w_q,
+                       const float* w_scales, T* qkv, const int* lens, const int* table,
+                       T* q_out, T* k_pool, T* v_pool, int batch, int hq, int hkv, int dim,
+                       int k, int page, int tbl_width, float theta, int pos_offset, bool neox,
+                       int dtype, hipStream_t s) {
+    const long long n = (long long)(hq + 2 * hkv) * dim;
+    rope_kv_check(n, lens, table, q_out, k_pool, v_pool, batch, hq, hkv, dim, page, tbl_width,
+                  pos_offset);
+    if (n > (1LL << 30)) inval("qgemm_rope_kv_append: too many heads");
+    if (k < 1) inval("qgemm_rope_kv_append: k must be >= 1");
+    if (batch == 0) return;
+    if (!a_q || !sa_dev || !w_q || !w_scales || !qkv)
+        inval("qgemm_rope_kv_append: null operand");
+    KFold fold;
+    if (qgemm_deferred(a_q, w_q, 0.0f, sa_dev, 0.0f, w_scales, qkv, dtype, batch, (int)n, k, s,
+                       fold))
+        rope_kv_launch<T, true>(nullptr, n, fold, qkv, lens, table, q_out, k_pool, v_pool,
+                                batch, hq, hkv, dim, page, tbl_width, theta, pos_offset, neox,
+                                s);
+    else
+        rope_kv_launch<T, false>(qkv, n, KFold{}, nullptr, lens, table, q_out, k_pool, v_pool,
+                                 batch, hq, hkv, dim, page, tbl_width, theta, pos_offset, neox,
+                                 s);
 }
 
 }  // namespace
@@ -624,6 +757,49 @@ int ft_rope_kv_append_paged_launch(const void* qkv, int dtype, long long ld,
         default:
             ft::inval("rope_kv_append: unknown dtype code");
         }
+    });
+}
+
+int ft_qgemm_rope_kv_append_paged_launch(const signed char* a_q, const float* sa_dev,
+                                         const signed char* w_q, const float* w_scales,
+                                         int k, int dtype, void* qkv, const int* lens,
+                                         const int* table, void* q_out, void* k_pool,
+                                         void* v_pool, int batch, int q_heads, int kv_heads,
+                                         int dim, int page, int tbl_width, float theta,
+                                         int pos_offset, int neox, uintptr_t stream) {
+    return ft::guarded([&] {
+        hipStream_t s = ft::as_stream(stream);
+#define FT_QRK(T)                                                                          \
+    ft::qgemm_rope_kv_run<T>(a_q, sa_dev, w_q, w_scales, (T*)qkv, lens, table, (T*)q_out,  \
+                             (T*)k_pool, (T*)v_pool, batch, q_heads, kv_heads, dim, k, page, \
+                             tbl_width, theta, pos_offset, neox != 0, dtype, s)
+        switch (dtype) {
+        case FT_DT_F32: FT_QRK(float); break;
+        case FT_DT_BF16: FT_QRK(ft::bf16); break;
+        case FT_DT_F16: FT_QRK(ft::f16); break;
+        default: ft::inval("qgemm_rope_kv_append: unknown dtype code");
+        }
+#undef FT_QRK
+    });
+}
+
+int ft_qgemm_rmsnorm_quant_launch(const signed char* a_q, const float* sa_dev,
+                                  const signed char* w_q, const float* w_scales, int dtype,
+                                  void* y, const void* residual, const float* w, float eps,
+                                  signed char* q, float* scale_out, int rows, int n, int k,
+                                  uintptr_t stream) {
+    return ft::guarded([&] {
+        hipStream_t s = ft::as_stream(stream);
+#define FT_QRQ(T)                                                                          \
+    ft::qgemm_rmsq_run<T>(a_q, sa_dev, w_q, w_scales, (T*)y, (const T*)residual, w, eps, q, \
+                          scale_out, rows, n, k, dtype, s)
+        switch (dtype) {
+        case FT_DT_F32: FT_QRQ(float); break;
+        case FT_DT_BF16: FT_QRQ(ft::bf16); break;
+        case FT_DT_F16: FT_QRQ(ft::f16); break;
+        default: ft::inval("qgemm_rmsnorm_quant: unknown dtype code");
+        }
+#undef FT_QRQ
     });
 }
 

@@ -39,6 +39,7 @@
 //   qgemm_scalar   any shape/alignment (K % 16 != 0, misaligned views).
 //   K == 0         zero fill (a kernel, not a memset, so it captures cleanly).
 #include "ft_common.hpp"
+#include "kfold.hpp"
 
 #include <algorithm>
 #include <cstdlib>
@@ -1859,7 +1860,7 @@ size_t out_elem_bytes(int out) {
 
 template <int OUT>
 void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
-                    hipStream_t s) {
+                    hipStream_t s, KFold* defer) {
     const bool aligned = (k % 16 == 0) && ((uintptr_t)a % 16 == 0) &&
                          ((uintptr_t)b % 16 == 0);
     // FT_QGEMM_KERNEL: 1 skinny, 2 tiled, 3 scalar, 4 big, 5 gemv, 6 decode
@@ -1987,6 +1988,17 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         else
             qgemm_skinny<4, OUT><<<grid, 256, 0, s>>>(a, b, e, m, n, k, ksplit, part);
         launch_check("qgemm skinny kernel launch");
+        if (ksplit > 1 && defer) {  // the caller's next launch folds them
+            defer->part = part;
+            defer->ksplit = ksplit;
+            defer->n = n;
+            defer->mn = (long long)m * n;
+            defer->sa_dev = e.sa_dev;
+            defer->sa = e.sa;
+            defer->sb_vec = e.sb_vec;
+            defer->sb = e.sb;
+            return;
+        }
         if (ksplit > 1) {
             const long long mn = (long long)m * n;
             qgemm_ksum<OUT><<<grid_1d(mn, 256, 1 << 30), 256, 0, s>>>(part, e, m, n, ksplit);
@@ -2030,7 +2042,7 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
 }
 
 void qgemm_run(const i8* a, const i8* b, Epi e, int out, int m, int n, int k,
-               hipStream_t s) {
+               hipStream_t s, KFold* defer = nullptr) {
     qgemm_check(m, n, k);
     if (m == 0 || n == 0) return;
     if (!e.y) inval("qgemm: null output");
@@ -2042,15 +2054,32 @@ void qgemm_run(const i8* a, const i8* b, Epi e, int out, int m, int n, int k,
     }
     if (!a || !b) inval("qgemm: null operand");
     switch (out) {
-    case kOutF32: qgemm_dispatch<kOutF32>(a, b, e, m, n, k, s); break;
-    case kOutBF16: qgemm_dispatch<kOutBF16>(a, b, e, m, n, k, s); break;
-    case kOutF16: qgemm_dispatch<kOutF16>(a, b, e, m, n, k, s); break;
-    case kOutI32: qgemm_dispatch<kOutI32>(a, b, e, m, n, k, s); break;
+    case kOutF32: qgemm_dispatch<kOutF32>(a, b, e, m, n, k, s, defer); break;
+    case kOutBF16: qgemm_dispatch<kOutBF16>(a, b, e, m, n, k, s, defer); break;
+    case kOutF16: qgemm_dispatch<kOutF16>(a, b, e, m, n, k, s, defer); break;
+    case kOutI32: qgemm_dispatch<kOutI32>(a, b, e, m, n, k, s, defer); break;
     default: inval("qgemm: unknown output type");
     }
 }
 
 }  // namespace
+
+bool qgemm_deferred(const signed char* a, const signed char* b, float sa, const float* sa_dev,
+                    float sb, const float* sb_vec, void* y, int y_dtype, int m, int n, int k,
+                    hipStream_t s, KFold& f) {
+    int out;
+    switch (y_dtype) {
+    case FT_DT_F32: out = kOutF32; break;
+    case FT_DT_BF16: out = kOutBF16; break;
+    case FT_DT_F16: out = kOutF16; break;
+    default: inval("qgemm: unknown output dtype code");
+    }
+    f = KFold{};
+    Epi e{y, sa, sa_dev, sb, sb_vec};
+    qgemm_run(a, b, e, out, m, n, k, s, &f);
+    return f.ksplit > 1;
+}
+
 }  // namespace ft
 
 extern "C" {

@@ -393,6 +393,30 @@ int ft_rope_kv_append_paged_launch(const void* qkv, int dtype, long long ld,
                                    int dim, int page, int tbl_width,
                                    float theta, int pos_offset, int neox,
                                    uintptr_t stream);
+/* W8A8 GEMM then the decode token's RoPE + paged KV append: qkv =
+ * ft_qgemm_launch_ex(a_q [batch, k], sa_dev, w_q [(q_heads + 2 kv_heads)
+ * * dim, k], per-channel w_scales, y_dtype = dtype) and then
+ * ft_rope_kv_append_paged_launch(qkv, dtype, ld = (q_heads + 2 kv_heads) *
+ * dim, ...), bit for bit (qkv is written too). When the GEMM splits K over
+ * workgroups, the RoPE kernel folds its partial sums itself (no fold
+ * launch). */
+int ft_qgemm_rope_kv_append_paged_launch(const signed char* a_q, const float* sa_dev,
+                                         const signed char* w_q, const float* w_scales,
+                                         int k, int dtype, void* qkv, const int* lens,
+                                         const int* table, void* q_out, void* k_pool,
+                                         void* v_pool, int batch, int q_heads, int kv_heads,
+                                         int dim, int page, int tbl_width, float theta,
+                                         int pos_offset, int neox, uintptr_t stream);
+/* W8A8 GEMM then RMSNorm (+ optional residual) -> per-tensor int8
+ * quantize: y [rows, n] = ft_qgemm_launch_ex(a_q, sa_dev, w_q [n, k],
+ * per-channel w_scales, y_dtype = dtype), then ft_rmsnorm_quant_launch(y,
+ * dtype, w, residual, q, scale_out, rows, n, eps), bit for bit. When the
+ * GEMM splits K, the row pass folds its partial sums (and stores y). */
+int ft_qgemm_rmsnorm_quant_launch(const signed char* a_q, const float* sa_dev,
+                                  const signed char* w_q, const float* w_scales, int dtype,
+                                  void* y, const void* residual, const float* w, float eps,
+                                  signed char* q, float* scale_out, int rows, int n, int k,
+                                  uintptr_t stream);
 /* Paged decode attention then per-tensor int8 quantize of its output:
  * out [batch, q_heads, dim] as ft_attention_decode_paged_launch* writes it
  * (arguments as there; dtype FT_DT_*), and codes [batch, q_heads, dim]

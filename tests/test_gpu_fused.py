@@ -1,13 +1,15 @@
 """GPU parity of the fused decode-chain steps (rmsnorm_quant, swiglu_quant,
-rope_kv_append_paged, attention_decode_paged_quant):
+rope_kv_append_paged, attention_decode_paged_quant, qgemm_rope_kv_append_paged,
+qgemm_rmsnorm_quant):
   - against the CPU oracle on the same seeded inputs: int8 codes and the
     scale bit-exact for rmsnorm_quant (the oracle follows the kernel's
     summation order); within one code step for swiglu_quant (device expf vs
     the host's); RoPE within 1e-6 (f32) / one storage ulp (bf16, fp16);
   - against this library's unfused GPU chain (rmsnorm -> quantize_int8,
     swiglu -> quantize_int8, rope(positions=lens) -> kv_append_paged,
-    attention_decode_paged -> quantize_int8): bit-exact, which is the fused
-    ops' contract."""
+    attention_decode_paged -> quantize_int8, qgemm_perchannel ->
+    rope_kv_append_paged, qgemm_perchannel -> rmsnorm_quant): bit-exact,
+    which is the fused ops' contract, on split and unsplit GEMMs."""
 
 import numpy as np
 import pytest
@@ -379,6 +381,98 @@ def test_attention_decode_paged_quant_empty_and_errors():
                                         np.zeros((2, 2, 4, 8), np.float32),
                                         np.zeros((2, 2, 4, 8), np.float32),
                                         np.zeros((1, 1), np.int32))
+
+
+# ---------------------------------------------------------------------------
+# GEMM + next step (the K-split partials folded by the next kernel)
+# ---------------------------------------------------------------------------
+
+def wq_dev(gen, rows, cols):
+    return (torch.randint(-127, 128, (rows, cols), device=DEV, generator=gen,
+                          dtype=torch.int32).to(torch.int8),
+            (torch.rand((rows,), device=DEV, generator=gen) * 9e-3 + 1e-3).float())
+
+
+# (b, hq, hkv, d, k, switches): C4's QKV (K split 4 by default); the same
+# unsplit; a split of 3 at a toy shape; 9 partials (two load batches) on a
+# forced skinny kernel; the M = 1 GEMV (never split)
+QKV_CASES = {
+    "c4": (64, 32, 8, 128, 4096, {}),
+    "c4_unsplit": (64, 32, 8, 128, 4096, {"FT_QGEMM_KSPLIT": 1}),
+    "split3": (20, 8, 2, 64, 1024, {"FT_QGEMM_KSPLIT": 3}),
+    "split9": (5, 4, 4, 32, 2304, {"FT_QGEMM_KERNEL": 1, "FT_QGEMM_KSPLIT": 9}),
+    "gemv": (1, 8, 2, 64, 512, {}),
+}
+
+
+@pytest.mark.parametrize("dt", ALL)
+@pytest.mark.parametrize("case", list(QKV_CASES))
+def test_qgemm_rope_kv_append_equals_the_two_ops(dt, case, tuning):
+    b, hq, hkv, d, k, sw = QKV_CASES[case]
+    for name, v in sw.items():
+        tuning(name, v)
+    gen = torch.Generator(device=DEV).manual_seed(list(QKV_CASES).index(case))
+    rng = np.random.default_rng(list(QKV_CASES).index(case))
+    page = 16
+    lens = rng.integers(0, 300, b).astype(np.int32)
+    width = int(lens.max()) // page + 1
+    nb = b * width + 3
+    a = torch.randint(-127, 128, (b, k), device=DEV, generator=gen,
+                      dtype=torch.int32).to(torch.int8)
+    sa = torch.tensor([0.0123], dtype=torch.float32, device=DEV)
+    w, ws = wq_dev(gen, (hq + 2 * hkv) * d, k)
+    kp = torch.randn((nb, hkv, page, d), device=DEV, generator=gen).to(dt)
+    vp = torch.randn((nb, hkv, page, d), device=DEV, generator=gen).to(dt)
+    tbl = t(rng.permutation(nb)[: b * width].reshape(b, width).astype(np.int32))
+    ln = t(lens)
+    kp_ref, vp_ref = kp.clone(), vp.clone()
+    qkv_ref = ft.qgemm_perchannel(a, sa, w, ws, out_dtype=dt)
+    q_ref = ft.rope_kv_append_paged(qkv_ref, hq, hkv, kp_ref, vp_ref, tbl, ln,
+                                    theta=500000.0, pos_offset=3, neox=True)
+    for rep in range(2):
+        q_rot, qkv = ft.qgemm_rope_kv_append_paged(a, sa, w, ws, hq, hkv, kp, vp, tbl, ln,
+                                                   theta=500000.0, pos_offset=3, neox=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(raw(qkv), raw(qkv_ref)), f"{case} rep {rep}: qkv differs"
+        assert np.array_equal(raw(q_rot), raw(q_ref)), f"{case} rep {rep}: q differs"
+        assert np.array_equal(raw(kp), raw(kp_ref)) and np.array_equal(raw(vp), raw(vp_ref))
+
+
+# (m, n, k, residual, switches): C4's o_proj (K split 4); the same unsplit;
+# 3 rows on a forced split of 9 (the one-launch small-row path of the chain
+# against the fold's two passes); rows past 4096 columns (the row kernel's
+# loop form); the decode GEMM (never split)
+RMSQ_CASES = {
+    "c4": (64, 4096, 4096, True, {}),
+    "c4_unsplit": (64, 4096, 4096, True, {"FT_QGEMM_KSPLIT": 1}),
+    "small_split9": (3, 1024, 2304, False, {"FT_QGEMM_KERNEL": 1, "FT_QGEMM_KSPLIT": 9}),
+    "wide": (40, 5000, 512, True, {"FT_QGEMM_KSPLIT": 2}),
+    "decode": (8, 2048, 1024, True, {}),
+}
+
+
+@pytest.mark.parametrize("dt", ALL)
+@pytest.mark.parametrize("case", list(RMSQ_CASES))
+def test_qgemm_rmsnorm_quant_equals_the_two_ops(dt, case, tuning):
+    m, n, k, res, sw = RMSQ_CASES[case]
+    for name, v in sw.items():
+        tuning(name, v)
+    gen = torch.Generator(device=DEV).manual_seed(50 + list(RMSQ_CASES).index(case))
+    a = torch.randint(-127, 128, (m, k), device=DEV, generator=gen,
+                      dtype=torch.int32).to(torch.int8)
+    sa = torch.tensor([0.0031], dtype=torch.float32, device=DEV)
+    w, ws = wq_dev(gen, n, k)
+    nw = (torch.rand((n,), device=DEV, generator=gen) + 0.5).float()
+    r = torch.randn((m, n), device=DEV, generator=gen).to(dt) if res else None
+    y_ref = ft.qgemm_perchannel(a, sa, w, ws, out_dtype=dt)
+    q_ref, s_ref = ft.rmsnorm_quant(y_ref, nw, residual=r, eps=1e-5, device_scale=True)
+    for rep in range(2):
+        y, q, s = ft.qgemm_rmsnorm_quant(a, sa, w, ws, nw, residual=r, eps=1e-5, out_dtype=dt,
+                                         device_scale=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(raw(y), raw(y_ref)), f"{case} rep {rep}: y differs"
+        assert torch.equal(q, q_ref), f"{case} rep {rep}: codes differ"
+        assert s.item() == s_ref.item()
 
 
 def test_decode_layer_graph_replays_equal_eager():
