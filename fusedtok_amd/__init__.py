@@ -95,6 +95,7 @@ __all__ = [
     "rope_kv_append_paged",
     "qgemm_rope_kv_append_paged",
     "qgemm_rmsnorm_quant",
+    "DecodeLayer",
     "argmax",
     "argmax_batched",
     "sample_topp",
@@ -1055,3 +1056,6 @@ def decode_step_batched(logits, sampled_ids, penalty=1.0, *, p=0.9, temperature=
             offs_dev.data_ptr(), float(penalty), float(p), float(temperature),
             seeds_dev.data_ptr(), out.data_ptr(), _stream())
     return out if device_out else out.cpu()
+
+
+from .layer import DecodeLayer  # noqa: E402  (uses the loaded extension)

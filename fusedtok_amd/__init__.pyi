@@ -38,6 +38,7 @@ __all__ = [
     "rope_kv_append_paged",
     "qgemm_rope_kv_append_paged",
     "qgemm_rmsnorm_quant",
+    "DecodeLayer",
     "argmax",
     "argmax_batched",
     "sample_topp",
@@ -136,3 +137,30 @@ def decode_step_batched(logits: Array, sampled_ids: Histories, penalty: float = 
                         seeds: Optional[IntArray] = ...,
                         ids_offsets: Optional[IntArray] = ..., cuda: bool = ...,
                         device_out: bool = ...) -> Array: ...
+
+class DecodeLayer:
+    hidden: int
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    inter: int
+    page: int
+    max_batch: int
+    dtype: torch.dtype
+    def __init__(self, *, norm1: torch.Tensor, w_qkv: torch.Tensor, s_qkv: torch.Tensor,
+                 w_o: torch.Tensor, s_o: torch.Tensor, norm2: torch.Tensor,
+                 w_gu: torch.Tensor, s_gu: torch.Tensor, w_down: torch.Tensor,
+                 s_down: torch.Tensor, q_heads: int, kv_heads: int, page: int,
+                 max_batch: int, dtype: torch.dtype = ..., eps: float = ...,
+                 theta: float = ..., neox: bool = ..., pos_offset: int = ...) -> None: ...
+    def forward(self, x: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                block_table: torch.Tensor, lens: torch.Tensor, *,
+                out: Optional[torch.Tensor] = ...) -> torch.Tensor: ...
+    def __call__(self, x: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                 block_table: torch.Tensor, lens: torch.Tensor, *,
+                 out: Optional[torch.Tensor] = ...) -> torch.Tensor: ...
+    def capture(self, x: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                block_table: torch.Tensor, lens: torch.Tensor, *,
+                out: Optional[torch.Tensor] = ...) -> torch.Tensor: ...
+    def replay(self) -> torch.Tensor: ...
+    def close(self) -> None: ...

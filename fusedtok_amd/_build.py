@@ -38,6 +38,7 @@ HIP_SOURCES = [
     "quantize.hip",
     "norm_rope_act.hip",
     "fused.hip",
+    "layer.hip",
     "prefill.hip",
     "sampling.hip",
 ]

@@ -465,6 +465,53 @@ PYBIND11_MODULE(_fusedtok, m) {
           py::arg("dtype"), py::arg("y"), py::arg("residual"), py::arg("weight"),
           py::arg("eps"), py::arg("q"), py::arg("scale"), py::arg("rows"), py::arg("n"),
           py::arg("k"), py::arg("stream") = 0);
+    // ---- decode layer object ---------------------------------------------
+    m.def("decode_layer_create",
+          [](int hidden, int hq, int hkv, int dim, int inter, int page, int max_batch, int dtype,
+             float eps, float theta, bool neox, int pos_offset, uintptr_t n1, uintptr_t n2,
+             uintptr_t wqkv, uintptr_t sqkv, uintptr_t wo, uintptr_t so, uintptr_t wgu,
+             uintptr_t sgu, uintptr_t wd, uintptr_t sd) {
+              ft_decode_layer_desc d{};
+              d.hidden = hidden; d.q_heads = hq; d.kv_heads = hkv; d.head_dim = dim;
+              d.inter = inter; d.page = page; d.max_batch = max_batch; d.dtype = dtype;
+              d.eps = eps; d.theta = theta; d.neox = neox ? 1 : 0; d.pos_offset = pos_offset;
+              d.norm1 = P<const float>(n1); d.norm2 = P<const float>(n2);
+              d.w_qkv = P<const signed char>(wqkv); d.s_qkv = P<const float>(sqkv);
+              d.w_o = P<const signed char>(wo); d.s_o = P<const float>(so);
+              d.w_gu = P<const signed char>(wgu); d.s_gu = P<const float>(sgu);
+              d.w_down = P<const signed char>(wd); d.s_down = P<const float>(sd);
+              ft_decode_layer* L = nullptr;
+              check(ft_decode_layer_create(&d, &L));
+              return reinterpret_cast<uintptr_t>(L);
+          },
+          py::arg("hidden"), py::arg("q_heads"), py::arg("kv_heads"), py::arg("head_dim"),
+          py::arg("inter"), py::arg("page"), py::arg("max_batch"), py::arg("dtype"),
+          py::arg("eps"), py::arg("theta"), py::arg("neox"), py::arg("pos_offset"),
+          py::arg("norm1"), py::arg("norm2"), py::arg("w_qkv"), py::arg("s_qkv"),
+          py::arg("w_o"), py::arg("s_o"), py::arg("w_gu"), py::arg("s_gu"), py::arg("w_down"),
+          py::arg("s_down"));
+#define FT_LAYER_CALL(NAME, FN)                                                          \
+    m.def(NAME,                                                                          \
+          [](uintptr_t L, uintptr_t x, uintptr_t y, uintptr_t kp, uintptr_t vp,          \
+             uintptr_t table, uintptr_t lens, int batch, int tbl_width, uintptr_t stream) { \
+              check(FN(P<ft_decode_layer>(L), P<const void>(x), P<void>(y), P<void>(kp),   \
+                       P<void>(vp), P<const int>(table), P<const int>(lens), batch,        \
+                       tbl_width, stream));                                              \
+          },                                                                             \
+          py::arg("layer"), py::arg("x"), py::arg("y"), py::arg("k_pool"),               \
+          py::arg("v_pool"), py::arg("table"), py::arg("lens"), py::arg("batch"),        \
+          py::arg("tbl_width"), py::arg("stream") = 0)
+    FT_LAYER_CALL("decode_layer_forward", ft_decode_layer_forward);
+    FT_LAYER_CALL("decode_layer_capture", ft_decode_layer_capture);
+#undef FT_LAYER_CALL
+    m.def("decode_layer_replay",
+          [](uintptr_t L, uintptr_t stream) {
+              check(ft_decode_layer_replay(P<ft_decode_layer>(L), stream));
+          },
+          py::arg("layer"), py::arg("stream") = 0);
+    m.def("decode_layer_destroy",
+          [](uintptr_t L) { check(ft_decode_layer_destroy(P<ft_decode_layer>(L))); },
+          py::arg("layer"));
     m.def("rope_kv_append_paged_launch",
           [](uintptr_t qkv, int dtype, long long ld, uintptr_t lens, uintptr_t table,
              uintptr_t q_out, uintptr_t k_pool, uintptr_t v_pool, int batch,

@@ -143,6 +143,15 @@ template <typename T>
 void quantize_tensor(const T* x, signed char* q, float* scale_out, long long n,
                      hipStream_t s);
 
+// QKV GEMM (K-split partials folded by the RoPE kernel) + RoPE + paged KV
+// append, as ft_qgemm_rope_kv_append_paged_launch; lens_next (optional)
+// receives lens[b] + 1 from the same kernel. fused.hip.
+void qkv_rope_step(int dtype, const signed char* a_q, const float* sa_dev,
+                   const signed char* w_q, const float* w_scales, int k, void* qkv,
+                   const int* lens, int* lens_next, const int* table, void* q_out,
+                   void* k_pool, void* v_pool, int batch, int hq, int hkv, int dim, int page,
+                   int tbl_width, float theta, int pos_offset, bool neox, hipStream_t s);
+
 // ---------------------------------------------------------------------------
 // device: storage traits
 // ---------------------------------------------------------------------------

@@ -534,9 +534,9 @@ void swiglu_quant_run(const T* g, const T* u, signed char* q, float* scale_out,
 template <typename T, bool NEOX, bool FOLD>
 __global__ __launch_bounds__(256) void rope_kv_kernel(
     const T* __restrict__ qkv, long long ld, KFold fold, T* __restrict__ qkv_out,
-    const int* __restrict__ lens, const int* __restrict__ table, T* __restrict__ q_out,
-    T* __restrict__ k_pool, T* __restrict__ v_pool, int batch, int hq, int hkv, int dim,
-    int page, int tbl_width, double theta, int pos_offset) {
+    const int* __restrict__ lens, int* __restrict__ lens_next, const int* __restrict__ table,
+    T* __restrict__ q_out, T* __restrict__ k_pool, T* __restrict__ v_pool, int batch, int hq,
+    int hkv, int dim, int page, int tbl_width, double theta, int pos_offset) {
     const int half = dim >> 1;
     const int heads = hq + 2 * hkv;
     const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -545,6 +545,8 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     const int rem = (int)(p - (long long)b * heads * half);
     const int h = rem / half, j = rem - (rem / half) * half;
     const int slot = lens[b];
+    // the sequence's length after the append, for the attention that follows
+    if (lens_next && rem == 0) lens_next[b] = slot + 1;
     const size_t row0 = (size_t)b * ld + (size_t)h * dim;
     const int i1 = NEOX ? j : 2 * j;
     const int i2 = NEOX ? j + half : 2 * j + 1;
@@ -617,18 +619,18 @@ template <typename T, bool FOLD>
 void rope_kv_launch(const T* qkv, long long ld, const KFold& fold, T* qkv_out, const int* lens,
                     const int* table, T* q_out, T* k_pool, T* v_pool, int batch, int hq,
                     int hkv, int dim, int page, int tbl_width, float theta, int pos_offset,
-                    bool neox, hipStream_t s) {
+                    bool neox, hipStream_t s, int* lens_next = nullptr) {
     if (batch == 0) return;
     const long long threads = (long long)batch * (hq + 2 * hkv) * (dim / 2);
     const unsigned grid = (unsigned)((threads + 255) / 256);
     if (neox)
         rope_kv_kernel<T, true, FOLD><<<grid, 256, 0, s>>>(
-            qkv, ld, fold, qkv_out, lens, table, q_out, k_pool, v_pool, batch, hq, hkv, dim,
-            page, tbl_width, (double)theta, pos_offset);
+            qkv, ld, fold, qkv_out, lens, lens_next, table, q_out, k_pool, v_pool, batch, hq,
+            hkv, dim, page, tbl_width, (double)theta, pos_offset);
     else
         rope_kv_kernel<T, false, FOLD><<<grid, 256, 0, s>>>(
-            qkv, ld, fold, qkv_out, lens, table, q_out, k_pool, v_pool, batch, hq, hkv, dim,
-            page, tbl_width, (double)theta, pos_offset);
+            qkv, ld, fold, qkv_out, lens, lens_next, table, q_out, k_pool, v_pool, batch, hq,
+            hkv, dim, page, tbl_width, (double)theta, pos_offset);
     launch_check("rope_kv_append kernel launch");
 }
 
@@ -652,7 +654,7 @@ void qgemm_rope_kv_run(const signed char* a_q, const float* sa_dev, const signed
                        const float* w_scales, T* qkv, const int* lens, const int* table,
                        T* q_out, T* k_pool, T* v_pool, int batch, int hq, int hkv, int dim,
                        int k, int page, int tbl_width, float theta, int pos_offset, bool neox,
-                       int dtype, hipStream_t s) {
+                       int dtype, hipStream_t s, int* lens_next = nullptr) {
     const long long n = (long long)(hq + 2 * hkv) * dim;
     rope_kv_check(n, lens, table, q_out, k_pool, v_pool, batch, hq, hkv, dim, page, tbl_width,
                   pos_offset);
@@ -666,14 +668,33 @@ void qgemm_rope_kv_run(const signed char* a_q, const float* sa_dev, const signed
                        fold))
         rope_kv_launch<T, true>(nullptr, n, fold, qkv, lens, table, q_out, k_pool, v_pool,
                                 batch, hq, hkv, dim, page, tbl_width, theta, pos_offset, neox,
-                                s);
+                                s, lens_next);
     else
         rope_kv_launch<T, false>(qkv, n, KFold{}, nullptr, lens, table, q_out, k_pool, v_pool,
                                  batch, hq, hkv, dim, page, tbl_width, theta, pos_offset, neox,
-                                 s);
+                                 s, lens_next);
 }
 
 }  // namespace
+
+void qkv_rope_step(int dtype, const signed char* a_q, const float* sa_dev,
+                   const signed char* w_q, const float* w_scales, int k, void* qkv,
+                   const int* lens, int* lens_next, const int* table, void* q_out,
+                   void* k_pool, void* v_pool, int batch, int hq, int hkv, int dim, int page,
+                   int tbl_width, float theta, int pos_offset, bool neox, hipStream_t s) {
+#define FT_QRK(T)                                                                           \
+    qgemm_rope_kv_run<T>(a_q, sa_dev, w_q, w_scales, (T*)qkv, lens, table, (T*)q_out,       \
+                         (T*)k_pool, (T*)v_pool, batch, hq, hkv, dim, k, page, tbl_width,    \
+                         theta, pos_offset, neox, dtype, s, lens_next)
+    switch (dtype) {
+    case FT_DT_F32: FT_QRK(float); break;
+    case FT_DT_BF16: FT_QRK(bf16); break;
+    case FT_DT_F16: FT_QRK(f16); break;
+    default: inval("qgemm_rope_kv_append: unknown dtype code");
+    }
+#undef FT_QRK
+}
+
 }  // namespace ft
 
 extern "C" {
@@ -768,18 +789,9 @@ int ft_qgemm_rope_kv_append_paged_launch(const signed char* a_q, const float* sa
                                          int dim, int page, int tbl_width, float theta,
                                          int pos_offset, int neox, uintptr_t stream) {
     return ft::guarded([&] {
-        hipStream_t s = ft::as_stream(stream);
-#define FT_QRK(T)                                                                          \
-    ft::qgemm_rope_kv_run<T>(a_q, sa_dev, w_q, w_scales, (T*)qkv, lens, table, (T*)q_out,  \
-                             (T*)k_pool, (T*)v_pool, batch, q_heads, kv_heads, dim, k, page, \
-                             tbl_width, theta, pos_offset, neox != 0, dtype, s)
-        switch (dtype) {
-        case FT_DT_F32: FT_QRK(float); break;
-        case FT_DT_BF16: FT_QRK(ft::bf16); break;
-        case FT_DT_F16: FT_QRK(ft::f16); break;
-        default: ft::inval("qgemm_rope_kv_append: unknown dtype code");
-        }
-#undef FT_QRK
+        ft::qkv_rope_step(dtype, a_q, sa_dev, w_q, w_scales, k, qkv, lens, nullptr, table,
+                          q_out, k_pool, v_pool, batch, q_heads, kv_heads, dim, page,
+                          tbl_width, theta, pos_offset, neox != 0, ft::as_stream(stream));
     });
 }
 

@@ -1,0 +1,251 @@
+// Decode-layer object: one Llama-shaped W8A8 decode layer run as the fused
+// chain of this library's ops, with its activation buffers allocated once at
+// creation (so a forward allocates nothing once the library's scratch has
+// grown to the shape) and a HIP-graph capture of the whole layer.
+//
+// Chain (T = the activation / KV storage type; every step bit-identical to
+// the unfused ops it replaces):
+//   rmsnorm_quant(x, norm1)                         -> q1, s1        1-2 launches
+//   QKV GEMM + RoPE + paged KV append (K-split
+//     partials folded by the RoPE kernel)           -> q_rot, pools  2
+//   paged decode over lens + 1 tokens + quantize    -> qa, sa        3
+//   o_proj GEMM + rmsnorm_quant(o + x, norm2)       -> q2, s2        3
+//   gate/up GEMM                                    -> h             1
+//   swiglu_quant(h[:, :inter], h[:, inter:])        -> q3, s3        2
+//   down GEMM                                       -> y             1-2
+// The reference has no layer op: a decode layer there is these ops called
+// one by one (cuda_launch.hpp:40-59, 185-216, 324-460).
+#include "ft_common.hpp"
+
+#include <mutex>
+
+struct ft_decode_layer {
+    ft_decode_layer_desc d;
+    int device = 0;
+    size_t esz = 2;
+    void* arena = nullptr;
+    // activation buffers for max_batch rows
+    signed char *q1 = nullptr, *qa = nullptr, *q2 = nullptr, *q3 = nullptr;
+    void *qkv = nullptr, *qrot = nullptr, *att = nullptr, *o = nullptr, *h = nullptr;
+    int* lens_next = nullptr;
+    float* scales = nullptr;  // s1, sa, s2, s3
+    hipGraphExec_t graph = nullptr;
+};
+
+namespace ft {
+namespace {
+
+void rc_check(int rc) {
+    if (rc != FT_OK) throw Error{rc, ft_last_error()};
+}
+
+size_t dtype_size(int dtype) {
+    switch (dtype) {
+    case FT_DT_F32: return 4;
+    case FT_DT_BF16:
+    case FT_DT_F16: return 2;
+    default: inval("decode layer: unknown dtype code");
+    }
+}
+
+void check_desc(const ft_decode_layer_desc& d) {
+    if (d.hidden < 4 || d.hidden % 16 != 0)
+        inval("decode layer: hidden must be a positive multiple of 16");
+    if (d.q_heads < 1 || d.kv_heads < 1 || d.q_heads % d.kv_heads != 0)
+        inval("decode layer: q_heads must be a positive multiple of kv_heads");
+    const int g = d.q_heads / d.kv_heads;
+    if (!(g == 1 || g == 2 || g == 4 || g == 8 || g == 16))
+        inval("decode layer: the GQA group must be 1, 2, 4, 8 or 16");
+    if (d.head_dim < 4 || d.head_dim % 4 != 0 || d.head_dim > 512)
+        inval("decode layer: head_dim must be a multiple of 4 in [4, 512]");
+    if ((d.q_heads * d.head_dim) % 16 != 0)
+        inval("decode layer: q_heads * head_dim must be a multiple of 16");
+    if (d.inter < 4 || d.inter % 16 != 0)
+        inval("decode layer: inter must be a positive multiple of 16");
+    if (d.page < 1) inval("decode layer: page must be >= 1");
+    if (d.max_batch < 1) inval("decode layer: max_batch must be >= 1");
+    if (d.pos_offset < 0) inval("decode layer: pos_offset must be >= 0");
+    if (!d.norm1 || !d.norm2 || !d.w_qkv || !d.s_qkv || !d.w_o || !d.s_o || !d.w_gu ||
+        !d.s_gu || !d.w_down || !d.s_down)
+        inval("decode layer: null weight");
+    (void)dtype_size(d.dtype);
+}
+
+struct Args {
+    const void* x;
+    void* y;
+    void* k_pool;
+    void* v_pool;
+    const int* table;
+    const int* lens;
+    int batch;
+    int tbl_width;
+};
+
+void forward(ft_decode_layer& L, const Args& a, hipStream_t s) {
+    const ft_decode_layer_desc& d = L.d;
+    if (a.batch < 0 || a.batch > d.max_batch)
+        inval("decode layer: batch must be in [0, max_batch]");
+    if (a.tbl_width < 1) inval("decode layer: table width must be >= 1");
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev != L.device) inval("decode layer: called with another device current");
+    if (a.batch == 0) return;
+    if (!a.x || !a.y || !a.k_pool || !a.v_pool || !a.table || !a.lens)
+        inval("decode layer: null operand");
+    const uintptr_t st = (uintptr_t)s;
+    const int B = a.batch, hd = d.q_heads * d.head_dim;
+    float* s1 = L.scales;
+    float* sa = L.scales + 1;
+    float* s2 = L.scales + 2;
+    float* s3 = L.scales + 3;
+    rc_check(ft_rmsnorm_quant_launch(a.x, d.dtype, d.norm1, nullptr, L.q1, s1, B, d.hidden,
+                                     d.eps, st));
+    qkv_rope_step(d.dtype, L.q1, s1, d.w_qkv, d.s_qkv, d.hidden, L.qkv, a.lens, L.lens_next,
+                  a.table, L.qrot, a.k_pool, a.v_pool, B, d.q_heads, d.kv_heads, d.head_dim,
+                  d.page, a.tbl_width, d.theta, d.pos_offset, d.neox != 0, s);
+    rc_check(ft_attention_decode_paged_quant_launch(L.qrot, a.k_pool, a.v_pool, a.table,
+                                                    L.lens_next, L.att, d.dtype, L.qa, sa, B,
+                                                    d.q_heads, d.kv_heads, d.page,
+                                                    a.tbl_width, d.head_dim, st));
+    rc_check(ft_qgemm_rmsnorm_quant_launch(L.qa, sa, d.w_o, d.s_o, d.dtype, L.o, a.x, d.norm2,
+                                           d.eps, L.q2, s2, B, d.hidden, hd, st));
+    rc_check(ft_qgemm_launch_ex(L.q2, d.w_gu, d.s_gu, 0.0f, 0.0f, s2, L.h, d.dtype, B,
+                                2 * d.inter, d.hidden, st));
+    rc_check(ft_swiglu_quant_launch(L.h, (const char*)L.h + (size_t)d.inter * L.esz, d.dtype,
+                                    L.q3, s3, B, d.inter, 2LL * d.inter, st));
+    rc_check(ft_qgemm_launch_ex(L.q3, d.w_down, d.s_down, 0.0f, 0.0f, s3, a.y, d.dtype, B,
+                                d.hidden, d.inter, st));
+}
+
+}  // namespace
+}  // namespace ft
+
+extern "C" {
+
+int ft_decode_layer_create(const ft_decode_layer_desc* desc, ft_decode_layer** out) {
+    return ft::guarded([&] {
+        if (!desc || !out) ft::inval("decode layer: null argument");
+        *out = nullptr;
+        ft::check_desc(*desc);
+        auto* L = new ft_decode_layer();
+        L->d = *desc;
+        L->esz = ft::dtype_size(desc->dtype);
+        try {
+            ft::hip_check(hipGetDevice(&L->device), "hipGetDevice");
+            const size_t B = (size_t)desc->max_batch;
+            const size_t hd = (size_t)desc->q_heads * desc->head_dim;
+            const size_t nqkv = (size_t)(desc->q_heads + 2 * desc->kv_heads) * desc->head_dim;
+            const size_t sizes[] = {
+                B * desc->hidden,                // q1
+                B * hd,                          // qa
+                B * desc->hidden,                // q2
+                B * desc->inter,                 // q3
+                B * nqkv * L->esz,               // qkv
+                B * hd * L->esz,                 // qrot
+                B * hd * L->esz,                 // att
+                B * desc->hidden * L->esz,       // o
+                B * 2 * desc->inter * L->esz,    // h
+                B * sizeof(int),                 // lens_next
+                4 * sizeof(float),               // scales
+            };
+            size_t off[11], total = 0;
+            for (int i = 0; i < 11; ++i) {
+                off[i] = total;
+                total += (sizes[i] + 255) & ~(size_t)255;
+            }
+            hipError_t e = hipMalloc(&L->arena, total);
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                L->arena = nullptr;
+                ft::hip_fail("decode layer buffer allocation", e);
+            }
+            char* base = (char*)L->arena;
+            L->q1 = (signed char*)(base + off[0]);
+            L->qa = (signed char*)(base + off[1]);
+            L->q2 = (signed char*)(base + off[2]);
+            L->q3 = (signed char*)(base + off[3]);
+            L->qkv = base + off[4];
+            L->qrot = base + off[5];
+            L->att = base + off[6];
+            L->o = base + off[7];
+            L->h = base + off[8];
+            L->lens_next = (int*)(base + off[9]);
+            L->scales = (float*)(base + off[10]);
+        } catch (...) {
+            delete L;
+            throw;
+        }
+        *out = L;
+    });
+}
+
+int ft_decode_layer_forward(ft_decode_layer* layer, const void* x, void* y, void* k_pool,
+                            void* v_pool, const int* table, const int* lens, int batch,
+                            int tbl_width, uintptr_t stream) {
+    return ft::guarded([&] {
+        if (!layer) ft::inval("decode layer: null layer");
+        ft::forward(*layer, ft::Args{x, y, k_pool, v_pool, table, lens, batch, tbl_width},
+                    ft::as_stream(stream));
+    });
+}
+
+int ft_decode_layer_capture(ft_decode_layer* layer, const void* x, void* y, void* k_pool,
+                            void* v_pool, const int* table, const int* lens, int batch,
+                            int tbl_width, uintptr_t stream) {
+    return ft::guarded([&] {
+        if (!layer) ft::inval("decode layer: null layer");
+        const ft::Args a{x, y, k_pool, v_pool, table, lens, batch, tbl_width};
+        hipStream_t s = ft::as_stream(stream);
+        // warm-up on the caller's stream: sizes the library's scratch for this
+        // shape (growth is refused under capture)
+        ft::forward(*layer, a, s);
+        ft::hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        hipStream_t cs = nullptr;
+        ft::hip_check(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking), "hipStreamCreate");
+        hipGraph_t g = nullptr;
+        hipGraphExec_t exec = nullptr;
+        try {
+            ft::hip_check(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal),
+                          "hipStreamBeginCapture");
+            try {
+                ft::forward(*layer, a, cs);
+            } catch (...) {
+                hipGraph_t broken = nullptr;
+                (void)hipStreamEndCapture(cs, &broken);
+                if (broken) (void)hipGraphDestroy(broken);
+                throw;
+            }
+            ft::hip_check(hipStreamEndCapture(cs, &g), "hipStreamEndCapture");
+            ft::hip_check(hipGraphInstantiate(&exec, g, nullptr, nullptr, 0),
+                          "hipGraphInstantiate");
+        } catch (...) {
+            if (g) (void)hipGraphDestroy(g);
+            (void)hipStreamDestroy(cs);
+            throw;
+        }
+        (void)hipGraphDestroy(g);
+        (void)hipStreamDestroy(cs);
+        if (layer->graph) (void)hipGraphExecDestroy(layer->graph);
+        layer->graph = exec;
+    });
+}
+
+int ft_decode_layer_replay(ft_decode_layer* layer, uintptr_t stream) {
+    return ft::guarded([&] {
+        if (!layer) ft::inval("decode layer: null layer");
+        if (!layer->graph) ft::inval("decode layer: nothing captured");
+        ft::hip_check(hipGraphLaunch(layer->graph, ft::as_stream(stream)), "hipGraphLaunch");
+    });
+}
+
+int ft_decode_layer_destroy(ft_decode_layer* layer) {
+    return ft::guarded([&] {
+        if (!layer) return;
+        if (layer->graph) (void)hipGraphExecDestroy(layer->graph);
+        if (layer->arena) (void)hipFree(layer->arena);
+        delete layer;
+    });
+}
+
+}  // extern "C"

@@ -434,6 +434,57 @@ int ft_attention_decode_paged_quant_launch(const void* q, const void* k_pool,
                                            uintptr_t stream);
 
 /* ------------------------------------------------------------------ */
+/* Decode layer (build addition). The reference has no layer op: a     */
+/* decode layer calls the ops above one by one. This object runs one   */
+/* Llama-shaped W8A8 decode layer as the fused chain                   */
+/*   rmsnorm_quant(x, norm1) -> qgemm_rope_kv_append_paged (QKV)        */
+/*   -> attention_decode_paged_quant over lens + 1 tokens               */
+/*   -> qgemm_rmsnorm_quant (o_proj, residual x, norm2)                 */
+/*   -> gate/up GEMM -> swiglu_quant -> down GEMM -> y                  */
+/* every step bit-identical to the unfused ops. Its activation buffers */
+/* are allocated once at create (for max_batch rows); the weights are  */
+/* borrowed and must outlive the layer. x, y [batch, hidden] and the   */
+/* pools [blocks, kv_heads, page, head_dim] are of `dtype`; table      */
+/* [batch, tbl_width] and lens [batch] are int32 (device; trusted).    */
+/* The token of sequence b sits at position lens[b] + pos_offset and   */
+/* is appended at slot lens[b]; lens is not advanced.                  */
+/* ------------------------------------------------------------------ */
+typedef struct ft_decode_layer ft_decode_layer;
+typedef struct ft_decode_layer_desc {
+    int hidden, q_heads, kv_heads, head_dim, inter;
+    int page;       /* KV pool page size in tokens */
+    int max_batch;  /* rows the activation buffers hold */
+    int dtype;      /* FT_DT_F32 / BF16 / F16: activations and KV */
+    float eps, theta;
+    int neox, pos_offset;
+    const float* norm1;        /* [hidden] */
+    const float* norm2;        /* [hidden] */
+    const signed char* w_qkv;  /* [(q_heads + 2 kv_heads) * head_dim, hidden] */
+    const float* s_qkv;        /* per output channel */
+    const signed char* w_o;    /* [hidden, q_heads * head_dim] */
+    const float* s_o;
+    const signed char* w_gu;   /* [2 * inter, hidden]: gate rows, then up rows */
+    const float* s_gu;
+    const signed char* w_down; /* [hidden, inter] */
+    const float* s_down;
+} ft_decode_layer_desc;
+int ft_decode_layer_create(const ft_decode_layer_desc* desc, ft_decode_layer** out);
+/* One forward on `stream`, with the device current at create. */
+int ft_decode_layer_forward(ft_decode_layer* layer, const void* x, void* y, void* k_pool,
+                            void* v_pool, const int* table, const int* lens, int batch,
+                            int tbl_width, uintptr_t stream);
+/* Runs one forward on `stream` (a warm-up that sizes the library's
+ * scratch for the shape, with the same writes a replay makes), then
+ * records the forward into a HIP graph kept by the layer (replacing an
+ * earlier one). A replay reads the operands' CURRENT contents at the
+ * captured addresses: write new inputs in place and replay. */
+int ft_decode_layer_capture(ft_decode_layer* layer, const void* x, void* y, void* k_pool,
+                            void* v_pool, const int* table, const int* lens, int batch,
+                            int tbl_width, uintptr_t stream);
+int ft_decode_layer_replay(ft_decode_layer* layer, uintptr_t stream);
+int ft_decode_layer_destroy(ft_decode_layer* layer);
+
+/* ------------------------------------------------------------------ */
 /* Post-logits sampling                                                */
 /* Greedy argmax: index of the first maximum of each row (a scan with  */
 /* strict >: NaN never wins except at index 0). Replaces argmax_launch */
