@@ -295,40 +295,42 @@ def bench_c4(torch, np, ft, dev):
     kp = torch.randn((pool, hkv, page, d), device=dev, generator=gen, dtype=bf)
     vp = torch.randn((pool, hkv, page, d), device=dev, generator=gen, dtype=bf)
     lens = torch.full((b,), c["ctx"], dtype=torch.int32, device=dev)
-    lens1 = lens + 1
     x = torch.randn((b, hid), device=dev, generator=gen).to(bf)
 
+    # the layer object runs the fused chain: rmsnorm_quant -> QKV GEMM with
+    # RoPE + paged append -> decode attention + quantize -> o_proj GEMM with
+    # residual RMSNorm + quantize -> gate/up GEMM -> swiglu_quant -> down
+    objs = [ft.DecodeLayer(norm1=L["wn1"], norm2=L["wn2"], w_qkv=L["qkv"][0],
+                           s_qkv=L["qkv"][1], w_o=L["o"][0], s_o=L["o"][1],
+                           w_gu=L["gu"][0], s_gu=L["gu"][1], w_down=L["down"][0],
+                           s_down=L["down"][1], q_heads=hq, kv_heads=hkv, page=page,
+                           max_batch=b, dtype=bf, eps=c["eps"], theta=c["theta"], neox=True,
+                           pos_offset=0)
+            for L in layers]
+    y = torch.empty_like(x)
+
     def layer(i):
-        L = layers[i % len(layers)]
-        q1, s1 = ft.rmsnorm_quant(x, L["wn1"], eps=c["eps"], device_scale=True)
-        qkv = ft.qgemm_perchannel(q1, s1, *L["qkv"], out_dtype=bf)
-        # position ctx = lens[b] + pos_offset 0
-        qr = ft.rope_kv_append_paged(qkv, hq, hkv, kp, vp, table, lens,
-                                     theta=c["theta"], pos_offset=0, neox=True)
-        att = ft.attention_decode_paged(qr, kp, vp, table, lens1)
-        qa, sa = ft.quantize_int8(att.reshape(b, hq * d), device_scale=True)
-        o = ft.qgemm_perchannel(qa, sa, *L["o"], out_dtype=bf)
-        q2, s2 = ft.rmsnorm_quant(o, L["wn2"], residual=x, eps=c["eps"],
-                                  device_scale=True)
-        h = ft.qgemm_perchannel(q2, s2, *L["gu"], out_dtype=bf)
-        q3, s3 = ft.swiglu_quant(h[:, :inter], h[:, inter:], device_scale=True)
-        return ft.qgemm_perchannel(q3, s3, *L["down"], out_dtype=bf)
+        # position ctx = lens[b] + pos_offset 0; attention over lens + 1
+        return objs[i % len(objs)].forward(x, kp, vp, table, lens, out=y)
     us = graph_time_us(torch, layer, 2 * len(layers), c["reps"])
     wbytes = sum(int(w[0].numel()) + 4 * int(w[1].numel())
                  for w in (layers[0]["qkv"], layers[0]["o"], layers[0]["gu"], layers[0]["down"]))
     kvbytes = b * (c["ctx"] + 1) * hkv * d * 2 * 2
     nbytes = wbytes + kvbytes
     gbs = nbytes / (us * 1e-6) / 1e9
-    del kp, vp, layers
+    for o in objs:
+        o.close()
+    del kp, vp, layers, objs
     return {"metric": "Llama-3-8B W8A8 decode layer (BASELINE config 4)",
             "value": round(us, 2), "unit": "us per layer",
             "tokens_per_s": round(b / (us * 1e-6), 1),
             "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "bytes_per_layer": nbytes, "dtype": "bf16 activations / KV, int8 GEMMs",
-            "config": {"workload": "rmsnorm_quant -> QKV qgemm -> rope_kv_append_paged "
-                                   "(NeoX, position 8192) -> attention_decode_paged -> "
-                                   "quantize -> o_proj qgemm -> rmsnorm_quant(+residual) "
-                                   "-> gate/up qgemm -> swiglu_quant -> down qgemm",
+            "config": {"workload": "DecodeLayer: rmsnorm_quant -> QKV qgemm + RoPE "
+                                   "(NeoX, position 8192) + paged append -> "
+                                   "attention_decode_paged + quantize -> o_proj qgemm + "
+                                   "rmsnorm_quant(+residual) -> gate/up qgemm -> "
+                                   "swiglu_quant -> down qgemm",
                        "batch": b, "context": c["ctx"], "layers_cycled": c["layers"],
                        "seed": c["seed"]}}
 

@@ -69,21 +69,22 @@ constexpr int kRowChunks = 4;  // 4-element chunks per thread held in registers
 
 // One workgroup per row: sum of squares -> inv, then the row's max |y|. A row
 // of up to 4096 columns stays in registers between the two passes.
-// FOLD: x is the output of a K-split GEMM, folded here from its partials
-// (and stored into x_out, as the GEMM would have stored it).
-template <typename T, bool RES, bool FOLD>
+// FK > 0: x is the output of a K-split GEMM, folded here from its partials
+// (fold width FK, kfold.hpp) and stored into x_out, as the GEMM would have.
+template <typename T, bool RES, int FK>
 __global__ __launch_bounds__(kFNT) void rmsq_rows(
     const T* __restrict__ x, const T* __restrict__ r, const float* __restrict__ w,
     RowStat* __restrict__ stat, int cols, float eps, KFold fold, T* __restrict__ x_out) {
     __shared__ float red[kFNT / 64];
     const size_t base = (size_t)blockIdx.x * cols;
     const int chunks = cols >> 2;
+    constexpr bool FOLD = FK > 0;
     float sa = 0.0f;
     if constexpr (FOLD) sa = kfold_sa(fold);
     // chunk c of the row as stored in T, widened to f32
     auto load_x4 = [&](int c) -> float4 {
         if constexpr (FOLD) {
-            const int4 a = kfold_sum4(fold, base + 4 * c);
+            const int4 a = kfold_sum4<FK>(fold, base + 4 * c);
             return make_float4(kfold_value<T>(a.x, kfold_scale(fold, sa, 4 * c)),
                                kfold_value<T>(a.y, kfold_scale(fold, sa, 4 * c + 1)),
                                kfold_value<T>(a.z, kfold_scale(fold, sa, 4 * c + 2)),
@@ -345,12 +346,22 @@ void rmsq_two_pass(const T* x, const KFold& fold, T* x_out, const float* w, cons
                    signed char* q, float* scale_out, int rows, int cols, float eps,
                    hipStream_t s) {
     RowStat* stat = (RowStat*)scratch(Scratch::QuantMax, (size_t)rows * sizeof(RowStat), s);
-    if (r)
-        rmsq_rows<T, true, FOLD><<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps,
-                                                                 fold, x_out);
-    else
-        rmsq_rows<T, false, FOLD><<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps,
-                                                                  fold, x_out);
+    const int fk = FOLD ? kfold_width(fold.ksplit) : 0;
+#define FT_ROWS(RES_, FK_)                                                                \
+    rmsq_rows<T, RES_, FK_><<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps, fold, \
+                                                            x_out)
+    if (r) {
+        if (fk == 0) FT_ROWS(true, 0);
+        else if (fk == 4) FT_ROWS(true, 4);
+        else if (fk == 8) FT_ROWS(true, 8);
+        else FT_ROWS(true, 1);
+    } else {
+        if (fk == 0) FT_ROWS(false, 0);
+        else if (fk == 4) FT_ROWS(false, 4);
+        else if (fk == 8) FT_ROWS(false, 8);
+        else FT_ROWS(false, 1);
+    }
+#undef FT_ROWS
     launch_check("rmsnorm_quant row kernel launch");
     if constexpr (FOLD) x = x_out;
     const long long n4 = (long long)rows * cols / 4;
@@ -395,7 +406,7 @@ void qgemm_rmsq_run(const signed char* a_q, const float* sa_dev, const signed ch
     if (rows == 0) return;
     if (!a_q || !sa_dev || !w_q || !w_scales) inval("qgemm_rmsnorm_quant: null operand");
     KFold fold;
-    if (qgemm_deferred(a_q, w_q, 0.0f, sa_dev, 0.0f, w_scales, y, dtype, rows, n, k, s, fold))
+    if (qgemm_deferred(a_q, w_q, sa_dev, w_scales, y, dtype, rows, n, k, s, fold))
         rmsq_two_pass<T, true>(nullptr, fold, y, w, r, q, scale_out, rows, n, eps, s);
     else
         rmsnorm_quant_run<T>(y, w, r, q, scale_out, rows, n, eps, s);
@@ -531,7 +542,7 @@ void swiglu_quant_run(const T* g, const T* u, signed char* q, float* scale_out,
 // Hq + Hkv rotated heads, plus one per (b, v head, pair) copied. The QKV row
 // of sequence b is qkv[b * ld + (head * D ..)], heads ordered q | k | v.
 // ---------------------------------------------------------------------------
-template <typename T, bool NEOX, bool FOLD>
+template <typename T, bool NEOX, int FK>
 __global__ __launch_bounds__(256) void rope_kv_kernel(
     const T* __restrict__ qkv, long long ld, KFold fold, T* __restrict__ qkv_out,
     const int* __restrict__ lens, int* __restrict__ lens_next, const int* __restrict__ table,
@@ -552,11 +563,12 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     const int i2 = NEOX ? j + half : 2 * j + 1;
     // the two inputs: the GEMM output as stored in T, read back or folded
     // from the K-split partials (and then also stored, as the GEMM would)
+    constexpr bool FOLD = FK > 0;
     float x1, x2;
     if constexpr (FOLD) {
         const float sa = kfold_sa(fold);
         const int c1 = h * dim + i1, c2 = h * dim + i2;
-        const int a1 = kfold_sum(fold, row0 + i1), a2 = kfold_sum(fold, row0 + i2);
+        const int a1 = kfold_sum<FK>(fold, row0 + i1), a2 = kfold_sum<FK>(fold, row0 + i2);
         x1 = kfold_value<T>(a1, kfold_scale(fold, sa, c1));
         x2 = kfold_value<T>(a2, kfold_scale(fold, sa, c2));
         St<T>::st(qkv_out + row0 + i1, x1);
@@ -623,14 +635,23 @@ void rope_kv_launch(const T* qkv, long long ld, const KFold& fold, T* qkv_out, c
     if (batch == 0) return;
     const long long threads = (long long)batch * (hq + 2 * hkv) * (dim / 2);
     const unsigned grid = (unsigned)((threads + 255) / 256);
-    if (neox)
-        rope_kv_kernel<T, true, FOLD><<<grid, 256, 0, s>>>(
-            qkv, ld, fold, qkv_out, lens, lens_next, table, q_out, k_pool, v_pool, batch, hq,
-            hkv, dim, page, tbl_width, (double)theta, pos_offset);
-    else
-        rope_kv_kernel<T, false, FOLD><<<grid, 256, 0, s>>>(
-            qkv, ld, fold, qkv_out, lens, lens_next, table, q_out, k_pool, v_pool, batch, hq,
-            hkv, dim, page, tbl_width, (double)theta, pos_offset);
+    const int fk = FOLD ? kfold_width(fold.ksplit) : 0;
+#define FT_ROPE(NEOX_, FK_)                                                                \
+    rope_kv_kernel<T, NEOX_, FK_><<<grid, 256, 0, s>>>(                                    \
+        qkv, ld, fold, qkv_out, lens, lens_next, table, q_out, k_pool, v_pool, batch, hq, \
+        hkv, dim, page, tbl_width, (double)theta, pos_offset)
+    if (neox) {
+        if (fk == 0) FT_ROPE(true, 0);
+        else if (fk == 4) FT_ROPE(true, 4);
+        else if (fk == 8) FT_ROPE(true, 8);
+        else FT_ROPE(true, 1);
+    } else {
+        if (fk == 0) FT_ROPE(false, 0);
+        else if (fk == 4) FT_ROPE(false, 4);
+        else if (fk == 8) FT_ROPE(false, 8);
+        else FT_ROPE(false, 1);
+    }
+#undef FT_ROPE
     launch_check("rope_kv_append kernel launch");
 }
 
@@ -664,7 +685,7 @@ void qgemm_rope_kv_run(const signed char* a_q, const float* sa_dev, const signed
     if (!a_q || !sa_dev || !w_q || !w_scales || !qkv)
         inval("qgemm_rope_kv_append: null operand");
     KFold fold;
-    if (qgemm_deferred(a_q, w_q, 0.0f, sa_dev, 0.0f, w_scales, qkv, dtype, batch, (int)n, k, s,
+    if (qgemm_deferred(a_q, w_q, sa_dev, w_scales, qkv, dtype, batch, (int)n, k, s,
                        fold))
         rope_kv_launch<T, true>(nullptr, n, fold, qkv, lens, table, q_out, k_pool, v_pool,
                                 batch, hq, hkv, dim, page, tbl_width, theta, pos_offset, neox,

@@ -5,9 +5,9 @@
 // The folded value of output (row, col) is the one the GEMM epilogue stores:
 //   acc = sum over j < ksplit of part[j * m * n + row * n + col]  (int32,
 //         exact in any order: |acc| <= 127 * 127 * K < 2^31 for K <= 131071)
-//   s   = f32(sa * sb[col])       (sa = *sa_dev when set; sb[col] = sb_vec[col]
-//                                  or the per-tensor sb)
-//   y   = T(f32(acc * s))         (two f32 roundings, then one to T)
+//   s   = f32(*sa_dev * sb_vec[col])   (device activation scale, per-channel
+//                                       weight scales)
+//   y   = T(f32(acc * s))              (two f32 roundings, then one to T)
 #pragma once
 
 #include "ft_common.hpp"
@@ -20,29 +20,25 @@ struct KFold {
     int n = 0;
     long long mn = 0;
     const float* sa_dev = nullptr;
-    float sa = 0.0f;
     const float* sb_vec = nullptr;
-    float sb = 0.0f;
 };
 
-// Runs y[m, n] = A[m, k] . B[n, k]^T (int8, per-channel or per-tensor scales,
-// y_dtype FT_DT_F32 / BF16 / F16) as ft_qgemm_launch_ex does. When the
-// dispatch splits K over workgroups, the int32 partials are left in the
-// library's GEMM scratch, `f` describes them and the result is true: the
-// caller's next launch on stream s must fold them (before any other GEMM
-// reuses that scratch). Otherwise y is written and the result is false.
-// qgemm.hip.
-bool qgemm_deferred(const signed char* a, const signed char* b, float sa, const float* sa_dev,
-                    float sb, const float* sb_vec, void* y, int y_dtype, int m, int n, int k,
+// Runs y[m, n] = A[m, k] . B[n, k]^T (int8; device activation scale *sa_dev,
+// per-channel weight scales sb_vec; y_dtype FT_DT_F32 / BF16 / F16) as
+// ft_qgemm_launch_ex does. When the dispatch splits K over workgroups, the
+// int32 partials are left in the library's GEMM scratch, `f` describes them
+// and the result is true: the caller's next launch on stream s must fold
+// them (before any other GEMM reuses that scratch). Otherwise y is written
+// and the result is false. qgemm.hip.
+bool qgemm_deferred(const signed char* a, const signed char* b, const float* sa_dev,
+                    const float* sb_vec, void* y, int y_dtype, int m, int n, int k,
                     hipStream_t s, KFold& f);
 
-__device__ __forceinline__ float kfold_sa(const KFold& f) {
-    return f.sa_dev ? *f.sa_dev : f.sa;
-}
+__device__ __forceinline__ float kfold_sa(const KFold& f) { return *f.sa_dev; }
 
 // composed scale of column col (one f32 rounding)
 __device__ __forceinline__ float kfold_scale(const KFold& f, float sa, int col) {
-    return sa * (f.sb_vec ? f.sb_vec[col] : f.sb);
+    return sa * f.sb_vec[col];
 }
 
 // the stored value widened back to f32 (T = float: the f32 product itself)
@@ -53,35 +49,42 @@ __device__ __forceinline__ float kfold_value(int acc, float s) {
     return (float)(T)v;
 }
 
-constexpr int kKFoldBatch = 8;  // partial loads in flight per output
+// Fold widths: a kernel instantiated with FK = 4 or 8 loads all partials
+// of an output in one batch of FK loads (ksplit <= FK; partial indices past
+// ksplit are clamped and their values dropped by a select after the load,
+// no branch between loads), so every load of a thread shares one memory
+// round trip; FK = 1 loops over batches of 8 (any ksplit); FK = 0: no fold.
+inline int kfold_width(int ksplit) { return ksplit <= 4 ? 4 : ksplit <= 8 ? 8 : 1; }
 
-// int32 sum over the partials of output idx = row * n + col. Loads are
-// issued in batches of 8 with the partial index clamped (a select after the
-// load, no branch between loads).
+// int32 sum over the partials of output idx = row * n + col
+template <int FK>
 __device__ __forceinline__ int kfold_sum(const KFold& f, size_t idx) {
+    constexpr int W = FK == 1 ? 8 : FK;
     int s = 0;
-    for (int j0 = 0; j0 < f.ksplit; j0 += kKFoldBatch) {
-        int v[kKFoldBatch];
+    for (int j0 = 0; j0 < (FK == 1 ? f.ksplit : 1); j0 += W) {
+        int v[W];
 #pragma unroll
-        for (int u = 0; u < kKFoldBatch; ++u)
+        for (int u = 0; u < W; ++u)
             v[u] = f.part[(size_t)min(j0 + u, f.ksplit - 1) * f.mn + idx];
 #pragma unroll
-        for (int u = 0; u < kKFoldBatch; ++u) s += j0 + u < f.ksplit ? v[u] : 0;
+        for (int u = 0; u < W; ++u) s += j0 + u < f.ksplit ? v[u] : 0;
     }
     return s;
 }
 
 // four consecutive outputs idx .. idx + 3 (idx % 4 == 0, n % 4 == 0)
+template <int FK>
 __device__ __forceinline__ int4 kfold_sum4(const KFold& f, size_t idx) {
+    constexpr int W = FK == 1 ? 8 : FK;
     int4 s = make_int4(0, 0, 0, 0);
-    for (int j0 = 0; j0 < f.ksplit; j0 += kKFoldBatch) {
-        int4 v[kKFoldBatch];
+    for (int j0 = 0; j0 < (FK == 1 ? f.ksplit : 1); j0 += W) {
+        int4 v[W];
 #pragma unroll
-        for (int u = 0; u < kKFoldBatch; ++u)
+        for (int u = 0; u < W; ++u)
             v[u] = *reinterpret_cast<const int4*>(
                 f.part + (size_t)min(j0 + u, f.ksplit - 1) * f.mn + idx);
 #pragma unroll
-        for (int u = 0; u < kKFoldBatch; ++u) {
+        for (int u = 0; u < W; ++u) {
             const bool live = j0 + u < f.ksplit;
             s.x += live ? v[u].x : 0;
             s.y += live ? v[u].y : 0;

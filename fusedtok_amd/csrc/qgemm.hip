@@ -1994,9 +1994,7 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
             defer->n = n;
             defer->mn = (long long)m * n;
             defer->sa_dev = e.sa_dev;
-            defer->sa = e.sa;
             defer->sb_vec = e.sb_vec;
-            defer->sb = e.sb;
             return;
         }
         if (ksplit > 1) {
@@ -2064,9 +2062,10 @@ void qgemm_run(const i8* a, const i8* b, Epi e, int out, int m, int n, int k,
 
 }  // namespace
 
-bool qgemm_deferred(const signed char* a, const signed char* b, float sa, const float* sa_dev,
-                    float sb, const float* sb_vec, void* y, int y_dtype, int m, int n, int k,
+bool qgemm_deferred(const signed char* a, const signed char* b, const float* sa_dev,
+                    const float* sb_vec, void* y, int y_dtype, int m, int n, int k,
                     hipStream_t s, KFold& f) {
+    if (!sa_dev || !sb_vec) inval("qgemm: a device scale and per-channel scales are required");
     int out;
     switch (y_dtype) {
     case FT_DT_F32: out = kOutF32; break;
@@ -2075,7 +2074,7 @@ bool qgemm_deferred(const signed char* a, const signed char* b, float sa, const 
     default: inval("qgemm: unknown output dtype code");
     }
     f = KFold{};
-    Epi e{y, sa, sa_dev, sb, sb_vec};
+    Epi e{y, 0.0f, sa_dev, 0.0f, sb_vec};
     qgemm_run(a, b, e, out, m, n, k, s, &f);
     return f.ksplit > 1;
 }
