@@ -867,8 +867,21 @@ void launch_stream(bool paged, int page_shift, int nseg, hipStream_t s, const T*
 struct Workspace {
     void* fixed = nullptr;
     size_t cap = 0;
+    // the contiguous decode's fallback (reference attention.cu:1514-1523,
+    // where it runs the single-pass kernel instead): when the library's
+    // buffer cannot be allocated (or grown under a capture), the partials go
+    // to the static per-device array of FT_NOALLOC_WORKSPACE_BYTES; the paged
+    // decode raises instead, as the reference's (attention.cu:1830-1844)
+    void* (*fallback)() = nullptr;
     void* get(size_t bytes, hipStream_t s) const {
-        if (!fixed) return scratch(Scratch::AttnPartials, bytes, s);
+        if (!fixed) {
+            try {
+                return scratch(Scratch::AttnPartials, bytes, s);
+            } catch (const Error& err) {
+                if (!fallback || err.code != FT_EHIP || bytes > FT_NOALLOC_WORKSPACE_BYTES) throw;
+                return fallback();
+            }
+        }
         if (bytes > cap)
             inval("attention: this call needs " + std::to_string(bytes) +
                   " bytes of split workspace; the static workspace holds " +
@@ -1101,6 +1114,14 @@ void* static_workspace() {
     }
     return g_static_ws[dev];
 }
+
+// the contiguous decode's workspace: the library's buffer, or the static
+// array when that cannot be allocated
+ft::Workspace contiguous_workspace() {
+    ft::Workspace w;
+    w.fallback = &static_workspace;
+    return w;
+}
 }  // namespace
 
 extern "C" {
@@ -1162,7 +1183,7 @@ int ft_attention_decode_launch(const float* q, const float* k, const float* v,
     return ft::guarded([&] {
         ft::attention_run<float>(q, k, v, nullptr, lens, out, batch, q_heads,
                                  kv_heads, cache_rows, 0, dim, false,
-                                 ft::as_stream(stream));
+                                 ft::as_stream(stream), contiguous_workspace());
     });
 }
 
@@ -1174,7 +1195,7 @@ int ft_attention_decode_launch_bf16(const void* q, const void* k,
         ft::attention_run<bf16>((const bf16*)q, (const bf16*)k, (const bf16*)v,
                                 nullptr, lens, (bf16*)out, batch, q_heads,
                                 kv_heads, cache_rows, 0, dim, false,
-                                ft::as_stream(stream));
+                                ft::as_stream(stream), contiguous_workspace());
     });
 }
 
@@ -1186,7 +1207,7 @@ int ft_attention_decode_launch_fp16(const void* q, const void* k,
         ft::attention_run<f16>((const f16*)q, (const f16*)k, (const f16*)v,
                                nullptr, lens, (f16*)out, batch, q_heads,
                                kv_heads, cache_rows, 0, dim, false,
-                               ft::as_stream(stream));
+                               ft::as_stream(stream), contiguous_workspace());
     });
 }
 

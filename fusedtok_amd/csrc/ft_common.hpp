@@ -109,6 +109,8 @@ enum class Tune : int {
     ArgSlices,             // FT_ARG_SLICES: argmax_batched slices per row
     SmpSingle,             // FT_SMP_SINGLE: sampling, one workgroup per row
     SmpSlices,             // FT_SMP_SLICES: sampling slices per row
+    FailScratch,           // FT_FAIL_SCRATCH (test hook): every scratch request
+                           // fails as an allocation failure would
     kCount
 };
 // The switch's value, or `dflt` when it is neither in the environment nor

@@ -74,7 +74,7 @@ constexpr const char* kTuneNames[(int)Tune::kCount] = {
     "FT_QGEMM_SK_WAVES",     "FT_QGEMM_SK_STAGES",
     "FT_QGEMM_BIG",          "FT_QGEMM_BAND",      "FT_RMSQ_SPLIT",
     "FT_RMSQ_GEMV_SPLIT",    "FT_PREFILL_FORCE_GENERIC", "FT_ARG_SLICES",
-    "FT_SMP_SINGLE",         "FT_SMP_SLICES"};
+    "FT_SMP_SINGLE",         "FT_SMP_SLICES",      "FT_FAIL_SCRATCH"};
 
 // value and presence per switch: the environment's (read once), then the
 // run-time override, which wins while set
@@ -123,6 +123,11 @@ bool stream_capturing(hipStream_t s) {
 
 namespace {
 void* scratch_impl(Scratch which, size_t bytes, hipStream_t s, bool zero) {
+    // test hook, checked before any HIP call so that a host without a
+    // device reaches it too
+    if (tune(Tune::FailScratch, 0))
+        throw Error{FT_EHIP, "device scratch allocation: out of memory "
+                             "(simulated by FT_FAIL_SCRATCH)"};
     const int dev = current_device();
     std::lock_guard<std::mutex> lock(state_mutex());
     ScratchSlot& slot = state_for(dev).slots[(int)which];

@@ -14,7 +14,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "fusedtok_amd.h")
 LIB = os.path.join(ROOT, "fusedtok_amd", "libfusedtok_amd.so")
 
-FT_OK, FT_EINVAL = 0, 1
+FT_OK, FT_EINVAL, FT_EHIP = 0, 1, 2
 
 
 def declared_symbols():
@@ -243,3 +243,23 @@ def test_tuning_switches_by_name(lib):
     assert lib.ft_set_tuning(b"FT_NO_SUCH_SWITCH", 1) == FT_EINVAL
     assert b"unknown tuning switch" in lib.ft_last_error()
     assert lib.ft_clear_tuning(None) == FT_EINVAL
+
+
+def test_scratch_allocation_failure_is_reported(lib):
+    # FT_FAIL_SCRATCH (test hook) fails every device-scratch request the way
+    # an allocation failure does. A quantize of 2^20 elements asks for its
+    # partial-maximum scratch before any launch, so the error path is reached
+    # (and the pointers never touched) without a device.
+    lib.ft_set_tuning.argtypes = [ctypes.c_char_p, ctypes.c_int]
+    lib.ft_clear_tuning.argtypes = [ctypes.c_char_p]
+    assert lib.ft_set_tuning(b"FT_FAIL_SCRATCH", 1) == FT_OK
+    try:
+        rc = lib.ft_quantize_int8_launch(_v(256), _v(256), _v(256), ctypes.c_longlong(1 << 20),
+                                         ctypes.c_uint64(0))
+        assert rc == FT_EHIP
+        assert b"FT_FAIL_SCRATCH" in lib.ft_last_error()
+        import fusedtok_amd as ft
+        with pytest.raises(RuntimeError, match="out of memory"):
+            ft._fusedtok.quantize_launch(256, 256, 256, 1 << 20, 0)
+    finally:
+        assert lib.ft_clear_tuning(b"FT_FAIL_SCRATCH") == FT_OK
