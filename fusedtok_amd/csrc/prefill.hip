@@ -10,7 +10,7 @@
 //
 // attn_prefill_mfma<T, D>: bf16 / fp16 storage, D in {64, 128}. A
 // workgroup owns 128 query rows of one (b, q head), 32 per wave; 64-row K
-// and V tiles stream through two LDS stages, V transposed on the way in.
+// and V tiles stream through two LDS stages, both row-major.
 // Everything is computed transposed, so every accumulator a lane holds
 // belongs to one query row (r = lane % 16, g = lane / 16; operand layout
 // of v_mfma_f32_16x16x32: A[r][8g+j], B[8g+j][r], C[4g+i][r]):
@@ -25,8 +25,13 @@
 //           score accumulators: for a 32-key step, lane (q, g) holds keys
 //           {4g+i} of block 2ks and {16+4g+i} of block 2ks+1, so the k
 //           slots are permuted (slot 8g+i <-> key 4g+i, slot 8g+4+i <->
-//           key 16+4g+i) and V^T is stored in LDS in that key order, so its
-//           A fragments are single 16-byte reads.
+//           key 16+4g+i). The V^T fragments come from the row-major V tile
+//           through ds_read_b64_tr_b16, two per fragment: within each
+//           16-lane group, destination lane i receives element i % 4 of
+//           the 4-element pieces addressed by source lanes 4r + i / 4
+//           (r = 0..3), so source lane s of group g addresses V row
+//           (keys) 4g + s / 4 (+16 for the second read), columns 16 db +
+//           4 (s % 4) .. + 3, and lane (d = i, g) gets keys 4g + r of d.
 //   bf16:   P is split into hi + lo bf16 parts (two MFMAs), so the weights
 //           carry ~16 mantissa bits; fp16 P carries 11.
 //   sums    where P is one fp16 operand, the row sums are ones . P^T on the
@@ -50,7 +55,6 @@ namespace {
 constexpr float kLog2eP = 1.4426950408889634f;
 constexpr int kPQ = 128;                  // query rows per workgroup
 constexpr int kPKV = 64;                  // key rows per tile
-constexpr int kVtPitch = kPKV * 2 + 16;   // bytes per V^T row (one d)
 constexpr float kLazy = 8.0f;             // log2 of the largest unnormalised weight
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -75,9 +79,8 @@ template <> struct PMma<f16> {
 template <int D>
 struct PCfg {
     static constexpr int kKPitch = D * 2 + 16;                 // bytes per K row
-    static constexpr int kStage = kPKV * kKPitch + D * kVtPitch;
-    static constexpr int kKChunks = kPKV * D / 8 / 256;        // 16-byte K chunks per thread
-    static constexpr int kVPieces = 16 * (D / 8);              // 4 keys x 8 d pieces
+    static constexpr int kStage = 2 * kPKV * kKPitch;          // K tile, then V tile
+    static constexpr int kKChunks = kPKV * D / 8 / 256;        // 16-byte chunks per thread
     static constexpr int kS = D / 32;                          // score k-steps
     static constexpr int kDB = D / 16;                         // output d blocks
 };
@@ -94,12 +97,6 @@ __device__ __forceinline__ int pack2(float a, float b) {
 // every bf16 significand; values below 2^-14 become fp16 subnormals)
 __device__ __forceinline__ unsigned bf2_to_h2(unsigned w) {
     return (unsigned)pack2<f16>(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
-}
-
-// position (in 4-key units) of key group G (keys 4G .. 4G+3 of a 64-key
-// tile) in a V^T row: the PV k-slot order described above
-__device__ __forceinline__ int vt_pos(int G) {
-    return 8 * (G >> 3) + 2 * (G & 3) + ((G & 7) >= 4 ? 1 : 0);
 }
 
 template <typename T, int D>
@@ -148,11 +145,8 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
     const int nkv_all = (seq + kPKV - 1) / kPKV;
     const int nkt = causal ? min(nkv_all, min(q0 + kPQ - 1, seq - 1) / kPKV + 1) : nkv_all;
 
-    // ---- staging: K rows as is, V transposed into the PV slot order -------
-    i32x4_t kreg[C::kKChunks];
-    i32x4_t vreg[4];
-    const bool vthr = tid < C::kVPieces;
-    const int vG = tid & 15, vc = tid >> 4;   // key group, d chunk of this thread's piece
+    // ---- staging: K and V rows as they are (V as fp16 on the fp16 PV path) -
+    i32x4_t kreg[C::kKChunks], vreg[C::kKChunks];
     auto load_tile = [&](int kt) {
         const int kv0 = kt * kPKV;
 #pragma unroll
@@ -160,45 +154,24 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
             const int c = tid + 256 * j;
             const int row = min(kv0 + c / (D / 8), seq - 1);
             kreg[j] = *reinterpret_cast<const i32x4_t*>(kh + (size_t)row * D + 8 * (c % (D / 8)));
-        }
-        if (vthr) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = min(kv0 + 4 * vG + r, seq - 1);
-                vreg[r] = *reinterpret_cast<const i32x4_t*>(vh + (size_t)row * D + 8 * vc);
-            }
+            vreg[j] = *reinterpret_cast<const i32x4_t*>(vh + (size_t)row * D + 8 * (c % (D / 8)));
         }
     };
-    // f16v (bf16 inputs): V^T stored as fp16 for the fp16 PV product
+    // f16v (bf16 inputs): V stored as fp16 for the fp16 PV product
     auto store_tile = [&](int st, bool f16v) {
         char* ks = smem + st * C::kStage;
-        char* vt = ks + kPKV * C::kKPitch;
+        char* vs = ks + kPKV * C::kKPitch;
 #pragma unroll
         for (int j = 0; j < C::kKChunks; ++j) {
             const int c = tid + 256 * j;
-            *reinterpret_cast<i32x4_t*>(ks + (c / (D / 8)) * C::kKPitch + 16 * (c % (D / 8))) =
-                kreg[j];
-        }
-        if (vthr) {
-            char* dst = vt + (8 * vc) * kVtPitch + 8 * vt_pos(vG);
+            const int off = (c / (D / 8)) * C::kKPitch + 16 * (c % (D / 8));
+            *reinterpret_cast<i32x4_t*>(ks + off) = kreg[j];
+            i32x4_t vv = vreg[j];
+            if (kF16PV && f16v) {
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {  // dwords w of the 4 rows: d = 8 vc + 2 w, +1
-                unsigned a0 = (unsigned)vreg[0][w], a1 = (unsigned)vreg[1][w];
-                unsigned a2 = (unsigned)vreg[2][w], a3 = (unsigned)vreg[3][w];
-                if (kF16PV && f16v) {
-                    a0 = bf2_to_h2(a0);
-                    a1 = bf2_to_h2(a1);
-                    a2 = bf2_to_h2(a2);
-                    a3 = bf2_to_h2(a3);
-                }
-                uint2 lo, hi;  // keys 0..3 of element 2w (low halves), 2w + 1 (high)
-                lo.x = (a0 & 0xffffu) | (a1 << 16);
-                lo.y = (a2 & 0xffffu) | (a3 << 16);
-                hi.x = (a0 >> 16) | (a1 & 0xffff0000u);
-                hi.y = (a2 >> 16) | (a3 & 0xffff0000u);
-                *reinterpret_cast<uint2*>(dst + (2 * w) * kVtPitch) = lo;
-                *reinterpret_cast<uint2*>(dst + (2 * w + 1) * kVtPitch) = hi;
+                for (int w = 0; w < 4; ++w) vv[w] = (int)bf2_to_h2((unsigned)vv[w]);
             }
+            *reinterpret_cast<i32x4_t*>(vs + off) = vv;
         }
     };
 
@@ -222,14 +195,12 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
     auto v_fits_f16 = [&]() {
         typedef unsigned short us2 __attribute__((ext_vector_type(2)));
         us2 mx = {0, 0};
-        if (vthr) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
+        for (int j = 0; j < C::kKChunks; ++j)
 #pragma unroll
-                for (int w = 0; w < 4; ++w)
-                    mx = __builtin_elementwise_max(
-                        mx, __builtin_bit_cast(us2, (unsigned)vreg[r][w] & 0x7fff7fffu));
-        }
+            for (int w = 0; w < 4; ++w)
+                mx = __builtin_elementwise_max(
+                    mx, __builtin_bit_cast(us2, (unsigned)vreg[j][w] & 0x7fff7fffu));
         const bool bad = mx[0] >= 0x4780u || mx[1] >= 0x4780u;  // >= 2^16
         return __syncthreads_or(bad ? 1 : 0) == 0;
     };
@@ -251,7 +222,20 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
             const bool active = !causal || kv0 <= wrow0 + 31;
             if (active) {
                 const char* ks = smem + (kt & 1) * C::kStage;
-                const char* vt = ks + kPKV * C::kKPitch;
+                const char* vs = ks + kPKV * C::kKPitch;
+                // V^T fragment (16 d rows from d0, keys 32 ks2 + slots): two
+                // transposing reads, keys 4g + (0..3) and 16 + 4g + (0..3)
+                auto vt_frag = [&](int d0, int ks2) {
+                    typedef short v4s __attribute__((ext_vector_type(4)));
+                    const char* p = vs + (32 * ks2 + 4 * g + (r16 >> 2)) * C::kKPitch +
+                                    (d0 + 4 * (r16 & 3)) * 2;
+                    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) v4s*)(p));
+                    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) v4s*)(p + 16 * C::kKPitch));
+                    typedef short v8s __attribute__((ext_vector_type(8)));
+                    return v8s{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                };
                 // scores S^T for 4 key blocks x 2 query blocks
                 f32x4 sc[4][2];
 #pragma unroll
@@ -366,8 +350,7 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
                     for (int db = 0; db < C::kDB; ++db)
 #pragma unroll
                         for (int ks2 = 0; ks2 < 2; ++ks2) {
-                            const h8 vf = *reinterpret_cast<const h8*>(
-                                vt + (16 * db + r16) * kVtPitch + (32 * ks2 + 8 * g) * 2);
+                            const h8 vf = __builtin_bit_cast(h8, vt_frag(16 * db, ks2));
 #pragma unroll
                             for (int qb = 0; qb < 2; ++qb)
                                 o[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
@@ -378,8 +361,7 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
                     for (int db = 0; db < C::kDB; ++db)
 #pragma unroll
                         for (int ks2 = 0; ks2 < 2; ++ks2) {
-                            const V8 vf = *reinterpret_cast<const V8*>(
-                                vt + (16 * db + r16) * kVtPitch + (32 * ks2 + 8 * g) * 2);
+                            const V8 vf = __builtin_bit_cast(V8, vt_frag(16 * db, ks2));
 #pragma unroll
                             for (int qb = 0; qb < 2; ++qb) {
                                 o[db][qb] = M::mma(vf, __builtin_bit_cast(V8, ph[qb][ks2]), o[db][qb]);
