@@ -111,6 +111,8 @@ enum class Tune : int {
     SmpSlices,             // FT_SMP_SLICES: sampling slices per row
     FailScratch,           // FT_FAIL_SCRATCH (test hook): every scratch request
                            // fails as an allocation failure would
+    PrefillPrepass,        // FT_PREFILL_PREPASS: bf16 V to fp16 in a pre-pass
+                           // (0 never: in the kernel; 1 large calls; 2 always)
     kCount
 };
 // The switch's value, or `dflt` when it is neither in the environment nor
@@ -126,7 +128,8 @@ enum class Scratch : int {
     QuantMax = 1,
     GemmPartials = 2,
     Sampling = 3,
-    kCount = 4
+    PrefillV = 4,
+    kCount = 5
 };
 void* scratch(Scratch which, size_t bytes, hipStream_t s);
 // Same, but memory is zero when first allocated (or re-allocated); kernels

@@ -56,6 +56,8 @@ constexpr float kLog2eP = 1.4426950408889634f;
 constexpr int kPQ = 128;                  // query rows per workgroup
 constexpr int kPKV = 64;                  // key rows per tile
 constexpr float kLazy = 8.0f;             // log2 of the largest unnormalised weight
+// bf16 V elements from which V is converted to fp16 once per call
+constexpr long long kPrepassMinElems = 1LL << 20;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
@@ -99,11 +101,45 @@ __device__ __forceinline__ unsigned bf2_to_h2(unsigned w) {
     return (unsigned)pack2<f16>(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
 }
 
-template <typename T, int D>
+// V of bf16 inputs converted to fp16 once per call (one workgroup per
+// 64-key tile of a (b, kv head) slab), with a flag per tile: 1 when every
+// |v| of the tile is below 2^16 (the conversion is then exact and the tile
+// takes the fp16 PV product). The attention kernel then stages those tiles
+// as they are, instead of converting and voting in every one of the
+// workgroups that read the tile (Hq / Hkv heads x S / 128 query tiles).
+__global__ __launch_bounds__(256) void prefill_v_to_f16(const bf16* __restrict__ v,
+                                                        f16* __restrict__ v16,
+                                                        unsigned char* __restrict__ ok, int seq,
+                                                        int dim, int nkt) {
+    typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+    const int slab = blockIdx.x / nkt, kt = blockIdx.x - (blockIdx.x / nkt) * nkt;
+    const size_t base = ((size_t)slab * seq + (size_t)kt * kPKV) * dim;
+    const int rows = min(kPKV, seq - kt * kPKV);
+    const int nchunk = rows * dim / 8;  // 16-byte chunks
+    us2 mx = {0, 0};
+    for (int c = threadIdx.x; c < nchunk; c += 256) {
+        i32x4_t x = *reinterpret_cast<const i32x4_t*>(v + base + 8 * (size_t)c);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, (unsigned)x[w] & 0x7fff7fffu));
+            x[w] = (int)bf2_to_h2((unsigned)x[w]);
+        }
+        *reinterpret_cast<i32x4_t*>(v16 + base + 8 * (size_t)c) = x;
+    }
+    const bool bad = mx[0] >= 0x4780u || mx[1] >= 0x4780u;  // >= 2^16
+    const int any_bad = __syncthreads_or(bad ? 1 : 0);
+    if (threadIdx.x == 0) ok[blockIdx.x] = any_bad ? 0 : 1;
+}
+
+// PRE (bf16 inputs): v16 / v_ok hold prefill_v_to_f16's output; the fp16 PV
+// tiles are staged from v16 without conversion and chosen by v_ok instead of
+// a workgroup vote (the same tiles, the same bits)
+template <typename T, int D, bool PRE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
                        const T* __restrict__ v, T* __restrict__ out, int batch,
-                       int hq, int hkv, int seq, int causal, float scale_log2) {
+                       int hq, int hkv, int seq, int causal, float scale_log2,
+                       const f16* __restrict__ v16, const unsigned char* __restrict__ v_ok) {
     using M = PMma<T>;
     using V8 = typename M::v8;
     using C = PCfg<D>;
@@ -130,6 +166,11 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
     const T* qh = q + ((size_t)b * hq + h) * seq * D;
     const T* kh = k + ((size_t)b * hkv + kvh) * seq * D;
     const T* vh = v + ((size_t)b * hkv + kvh) * seq * D;
+    // the slab's fp16 copy (same element offsets) and tile flags
+    const T* vh16 = PRE ? reinterpret_cast<const T*>(v16 + ((size_t)b * hkv + kvh) * seq * D)
+                        : vh;
+    const unsigned char* okh = PRE ? v_ok + ((size_t)b * hkv + kvh) * ((seq + kPKV - 1) / kPKV)
+                                   : nullptr;
 
     // the wave's Q as B operands: row q0 + 32 wave + 16 qb + r16, elements
     // 32 s + 8 g .. +7 (rows past S read row S - 1; never stored)
@@ -147,14 +188,16 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
 
     // ---- staging: K and V rows as they are (V as fp16 on the fp16 PV path) -
     i32x4_t kreg[C::kKChunks], vreg[C::kKChunks];
-    auto load_tile = [&](int kt) {
+    // from16: the tile's fp16 copy (PRE)
+    auto load_tile = [&](int kt, bool from16) {
         const int kv0 = kt * kPKV;
+        const T* vsrc = from16 ? vh16 : vh;
 #pragma unroll
         for (int j = 0; j < C::kKChunks; ++j) {
             const int c = tid + 256 * j;
             const int row = min(kv0 + c / (D / 8), seq - 1);
             kreg[j] = *reinterpret_cast<const i32x4_t*>(kh + (size_t)row * D + 8 * (c % (D / 8)));
-            vreg[j] = *reinterpret_cast<const i32x4_t*>(vh + (size_t)row * D + 8 * (c % (D / 8)));
+            vreg[j] = *reinterpret_cast<const i32x4_t*>(vsrc + (size_t)row * D + 8 * (c % (D / 8)));
         }
     };
     // f16v (bf16 inputs): V stored as fp16 for the fp16 PV product
@@ -167,7 +210,7 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
             const int off = (c / (D / 8)) * C::kKPitch + 16 * (c % (D / 8));
             *reinterpret_cast<i32x4_t*>(ks + off) = kreg[j];
             i32x4_t vv = vreg[j];
-            if (kF16PV && f16v) {
+            if (kF16PV && !PRE && f16v) {
 #pragma unroll
                 for (int w = 0; w < 4; ++w) vv[w] = (int)bf2_to_h2((unsigned)vv[w]);
             }
@@ -205,8 +248,14 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
         return __syncthreads_or(bad ? 1 : 0) == 0;
     };
 
-    load_tile(0);
-    const bool f16_first = kF16PV && v_fits_f16();
+    bool f16_first;
+    if constexpr (PRE) {
+        f16_first = okh[0] != 0;
+        load_tile(0, f16_first);
+    } else {
+        load_tile(0, false);
+        f16_first = kF16PV && v_fits_f16();
+    }
     store_tile(0, f16_first);
     __syncthreads();
     // Tiles kt0 .. : the fp16 PV loop (F16) runs while each next tile votes
@@ -217,7 +266,9 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
         constexpr bool F16 = decltype(f16_tag)::value;
         constexpr bool kMmaSum = F16 || !M::kSplit;
         for (int kt = kt0; kt < nkt; ++kt) {
-            if (kt + 1 < nkt) load_tile(kt + 1);
+            // PRE: the next tile's flag picks its source before the load
+            const bool pre_next = PRE && F16 && kt + 1 < nkt && okh[kt + 1] != 0;
+            if (kt + 1 < nkt) load_tile(kt + 1, pre_next);
             const int kv0 = kt * kPKV;
             const bool active = !causal || kv0 <= wrow0 + 31;
             if (active) {
@@ -373,7 +424,7 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
                 }
             }
             if (kt + 1 < nkt) {
-                const bool next_f16 = F16 && v_fits_f16();
+                const bool next_f16 = PRE ? pre_next : F16 && v_fits_f16();
                 store_tile((kt + 1) & 1, next_f16);
                 __syncthreads();
                 if (F16 && !next_f16) return kt + 1;
@@ -487,12 +538,35 @@ void prefill_run(const T* q, const T* k, const T* v, T* out, int batch, int hq, 
             const long long grid = (long long)batch * hq * nqt;
             if (grid > 0x7fffffffLL) inval("attention prefill problem too large for one launch");
             const float sl2 = scale * kLog2eP;
-            if (dim == 128)
-                attn_prefill_mfma<T, 128><<<(unsigned)grid, 256, 0, s>>>(
-                    q, k, v, out, batch, hq, hkv, seq, causal ? 1 : 0, sl2);
-            else
-                attn_prefill_mfma<T, 64><<<(unsigned)grid, 256, 0, s>>>(
-                    q, k, v, out, batch, hq, hkv, seq, causal ? 1 : 0, sl2);
+            // bf16: V to fp16 once per call when the problem is large enough
+            // for the extra launch to pay (FT_PREFILL_PREPASS: 0 in the kernel,
+            // 2 always)
+            const long long vel = (long long)batch * hkv * seq * dim;
+            const int nkv = (seq + kPKV - 1) / kPKV;
+            const int pp = tune(Tune::PrefillPrepass, 1);  // 0 never, 1 auto, 2 always
+            const bool pre = std::is_same<T, bf16>::value &&
+                             (pp == 2 || (pp == 1 && vel >= kPrepassMinElems));
+            f16* v16 = nullptr;
+            unsigned char* v_ok = nullptr;
+            if (pre) {
+                const size_t vbytes = ((size_t)vel * 2 + 255) & ~(size_t)255;
+                char* ws = (char*)scratch(Scratch::PrefillV,
+                                          vbytes + (size_t)batch * hkv * nkv, s);
+                v16 = (f16*)ws;
+                v_ok = (unsigned char*)(ws + vbytes);
+                prefill_v_to_f16<<<(unsigned)((long long)batch * hkv * nkv), 256, 0, s>>>(
+                    (const bf16*)v, v16, v_ok, seq, dim, nkv);
+                launch_check("attention prefill V conversion launch");
+            }
+#define FT_PF(DD, PP)                                                                 \
+    attn_prefill_mfma<T, DD, PP><<<(unsigned)grid, 256, 0, s>>>(                      \
+        q, k, v, out, batch, hq, hkv, seq, causal ? 1 : 0, sl2, v16, v_ok)
+            if (dim == 128) {
+                if (pre) FT_PF(128, true); else FT_PF(128, false);
+            } else {
+                if (pre) FT_PF(64, true); else FT_PF(64, false);
+            }
+#undef FT_PF
             launch_check("attention prefill kernel launch");
             return;
         }

@@ -74,7 +74,8 @@ constexpr const char* kTuneNames[(int)Tune::kCount] = {
     "FT_QGEMM_SK_WAVES",     "FT_QGEMM_SK_STAGES",
     "FT_QGEMM_BIG",          "FT_QGEMM_BAND",      "FT_RMSQ_SPLIT",
     "FT_RMSQ_GEMV_SPLIT",    "FT_PREFILL_FORCE_GENERIC", "FT_ARG_SLICES",
-    "FT_SMP_SINGLE",         "FT_SMP_SLICES",      "FT_FAIL_SCRATCH"};
+    "FT_SMP_SINGLE",         "FT_SMP_SLICES",      "FT_FAIL_SCRATCH",
+    "FT_PREFILL_PREPASS"};
 
 // value and presence per switch: the environment's (read once), then the
 // run-time override, which wins while set

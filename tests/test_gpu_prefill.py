@@ -72,6 +72,30 @@ def test_prefill_bf16_large_v_tiles_take_the_split_path(d, causal):
     _check_half(ft.attention_prefill(q, k, v2, causal=causal), q, k, v2, causal)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("big", [False, True])
+def test_prefill_bf16_v_prepass_equals_in_kernel_conversion(d, causal, big, tuning):
+    # bf16 inputs: V converted to fp16 by a pre-pass (with a per-tile range
+    # flag) or by every workgroup as it stages the tile (with a vote): the
+    # same tiles take the fp16 PV product, so the outputs are the same bits.
+    # S = 300 leaves a partial last tile; `big` puts values >= 2^16 in tiles
+    # 2 and 3 (the hand-over to the bf16 split path).
+    rng = np.random.default_rng(40 + d + 2 * causal + big)
+    dt = torch.bfloat16
+    q, k, v = _inputs(rng, 2, 8, 2, 300, d, dt)
+    if big:
+        v[:, :, 130:200] = torch.from_numpy(
+            7.0e4 + 1.0e3 * rng.standard_normal((2, 2, 70, d)).astype(np.float32)).to(DEV, dt)
+    tuning("FT_PREFILL_PREPASS", 0)
+    inkernel = ft.attention_prefill(q, k, v, causal=causal)
+    tuning("FT_PREFILL_PREPASS", 2)
+    pre = ft.attention_prefill(q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(pre, inkernel)
+    _check_half(pre, q, k, v, causal)
+
+
 @pytest.mark.parametrize("dt", HALF)
 def test_prefill_mfma_first_row_is_v0_and_s1_is_decode(dt):
     rng = np.random.default_rng(5)
