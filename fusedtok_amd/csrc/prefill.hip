@@ -287,14 +287,19 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
                     typedef short v8s __attribute__((ext_vector_type(8)));
                     return v8s{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 };
-                // scores S^T for 4 key blocks x 2 query blocks
+                // scores S^T for 4 key blocks x 2 query blocks: k-step outer,
+                // so the 8 accumulator chains interleave on the matrix core
+                // (each chain still sums its k-steps in order)
                 f32x4 sc[4][2];
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb) {
                     sc[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
                     sc[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
 #pragma unroll
-                    for (int s = 0; s < C::kS; ++s) {
+                for (int s = 0; s < C::kS; ++s) {
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb) {
                         const V8 kf = *reinterpret_cast<const V8*>(
                             ks + (16 * kb + r16) * C::kKPitch + (32 * s + 8 * g) * 2);
                         sc[kb][0] = M::mma(kf, qf[0][s], sc[kb][0]);
