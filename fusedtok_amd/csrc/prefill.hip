@@ -19,7 +19,8 @@
 //           B = Q^T (the wave's Q in registers for the whole kernel);
 //           lane (q, g) gets keys 4g + i of each 16-key block.
 //   softmax online per query row: the 64 keys of a row sit in the 4 lanes
-//           {q, q+16, q+32, q+48}: two xor shuffles for the tile maximum;
+//           {q, q+16, q+32, q+48}: two lane swaps (v_permlane32/16_swap,
+//           no LDS) for the tile maximum;
 //           the rescale of the running output is a per-lane multiply.
 //   PV      O^T[d][q] += V^T[d][kv] . P^T[kv][q]: B = P straight from the
 //           score accumulators: for a 32-key step, lane (q, g) holds keys
@@ -99,6 +100,19 @@ __device__ __forceinline__ int pack2(float a, float b) {
 // every bf16 significand; values below 2^-14 become fp16 subnormals)
 __device__ __forceinline__ unsigned bf2_to_h2(unsigned w) {
     return (unsigned)pack2<f16>(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
+}
+
+// maximum over lanes l, l ^ 16, l ^ 32, l ^ 48 without LDS: with both
+// operands x, v_permlane32_swap leaves x[l] and x[l ^ 32] in the two
+// results of every lane (lanes < 32: (x[l], x[l + 32]); lanes >= 32:
+// (x[l - 32], x[l])), v_permlane16_swap likewise x[l] and x[l ^ 16]
+__device__ __forceinline__ float max4_rows(float x) {
+    const unsigned u = __float_as_uint(x);
+    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const unsigned w = __float_as_uint(y);
+    const auto c = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
 }
 
 // V of bf16 inputs converted to fp16 once per call (one workgroup per
@@ -330,8 +344,7 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
                     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                         for (int i = 0; i < 4; ++i) mt = fmaxf(mt, sc[kb][qb][i]);
-                    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-                    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+                    mt = max4_rows(mt);
                     // lazy rescale: the running maximum moves only when the tile's
                     // exceeds it by more than kLazy / c (weights then stay
                     // <= 2^kLazy); a wave whose rows all keep theirs skips the
