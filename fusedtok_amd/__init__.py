@@ -95,6 +95,7 @@ __all__ = [
     "rope_kv_append_paged",
     "qgemm_rope_kv_append_paged",
     "qgemm_rmsnorm_quant",
+    "qgemm_swiglu_quant",
     "DecodeLayer",
     "argmax",
     "argmax_batched",
@@ -921,6 +922,33 @@ def qgemm_rmsnorm_quant(a_q, a_scale, w_q, w_scales, weight, *, residual=None, e
             y.data_ptr(), None if residual is None else residual.data_ptr(), w.data_ptr(),
             float(eps), q.data_ptr(), scale.data_ptr(), g.M, g.N, g.K, _stream())
     return (y, q, scale) if device_scale else (y, q, float(scale))
+
+
+def qgemm_swiglu_quant(a_q, a_scale, w_q, w_scales, *, out_dtype=None, device_scale=False):
+    """The gate/up projection followed by the SwiGLU's quantize: ``h =
+    qgemm_perchannel(a_q, a_scale, w_q, w_scales, out_dtype=out_dtype)``
+    with ``w_q`` = [2 * inter, K] (gate rows, then up rows), then ``q, s =
+    swiglu_quant(h[:, :inter], h[:, inter:])``, bit for bit. Returns ``(h,
+    q, scale)``. Where the GEMM runs unsplit on the skinny kernel (16 < M <=
+    64), its epilogue takes the SwiGLU maximum, so the chain is two launches
+    instead of three. ``device_scale=True`` returns the scale as a
+    1-element GPU float32 tensor without synchronising."""
+    g = _fused_gemm_operands(a_q, w_q, w_scales, "qgemm_swiglu_quant")
+    dt = _out_dtype(out_dtype)
+    if g.N % 2:
+        raise ValueError("qgemm_swiglu_quant: w_q must have an even row count (gate | up)")
+    inter = g.N // 2
+    h = torch.empty((g.M, g.N), dtype=dt, device=a_q.device)
+    q = torch.empty((g.M, inter), dtype=torch.int8, device=a_q.device)
+    scale = torch.empty(1, dtype=torch.float32, device=a_q.device)
+    if g.M == 0 or inter == 0:
+        scale.fill_(1.0)
+    else:
+        sa = _device_scale(a_scale, a_q.device)
+        _fusedtok.qgemm_swiglu_quant_launch(
+            g.ptr("a_q"), sa.data_ptr(), g.ptr("b_q"), g.ptr("b_scales"), _CODE[dt],
+            h.data_ptr(), q.data_ptr(), scale.data_ptr(), g.M, inter, g.K, _stream())
+    return (h, q, scale) if device_scale else (h, q, float(scale))
 
 
 # ---------------------------------------------------------------------------

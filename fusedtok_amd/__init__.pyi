@@ -38,6 +38,7 @@ __all__ = [
     "rope_kv_append_paged",
     "qgemm_rope_kv_append_paged",
     "qgemm_rmsnorm_quant",
+    "qgemm_swiglu_quant",
     "DecodeLayer",
     "argmax",
     "argmax_batched",
@@ -108,6 +109,7 @@ def rope_kv_append_paged(qkv: torch.Tensor, q_heads: int, kv_heads: int,
                          k_pool: torch.Tensor, v_pool: torch.Tensor,
                          block_table: IntArray, lens: IntArray, *,
                          theta: float = ..., pos_offset: int = ...,
+                         neox: bool = ...) -> torch.Tensor: ...
 def qgemm_rope_kv_append_paged(a_q: torch.Tensor, a_scale: Scale, w_q: torch.Tensor,
                                w_scales: Union[torch.Tensor, Sequence[float]], q_heads: int,
                                kv_heads: int, k_pool: torch.Tensor, v_pool: torch.Tensor,
@@ -119,7 +121,10 @@ def qgemm_rmsnorm_quant(a_q: torch.Tensor, a_scale: Scale, w_q: torch.Tensor,
                         residual: Optional[torch.Tensor] = ..., eps: float = ...,
                         out_dtype: Optional[torch.dtype] = ..., device_scale: bool = ...
                         ) -> Tuple[torch.Tensor, torch.Tensor, Scale]: ...
-                         neox: bool = ...) -> torch.Tensor: ...
+def qgemm_swiglu_quant(a_q: torch.Tensor, a_scale: Scale, w_q: torch.Tensor,
+                       w_scales: Union[torch.Tensor, Sequence[float]], *,
+                       out_dtype: Optional[torch.dtype] = ..., device_scale: bool = ...
+                       ) -> Tuple[torch.Tensor, torch.Tensor, Scale]: ...
 
 # -- post-logits sampling -------------------------------------------------------
 def argmax(x: Array, *, cuda: bool = ...) -> int: ...

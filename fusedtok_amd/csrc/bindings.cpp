@@ -465,6 +465,17 @@ PYBIND11_MODULE(_fusedtok, m) {
           py::arg("dtype"), py::arg("y"), py::arg("residual"), py::arg("weight"),
           py::arg("eps"), py::arg("q"), py::arg("scale"), py::arg("rows"), py::arg("n"),
           py::arg("k"), py::arg("stream") = 0);
+    m.def("qgemm_swiglu_quant_launch",
+          [](uintptr_t a, uintptr_t sa, uintptr_t w, uintptr_t ws, int dtype, uintptr_t h,
+             uintptr_t q, uintptr_t scale, int rows, int inter, int k, uintptr_t stream) {
+              check(ft_qgemm_swiglu_quant_launch(
+                  P<const signed char>(a), P<const float>(sa), P<const signed char>(w),
+                  P<const float>(ws), dtype, P<void>(h), P<signed char>(q), P<float>(scale),
+                  rows, inter, k, stream));
+          },
+          py::arg("a_q"), py::arg("sa_dev"), py::arg("w_q"), py::arg("w_scales"),
+          py::arg("dtype"), py::arg("h"), py::arg("q"), py::arg("scale"), py::arg("rows"),
+          py::arg("inter"), py::arg("k"), py::arg("stream") = 0);
     // ---- decode layer object ---------------------------------------------
     m.def("decode_layer_create",
           [](int hidden, int hq, int hkv, int dim, int inter, int page, int max_batch, int dtype,

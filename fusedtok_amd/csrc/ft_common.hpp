@@ -242,6 +242,13 @@ __device__ __forceinline__ signed char quant1(float x, float inv) {
     return (signed char)fmaxf(-127.0f, fminf(127.0f, rintf(x * inv)));
 }
 
+// SwiGLU of one element, silu(g) * u = g / (1 + e^-g) * u (reference
+// activations.cu:68-72, 501-511). One definition for swiglu_quant and for
+// the gate/up GEMM epilogue that takes its maximum, so both round alike.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return g / (1.0f + expf(-g)) * u;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

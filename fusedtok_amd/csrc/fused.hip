@@ -415,10 +415,6 @@ void qgemm_rmsq_run(const signed char* a_q, const float* sa_dev, const signed ch
 // ---------------------------------------------------------------------------
 // swiglu_quant: element (row, c) of gate / up at row * ld + c
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float silu_mul(float g, float u) {
-    return g / (1.0f + expf(-g)) * u;
-}
-
 // VEC: cols and the row stride are multiples of 4 and g / u / q aligned to
 // 4 elements: each thread takes 4 consecutive elements of a row per load
 // (one 8-byte load per operand for half types), so a thread's few elements
@@ -534,6 +530,45 @@ void swiglu_quant_run(const T* g, const T* u, signed char* q, float* scale_out,
         swq_quant<T, false><<<g2, kFNT, 0, s>>>(g, u, part, (int)g1, q, scale_out, rows,
                                                 cols, ld);
     }
+    launch_check("swiglu_quant quantize kernel launch");
+}
+
+// gate/up GEMM (a_q codes with the device scale *sa_dev; w_gu [2 inter, k],
+// gate rows then up rows, per-channel w_scales) -> h [rows, 2 inter] in T,
+// then swiglu_quant(h[:, :inter], h[:, inter:]). Where the GEMM runs
+// unsplit on the skinny ring kernel, its epilogue takes the SwiGLU maxima
+// (the maximum is exact in any order), and only the codes pass is left.
+template <typename T>
+void qgemm_swq_run(const signed char* a_q, const float* sa_dev, const signed char* w_gu,
+                   const float* w_scales, T* h, signed char* q, float* scale_out, int rows,
+                   int inter, int k, int dtype, hipStream_t s) {
+    if (rows < 0 || inter < 1 || k < 0)
+        inval("qgemm_swiglu_quant: rows and k must be >= 0, inter >= 1");
+    if (rows == 0) return;
+    if (!a_q || !sa_dev || !w_gu || !w_scales || !h || !q || !scale_out)
+        inval("qgemm_swiglu_quant: null operand");
+    const long long ld = 2LL * inter;
+    float* part = nullptr;
+    int nparts = 0;
+    if (!qgemm_swiglu_max(a_q, w_gu, sa_dev, w_scales, h, dtype, rows, inter, k, s, part,
+                          nparts)) {
+        const int rc = ft_qgemm_launch_ex(a_q, w_gu, w_scales, 0.0f, 0.0f, sa_dev, h, dtype,
+                                          rows, 2 * inter, k, (uintptr_t)s);
+        if (rc != FT_OK) throw Error{rc, ft_last_error()};
+        swiglu_quant_run<T>(h, h + inter, q, scale_out, rows, inter, ld, s);
+        return;
+    }
+    const size_t a4 = 4 * sizeof(T);
+    const bool vec = inter % 4 == 0 && (uintptr_t)h % a4 == 0 &&
+                     (uintptr_t)(h + inter) % a4 == 0 && (uintptr_t)q % 4 == 0;
+    const long long n = (long long)rows * inter / (vec ? 4 : 1);
+    const unsigned grid = grid_1d(n, kFNT, dev_info().cu_count * 4);
+    if (vec)
+        swq_quant<T, true><<<grid, kFNT, 0, s>>>(h, h + inter, part, nparts, q, scale_out, rows,
+                                                 inter, ld);
+    else
+        swq_quant<T, false><<<grid, kFNT, 0, s>>>(h, h + inter, part, nparts, q, scale_out,
+                                                  rows, inter, ld);
     launch_check("swiglu_quant quantize kernel launch");
 }
 
@@ -833,6 +868,24 @@ int ft_qgemm_rmsnorm_quant_launch(const signed char* a_q, const float* sa_dev,
         default: ft::inval("qgemm_rmsnorm_quant: unknown dtype code");
         }
 #undef FT_QRQ
+    });
+}
+
+int ft_qgemm_swiglu_quant_launch(const signed char* a_q, const float* sa_dev,
+                                 const signed char* w_gu, const float* w_scales, int dtype,
+                                 void* h, signed char* q, float* scale_out, int rows, int inter,
+                                 int k, uintptr_t stream) {
+    return ft::guarded([&] {
+        hipStream_t s = ft::as_stream(stream);
+#define FT_QSQ(T) \
+    ft::qgemm_swq_run<T>(a_q, sa_dev, w_gu, w_scales, (T*)h, q, scale_out, rows, inter, k, dtype, s)
+        switch (dtype) {
+        case FT_DT_F32: FT_QSQ(float); break;
+        case FT_DT_BF16: FT_QSQ(ft::bf16); break;
+        case FT_DT_F16: FT_QSQ(ft::f16); break;
+        default: ft::inval("qgemm_swiglu_quant: unknown dtype code");
+        }
+#undef FT_QSQ
     });
 }
 

@@ -34,6 +34,17 @@ bool qgemm_deferred(const signed char* a, const signed char* b, const float* sa_
                     const float* sb_vec, void* y, int y_dtype, int m, int n, int k,
                     hipStream_t s, KFold& f);
 
+// The gate/up GEMM of swiglu_quant: y [m, 2 inter] = A . B^T as
+// ft_qgemm_launch_ex writes it (B: inter gate rows, then inter up rows).
+// Where the dispatch would run it unsplit on the skinny ring kernel, that
+// kernel also takes each workgroup's max |silu(g) * u| over the stored
+// values: part[0 .. nparts) (library scratch, valid until the next scratch
+// user on stream s) and the result is true. Otherwise nothing is launched
+// and the result is false. qgemm.hip.
+bool qgemm_swiglu_max(const signed char* a, const signed char* b, const float* sa_dev,
+                      const float* sb_vec, void* y, int y_dtype, int m, int inter, int k,
+                      hipStream_t s, float*& part, int& nparts);
+
 __device__ __forceinline__ float kfold_sa(const KFold& f) { return *f.sa_dev; }
 
 // composed scale of column col (one f32 rounding)

@@ -10,8 +10,9 @@
 //     partials folded by the RoPE kernel)           -> q_rot, pools  2
 //   paged decode over lens + 1 tokens + quantize    -> qa, sa        3
 //   o_proj GEMM + rmsnorm_quant(o + x, norm2)       -> q2, s2        3
-//   gate/up GEMM                                    -> h             1
-//   swiglu_quant(h[:, :inter], h[:, inter:])        -> q3, s3        2
+//   gate/up GEMM + swiglu_quant(h[:, :inter],
+//     h[:, inter:]) (SwiGLU maxima in the GEMM
+//     epilogue on the skinny kernel)                -> h, q3, s3     2-3
 //   down GEMM                                       -> y             1-2
 // The reference has no layer op: a decode layer there is these ops called
 // one by one (cuda_launch.hpp:40-59, 185-216, 324-460).
@@ -110,10 +111,8 @@ void forward(ft_decode_layer& L, const Args& a, hipStream_t s) {
                                                     a.tbl_width, d.head_dim, st));
     rc_check(ft_qgemm_rmsnorm_quant_launch(L.qa, sa, d.w_o, d.s_o, d.dtype, L.o, a.x, d.norm2,
                                            d.eps, L.q2, s2, B, d.hidden, hd, st));
-    rc_check(ft_qgemm_launch_ex(L.q2, d.w_gu, d.s_gu, 0.0f, 0.0f, s2, L.h, d.dtype, B,
-                                2 * d.inter, d.hidden, st));
-    rc_check(ft_swiglu_quant_launch(L.h, (const char*)L.h + (size_t)d.inter * L.esz, d.dtype,
-                                    L.q3, s3, B, d.inter, 2LL * d.inter, st));
+    rc_check(ft_qgemm_swiglu_quant_launch(L.q2, s2, d.w_gu, d.s_gu, d.dtype, L.h, L.q3, s3, B,
+                                          d.inter, d.hidden, st));
     rc_check(ft_qgemm_launch_ex(L.q3, d.w_down, d.s_down, 0.0f, 0.0f, s3, a.y, d.dtype, B,
                                 d.hidden, d.inter, st));
 }

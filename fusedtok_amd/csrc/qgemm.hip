@@ -112,6 +112,16 @@ __device__ __forceinline__ void epi_store_scaled(const Epi& e, int n, int row, i
     }
 }
 
+// the value epi_store_scaled stores for (acc, s), widened back to f32
+template <int OUT>
+__device__ __forceinline__ float epi_stored(int acc, float s) {
+    float val = (float)acc * s;
+    asm("" : "+v"(val));
+    if constexpr (OUT == kOutBF16) return (float)(bf16)val;
+    if constexpr (OUT == kOutF16) return (float)(f16)val;
+    return val;
+}
+
 template <int OUT>
 __device__ __forceinline__ void epi_store(const Epi& e, float sa, int n,
                                           int row, int col, int acc) {
@@ -716,20 +726,31 @@ __device__ __forceinline__ void sl_issue(const i8* a, const i8* b, const size_t*
                                          0, 0);
 }
 
-template <int MT, int NSTAGE, int NW, int OUT>
+// SWQ: the gate/up GEMM of a SwiGLU, n = 2 * inter (B holds the gate rows,
+// then the up rows), inter % (8 * NW) == 0, ksplit == 1. The first NW / 2
+// waves of workgroup x take gate columns 8 NW x + 16 w .., the other NW / 2
+// the up columns inter + the same, so every gate output and its up partner
+// are in one workgroup. After y is stored, the epilogue takes the
+// workgroup's max |silu(g) * u| over the stored values into swq_part[x]:
+// the partial maxima swiglu_quant folds, without its own pass over y.
+template <int MT, int NSTAGE, int NW, int OUT, bool SWQ>
 __global__ __launch_bounds__(64 * NW) void qgemm_skinny_lds(
     const i8* __restrict__ a, const i8* __restrict__ b, Epi e, int m, int n,
-    int k, int ksplit, int* __restrict__ part) {
+    int k, int ksplit, int* __restrict__ part, int inter, float* __restrict__ swq_part) {
     constexpr int kArows = 16 * MT;
     constexpr int kStage = (kArows + 16 * NW) * kSlChunk;
     constexpr int kAIns = kArows / 4 / NW;  // A DMA instructions per wave per chunk
     static_assert(NSTAGE == 2 || NSTAGE == 3, "stage count");
     static_assert(kAIns * NW * 4 == kArows, "A rows split evenly over the waves");
+    static_assert(!SWQ || (16 * MT * (8 * NW + 1) + NW) * 4 <= NSTAGE * kStage,
+                  "the SwiGLU exchange fits in the ring");
     __shared__ __attribute__((aligned(16))) char lds[NSTAGE * kStage];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
-    const int n0 = (blockIdx.x * NW + wave) * 16;
+    constexpr int kHalf = NW / 2;
+    const int n0 = SWQ ? (wave < kHalf ? 0 : inter) + ((int)blockIdx.x * kHalf + wave % kHalf) * 16
+                       : ((int)blockIdx.x * NW + wave) * 16;
     const bool live = n0 < n;
     const int ks = blockIdx.y;
     const int chunks = k / kSlChunk;
@@ -801,6 +822,50 @@ __global__ __launch_bounds__(64 * NW) void qgemm_skinny_lds(
             for (int t = 0; t < MT; ++t)
                 acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[t][u], fw[u], acc[t], 0, 0, 0);
         st = st + 1 == NSTAGE ? 0 : st + 1;
+    }
+    if constexpr (SWQ) {
+        // every column is real (the grid covers inter exactly); rows past m
+        // hold products of clamped A rows and are neither stored nor folded
+        const int col = n0 + r;
+        const float sa = epi_sa(e);
+        const float sc = e.sb_vec ? sa * e.sb_vec[col] : sa * e.sb;
+        float sv[MT][4];
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = 16 * t + 4 * g + i;
+                sv[t][i] = epi_stored<OUT>(acc[t][i], sc);
+                if (row < m) epi_store_scaled<OUT>(e, n, row, col, acc[t][i], sc);
+            }
+        // the up values through LDS (the ring is free once every wave is
+        // past its last chunk), then each gate lane folds its outputs
+        constexpr int kXP = 16 * kHalf + 1;  // floats per row (bank spread)
+        float* xch = reinterpret_cast<float*>(lds);
+        float* red = xch + 16 * MT * kXP;
+        const int cl = 16 * (wave % kHalf) + r;
+        __syncthreads();
+        if (wave >= kHalf) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xch[(16 * t + 4 * g + i) * kXP + cl] = sv[t][i];
+        }
+        __syncthreads();
+        float mx = 0.0f;
+        if (wave < kHalf) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = 16 * t + 4 * g + i;
+                    if (row < m)
+                        mx = fmaxf(mx, fabsf(silu_mul(sv[t][i], xch[row * kXP + cl])));
+                }
+        }
+        mx = block_max<64 * NW>(mx, red);
+        if (threadIdx.x == 0) swq_part[blockIdx.x] = mx;
+        return;
     }
     const int col = n0 + r;
     const bool own = live && col < n;
@@ -1969,8 +2034,9 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
                                  (size_t)ksplit * m * n * sizeof(int), s);
         dim3 grid(col_wgs, ksplit);
         if (ring) {
-#define FT_SK_LDS(MT, S, NW) \
-    qgemm_skinny_lds<MT, S, NW, OUT><<<grid, 64 * NW, 0, s>>>(a, b, e, m, n, k, ksplit, part)
+#define FT_SK_LDS(MT, S, NW)                                                             \
+    qgemm_skinny_lds<MT, S, NW, OUT, false><<<grid, 64 * NW, 0, s>>>(a, b, e, m, n, k, ksplit, \
+                                                                     part, 0, nullptr)
             if (mt <= 1) {
                 if (stages == 3) FT_SK_LDS(1, 3, 4); else FT_SK_LDS(1, 2, 4);
             } else if (mt <= 2) {
@@ -2060,7 +2126,60 @@ void qgemm_run(const i8* a, const i8* b, Epi e, int out, int m, int n, int k,
     }
 }
 
+// The skinny ring kernel with the SwiGLU maxima in its epilogue, launched
+// only where qgemm_dispatch takes qgemm_skinny_lds unsplit for the same
+// shape (same waves, stages and column tiles), so y is the same bits.
+template <int OUT>
+bool swiglu_max_launch(const i8* a, const i8* b, const Epi& e, int m, int inter, int k,
+                       hipStream_t s, float*& part, int& nparts) {
+    const int n = 2 * inter;
+    const bool aligned = (k % 16 == 0) && ((uintptr_t)a % 16 == 0) && ((uintptr_t)b % 16 == 0);
+    if (!aligned || tune(Tune::QgemmKernel, 0) != 0 || m <= 16 || m > 64) return false;
+    if (k % kSlChunk != 0 || tune(Tune::QgemmSkRegs, 0) != 0) return false;
+    if (tune(Tune::QgemmSkStages, 3) == 2 || tune(Tune::QgemmKsplit, 0) != 0) return false;
+    const int cus = dev_info().cu_count;
+    const int mt = (m + 15) / 16;  // 2 or 4
+    const int wide = (n + 127) / 128;
+    const int nw_pick = 4 * wide >= 3 * cus ? 8 : 4;
+    const int nw = tune(Tune::QgemmSkWaves, nw_pick) == 8 ? 8 : 4;
+    if (inter % (8 * nw) != 0) return false;
+    const int lds_bytes = (16 * (mt <= 2 ? 2 : 4) + 16 * nw) * kSlChunk * 3;
+    const int slots = std::max(1, (160 << 10) / lds_bytes) * cus;
+    const int col_wgs = inter / (8 * nw);
+    if (4 * col_wgs < 3 * slots) return false;  // the dispatch would split K
+    part = (float*)scratch(Scratch::QuantMax, (size_t)col_wgs * sizeof(float), s);
+    nparts = col_wgs;
+    dim3 grid(col_wgs, 1);
+#define FT_SK_SWQ(MT, NW)                                                                   \
+    qgemm_skinny_lds<MT, 3, NW, OUT, true><<<grid, 64 * NW, 0, s>>>(a, b, e, m, n, k, 1,    \
+                                                                    nullptr, inter, part)
+    if (mt <= 2) {
+        if (nw == 8) FT_SK_SWQ(2, 8); else FT_SK_SWQ(2, 4);
+    } else {
+        if (nw == 8) FT_SK_SWQ(4, 8); else FT_SK_SWQ(4, 4);
+    }
+#undef FT_SK_SWQ
+    launch_check("qgemm swiglu-max kernel launch");
+    return true;
+}
+
 }  // namespace
+
+bool qgemm_swiglu_max(const signed char* a, const signed char* b, const float* sa_dev,
+                      const float* sb_vec, void* y, int y_dtype, int m, int inter, int k,
+                      hipStream_t s, float*& part, int& nparts) {
+    if (!sa_dev || !sb_vec) inval("qgemm: a device scale and per-channel scales are required");
+    if (inter < 1 || (long long)m * 2 * inter > (1LL << 31) - 1) return false;
+    qgemm_check(m, 2 * inter, k);
+    if (m == 0 || k == 0 || !y || !a || !b) return false;
+    Epi e{y, 0.0f, sa_dev, 0.0f, sb_vec};
+    switch (y_dtype) {
+    case FT_DT_F32: return swiglu_max_launch<kOutF32>(a, b, e, m, inter, k, s, part, nparts);
+    case FT_DT_BF16: return swiglu_max_launch<kOutBF16>(a, b, e, m, inter, k, s, part, nparts);
+    case FT_DT_F16: return swiglu_max_launch<kOutF16>(a, b, e, m, inter, k, s, part, nparts);
+    default: inval("qgemm: unknown output dtype code");
+    }
+}
 
 bool qgemm_deferred(const signed char* a, const signed char* b, const float* sa_dev,
                     const float* sb_vec, void* y, int y_dtype, int m, int n, int k,

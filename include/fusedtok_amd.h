@@ -417,6 +417,19 @@ int ft_qgemm_rmsnorm_quant_launch(const signed char* a_q, const float* sa_dev,
                                   void* y, const void* residual, const float* w, float eps,
                                   signed char* q, float* scale_out, int rows, int n, int k,
                                   uintptr_t stream);
+/* W8A8 gate/up GEMM then SwiGLU -> per-tensor int8 quantize: h [rows,
+ * 2 inter] = ft_qgemm_launch_ex(a_q, sa_dev, w_gu [2 inter, k] (the inter
+ * gate rows, then the inter up rows), per-channel w_scales, y_dtype =
+ * dtype), then ft_swiglu_quant_launch(h, h + inter, dtype, q, scale_out,
+ * rows, inter, 2 inter), bit for bit (q [rows, inter] int8, *scale_out a
+ * DEVICE float). Where the GEMM runs unsplit on the skinny kernel (16 <
+ * rows <= 64), each GEMM workgroup holds matching gate and up columns and
+ * its epilogue takes the maximum |silu(g) * u| of the stored h, so the
+ * SwiGLU's own maximum pass is not launched. */
+int ft_qgemm_swiglu_quant_launch(const signed char* a_q, const float* sa_dev,
+                                 const signed char* w_gu, const float* w_scales, int dtype,
+                                 void* h, signed char* q, float* scale_out, int rows, int inter,
+                                 int k, uintptr_t stream);
 /* Paged decode attention then per-tensor int8 quantize of its output:
  * out [batch, q_heads, dim] as ft_attention_decode_paged_launch* writes it
  * (arguments as there; dtype FT_DT_*), and codes [batch, q_heads, dim]
@@ -440,7 +453,7 @@ int ft_attention_decode_paged_quant_launch(const void* q, const void* k_pool,
 /*   rmsnorm_quant(x, norm1) -> qgemm_rope_kv_append_paged (QKV)        */
 /*   -> attention_decode_paged_quant over lens + 1 tokens               */
 /*   -> qgemm_rmsnorm_quant (o_proj, residual x, norm2)                 */
-/*   -> gate/up GEMM -> swiglu_quant -> down GEMM -> y                  */
+/*   -> qgemm_swiglu_quant (gate/up) -> down GEMM -> y                  */
 /* every step bit-identical to the unfused ops. Its activation buffers */
 /* are allocated once at create (for max_batch rows); the weights are  */
 /* borrowed and must outlive the layer. x, y [batch, hidden] and the   */

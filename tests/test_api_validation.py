@@ -121,6 +121,8 @@ def test_stub_and_marker_cover_the_public_surface():
     pkg = pathlib.Path(ft.__file__).parent
     assert (pkg / "py.typed").is_file()
     text = (pkg / "__init__.pyi").read_text()
+    import ast
+    ast.parse(text)  # a stub type checkers can read
     for name in ft.__all__:
         assert f"def {name}(" in text or f"class {name}:" in text, name
     listed = re.findall(r'"(\w+)"', re.search(r"__all__ = \[(.*?)\]", text, re.S).group(1))

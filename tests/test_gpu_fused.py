@@ -475,6 +475,69 @@ def test_qgemm_rmsnorm_quant_equals_the_two_ops(dt, case, tuning):
         assert s.item() == s_ref.item()
 
 
+# (m, inter, k, switches) of the gate/up GEMM + swiglu_quant. Per the GEMM
+# dispatch rules, the first five run unsplit on the skinny ring kernel with
+# the SwiGLU maxima in its epilogue: C4's shape (8 waves, 4 row blocks) at a
+# short and at its full K, 40 rows (4 row blocks, 24 rows past M), 17 rows
+# (2 row blocks), and 4-wave workgroups (forced). The last three take the
+# GEMM + swiglu_quant fallback: a K split (inter too small to fill the
+# CUs), the decode GEMM (m <= 16), and inter not a multiple of the paired
+# column tile.
+SWQ_CASES = {
+    "c4": (64, 14336, 512, {}),
+    "c4_full_k": (64, 14336, 4096, {}),
+    "rows40": (40, 12288, 256, {}),
+    "rows17": (17, 12288, 256, {}),
+    "nw4": (64, 6144, 512, {"FT_QGEMM_SK_WAVES": 4}),
+    "split": (64, 768, 1024, {}),
+    "decode": (8, 12288, 512, {}),
+    "odd_tile": (64, 12320, 256, {}),
+}
+
+
+@pytest.mark.parametrize("dt", ALL)
+@pytest.mark.parametrize("case", list(SWQ_CASES))
+def test_qgemm_swiglu_quant_equals_the_two_ops(dt, case, tuning):
+    m, inter, k, sw = SWQ_CASES[case]
+    for name, v in sw.items():
+        tuning(name, v)
+    gen = torch.Generator(device=DEV).manual_seed(90 + list(SWQ_CASES).index(case))
+    a = torch.randint(-127, 128, (m, k), device=DEV, generator=gen,
+                      dtype=torch.int32).to(torch.int8)
+    sa = torch.tensor([0.0007], dtype=torch.float32, device=DEV)
+    w, ws = wq_dev(gen, 2 * inter, k)
+    h_ref = ft.qgemm_perchannel(a, sa, w, ws, out_dtype=dt)
+    q_ref, s_ref = ft.swiglu_quant(h_ref[:, :inter], h_ref[:, inter:], device_scale=True)
+    for rep in range(2):
+        h, q, s = ft.qgemm_swiglu_quant(a, sa, w, ws, out_dtype=dt, device_scale=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(raw(h), raw(h_ref)), f"{case} rep {rep}: h differs"
+        assert torch.equal(q, q_ref), f"{case} rep {rep}: codes differ"
+        assert s.item() == s_ref.item(), f"{case} rep {rep}: scale differs"
+
+
+def test_qgemm_swiglu_quant_maximum_from_the_epilogue_and_errors():
+    # the SwiGLU maximum sits in one element: a single large activation row
+    # entry times a large weight entry (gate) makes one output dominate, so
+    # a lost workgroup partial or a wrong gate/up pairing changes the scale
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    m, inter, k = 64, 14336, 256
+    a = torch.randint(-3, 4, (m, k), device=DEV, generator=gen, dtype=torch.int32).to(torch.int8)
+    w, ws = wq_dev(gen, 2 * inter, k)
+    w = (w // 16).contiguous()
+    a[37, 5] = 127
+    w[9001, 5] = 127            # gate column 9001
+    w[inter + 9001, 5] = -127   # its up partner
+    sa = torch.tensor([0.01], dtype=torch.float32, device=DEV)
+    h_ref = ft.qgemm_perchannel(a, sa, w, ws, out_dtype=torch.bfloat16)
+    q_ref, s_ref = ft.swiglu_quant(h_ref[:, :inter], h_ref[:, inter:])
+    h, q, s = ft.qgemm_swiglu_quant(a, sa, w, ws, out_dtype=torch.bfloat16)
+    assert s == s_ref and torch.equal(q, q_ref)
+    assert q[37, 9001].item() in (-127, 127)
+    with pytest.raises(ValueError, match="even row count"):
+        ft.qgemm_swiglu_quant(a, sa, w[:-1].contiguous(), ws[:-1].contiguous())
+
+
 def test_decode_layer_graph_replays_equal_eager():
     dev = torch.device(DEV)
     gen = torch.Generator(device=dev).manual_seed(77)
