@@ -25,7 +25,8 @@ lens[b] + 1 tokens.
               the 5.0 POP/s dense int8 MFMA peak.
   chains    = BASELINE config 2 (RMSNorm -> int8 quantize -> W8A8 GEMM,
               M in {1, 8, 16}, K=4096, N=11008, fp16 in/out) and config 4
-              (one Llama-3-8B W8A8 decode layer at batch 64, context 8192),
+              (one Llama-3-8B W8A8 decode layer at batch 64, context 8192;
+              also per layer of a 4-layer DecodeStack),
               each replayed as a captured HIP graph (the launch sequence of
               a decode loop without per-call Python cost); weights are
               cycled over enough copies to exceed the 256 MB last-level
@@ -72,7 +73,7 @@ C3 = dict(batch=32, hq=32, hkv=8, dim=128, page=16, len_lo=512, len_hi=32768,
 C5A = dict(m=4096, k=8192, n=28672, seed=5)
 C2 = dict(ms=(1, 8, 16), k=4096, n=11008, seed=2, copies=8, reps=20)
 C4 = dict(batch=64, ctx=8192, hidden=4096, hq=32, hkv=8, dim=128, inter=14336,
-          page=16, eps=1e-5, theta=500000.0, layers=2, seed=4, reps=10)
+          page=16, eps=1e-5, theta=500000.0, layers=2, stack_depth=4, seed=4, reps=10)
 C1 = dict(batch=1, hq=32, hkv=32, t=4096, dim=128, copies=8, seed=1, reps=20)
 C5B = dict(batch=8, hq=64, hkv=8, ctx=131072, dim=128, page=16, seed=51)
 
@@ -324,6 +325,17 @@ def bench_c4(torch, np, ft, dev):
         # position ctx = lens[b] + pos_offset 0; attention over lens + 1
         return objs[i % len(objs)].forward(x, kp, vp, table, lens, out=y)
     us = graph_time_us(torch, layer, 2 * len(layers), c["reps"])
+    # the same layers chained as a model runs them: a DecodeStack of
+    # stack_depth layers (the weight sets cycled), where each layer's first
+    # RMSNorm folds the previous down GEMM's K-split partials
+    chain = [objs[i % len(objs)] for i in range(c["stack_depth"])]
+    stack = ft.DecodeStack(chain)
+    kps, vps = [kp] * len(chain), [vp] * len(chain)
+
+    def stacked(i):
+        return stack.forward(x, kps, vps, table, lens, out=y)
+    us_stack = graph_time_us(torch, stacked, 2, c["reps"]) / len(chain)
+    stack.close()
     wbytes = sum(int(w[0].numel()) + 4 * int(w[1].numel())
                  for w in (layers[0]["qkv"], layers[0]["o"], layers[0]["gu"], layers[0]["down"]))
     kvbytes = b * (c["ctx"] + 1) * hkv * d * 2 * 2
@@ -336,6 +348,8 @@ def bench_c4(torch, np, ft, dev):
             "value": round(us, 2), "unit": "us per layer",
             "tokens_per_s": round(b / (us * 1e-6), 1),
             "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "stacked_us_per_layer": round(us_stack, 2),
+            "stacked_frac_of_hbm_peak": round(nbytes / (us_stack * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "bytes_per_layer": nbytes, "dtype": "bf16 activations / KV, int8 GEMMs",
             "config": {"workload": "DecodeLayer: rmsnorm_quant -> QKV qgemm + RoPE "
                                    "(NeoX, position 8192) + paged append -> "
@@ -343,6 +357,7 @@ def bench_c4(torch, np, ft, dev):
                                    "rmsnorm_quant(+residual) -> gate/up qgemm -> "
                                    "swiglu_quant -> down qgemm",
                        "batch": b, "context": c["ctx"], "layers_cycled": c["layers"],
+                       "stack_depth": c["stack_depth"],
                        "seed": c["seed"]}}
 
 
@@ -846,7 +861,8 @@ def main():
         log("config 2:", json.dumps(chains[0]["results"]))
         torch.cuda.empty_cache()
         chains.append(bench_c4(torch, np, ft, dev))
-        log(f"config 4: {chains[1]['value']} us per layer")
+        log(f"config 4: {chains[1]['value']} us per layer, "
+            f"{chains[1]['stacked_us_per_layer']} us per layer chained in a DecodeStack")
         torch.cuda.empty_cache()
 
     decode_more = None

@@ -97,6 +97,7 @@ __all__ = [
     "qgemm_rmsnorm_quant",
     "qgemm_swiglu_quant",
     "DecodeLayer",
+    "DecodeStack",
     "argmax",
     "argmax_batched",
     "sample_topp",
@@ -1086,4 +1087,4 @@ def decode_step_batched(logits, sampled_ids, penalty=1.0, *, p=0.9, temperature=
     return out if device_out else out.cpu()
 
 
-from .layer import DecodeLayer  # noqa: E402  (uses the loaded extension)
+from .layer import DecodeLayer, DecodeStack  # noqa: E402  (uses the loaded extension)

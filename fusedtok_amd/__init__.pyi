@@ -3,7 +3,7 @@
 # hot path (reference python/fusedtok/__init__.pyi:99-107,208-236); the
 # build's additions are the extra keywords and the fused / test-hook ops.
 
-from typing import Optional, Sequence, Tuple, Union, overload
+from typing import List, Optional, Sequence, Tuple, Union, overload
 
 import numpy as np
 import torch
@@ -40,6 +40,7 @@ __all__ = [
     "qgemm_rmsnorm_quant",
     "qgemm_swiglu_quant",
     "DecodeLayer",
+    "DecodeStack",
     "argmax",
     "argmax_batched",
     "sample_topp",
@@ -167,5 +168,23 @@ class DecodeLayer:
     def capture(self, x: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                 block_table: torch.Tensor, lens: torch.Tensor, *,
                 out: Optional[torch.Tensor] = ...) -> torch.Tensor: ...
+    def replay(self) -> torch.Tensor: ...
+    def close(self) -> None: ...
+
+class DecodeStack:
+    layers: List[DecodeLayer]
+    hidden: int
+    max_batch: int
+    dtype: torch.dtype
+    def __init__(self, layers: Sequence[DecodeLayer]) -> None: ...
+    def forward(self, x: torch.Tensor, k_pools: Sequence[torch.Tensor],
+                v_pools: Sequence[torch.Tensor], block_table: torch.Tensor,
+                lens: torch.Tensor, *, out: Optional[torch.Tensor] = ...) -> torch.Tensor: ...
+    def __call__(self, x: torch.Tensor, k_pools: Sequence[torch.Tensor],
+                 v_pools: Sequence[torch.Tensor], block_table: torch.Tensor,
+                 lens: torch.Tensor, *, out: Optional[torch.Tensor] = ...) -> torch.Tensor: ...
+    def capture(self, x: torch.Tensor, k_pools: Sequence[torch.Tensor],
+                v_pools: Sequence[torch.Tensor], block_table: torch.Tensor,
+                lens: torch.Tensor, *, out: Optional[torch.Tensor] = ...) -> torch.Tensor: ...
     def replay(self) -> torch.Tensor: ...
     def close(self) -> None: ...

@@ -8,6 +8,9 @@
 // The host arithmetic lives entirely in the C library; nothing here
 // computes.
 #include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <vector>
 
 #include <cstdint>
 #include <string>
@@ -523,6 +526,42 @@ PYBIND11_MODULE(_fusedtok, m) {
     m.def("decode_layer_destroy",
           [](uintptr_t L) { check(ft_decode_layer_destroy(P<ft_decode_layer>(L))); },
           py::arg("layer"));
+    // ---- decode stack object ---------------------------------------------
+    m.def("decode_stack_create",
+          [](const std::vector<uintptr_t>& layers) {
+              std::vector<ft_decode_layer*> ls;
+              for (uintptr_t L : layers) ls.push_back(P<ft_decode_layer>(L));
+              ft_decode_stack* S = nullptr;
+              check(ft_decode_stack_create(ls.data(), (int)ls.size(), &S));
+              return reinterpret_cast<uintptr_t>(S);
+          },
+          py::arg("layers"));
+#define FT_STACK_CALL(NAME, FN)                                                           \
+    m.def(NAME,                                                                           \
+          [](uintptr_t S, uintptr_t x, uintptr_t y, const std::vector<uintptr_t>& kps,    \
+             const std::vector<uintptr_t>& vps, uintptr_t table, uintptr_t lens, int batch, \
+             int tbl_width, uintptr_t stream) {                                           \
+              std::vector<void*> kp, vp;                                                  \
+              for (uintptr_t a : kps) kp.push_back(P<void>(a));                           \
+              for (uintptr_t a : vps) vp.push_back(P<void>(a));                           \
+              check(FN(P<ft_decode_stack>(S), P<const void>(x), P<void>(y), kp.data(),     \
+                       vp.data(), P<const int>(table), P<const int>(lens), batch,         \
+                       tbl_width, stream));                                               \
+          },                                                                              \
+          py::arg("stack"), py::arg("x"), py::arg("y"), py::arg("k_pools"),               \
+          py::arg("v_pools"), py::arg("table"), py::arg("lens"), py::arg("batch"),        \
+          py::arg("tbl_width"), py::arg("stream") = 0)
+    FT_STACK_CALL("decode_stack_forward", ft_decode_stack_forward);
+    FT_STACK_CALL("decode_stack_capture", ft_decode_stack_capture);
+#undef FT_STACK_CALL
+    m.def("decode_stack_replay",
+          [](uintptr_t S, uintptr_t stream) {
+              check(ft_decode_stack_replay(P<ft_decode_stack>(S), stream));
+          },
+          py::arg("stack"), py::arg("stream") = 0);
+    m.def("decode_stack_destroy",
+          [](uintptr_t S) { check(ft_decode_stack_destroy(P<ft_decode_stack>(S))); },
+          py::arg("stack"));
     m.def("rope_kv_append_paged_launch",
           [](uintptr_t qkv, int dtype, long long ld, uintptr_t lens, uintptr_t table,
              uintptr_t q_out, uintptr_t k_pool, uintptr_t v_pool, int batch,

@@ -533,6 +533,31 @@ void swiglu_quant_run(const T* g, const T* u, signed char* q, float* scale_out,
     launch_check("swiglu_quant quantize kernel launch");
 }
 
+}  // namespace
+
+void rmsnorm_quant_folded(int dtype, const KFold& fold, void* x_out, const float* w,
+                          signed char* q, float* scale_out, int rows, int cols, float eps,
+                          hipStream_t s) {
+    if (fold.ksplit < 2 || fold.n != cols || fold.mn != (long long)rows * cols)
+        inval("rmsnorm_quant_folded: partials do not match the rows");
+#define FT_RQF(T)                                                                         \
+    do {                                                                                  \
+        rmsq_check<T>((const T*)x_out, w, nullptr, q, scale_out, rows, cols);             \
+        if (rows > 0)                                                                     \
+            rmsq_two_pass<T, true>(nullptr, fold, (T*)x_out, w, nullptr, q, scale_out, rows, \
+                                   cols, eps, s);                                         \
+    } while (0)
+    switch (dtype) {
+    case FT_DT_F32: FT_RQF(float); break;
+    case FT_DT_BF16: FT_RQF(bf16); break;
+    case FT_DT_F16: FT_RQF(f16); break;
+    default: inval("rmsnorm_quant_folded: unknown dtype code");
+    }
+#undef FT_RQF
+}
+
+namespace {
+
 // gate/up GEMM (a_q codes with the device scale *sa_dev; w_gu [2 inter, k],
 // gate rows then up rows, per-channel w_scales) -> h [rows, 2 inter] in T,
 // then swiglu_quant(h[:, :inter], h[:, inter:]). Where the GEMM runs

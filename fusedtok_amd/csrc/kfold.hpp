@@ -45,6 +45,14 @@ bool qgemm_swiglu_max(const signed char* a, const signed char* b, const float* s
                       const float* sb_vec, void* y, int y_dtype, int m, int inter, int k,
                       hipStream_t s, float*& part, int& nparts);
 
+// rmsnorm_quant (no residual) of a K-split GEMM's output still held as its
+// partials: the row pass folds them and stores the rows into x_out (as the
+// GEMM epilogue would), then the codes and the device scale; the same bits
+// as the fold launch followed by rmsnorm_quant. dtype FT_DT_*. fused.hip.
+void rmsnorm_quant_folded(int dtype, const KFold& fold, void* x_out, const float* w,
+                          signed char* q, float* scale_out, int rows, int cols, float eps,
+                          hipStream_t s);
+
 __device__ __forceinline__ float kfold_sa(const KFold& f) { return *f.sa_dev; }
 
 // composed scale of column col (one f32 rounding)

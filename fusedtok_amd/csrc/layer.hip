@@ -17,8 +17,11 @@
 // The reference has no layer op: a decode layer there is these ops called
 // one by one (cuda_launch.hpp:40-59, 185-216, 324-460).
 #include "ft_common.hpp"
+#include "kfold.hpp"
 
+#include <algorithm>
 #include <mutex>
+#include <vector>
 
 struct ft_decode_layer {
     ft_decode_layer_desc d;
@@ -83,7 +86,19 @@ struct Args {
     int tbl_width;
 };
 
-void forward(ft_decode_layer& L, const Args& a, hipStream_t s) {
+// Layer input handed over by the previous layer of a stack: its down
+// GEMM's K-split partials (fold.ksplit > 1), folded by this layer's first
+// RMSNorm row pass, which stores the rows into `store` (this layer's x).
+struct HandIn {
+    KFold fold;
+    void* store = nullptr;
+};
+
+// in: a folded input (a.x unused), or null. defer: where this layer's down
+// GEMM may leave its K-split partials for the next layer (y not written
+// when defer->ksplit > 1 on return), or null (y always written).
+void forward(ft_decode_layer& L, const Args& a, hipStream_t s, const HandIn* in = nullptr,
+             KFold* defer = nullptr) {
     const ft_decode_layer_desc& d = L.d;
     if (a.batch < 0 || a.batch > d.max_batch)
         inval("decode layer: batch must be in [0, max_batch]");
@@ -92,16 +107,23 @@ void forward(ft_decode_layer& L, const Args& a, hipStream_t s) {
     hip_check(hipGetDevice(&dev), "hipGetDevice");
     if (dev != L.device) inval("decode layer: called with another device current");
     if (a.batch == 0) return;
-    if (!a.x || !a.y || !a.k_pool || !a.v_pool || !a.table || !a.lens)
+    const bool folded = in && in->fold.ksplit > 1;
+    if ((!folded && !a.x) || (folded && !in->store) || !a.y || !a.k_pool || !a.v_pool ||
+        !a.table || !a.lens)
         inval("decode layer: null operand");
+    const void* x = folded ? in->store : a.x;  // this layer's input rows (and residual)
     const uintptr_t st = (uintptr_t)s;
     const int B = a.batch, hd = d.q_heads * d.head_dim;
     float* s1 = L.scales;
     float* sa = L.scales + 1;
     float* s2 = L.scales + 2;
     float* s3 = L.scales + 3;
-    rc_check(ft_rmsnorm_quant_launch(a.x, d.dtype, d.norm1, nullptr, L.q1, s1, B, d.hidden,
-                                     d.eps, st));
+    if (folded)
+        rmsnorm_quant_folded(d.dtype, in->fold, in->store, d.norm1, L.q1, s1, B, d.hidden, d.eps,
+                             s);
+    else
+        rc_check(ft_rmsnorm_quant_launch(a.x, d.dtype, d.norm1, nullptr, L.q1, s1, B, d.hidden,
+                                         d.eps, st));
     qkv_rope_step(d.dtype, L.q1, s1, d.w_qkv, d.s_qkv, d.hidden, L.qkv, a.lens, L.lens_next,
                   a.table, L.qrot, a.k_pool, a.v_pool, B, d.q_heads, d.kv_heads, d.head_dim,
                   d.page, a.tbl_width, d.theta, d.pos_offset, d.neox != 0, s);
@@ -109,12 +131,112 @@ void forward(ft_decode_layer& L, const Args& a, hipStream_t s) {
                                                     L.lens_next, L.att, d.dtype, L.qa, sa, B,
                                                     d.q_heads, d.kv_heads, d.page,
                                                     a.tbl_width, d.head_dim, st));
-    rc_check(ft_qgemm_rmsnorm_quant_launch(L.qa, sa, d.w_o, d.s_o, d.dtype, L.o, a.x, d.norm2,
+    rc_check(ft_qgemm_rmsnorm_quant_launch(L.qa, sa, d.w_o, d.s_o, d.dtype, L.o, x, d.norm2,
                                            d.eps, L.q2, s2, B, d.hidden, hd, st));
     rc_check(ft_qgemm_swiglu_quant_launch(L.q2, s2, d.w_gu, d.s_gu, d.dtype, L.h, L.q3, s3, B,
                                           d.inter, d.hidden, st));
-    rc_check(ft_qgemm_launch_ex(L.q3, d.w_down, d.s_down, 0.0f, 0.0f, s3, a.y, d.dtype, B,
-                                d.hidden, d.inter, st));
+    if (defer)
+        qgemm_deferred(L.q3, d.w_down, s3, d.s_down, a.y, d.dtype, B, d.hidden, d.inter, s,
+                       *defer);
+    else
+        rc_check(ft_qgemm_launch_ex(L.q3, d.w_down, d.s_down, 0.0f, 0.0f, s3, a.y, d.dtype, B,
+                                    d.hidden, d.inter, st));
+}
+
+// ---- decode stack --------------------------------------------------------
+void check_stack_layers(ft_decode_layer* const* layers, int n) {
+    if (!layers || n < 1) inval("decode stack: needs at least one layer");
+    for (int i = 0; i < n; ++i)
+        if (!layers[i]) inval("decode stack: null layer");
+    const ft_decode_layer_desc& d0 = layers[0]->d;
+    for (int i = 1; i < n; ++i) {
+        const ft_decode_layer& L = *layers[i];
+        if (L.d.hidden != d0.hidden || L.d.dtype != d0.dtype || L.device != layers[0]->device)
+            inval("decode stack: layers must share the device, dtype and hidden size");
+    }
+}
+
+}  // namespace
+}  // namespace ft
+
+struct ft_decode_stack {
+    std::vector<ft_decode_layer*> layers;  // borrowed
+    int device = 0;
+    int max_batch = 0;
+    void* buf[2] = {nullptr, nullptr};     // activations between layers
+    hipGraphExec_t graph = nullptr;
+};
+
+namespace ft {
+namespace {
+
+struct StackArgs {
+    const void* x;
+    void* y;
+    void* const* k_pools;
+    void* const* v_pools;
+    const int* table;
+    const int* lens;
+    int batch;
+    int tbl_width;
+};
+
+// x -> layer 0 -> .. -> y. Layer i < n - 1 writes (or, K split, leaves as
+// partials for layer i + 1 to fold into) buffer i % 2, layer i + 1's input.
+void stack_forward(ft_decode_stack& S, const StackArgs& a, hipStream_t s) {
+    const int n = (int)S.layers.size();
+    if (a.batch < 0 || a.batch > S.max_batch)
+        inval("decode stack: batch must be in [0, max_batch]");
+    if (!a.k_pools || !a.v_pools) inval("decode stack: null pool array");
+    HandIn hand;
+    const void* x = a.x;
+    for (int i = 0; i < n; ++i) {
+        const bool last = i == n - 1;
+        void* y = last ? a.y : S.buf[i % 2];
+        const Args la{x, y, a.k_pools[i], a.v_pools[i], a.table, a.lens, a.batch, a.tbl_width};
+        KFold out;
+        forward(*S.layers[i], la, s, hand.fold.ksplit > 1 ? &hand : nullptr,
+                last ? nullptr : &out);
+        if (!last) {
+            hand.fold = out;  // ksplit 0: y was written and is the next input
+            hand.store = y;
+            x = y;
+        }
+    }
+}
+
+// Runs fwd(s) once on s (a warm-up that sizes the library's scratch for
+// the shape: growth is refused under capture), then records fwd on a
+// private stream into an instantiated HIP graph.
+template <typename F>
+hipGraphExec_t capture_graph(hipStream_t s, F&& fwd) {
+    fwd(s);
+    hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    hipStream_t cs = nullptr;
+    hip_check(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking), "hipStreamCreate");
+    hipGraph_t g = nullptr;
+    hipGraphExec_t exec = nullptr;
+    try {
+        hip_check(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal),
+                  "hipStreamBeginCapture");
+        try {
+            fwd(cs);
+        } catch (...) {
+            hipGraph_t broken = nullptr;
+            (void)hipStreamEndCapture(cs, &broken);
+            if (broken) (void)hipGraphDestroy(broken);
+            throw;
+        }
+        hip_check(hipStreamEndCapture(cs, &g), "hipStreamEndCapture");
+        hip_check(hipGraphInstantiate(&exec, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    } catch (...) {
+        if (g) (void)hipGraphDestroy(g);
+        (void)hipStreamDestroy(cs);
+        throw;
+    }
+    (void)hipGraphDestroy(g);
+    (void)hipStreamDestroy(cs);
+    return exec;
 }
 
 }  // namespace
@@ -195,36 +317,8 @@ int ft_decode_layer_capture(ft_decode_layer* layer, const void* x, void* y, void
     return ft::guarded([&] {
         if (!layer) ft::inval("decode layer: null layer");
         const ft::Args a{x, y, k_pool, v_pool, table, lens, batch, tbl_width};
-        hipStream_t s = ft::as_stream(stream);
-        // warm-up on the caller's stream: sizes the library's scratch for this
-        // shape (growth is refused under capture)
-        ft::forward(*layer, a, s);
-        ft::hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
-        hipStream_t cs = nullptr;
-        ft::hip_check(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking), "hipStreamCreate");
-        hipGraph_t g = nullptr;
-        hipGraphExec_t exec = nullptr;
-        try {
-            ft::hip_check(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal),
-                          "hipStreamBeginCapture");
-            try {
-                ft::forward(*layer, a, cs);
-            } catch (...) {
-                hipGraph_t broken = nullptr;
-                (void)hipStreamEndCapture(cs, &broken);
-                if (broken) (void)hipGraphDestroy(broken);
-                throw;
-            }
-            ft::hip_check(hipStreamEndCapture(cs, &g), "hipStreamEndCapture");
-            ft::hip_check(hipGraphInstantiate(&exec, g, nullptr, nullptr, 0),
-                          "hipGraphInstantiate");
-        } catch (...) {
-            if (g) (void)hipGraphDestroy(g);
-            (void)hipStreamDestroy(cs);
-            throw;
-        }
-        (void)hipGraphDestroy(g);
-        (void)hipStreamDestroy(cs);
+        hipGraphExec_t exec = ft::capture_graph(
+            ft::as_stream(stream), [&](hipStream_t cs) { ft::forward(*layer, a, cs); });
         if (layer->graph) (void)hipGraphExecDestroy(layer->graph);
         layer->graph = exec;
     });
@@ -244,6 +338,83 @@ int ft_decode_layer_destroy(ft_decode_layer* layer) {
         if (layer->graph) (void)hipGraphExecDestroy(layer->graph);
         if (layer->arena) (void)hipFree(layer->arena);
         delete layer;
+    });
+}
+
+int ft_decode_stack_create(ft_decode_layer* const* layers, int n_layers,
+                           ft_decode_stack** out) {
+    return ft::guarded([&] {
+        if (!out) ft::inval("decode stack: null argument");
+        *out = nullptr;
+        ft::check_stack_layers(layers, n_layers);
+        int dev = 0;
+        ft::hip_check(hipGetDevice(&dev), "hipGetDevice");
+        if (dev != layers[0]->device)
+            ft::inval("decode stack: create it with the layers' device current");
+        auto* S = new ft_decode_stack();
+        S->layers.assign(layers, layers + n_layers);
+        S->device = dev;
+        S->max_batch = layers[0]->d.max_batch;
+        for (int i = 1; i < n_layers; ++i)
+            S->max_batch = std::min(S->max_batch, layers[i]->d.max_batch);
+        const size_t bytes =
+            (((size_t)S->max_batch * layers[0]->d.hidden * layers[0]->esz) + 255) & ~(size_t)255;
+        if (n_layers > 1) {
+            hipError_t e = hipMalloc(&S->buf[0], 2 * bytes);
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                delete S;
+                ft::hip_fail("decode stack buffer allocation", e);
+            }
+            S->buf[1] = (char*)S->buf[0] + bytes;
+        }
+        *out = S;
+    });
+}
+
+int ft_decode_stack_forward(ft_decode_stack* stack, const void* x, void* y,
+                            void* const* k_pools, void* const* v_pools, const int* table,
+                            const int* lens, int batch, int tbl_width, uintptr_t stream) {
+    return ft::guarded([&] {
+        if (!stack) ft::inval("decode stack: null stack");
+        ft::stack_forward(*stack, ft::StackArgs{x, y, k_pools, v_pools, table, lens, batch,
+                                                tbl_width},
+                          ft::as_stream(stream));
+    });
+}
+
+int ft_decode_stack_capture(ft_decode_stack* stack, const void* x, void* y,
+                            void* const* k_pools, void* const* v_pools, const int* table,
+                            const int* lens, int batch, int tbl_width, uintptr_t stream) {
+    return ft::guarded([&] {
+        if (!stack) ft::inval("decode stack: null stack");
+        if (!k_pools || !v_pools) ft::inval("decode stack: null pool array");
+        // the pool pointers are copied: the caller's arrays need not outlive
+        // the call
+        const std::vector<void*> kp(k_pools, k_pools + stack->layers.size());
+        const std::vector<void*> vp(v_pools, v_pools + stack->layers.size());
+        const ft::StackArgs a{x, y, kp.data(), vp.data(), table, lens, batch, tbl_width};
+        hipGraphExec_t exec = ft::capture_graph(
+            ft::as_stream(stream), [&](hipStream_t cs) { ft::stack_forward(*stack, a, cs); });
+        if (stack->graph) (void)hipGraphExecDestroy(stack->graph);
+        stack->graph = exec;
+    });
+}
+
+int ft_decode_stack_replay(ft_decode_stack* stack, uintptr_t stream) {
+    return ft::guarded([&] {
+        if (!stack) ft::inval("decode stack: null stack");
+        if (!stack->graph) ft::inval("decode stack: nothing captured");
+        ft::hip_check(hipGraphLaunch(stack->graph, ft::as_stream(stream)), "hipGraphLaunch");
+    });
+}
+
+int ft_decode_stack_destroy(ft_decode_stack* stack) {
+    return ft::guarded([&] {
+        if (!stack) return;
+        if (stack->graph) (void)hipGraphExecDestroy(stack->graph);
+        if (stack->buf[0]) (void)hipFree(stack->buf[0]);
+        delete stack;
     });
 }
 

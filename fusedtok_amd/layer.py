@@ -172,3 +172,96 @@ class DecodeLayer:
             self.close()
         except Exception:
             pass
+
+
+class DecodeStack:
+    """Layers chained in one forward: ``y = layers[-1](... layers[0](x))``,
+    the same results as calling the layers one after another, bit for bit.
+    Where a layer's down GEMM splits K, the next layer's first RMSNorm row
+    pass folds its partial sums (csrc/layer.hip, C ABI ft_decode_stack_*):
+    one launch per chained layer fewer than the layer objects called one by
+    one. ``capture`` records the whole chain into one HIP graph.
+
+    The layers (DecodeLayer objects on one device with one dtype and hidden
+    size) are kept referenced; a layer may appear more than once. Each layer
+    has its own KV pools (``k_pools`` / ``v_pools``: sequences of tensors,
+    one per layer); the block table and lens are shared.
+    """
+
+    def __init__(self, layers):
+        layers = list(layers)
+        if not layers or not all(isinstance(L, DecodeLayer) for L in layers):
+            raise TypeError("DecodeStack needs a non-empty sequence of DecodeLayer objects")
+        first = layers[0]
+        for L in layers[1:]:
+            if (L.device != first.device or L.dtype is not first.dtype
+                    or L.hidden != first.hidden):
+                raise ValueError("DecodeStack layers must share the device, dtype and hidden size")
+        if any(L._h is None for L in layers):
+            raise ValueError("DecodeStack: a layer has been closed")
+        self.layers = layers
+        self.device, self.dtype, self.hidden = first.device, first.dtype, first.hidden
+        self.max_batch = min(L.max_batch for L in layers)
+        with torch.cuda.device(self.device):
+            self._h = _fusedtok.decode_stack_create([L._h for L in layers])
+        self._captured = None
+
+    def _operands(self, x, k_pools, v_pools, block_table, lens, out):
+        k_pools, v_pools = list(k_pools), list(v_pools)
+        n = len(self.layers)
+        if len(k_pools) != n or len(v_pools) != n:
+            raise ValueError(f"k_pools and v_pools must hold one pool per layer ({n})")
+        ops = None
+        for L, kp, vp in zip(self.layers, k_pools, v_pools):
+            ops, b, width = L._operands(x, kp, vp, block_table, lens, out)
+            out = ops[1]
+        return ops[0], ops[1], k_pools, v_pools, ops[4], ops[5], b, width
+
+    def _args(self, x, k_pools, v_pools, block_table, lens, out):
+        if self._h is None or any(L._h is None for L in self.layers):
+            raise RuntimeError("DecodeStack: the stack or one of its layers has been closed")
+        x, y, kps, vps, table, ln, b, width = self._operands(x, k_pools, v_pools, block_table,
+                                                             lens, out)
+        if b > self.max_batch:
+            raise ValueError("batch exceeds the stack's max_batch")
+        return (x, y, kps, vps, table, ln), (
+            x.data_ptr(), y.data_ptr(), [t.data_ptr() for t in kps],
+            [t.data_ptr() for t in vps], table.data_ptr(), ln.data_ptr(), b, width)
+
+    def forward(self, x, k_pools, v_pools, block_table, lens, *, out=None):
+        """One decode step through every layer: returns y [batch, hidden];
+        each layer appends its sequence's K/V at slot lens[b] of its own
+        pools (lens not advanced)."""
+        keep, args = self._args(x, k_pools, v_pools, block_table, lens, out)
+        _fusedtok.decode_stack_forward(self._h, *args, _stream())
+        return keep[1]
+
+    __call__ = forward
+
+    def capture(self, x, k_pools, v_pools, block_table, lens, *, out=None):
+        """Warm-up forward, then the chain recorded into one HIP graph bound
+        to these tensors (kept referenced until the next capture). Returns
+        the output tensor every replay writes."""
+        keep, args = self._args(x, k_pools, v_pools, block_table, lens, out)
+        _fusedtok.decode_stack_capture(self._h, *args, _stream())
+        self._captured = keep
+        return keep[1]
+
+    def replay(self):
+        """Launch the captured chain on the current stream."""
+        if self._captured is None:
+            raise RuntimeError("DecodeStack.replay: nothing captured")
+        _fusedtok.decode_stack_replay(self._h, _stream())
+        return self._captured[1]
+
+    def close(self):
+        h, self._h = getattr(self, "_h", None), None
+        if h:
+            _fusedtok.decode_stack_destroy(h)
+        self._captured = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

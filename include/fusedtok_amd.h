@@ -497,6 +497,31 @@ int ft_decode_layer_capture(ft_decode_layer* layer, const void* x, void* y, void
 int ft_decode_layer_replay(ft_decode_layer* layer, uintptr_t stream);
 int ft_decode_layer_destroy(ft_decode_layer* layer);
 
+/* Decode stack (build addition, no reference counterpart): n layers    */
+/* chained x -> layer 0 -> layer 1 -> ... -> y, each layer's output the */
+/* next one's input, with the same results as n ft_decode_layer_forward */
+/* calls bit for bit. Where a layer's down GEMM splits K, its int32     */
+/* partials are folded by the next layer's first RMSNorm row pass       */
+/* instead of a fold launch of their own. The layers are borrowed (same */
+/* device, dtype and hidden size; they must outlive the stack, and a    */
+/* layer may appear more than once); table and lens are shared by all   */
+/* layers, k_pools / v_pools are HOST arrays of n device pool pointers. */
+/* The stack holds two [max_batch, hidden] buffers for the activations  */
+/* between layers (max_batch = the smallest of its layers').            */
+typedef struct ft_decode_stack ft_decode_stack;
+int ft_decode_stack_create(ft_decode_layer* const* layers, int n_layers,
+                           ft_decode_stack** out);
+int ft_decode_stack_forward(ft_decode_stack* stack, const void* x, void* y,
+                            void* const* k_pools, void* const* v_pools, const int* table,
+                            const int* lens, int batch, int tbl_width, uintptr_t stream);
+/* Warm-up forward, then the whole chain recorded into one HIP graph    */
+/* (the layer capture contract above, for all n layers).                */
+int ft_decode_stack_capture(ft_decode_stack* stack, const void* x, void* y,
+                            void* const* k_pools, void* const* v_pools, const int* table,
+                            const int* lens, int batch, int tbl_width, uintptr_t stream);
+int ft_decode_stack_replay(ft_decode_stack* stack, uintptr_t stream);
+int ft_decode_stack_destroy(ft_decode_stack* stack);
+
 /* ------------------------------------------------------------------ */
 /* Post-logits sampling                                                */
 /* Greedy argmax: index of the first maximum of each row (a scan with  */

@@ -182,3 +182,119 @@ def test_layer_argument_errors():
     with pytest.raises(ValueError, match="s_o must have shape"):
         ft.DecodeLayer(q_heads=8, kv_heads=2, page=16, max_batch=1, dtype=dt, **bad)
     layer.close()
+
+
+# ---------------------------------------------------------------------------
+# DecodeStack: layers chained in one forward (ft_decode_stack_*)
+# ---------------------------------------------------------------------------
+# 20 rows take the skinny GEMM with a K split of the down projection (3
+# partials, folded by the next layer's RMSNorm row pass); 4 rows the decode
+# GEMM (never split: the plain hand-over)
+MID = dict(b=20, hq=8, hkv=2, d=64, hidden=512, inter=768, page=16,
+           lens=[5, 300, 17, 100, 64, 1, 250, 33, 80, 9, 120, 7, 40, 200, 2, 150, 60, 11, 90, 30])
+# the same rows with a longer down projection: split 8 (one batch of 8
+# partial loads) and split 16 (the fold loops over batches of 8)
+MID8 = dict(MID, inter=2048)
+MID16 = dict(MID, inter=4096)
+
+
+def make_stack_case(cfg, dt, n_layers, seed):
+    w0, x, kp, vp, table, lens = make_case(cfg, dt, seed)
+    ws, kps, vps = [w0], [kp], [vp]
+    for i in range(1, n_layers):
+        w, _, kpi, vpi, _, _ = make_case(cfg, dt, seed + 100 * i)
+        ws.append(w)
+        kps.append(kpi)
+        vps.append(vpi)
+    return ws, x, kps, vps, table, lens
+
+
+@pytest.mark.parametrize("name,dt,n", [("toy", torch.bfloat16, 3), ("mid", torch.float32, 3),
+                                       ("mid", torch.bfloat16, 4), ("mid", torch.float16, 2),
+                                       ("c4", torch.bfloat16, 2), ("mid", torch.bfloat16, 1),
+                                       ("mid8", torch.bfloat16, 2), ("mid16", torch.float32, 2),
+                                       ("mid16", torch.float16, 3)])
+def test_stack_equals_the_layers_called_in_turn(name, dt, n):
+    cfg = {"toy": TOY, "mid": MID, "mid8": MID8, "mid16": MID16, "c4": C4}[name]
+    ws, x, kps, vps, table, lens = make_stack_case(cfg, dt, n, 21)
+    layers = [make_layer(cfg, w, dt) for w in ws]
+    kps_ref, vps_ref = [t.clone() for t in kps], [t.clone() for t in vps]
+    cur = x
+    for L, kp, vp in zip(layers, kps_ref, vps_ref):
+        cur = L(cur, kp, vp, table, lens)
+    torch.cuda.synchronize()
+    y_ref = cur.clone()
+    stack = ft.DecodeStack(layers)
+    for rep in range(2):
+        y = stack(x, kps, vps, table, lens)
+        torch.cuda.synchronize()
+        assert np.array_equal(raw(y), raw(y_ref)), f"{name} n={n} rep {rep}: y differs"
+    for i in range(n):
+        assert torch.equal(kps[i], kps_ref[i]) and torch.equal(vps[i], vps_ref[i]), f"pools {i}"
+    # a layer used twice in one stack (shared weights, separate pools)
+    if n >= 2:
+        twice = ft.DecodeStack([layers[0], layers[0]])
+        kp2 = [kps[0].clone(), kps[1].clone()]
+        vp2 = [vps[0].clone(), vps[1].clone()]
+        kq = [t.clone() for t in kp2]
+        vq = [t.clone() for t in vp2]
+        y1 = layers[0](x, kq[0], vq[0], table, lens)
+        y2_ref = layers[0](y1, kq[1], vq[1], table, lens).clone()
+        y2 = twice(x, kp2, vp2, table, lens)
+        torch.cuda.synchronize()
+        assert np.array_equal(raw(y2), raw(y2_ref))
+        twice.close()
+    stack.close()
+    for L in layers:
+        L.close()
+
+
+def test_stack_graph_replays_and_rewritten_inputs():
+    dt = torch.bfloat16
+    ws, x, kps, vps, table, lens = make_stack_case(MID, dt, 3, 31)
+    layers = [make_layer(MID, w, dt) for w in ws]
+    stack = ft.DecodeStack(layers)
+    ref = stack(x, [t.clone() for t in kps], [t.clone() for t in vps], table, lens).clone()
+    y = stack.capture(x, kps, vps, table, lens)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref), "warm-up of the capture differs"
+    for rep in range(3):
+        y.zero_()
+        stack.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), f"replay {rep} differs from the eager stack"
+        eager = stack(x, [t.clone() for t in kps], [t.clone() for t in vps], table, lens)
+        torch.cuda.synchronize()
+        assert torch.equal(eager, ref)
+    gen = torch.Generator(device=DEV).manual_seed(98)
+    x.copy_(torch.randn(x.shape, device=DEV, generator=gen).to(dt))
+    ref2 = stack(x, [t.clone() for t in kps], [t.clone() for t in vps], table, lens).clone()
+    stack.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref2) and not torch.equal(ref2, ref)
+    stack.close()
+    for L in layers:
+        L.close()
+
+
+def test_stack_argument_errors():
+    dt = torch.bfloat16
+    ws, x, kps, vps, table, lens = make_stack_case(TOY, dt, 2, 41)
+    layers = [make_layer(TOY, w, dt) for w in ws]
+    with pytest.raises(TypeError, match="non-empty sequence"):
+        ft.DecodeStack([])
+    other = make_layer(TOY, {k: (v.float() if v.dtype is torch.bfloat16 else v)
+                             for k, v in ws[0].items()}, torch.float32)
+    with pytest.raises(ValueError, match="share the device, dtype and hidden"):
+        ft.DecodeStack([layers[0], other])
+    stack = ft.DecodeStack(layers)
+    with pytest.raises(ValueError, match="one pool per layer"):
+        stack(x, kps[:1], vps[:1], table, lens)
+    with pytest.raises(RuntimeError, match="nothing captured"):
+        stack.replay()
+    layers[1].close()
+    with pytest.raises(RuntimeError, match="has been closed"):
+        stack(x, kps, vps, table, lens)
+    stack.close()
+    layers[0].close()
+    other.close()
