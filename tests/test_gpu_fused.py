@@ -168,6 +168,50 @@ def test_rmsnorm_qgemm_equals_the_two_ops(dt, rows, n, k, res, odt, tuning):
     assert torch.equal(yt, ft.qgemm(q2, s2, b, 0.004, out_dtype=odt))
 
 
+@pytest.mark.parametrize("dt", ALL)
+@pytest.mark.parametrize("rows,n,k,res", [
+    # C2's shape at 2, 8 and 16 rows (one-workgroup normalisation up to 4
+    # rows, the row + quantize kernels above; the decode GEMMs)
+    (2, 11008, 4096, False), (8, 11008, 4096, True), (16, 11008, 4096, False),
+    (16, 28672, 4096, True),
+    # K = 512, N not a multiple of 16, few column tiles
+    (5, 1000, 512, True), (13, 4000, 2048, False),
+    (16, 40, 1024, True), (4, 17, 4096, False), (3, 300, 512, True),
+    (7, 300, 4608, False), (9, 64, 1000, True), (17, 64, 512, False)])
+def test_rmsnorm_qgemm_several_rows_equals_the_two_ops(dt, rows, n, k, res, tuning):
+    # more than one row: the codes, the scale and the output must equal
+    # rmsnorm_quant followed by qgemm_perchannel and the oracle chain
+    odt = {torch.float32: torch.bfloat16, torch.bfloat16: torch.float16,
+           torch.float16: torch.float16}[dt]
+    rng = np.random.default_rng(rows * 37 + n + k + res)
+    x = rng.standard_normal((rows, k)).astype(np.float32) * 2
+    x[rows // 2, : k // 5] *= 30.0  # one row dominates the tensor maximum
+    x = t(x, dt)
+    w = t(rng.uniform(0.5, 1.5, k).astype(np.float32))
+    r = t(rng.standard_normal((rows, k)).astype(np.float32), dt) if res else None
+    b = t(rng.integers(-127, 128, (n, k)).astype(np.int8))
+    sb = t(rng.uniform(1e-3, 1e-2, n).astype(np.float32))
+    y, q, s = ft.rmsnorm_qgemm(x, w, b, sb, residual=r, eps=1e-5, out_dtype=odt)
+    q2, s2 = ft.rmsnorm_quant(x, w, residual=r, eps=1e-5, device_scale=True)
+    y2 = ft.qgemm_perchannel(q2, s2, b, sb, out_dtype=odt)
+    assert torch.equal(q, q2) and torch.equal(s, s2) and torch.equal(y, y2)
+    eq, es = oracle.rmsnorm_quant(as_f32(x), w.cpu().numpy(), None if r is None else as_f32(r),
+                                  1e-5)
+    np.testing.assert_array_equal(q.cpu().numpy(), eq)
+    assert float(s) == es
+    cols = np.arange(0, n, max(1, n // 512))  # a column sample keeps the oracle GEMM short
+    ref = oracle.qgemm_perchannel(eq, es, np.ascontiguousarray(b.cpu().numpy()[cols]),
+                                  np.ascontiguousarray(sb.cpu().numpy()[cols]))
+    assert torch.equal(y.cpu()[:, cols], torch.from_numpy(ref).to(odt))
+    # the two-step chain of the same entry point, and a per-tensor weight scale
+    tuning("FT_RMSQ_GEMV_SPLIT", 1)
+    y3, q3, s3 = ft.rmsnorm_qgemm(x, w, b, sb, residual=r, eps=1e-5, out_dtype=odt)
+    tuning.clear("FT_RMSQ_GEMV_SPLIT")
+    assert torch.equal(y3, y) and torch.equal(q3, q) and torch.equal(s3, s)
+    yt, _, _ = ft.rmsnorm_qgemm(x, w, b, 0.004, residual=r, eps=1e-5, out_dtype=odt)
+    assert torch.equal(yt, ft.qgemm(q2, s2, b, 0.004, out_dtype=odt))
+
+
 def test_rmsnorm_quant_device_scale_zero_rows_and_1d():
     rng = np.random.default_rng(3)
     x = t(rng.standard_normal(512).astype(np.float32), torch.bfloat16)
