@@ -263,3 +263,48 @@ def test_scratch_allocation_failure_is_reported(lib):
             ft._fusedtok.quantize_launch(256, 256, 256, 1 << 20, 0)
     finally:
         assert lib.ft_clear_tuning(b"FT_FAIL_SCRATCH") == FT_OK
+
+
+def test_decode_layer_and_stack_invalid_arguments(lib):
+    # every check here runs before the entry point's first HIP call
+    P, I, U = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    out = ctypes.c_void_p(1)
+    cr = lib.ft_decode_layer_create
+    cr.argtypes = [P, P]
+    assert cr(None, ctypes.byref(out)) == FT_EINVAL
+    desc = (ctypes.c_char * 512)()  # zeroed: hidden 0 fails the shape checks
+    assert cr(desc, ctypes.byref(out)) == FT_EINVAL
+    assert out.value is None  # *out cleared before validation
+    assert b"hidden" in lib.ft_last_error()
+    fw = lib.ft_decode_layer_forward
+    fw.argtypes = [P, P, P, P, P, P, P, I, I, U]
+    assert fw(None, None, None, None, None, None, None, 1, 1, 0) == FT_EINVAL
+    cp = lib.ft_decode_layer_capture
+    cp.argtypes = [P, P, P, P, P, P, P, I, I, U]
+    assert cp(None, None, None, None, None, None, None, 1, 1, 0) == FT_EINVAL
+    rp = lib.ft_decode_layer_replay
+    rp.argtypes = [P, U]
+    assert rp(None, 0) == FT_EINVAL
+    lib.ft_decode_layer_destroy.argtypes = [P]
+    assert lib.ft_decode_layer_destroy(None) == FT_OK
+
+    sc = lib.ft_decode_stack_create
+    sc.argtypes = [P, I, P]
+    out = ctypes.c_void_p(1)
+    assert sc(None, 1, ctypes.byref(out)) == FT_EINVAL and out.value is None
+    nulls = (ctypes.c_void_p * 2)(None, None)
+    assert sc(nulls, 2, ctypes.byref(out)) == FT_EINVAL
+    assert b"null layer" in lib.ft_last_error()
+    assert sc(nulls, 0, ctypes.byref(out)) == FT_EINVAL
+    assert sc(nulls, 2, None) == FT_EINVAL
+    sf = lib.ft_decode_stack_forward
+    sf.argtypes = [P, P, P, P, P, P, P, I, I, U]
+    assert sf(None, None, None, None, None, None, None, 1, 1, 0) == FT_EINVAL
+    sp = lib.ft_decode_stack_capture
+    sp.argtypes = [P, P, P, P, P, P, P, I, I, U]
+    assert sp(None, None, None, None, None, None, None, 1, 1, 0) == FT_EINVAL
+    sr = lib.ft_decode_stack_replay
+    sr.argtypes = [P, U]
+    assert sr(None, 0) == FT_EINVAL
+    lib.ft_decode_stack_destroy.argtypes = [P]
+    assert lib.ft_decode_stack_destroy(None) == FT_OK
