@@ -1027,14 +1027,15 @@ def sample_topp_batched(logits, p, *, temperature=1.0, seeds=None, cuda=False,
                                                         temperature=temperature,
                                                         seeds=seeds))
     seed_vec = _sargs.seed_vector(seeds, c.rows)
-    (seeds_dev,) = _sargs.upload_int64([seed_vec], c.device)
     out = torch.empty(c.rows, dtype=torch.int64, device=c.device)
     if c.rows:
         if c.n == 0:
             raise ValueError("sample of empty logits")
-        _fusedtok.sample_topp_batched_launch(c.ptr("logits"), c.rows, c.n, float(p),
-                                             float(temperature), seeds_dev.data_ptr(),
-                                             out.data_ptr(), _stream())
+        _sargs.launch_with_int64(
+            [seed_vec], c.device, _fusedtok.host_device_address,
+            lambda a: _fusedtok.sample_topp_batched_launch(
+                c.ptr("logits"), c.rows, c.n, float(p), float(temperature), a[0],
+                out.data_ptr(), _stream()))
     return out if device_out else out.cpu()
 
 
@@ -1074,16 +1075,18 @@ def decode_step_batched(logits, sampled_ids, penalty=1.0, *, p=0.9, temperature=
             a["logits"], sampled_ids, penalty, p=p, temperature=temperature, seeds=seeds,
             ids_offsets=ids_offsets))
     flat, offsets = _sargs.histories_csr(sampled_ids, ids_offsets, c.rows, c.n)
-    ids_dev, offs_dev, seeds_dev = _sargs.upload_int64(
-        [flat, offsets, _sargs.seed_vector(seeds, c.rows)], c.device)
+    seed_vec = _sargs.seed_vector(seeds, c.rows)
     out = torch.empty(c.rows, dtype=torch.int64, device=c.device)
     if c.rows:
         if c.n == 0:
             raise ValueError("sample of empty logits")
-        _fusedtok.decode_step_batched_launch(
-            c.ptr("logits"), c.rows, c.n, ids_dev.data_ptr() if flat.size else None,
-            offs_dev.data_ptr(), float(penalty), float(p), float(temperature),
-            seeds_dev.data_ptr(), out.data_ptr(), _stream())
+        # histories, offsets and seeds read in place from pinned host memory
+        _sargs.launch_with_int64(
+            [flat, offsets, seed_vec], c.device, _fusedtok.host_device_address,
+            lambda a: _fusedtok.decode_step_batched_launch(
+                c.ptr("logits"), c.rows, c.n, a[0] if flat.size else None, a[1],
+                float(penalty), float(p), float(temperature), a[2], out.data_ptr(),
+                _stream()))
     return out if device_out else out.cpu()
 
 

@@ -121,43 +121,61 @@ def histories_csr(sampled_ids, ids_offsets, rows, vocab):
     return np.ascontiguousarray(flat), np.ascontiguousarray(offs)
 
 
-# Small per-call int64 vectors (histories, offsets, seeds) go up in one
-# non-blocking copy from a ring of pinned host buffers: a pageable copy per
-# vector made every call wait for the GPU to drain before the host could
-# prepare the next one. A slot is refilled only after the copy that read it
-# has completed (its event).
+# Small per-call int64 vectors (histories, offsets, seeds) are staged in a
+# ring of pinned host buffers. The kernels read them in place through the
+# buffer's device mapping (no copy on the stream: an asynchronous copy's
+# completion reached the compute queue only tens of microseconds after the
+# kernels were queued); where the runtime reports no mapping, one
+# non-blocking copy per call takes them up instead. A slot is refilled only
+# after the work that read it has completed (its event). A pageable copy
+# per vector made every call wait for the GPU to drain.
 class _PinnedRing:
     def __init__(self, slots=4):
-        self.slots = [[None, None] for _ in range(slots)]  # [buffer, event]
+        self.slots = [[None, None, 0] for _ in range(slots)]  # [buffer, event, device address]
         self.turn = 0
 
-    def upload(self, arrays, device):
+    def _fill(self, arrays, mapper=None):
         sizes = [int(a.size) for a in arrays]
         total = max(1, sum(sizes))
         slot = self.slots[self.turn % len(self.slots)]
         self.turn += 1
-        buf, done = slot
+        buf, done = slot[0], slot[1]
         if done is not None:
             done.synchronize()
         if buf is None or buf.numel() < total:
             grow = max(total, 1024, 0 if buf is None else 2 * buf.numel())
             buf = torch.empty(grow, dtype=torch.int64, pin_memory=True)
+            slot[0], slot[2] = buf, (mapper(buf.data_ptr()) if mapper else 0)
         view = buf.numpy()
         bounds = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
         for a, lo, hi in zip(arrays, bounds[:-1], bounds[1:]):
             view[lo:hi] = a.reshape(-1)
-        dev = torch.empty(total, dtype=torch.int64, device=device)
-        dev.copy_(buf[:total], non_blocking=True)
+        return slot, total, bounds
+
+    def launch_in_place(self, arrays, device, mapper, launch):
+        """launch(addresses): the vectors' device-accessible addresses
+        (int), read in place from pinned host memory when `mapper` gives the
+        buffer a device address, else from an uploaded copy. The slot's
+        event follows the launch on the current stream."""
+        slot, total, bounds = self._fill(arrays, mapper)
+        base = slot[2]
+        if base:
+            launch([base + 8 * int(lo) for lo in bounds[:-1]])
+        else:  # no device mapping: one copy of the slot
+            dev = torch.empty(total, dtype=torch.int64, device=device)
+            dev.copy_(slot[0][:total], non_blocking=True)
+            launch([dev.data_ptr() + 8 * int(lo) for lo in bounds[:-1]])
         ev = torch.cuda.Event()
         ev.record(torch.cuda.current_stream(device))
-        slot[0], slot[1] = buf, ev
-        return [dev[lo:hi] for lo, hi in zip(bounds[:-1], bounds[1:])]
+        slot[1] = ev
 
 
 _RING = _PinnedRing()
 
 
-def upload_int64(arrays, device):
-    """Host int64 numpy vectors -> device int64 tensors (views of one
-    buffer), ordered on the current stream."""
-    return _RING.upload(arrays, device)
+def launch_with_int64(arrays, device, mapper, launch):
+    """Host int64 numpy vectors staged for one launch: launch(addresses)
+    gets device-accessible addresses of them (pinned host memory read in
+    place, or an uploaded copy); `mapper(host_ptr)` returns the device
+    address of pinned host memory or 0."""
+    _RING.launch_in_place(arrays, device, mapper, launch)

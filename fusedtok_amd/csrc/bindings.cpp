@@ -46,6 +46,15 @@ PYBIND11_MODULE(_fusedtok, m) {
     m.def("cuda_available", []() { return ft_device_available() != 0; },
           "True if a usable HIP device is present");
     m.def("version", []() { return std::string(ft_version()); });
+    m.def("host_device_address",
+          [](uintptr_t host) {
+              void* dev = nullptr;
+              return ft_host_device_address(reinterpret_cast<const void*>(host), &dev) == FT_OK
+                         ? reinterpret_cast<uintptr_t>(dev)
+                         : uintptr_t(0);
+          },
+          py::arg("host"),
+          "device address of pinned host memory, or 0 when it has no device mapping");
     m.def("set_tuning",
           [](const std::string& name, int value) { check(ft_set_tuning(name.c_str(), value)); },
           py::arg("name"), py::arg("value"),

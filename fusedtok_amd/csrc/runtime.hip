@@ -187,6 +187,25 @@ int ft_device_available(void) {
 
 const char* ft_version(void) { return "0.1.0"; }
 
+int ft_host_device_address(const void* host, void** dev) {
+    return ft::guarded([&] {
+        if (!host || !dev) ft::inval("host_device_address: null argument");
+        *dev = nullptr;
+        hipPointerAttribute_t at{};
+        const hipError_t e = hipPointerGetAttributes(&at, host);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            ft::inval("host_device_address: not memory the HIP runtime knows");
+        }
+        if (at.type != hipMemoryTypeHost || !at.devicePointer)
+            ft::inval("host_device_address: not pinned host memory mapped to the device");
+        // the attributes may describe the allocation's base: keep the offset
+        const size_t off = at.hostPointer ? (size_t)((const char*)host - (const char*)at.hostPointer)
+                                          : 0;
+        *dev = (char*)at.devicePointer + off;
+    });
+}
+
 int ft_set_tuning(const char* name, int value) {
     return ft::guarded([&] {
         const int i = ft::tune_index(name);

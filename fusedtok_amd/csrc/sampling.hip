@@ -445,6 +445,9 @@ __global__ __launch_bounds__(kSmpNT) void sample_topp_rows(
     __shared__ SmpShared sh;
     const int r = blockIdx.x;
     const int tid = threadIdx.x;
+    // the seed first: it may sit in host memory, and its round trip then
+    // overlaps the passes below
+    const u64 seed = seeds ? seeds[r] : seed0;
     SampleRow row{x + (size_t)r * n, n, inv_t, pen, nullptr, 0};
     const bool penal = ids != nullptr && pen != 1.0f;
     if (penal) {
@@ -494,7 +497,7 @@ __global__ __launch_bounds__(kSmpNT) void sample_topp_rows(
     select_prefix(row, vmax, T, sh, none);
     const u64 nucleus = sh.r_mass;
     // draw: prefix mass >= u * nucleus mass
-    const float u = splitmix_uniform(seeds ? seeds[r] : seed0);
+    const float u = splitmix_uniform(seed);
     double td = ceil((double)u * (double)nucleus);
     T = td < 1.0 ? 1ULL : (u64)td;
     if (T > nucleus) T = nucleus;
@@ -640,6 +643,9 @@ __global__ __launch_bounds__(kSliceNT) void smp_slice_hist(SliceArgs a) {
 __global__ __launch_bounds__(kSmpNT) void smp_plan(SliceArgs a) {
     __shared__ SmpShared sh;
     const int r = blockIdx.x, tid = threadIdx.x;
+    // the seed first: it may sit in host memory, and its round trip then
+    // overlaps the histogram merge below
+    const u64 seed = a.seeds ? a.seeds[r] : a.seed0;
     const float vmax = row_max_of(a, r);
     if (!(vmax > -INFINITY)) {
         if (tid == 0) a.plan[r] = SmpPlan{0ULL, vmax, 0, 0, 0};
@@ -669,7 +675,7 @@ __global__ __launch_bounds__(kSmpNT) void smp_plan(SliceArgs a) {
     const u64 after_b1 = sh.r_above + sh.h_mass[b1];  // nucleus mass is in [T1, after_b1]
     __syncthreads();
     // the draw threshold for the extreme nucleus masses
-    const float u = splitmix_uniform(a.seeds ? a.seeds[r] : a.seed0);
+    const float u = splitmix_uniform(seed);
     auto draw_t = [&](u64 nucleus) {
         const double td = ceil((double)u * (double)nucleus);
         u64 T = td < 1.0 ? 1ULL : (u64)td;
@@ -726,6 +732,7 @@ __global__ __launch_bounds__(kSliceNT) void smp_gather(SliceArgs a) {
 __global__ __launch_bounds__(kSmpNT) void smp_finish(SliceArgs a) {
     __shared__ SmpShared sh;
     const int r = blockIdx.x, tid = threadIdx.x;
+    const u64 seed = a.seeds ? a.seeds[r] : a.seed0;  // first, as in smp_plan
     const SmpPlan pl = a.plan[r];
     if (!(pl.vmax > -INFINITY)) {
         // every value -inf (or NaN): as sample_topp_rows
@@ -762,7 +769,7 @@ __global__ __launch_bounds__(kSmpNT) void smp_finish(SliceArgs a) {
     if (T > total) T = total;
     select_prefix(row, pl.vmax, T, sh, pre);
     const u64 nucleus = sh.r_mass;
-    const float u = splitmix_uniform(a.seeds ? a.seeds[r] : a.seed0);
+    const float u = splitmix_uniform(seed);
     const double td = ceil((double)u * (double)nucleus);
     T = td < 1.0 ? 1ULL : (u64)td;
     if (T > nucleus) T = nucleus;

@@ -60,6 +60,14 @@ int ft_device_available(void);
 /* Library version string. */
 const char* ft_version(void);
 
+/* Device address of pinned host memory (hipHostMalloc, torch's          */
+/* pin_memory=True), so that a launcher can read small host-staged      */
+/* vectors in place instead of waiting on a copy; FT_EINVAL when the    */
+/* runtime reports no device mapping. Build addition with no reference */
+/* counterpart, for callers that stage per-call vectors (the samplers'  */
+/* histories, offsets and seeds).                                       */
+int ft_host_device_address(const void* host, void** dev);
+
 /* Build addition (tests and measurement sweeps; no reference counterpart):
  * tuning switches. Each FT_* switch (FT_ATTN_SEGS, FT_QGEMM_KERNEL, ...) is
  * read from the environment once per process, on first use;
@@ -556,7 +564,9 @@ int ft_sample_topp_batched_launch(const float* x, int rows, int n, float p, floa
 /* offs[r+1]) (DEVICE int64 offsets, rows + 1 entries). Replaces        */
 /* decode_step_launch (cuda_launch.hpp:138-141) and                     */
 /* decode_step_batched_launch (:179-183), writing tokens to DEVICE      */
-/* memory without a host sync.                                          */
+/* memory without a host sync. ids, offs and seeds may also be pinned  */
+/* host memory at its device address (ft_host_device_address): the     */
+/* kernels then read them in place, with no copy on the stream.         */
 int ft_decode_step_launch(const float* x, const long long* ids, int n, int m,
                           float penalty, float p, float t, unsigned long long seed,
                           long long* out, uintptr_t stream);

@@ -308,3 +308,11 @@ def test_decode_layer_and_stack_invalid_arguments(lib):
     assert sr(None, 0) == FT_EINVAL
     lib.ft_decode_stack_destroy.argtypes = [P]
     assert lib.ft_decode_stack_destroy(None) == FT_OK
+
+
+def test_host_device_address_null_arguments(lib):
+    f = lib.ft_host_device_address
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    dev = ctypes.c_void_p(1)
+    assert f(None, ctypes.byref(dev)) == FT_EINVAL
+    assert f(ctypes.byref(dev), None) == FT_EINVAL

@@ -250,3 +250,40 @@ def test_sliced_pipeline_any_slice_count(slices, tuning):
         b = ft.decode_step_batched(lt, hist, 1.2, p=p, temperature=temp, seeds=seeds).tolist()
         tuning.clear("FT_SMP_SINGLE")
         assert a == b, (p, temp)
+
+
+def test_staged_vectors_read_in_place_or_through_a_copy(monkeypatch):
+    # The batched samplers' histories, offsets and seeds are staged in
+    # pinned host memory and read in place through its device address; where
+    # the runtime reports none, one copy takes them up. Both give the same
+    # tokens, call after call (the ring's slots are reused after their
+    # events).
+    from fusedtok_amd import _sampling_args as sargs
+    lib = ft._fusedtok
+    pinned = torch.empty(64, dtype=torch.int64, pin_memory=True)
+    addr = lib.host_device_address(pinned.data_ptr())
+    assert addr != 0
+    assert lib.host_device_address(pinned.data_ptr() + 8) == addr + 8
+    assert lib.host_device_address(torch.empty(8, device=DEV).data_ptr()) == 0
+    pageable = np.zeros(64, np.int64)
+    assert lib.host_device_address(pageable.ctypes.data) == 0
+
+    rng = np.random.default_rng(77)
+    rows, n = 12, 50000
+    logits = (rng.standard_normal((rows, n)) * 2).astype(np.float32)
+    lt = t(logits)
+    seeds = list(range(40, 40 + rows))
+    hist = [rng.integers(0, n, size=int(rng.integers(0, 50))).tolist() for _ in range(rows)]
+    first = ft.decode_step_batched(lt, hist, 1.2, p=0.9, temperature=0.8, seeds=seeds).tolist()
+    first_s = ft.sample_topp_batched(lt, 0.9, temperature=0.8, seeds=seeds).tolist()
+    for _ in range(9):  # more calls than ring slots
+        assert ft.decode_step_batched(lt, hist, 1.2, p=0.9, temperature=0.8,
+                                      seeds=seeds, device_out=True).tolist() == first
+    for r in range(rows):
+        assert _agree(first[r], logits[r], 0.9, 0.8, seeds[r], np.array(hist[r], np.int64), 1.2)
+    monkeypatch.setattr(sargs, "_RING", sargs._PinnedRing())
+    monkeypatch.setattr(lib, "host_device_address", lambda ptr: 0)
+    for _ in range(6):
+        assert ft.decode_step_batched(lt, hist, 1.2, p=0.9, temperature=0.8,
+                                      seeds=seeds).tolist() == first
+        assert ft.sample_topp_batched(lt, 0.9, temperature=0.8, seeds=seeds).tolist() == first_s
