@@ -74,39 +74,38 @@ struct SampleRow {
 };
 
 // Visit tokens [lo, hi) of a row (lo a multiple of 4) as f(i, v_i): 16-byte
-// loads, four in flight per thread (the rows are read several times; one
+// loads, U in flight per thread (the rows are read several times; one
 // dependent 4-byte load per thread per step left each pass latency-bound).
-template <int NT, typename F>
+// The order of the f calls is not fixed: every caller's result is
+// independent of it (maxima, integer sums, candidates resolved by key).
+template <int NT, int U = 4, typename F>
 __device__ __forceinline__ void slice_scan(const SampleRow& row, int lo, int hi, F&& f) {
     const float* x = row.x;
     const int tid = threadIdx.x;
     int done = lo;
     if (((uintptr_t)(x + lo) & 15) == 0) {
-        const int n4 = hi >> 2;
+        const int c0 = lo >> 2, n4 = hi >> 2;
         const float4* x4 = reinterpret_cast<const float4*>(x);
-        int c = (lo >> 2) + tid;
-        for (; c + 3 * NT < n4; c += 4 * NT) {
-            float4 q[4];
+        // batches of U * NT vectors: a thread's U loads are issued together
+        // (indices past the end clamped to the last vector and not used), so
+        // each batch costs one memory round trip
+        for (int base = c0; base < n4; base += U * NT) {
+            float4 q[U];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) q[u] = x4[c + u * NT];
+            for (int u = 0; u < U; ++u) q[u] = x4[min(base + u * NT + tid, n4 - 1)];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int i = 4 * (c + u * NT);
-                f(i, row.val_of(i, q[u].x));
-                f(i + 1, row.val_of(i + 1, q[u].y));
-                f(i + 2, row.val_of(i + 2, q[u].z));
-                f(i + 3, row.val_of(i + 3, q[u].w));
+            for (int u = 0; u < U; ++u) {
+                const int c = base + u * NT + tid;
+                if (c < n4) {
+                    const int i = 4 * c;
+                    f(i, row.val_of(i, q[u].x));
+                    f(i + 1, row.val_of(i + 1, q[u].y));
+                    f(i + 2, row.val_of(i + 2, q[u].z));
+                    f(i + 3, row.val_of(i + 3, q[u].w));
+                }
             }
         }
-        for (; c < n4; c += NT) {
-            const float4 q = x4[c];
-            const int i = 4 * c;
-            f(i, row.val_of(i, q.x));
-            f(i + 1, row.val_of(i + 1, q.y));
-            f(i + 2, row.val_of(i + 2, q.z));
-            f(i + 3, row.val_of(i + 3, q.w));
-        }
-        done = 4 * n4;
+        done = max(lo, 4 * n4);
     }
     for (int i = done + tid; i < hi; i += NT) f(i, row.val_of(i, x[i]));
 }
@@ -532,6 +531,8 @@ __global__ __launch_bounds__(kSmpNT) void sample_topp_rows(
 constexpr int kSliceNT = 256;
 constexpr int kMinSlice = 8192;    // tokens per slice at least
 constexpr int kSliceCap = 1024;    // gathered candidates per slice
+constexpr int kSliceLoads = 16;    // 16-byte loads in flight per thread: a
+                                   // 16k-token slice in one round trip
 // LDS bitmap words of one slice: the sliced path runs with S >= 2, so a
 // slice holds at most ceil(n / 2) + 31 tokens, n <= kMaxBitmapVocab
 constexpr int kSliceWords = (kMaxBitmapVocab / 2 + 32) / 32 + 1;
@@ -611,7 +612,7 @@ __global__ __launch_bounds__(kSliceNT) void smp_slice_max(SliceArgs a) {
         row.bit0 = w0 * 32;
     }
     float vmax = -INFINITY;
-    slice_scan<kSliceNT>(row, lo, hi, [&](int, float v) { vmax = fmaxf(vmax, v); });
+    slice_scan<kSliceNT, kSliceLoads>(row, lo, hi, [&](int, float v) { vmax = fmaxf(vmax, v); });
     vmax = block_max<kSliceNT>(vmax, red);
     if (threadIdx.x == 0) a.smax[blockIdx.x] = vmax;
 }
@@ -631,7 +632,7 @@ __global__ __launch_bounds__(kSliceNT) void smp_slice_hist(SliceArgs a) {
     const int lo = min(a.n, s * a.slen), hi = min(a.n, lo + a.slen);
     for (int b = threadIdx.x; b < kDistBins; b += kSliceNT) hm[b] = 0;
     const SampleRow row = slice_row_lds(a, r, lo, hi, lbits);  // (synchronises)
-    slice_scan<kSliceNT>(row, lo, hi, [&](int, float v) {
+    slice_scan<kSliceNT, kSliceLoads>(row, lo, hi, [&](int, float v) {
         const u64 q = mass_fx(v, vmax);
         if (q) atomicAdd(&hm[dist_bin(v, vmax)], q);
     });
@@ -701,7 +702,7 @@ __global__ __launch_bounds__(kSliceNT) void smp_gather(SliceArgs a) {
     const int lane = threadIdx.x & 63;
     if (threadIdx.x == 0) lcount = 0;
     const SampleRow row = slice_row_lds(a, r, lo, hi, lbits);  // (synchronises)
-    slice_scan<kSliceNT>(row, lo, hi, [&](int i, float v) {
+    slice_scan<kSliceNT, kSliceLoads>(row, lo, hi, [&](int i, float v) {
         const int b = dist_bin(v, pl.vmax);
         const bool cand = b == pl.b1 || (b >= pl.c_lo && b <= pl.c_hi);
         // one reservation per wave: the lowest candidate lane adds the
