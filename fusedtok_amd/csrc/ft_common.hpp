@@ -267,11 +267,14 @@ __device__ __forceinline__ float wave_max(float v) {
 // issue order, so no barrier instruction is needed; the wavefront-scope
 // release/acquire pair and the wave barrier tell the compiler that LDS
 // accesses may not move across this point, which per-lane alias analysis
-// alone would allow when it can prove one lane's addresses distinct.
+// alone would allow when it can prove one lane's addresses distinct. The
+// fences name the local address space only: global loads (a kernel's
+// prefetches) stay free to move across (decode attention, config 3: 1%
+// faster than fences over every address space).
 __device__ __forceinline__ void wave_lds_order() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 }
 
 // Block-wide reductions for blockDim.x == NT (multiple of 64). `red` is
