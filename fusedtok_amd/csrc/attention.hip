@@ -359,7 +359,10 @@ __device__ __forceinline__ long long stream_seg_len(long long total, int nseg, i
     return s < min_seg ? (long long)min_seg : s;
 }
 
-template <typename T, int MODE>
+// AMAX: also write max |stored out| per (sequence, head) for the fused
+// quantize (a compile-time switch: a run-time test of the pointer made the
+// plain decode 3% slower, config 3: 396.9 against 384.7 us on one box).
+template <typename T, int MODE, bool AMAX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_decode_stream(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
@@ -642,7 +645,7 @@ void attn_decode_stream(
                 const float inv = 1.0f / lsum;
                 const float4 ov = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
                 St<T>::st4(orow + (size_t)hh * D + 4 * d4, ov);
-                if (amax) {
+                if constexpr (AMAX) {
                     // max |stored value| of this head: its D / 4 = 32 chunks
                     // sit in 32 consecutive lanes (a half wave)
                     float m = stored_absmax4<T>(ov);
@@ -671,7 +674,7 @@ void attn_decode_stream(
 // Lanes split into 2 groups of 32 (one float4 column of D = 128 each) that
 // walk alternate pieces; the groups are summed with one xor shuffle.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, bool AMAX>
 __global__ __launch_bounds__(64) void attn_combine_stream(
     const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
     const long long* __restrict__ pref, T* __restrict__ out, float* __restrict__ amax,
@@ -685,7 +688,7 @@ __global__ __launch_bounds__(64) void attn_combine_stream(
     const int len = (int)(pref[b + 1] - pref[b]);
     if (len == 0) {
         if (lane < D / 4) St<T>::st4(o + 4 * lane, make_float4(0.f, 0.f, 0.f, 0.f));
-        if (amax && lane == 0) amax[blockIdx.x] = 0.0f;
+        if (AMAX && lane == 0) amax[blockIdx.x] = 0.0f;
         return;
     }
     const long long S = stream_seg_len(pref[batch] * hkv, nseg, min_seg);
@@ -719,7 +722,7 @@ __global__ __launch_bounds__(64) void attn_combine_stream(
     const float inv = 1.0f / lsum;
     const float4 ov = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
     St<T>::st4(o + 4 * d4, ov);
-    if (amax) {
+    if constexpr (AMAX) {
         float m = stored_absmax4<T>(ov);
 #pragma unroll
         for (int o2 = 16; o2 > 0; o2 >>= 1) m = fmaxf(m, __shfl_xor(m, o2, 64));
@@ -839,24 +842,43 @@ bool mfma_eligible(const T* q, const T* k, const T* v, int group, int dim) {
 
 // attn_decode_stream in the row mode of the layout (paged with a power-of-2
 // page, paged with any page, contiguous).
+template <typename T, bool AMAX>
+void launch_stream_t(bool paged, int page_shift, int nseg, hipStream_t s, const T* q,
+                     const T* k, const T* v, const int* table, const int* lens, float* ws_ml,
+                     float* ws_acc, long long* pref, T* out, float* amax, int batch, int hq,
+                     int hkv, int group, int rows_or_page, int tbl_width, int span,
+                     float scale_log2, int min_seg) {
+    if (paged && page_shift >= 0)
+        attn_decode_stream<T, kRowsPagedPow2, AMAX><<<(unsigned)nseg, 256, 0, s>>>(
+            q, k, v, table, lens, ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group,
+            rows_or_page, page_shift, tbl_width, span, scale_log2, min_seg);
+    else if (paged)
+        attn_decode_stream<T, kRowsPagedDiv, AMAX><<<(unsigned)nseg, 256, 0, s>>>(
+            q, k, v, table, lens, ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group,
+            rows_or_page, -1, tbl_width, span, scale_log2, min_seg);
+    else
+        attn_decode_stream<T, kRowsContig, AMAX><<<(unsigned)nseg, 256, 0, s>>>(
+            q, k, v, nullptr, lens, ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group,
+            rows_or_page, -1, 0, span, scale_log2, min_seg);
+}
+
+// attn_decode_stream in the row mode of the layout (paged with a power-of-2
+// page, paged with any page, contiguous), with the per-head maxima when
+// amax is given
 template <typename T>
 void launch_stream(bool paged, int page_shift, int nseg, hipStream_t s, const T* q,
                    const T* k, const T* v, const int* table, const int* lens, float* ws_ml,
                    float* ws_acc, long long* pref, T* out, float* amax, int batch, int hq,
                    int hkv, int group, int rows_or_page, int tbl_width, int span,
                    float scale_log2, int min_seg) {
-    if (paged && page_shift >= 0)
-        attn_decode_stream<T, kRowsPagedPow2><<<(unsigned)nseg, 256, 0, s>>>(
-            q, k, v, table, lens, ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group,
-            rows_or_page, page_shift, tbl_width, span, scale_log2, min_seg);
-    else if (paged)
-        attn_decode_stream<T, kRowsPagedDiv><<<(unsigned)nseg, 256, 0, s>>>(
-            q, k, v, table, lens, ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group,
-            rows_or_page, -1, tbl_width, span, scale_log2, min_seg);
+    if (amax)
+        launch_stream_t<T, true>(paged, page_shift, nseg, s, q, k, v, table, lens, ws_ml,
+                                 ws_acc, pref, out, amax, batch, hq, hkv, group, rows_or_page,
+                                 tbl_width, span, scale_log2, min_seg);
     else
-        attn_decode_stream<T, kRowsContig><<<(unsigned)nseg, 256, 0, s>>>(
-            q, k, v, nullptr, lens, ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group,
-            rows_or_page, -1, 0, span, scale_log2, min_seg);
+        launch_stream_t<T, false>(paged, page_shift, nseg, s, q, k, v, table, lens, ws_ml,
+                                  ws_acc, pref, out, nullptr, batch, hq, hkv, group,
+                                  rows_or_page, tbl_width, span, scale_log2, min_seg);
 }
 
 // Device workspace of one decode call (split partials and the length
@@ -943,8 +965,12 @@ bool attention_run(const T* q, const T* k, const T* v, const int* table,
                              pref, out, amax, batch, hq, hkv, group, rows_or_page, tbl_width,
                              (int)span, scale_log2, min_seg);
             launch_check("attention decode kernel launch");
-            attn_combine_stream<T><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
-                ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group, nseg, min_seg);
+            if (amax)
+                attn_combine_stream<T, true><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
+                    ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group, nseg, min_seg);
+            else
+                attn_combine_stream<T, false><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
+                    ws_ml, ws_acc, pref, out, nullptr, batch, hq, hkv, group, nseg, min_seg);
             launch_check("attention combine kernel launch");
             return true;  // the stream kernels wrote amax when asked
         }
