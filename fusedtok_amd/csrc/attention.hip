@@ -359,18 +359,15 @@ __device__ __forceinline__ long long stream_seg_len(long long total, int nseg, i
     return s < min_seg ? (long long)min_seg : s;
 }
 
-// AMAX: also write max |stored out| per (sequence, head) for the fused
-// quantize (a compile-time switch: a run-time test of the pointer made the
-// plain decode 3% slower, config 3: 396.9 against 384.7 us on one box).
-template <typename T, int MODE, bool AMAX>
+template <typename T, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_decode_stream(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int* __restrict__ table, const int* __restrict__ lens,
     float* __restrict__ ws_ml, float* __restrict__ ws_acc,
-    long long* __restrict__ pref_out, T* __restrict__ out, float* __restrict__ amax,
-    int batch, int hq, int hkv, int group, int rows_or_page, int page_shift, int tbl_width,
-    int span, float scale_log2, int min_seg) {
+    long long* __restrict__ pref_out, T* __restrict__ out, int batch, int hq, int hkv,
+    int group, int rows_or_page, int page_shift, int tbl_width, int span, float scale_log2,
+    int min_seg) {
     using M = Mfma<T>;
     using V8 = typename M::v8;
     constexpr int D = kMfmaDim;
@@ -643,16 +640,8 @@ void attn_decode_stream(
             }
             if (whole) {
                 const float inv = 1.0f / lsum;
-                const float4 ov = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
-                St<T>::st4(orow + (size_t)hh * D + 4 * d4, ov);
-                if constexpr (AMAX) {
-                    // max |stored value| of this head: its D / 4 = 32 chunks
-                    // sit in 32 consecutive lanes (a half wave)
-                    float m = stored_absmax4<T>(ov);
-#pragma unroll
-                    for (int o2 = 16; o2 > 0; o2 >>= 1) m = fmaxf(m, __shfl_xor(m, o2, 64));
-                    if (d4 == 0) amax[(size_t)b * hq + (size_t)kv * group + hh] = m;
-                }
+                St<T>::st4(orow + (size_t)hh * D + 4 * d4,
+                           make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv));
             } else {
                 *reinterpret_cast<float4*>(ws_acc + (slot0 + hh) * D + 4 * d4) = o;
                 if (d4 == 0) {
@@ -694,7 +683,19 @@ __global__ __launch_bounds__(64) void attn_combine_stream(
     const long long S = stream_seg_len(pref[batch] * hkv, nseg, min_seg);
     const long long start = pref[b] * hkv + (long long)kv * len;
     const int s_lo = (int)(start / S), s_hi = (int)((start + len - 1) / S);
-    if (s_lo == s_hi) return;  // stored whole by the decode kernel
+    if (s_lo == s_hi) {
+        // stored whole by the decode kernel: the maximum from the stored
+        // values, read back here. Computed in the decode kernel's store
+        // phase instead, it slowed that kernel's main loop (batch 64,
+        // context 8192: attention + quantize 357.4 against 348.1 us here).
+        if constexpr (AMAX) {
+            float m = stored_absmax4<T>(St<T>::ld4(o + 4 * (lane & 31)));
+#pragma unroll
+            for (int o2 = 16; o2 > 0; o2 >>= 1) m = fmaxf(m, __shfl_xor(m, o2, 64));
+            if (lane == 0) amax[blockIdx.x] = m;
+        }
+        return;
+    }
     const int row = b * hkv + kv;
     const int np = s_hi - s_lo + 1;
     auto slot = [&](int i) { return ((size_t)s_lo + i + row) * group + gi; };
@@ -842,43 +843,24 @@ bool mfma_eligible(const T* q, const T* k, const T* v, int group, int dim) {
 
 // attn_decode_stream in the row mode of the layout (paged with a power-of-2
 // page, paged with any page, contiguous).
-template <typename T, bool AMAX>
-void launch_stream_t(bool paged, int page_shift, int nseg, hipStream_t s, const T* q,
-                     const T* k, const T* v, const int* table, const int* lens, float* ws_ml,
-                     float* ws_acc, long long* pref, T* out, float* amax, int batch, int hq,
-                     int hkv, int group, int rows_or_page, int tbl_width, int span,
-                     float scale_log2, int min_seg) {
-    if (paged && page_shift >= 0)
-        attn_decode_stream<T, kRowsPagedPow2, AMAX><<<(unsigned)nseg, 256, 0, s>>>(
-            q, k, v, table, lens, ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group,
-            rows_or_page, page_shift, tbl_width, span, scale_log2, min_seg);
-    else if (paged)
-        attn_decode_stream<T, kRowsPagedDiv, AMAX><<<(unsigned)nseg, 256, 0, s>>>(
-            q, k, v, table, lens, ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group,
-            rows_or_page, -1, tbl_width, span, scale_log2, min_seg);
-    else
-        attn_decode_stream<T, kRowsContig, AMAX><<<(unsigned)nseg, 256, 0, s>>>(
-            q, k, v, nullptr, lens, ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group,
-            rows_or_page, -1, 0, span, scale_log2, min_seg);
-}
-
-// attn_decode_stream in the row mode of the layout (paged with a power-of-2
-// page, paged with any page, contiguous), with the per-head maxima when
-// amax is given
 template <typename T>
 void launch_stream(bool paged, int page_shift, int nseg, hipStream_t s, const T* q,
                    const T* k, const T* v, const int* table, const int* lens, float* ws_ml,
-                   float* ws_acc, long long* pref, T* out, float* amax, int batch, int hq,
-                   int hkv, int group, int rows_or_page, int tbl_width, int span,
-                   float scale_log2, int min_seg) {
-    if (amax)
-        launch_stream_t<T, true>(paged, page_shift, nseg, s, q, k, v, table, lens, ws_ml,
-                                 ws_acc, pref, out, amax, batch, hq, hkv, group, rows_or_page,
-                                 tbl_width, span, scale_log2, min_seg);
+                   float* ws_acc, long long* pref, T* out, int batch, int hq, int hkv,
+                   int group, int rows_or_page, int tbl_width, int span, float scale_log2,
+                   int min_seg) {
+    if (paged && page_shift >= 0)
+        attn_decode_stream<T, kRowsPagedPow2><<<(unsigned)nseg, 256, 0, s>>>(
+            q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
+            rows_or_page, page_shift, tbl_width, span, scale_log2, min_seg);
+    else if (paged)
+        attn_decode_stream<T, kRowsPagedDiv><<<(unsigned)nseg, 256, 0, s>>>(
+            q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
+            rows_or_page, -1, tbl_width, span, scale_log2, min_seg);
     else
-        launch_stream_t<T, false>(paged, page_shift, nseg, s, q, k, v, table, lens, ws_ml,
-                                  ws_acc, pref, out, nullptr, batch, hq, hkv, group,
-                                  rows_or_page, tbl_width, span, scale_log2, min_seg);
+        attn_decode_stream<T, kRowsContig><<<(unsigned)nseg, 256, 0, s>>>(
+            q, k, v, nullptr, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
+            rows_or_page, -1, 0, span, scale_log2, min_seg);
 }
 
 // Device workspace of one decode call (split partials and the length
@@ -962,7 +944,7 @@ bool attention_run(const T* q, const T* k, const T* v, const int* table,
             float* ws_acc = ws_ml + ml_floats;
             long long* pref = (long long*)(ws_acc + acc_floats);
             launch_stream<T>(paged, page_shift, nseg, s, q, k, v, table, lens, ws_ml, ws_acc,
-                             pref, out, amax, batch, hq, hkv, group, rows_or_page, tbl_width,
+                             pref, out, batch, hq, hkv, group, rows_or_page, tbl_width,
                              (int)span, scale_log2, min_seg);
             launch_check("attention decode kernel launch");
             if (amax)
@@ -972,7 +954,7 @@ bool attention_run(const T* q, const T* k, const T* v, const int* table,
                 attn_combine_stream<T, false><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
                     ws_ml, ws_acc, pref, out, nullptr, batch, hq, hkv, group, nseg, min_seg);
             launch_check("attention combine kernel launch");
-            return true;  // the stream kernels wrote amax when asked
+            return true;  // the combine kernel wrote amax when asked
         }
     }
     const long long target = (long long)dev_info().cu_count * 16;
@@ -1085,9 +1067,10 @@ using ft::f16;
 namespace ft {
 namespace {
 // Paged decode followed by the per-tensor int8 quantize of its output. On
-// the stream kernels' path the decode and combine kernels also write the max
-// |stored output| of every (sequence, q head), so the quantize is one launch
-// over those B * Hq maxima; other paths quantize the output in full.
+// the stream kernels' path the combine kernel also writes the max |stored
+// output| of every (sequence, q head) (split rows from its fold, whole rows
+// read back), so the quantize is one launch over those B * Hq maxima; other
+// paths quantize the output in full.
 template <typename T>
 void attention_paged_quant_run(const T* q, const T* k_pool, const T* v_pool, const int* table,
                                const int* lens, T* out, signed char* codes, float* scale_out,

@@ -444,7 +444,7 @@ int ft_qgemm_swiglu_quant_launch(const signed char* a_q, const float* sa_dev,
  * int8 plus *scale_out (DEVICE float) bit-identical to quantizing that
  * stored out (ft_quantize_int8_launch for float32, its bf16 / fp16 form
  * otherwise) -- the decode layer's o_proj input. On the split-stream
- * attention path the attention kernels also write the max |out| of each
+ * attention path the combine kernel also writes the max |out| of each
  * (sequence, q head) and the quantize is one launch over those maxima. */
 int ft_attention_decode_paged_quant_launch(const void* q, const void* k_pool,
                                            const void* v_pool, const int* table,
