@@ -298,3 +298,29 @@ def test_stack_argument_errors():
     stack.close()
     layers[0].close()
     other.close()
+
+
+def test_stack_max_batch_is_the_smallest_and_empty_batches():
+    # the stack's hand-over buffers hold the smallest max_batch of its
+    # layers; a larger batch is refused before anything runs, an empty
+    # batch returns an empty output
+    dt = torch.bfloat16
+    ws, x, kps, vps, table, lens = make_stack_case(TOY, dt, 2, 51)
+    big = make_layer(TOY, ws[0], dt, max_batch=8)
+    small = make_layer(TOY, ws[1], dt, max_batch=TOY["b"])
+    stack = ft.DecodeStack([big, small])
+    assert stack.max_batch == TOY["b"]
+    kq, vq = [t.clone() for t in kps], [t.clone() for t in vps]
+    y1 = big(x, kq[0], vq[0], table, lens)
+    y_ref = small(y1, kq[1], vq[1], table, lens).clone()
+    y = stack(x, kps, vps, table, lens)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref)
+    x5 = torch.cat([x, x[:1]])
+    with pytest.raises(ValueError, match="max_batch"):
+        stack(x5, kps, vps, torch.cat([table, table[:1]]), torch.cat([lens, lens[:1]]))
+    y0 = stack(x[:0], kps, vps, table[:0], lens[:0])
+    assert y0.shape == (0, TOY["hidden"])
+    stack.close()
+    big.close()
+    small.close()
