@@ -510,10 +510,15 @@ __global__ __launch_bounds__(kSmpNT) void sample_topp_rows(
 // over the logits; the per-row steps run on one workgroup per row. Same
 // arithmetic and order as sample_topp_rows (integer masses: every merge is
 // exact), so the tokens are identical.
-//   1 smp_slice_max    slice maxima; the slice's penalty bits to global
-//   2 smp_slice_hist   slice distance histograms (mass, count) from the row
-//                      maximum
-//   3 smp_plan         per row: merged histogram, total, the nucleus bin b1
+//   1 smp_slice_max    slice maxima; the slice's penalty bits to global;
+//                      slice s clears its share of the row's histogram
+//   2 smp_slice_hist   slice distance histograms from the row maximum, in
+//                      LDS, then added into the row's histogram (integer
+//                      atomics, so the sum does not depend on their order;
+//                      writing S slice histograms for smp_plan to merge
+//                      made the merge read S x 16 KB per row from one
+//                      workgroup, ~15 us at 64 x 128k)
+//   3 smp_plan         per row: total, the nucleus bin b1
 //                      and the range [c_lo, c_hi] of bins the draw can
 //                      cross (the nucleus mass lies in b1's prefix range and
 //                      the draw threshold is monotone in it)
@@ -552,8 +557,7 @@ struct SliceArgs {
     int m_single;
     unsigned* bits;            // rows x words
     float* smax;               // rows x S
-    u64* hmass;                // rows x S x kDistBins
-    u64* mhist;                // rows x kDistBins
+    u64* mhist;                // rows x kDistBins: the row's merged histogram
     SmpPlan* plan;             // rows
     int* gcnt;                 // rows x S
     u64* gkey;                 // rows x S x kSliceCap
@@ -561,6 +565,7 @@ struct SliceArgs {
     float p;
     const u64* seeds;
     u64 seed0;
+    u64* seedv;                // rows: each row's seed, copied by smp_slice_max
     long long* out;
 };
 
@@ -593,6 +598,12 @@ __global__ __launch_bounds__(kSliceNT) void smp_slice_max(SliceArgs a) {
     __shared__ float red[kSliceNT / 64];
     const int r = blockIdx.x / a.S, s = blockIdx.x - r * a.S;
     const int lo = min(a.n, s * a.slen), hi = min(a.n, lo + a.slen);
+    // The row's seed, copied to device memory for smp_plan and smp_finish:
+    // the seeds (like the histories) may sit in host memory, and this read
+    // overlaps the offsets' round trip here instead of adding one there.
+    const bool seed_lane = s == 0 && threadIdx.x == 0;
+    u64 seed = 0;
+    if (seed_lane) seed = a.seeds ? a.seeds[r] : a.seed0;
     SampleRow row{a.x + (size_t)r * a.n, a.n, a.inv_t, a.pen, nullptr, 0};
     if (a.ids) {
         // this slice's words of the row's bitmap (slices own whole words)
@@ -611,10 +622,16 @@ __global__ __launch_bounds__(kSliceNT) void smp_slice_max(SliceArgs a) {
         row.bits = lbits;
         row.bit0 = w0 * 32;
     }
+    // this slice's share of the row histogram smp_slice_hist adds into
+    u64* mh = a.mhist + (size_t)r * kDistBins;
+    for (int b = s * kDistBins / a.S + (int)threadIdx.x; b < (s + 1) * kDistBins / a.S;
+         b += kSliceNT)
+        mh[b] = 0;
     float vmax = -INFINITY;
     slice_scan<kSliceNT, kSliceLoads>(row, lo, hi, [&](int, float v) { vmax = fmaxf(vmax, v); });
     vmax = block_max<kSliceNT>(vmax, red);
     if (threadIdx.x == 0) a.smax[blockIdx.x] = vmax;
+    if (seed_lane) a.seedv[r] = seed;
 }
 
 __device__ __forceinline__ float row_max_of(const SliceArgs& a, int r) {
@@ -637,41 +654,53 @@ __global__ __launch_bounds__(kSliceNT) void smp_slice_hist(SliceArgs a) {
         if (q) atomicAdd(&hm[dist_bin(v, vmax)], q);
     });
     __syncthreads();
-    u64* gm = a.hmass + (size_t)blockIdx.x * kDistBins;
-    for (int b = threadIdx.x; b < kDistBins; b += kSliceNT) gm[b] = hm[b];
+    u64* mh = a.mhist + (size_t)r * kDistBins;
+    for (int b = threadIdx.x; b < kDistBins; b += kSliceNT)
+        if (hm[b]) atomicAdd(mh + b, hm[b]);
 }
 
 __global__ __launch_bounds__(kSmpNT) void smp_plan(SliceArgs a) {
     __shared__ SmpShared sh;
     const int r = blockIdx.x, tid = threadIdx.x;
-    // the seed first: it may sit in host memory, and its round trip then
-    // overlaps the histogram merge below
-    const u64 seed = a.seeds ? a.seeds[r] : a.seed0;
+    const u64 seed = a.seedv[r];
     const float vmax = row_max_of(a, r);
     if (!(vmax > -INFINITY)) {
         if (tid == 0) a.plan[r] = SmpPlan{0ULL, vmax, 0, 0, 0};
         return;
     }
-    for (int b = tid; b < kDistBins; b += kSmpNT) {
-        u64 m = 0;
-        for (int s = 0; s < a.S; ++s) m += a.hmass[((size_t)r * a.S + s) * kDistBins + b];
-        sh.h_mass[b] = m;
-        a.mhist[(size_t)r * kDistBins + b] = m;
-    }
+    // one scan of the histogram serves the three bin queries below: thread
+    // t owns bins 2t and 2t + 1, as in find_bin
+    static_assert(kDistBins == 2 * kSmpNT, "two bins per thread");
+    const u64* mh = a.mhist + (size_t)r * kDistBins;
+    const u64 m0 = mh[2 * tid], m1 = mh[2 * tid + 1];
+    sh.h_mass[2 * tid] = m0;
+    sh.h_mass[2 * tid + 1] = m1;
+    const u64 incl = block_scan(m0 + m1, sh.wsum);  // (its barriers order the stores)
+    const u64 excl = incl - m0 - m1;
+    if (tid == kSmpNT - 1) sh.r_mass = incl;
     __syncthreads();
-    u64 total;
-    {
-        const u64 incl = block_scan(sh.h_mass[2 * tid] + sh.h_mass[2 * tid + 1], sh.wsum);
-        if (tid == kSmpNT - 1) sh.r_mass = incl;
+    const u64 total = sh.r_mass;
+    // find_bin's result from the scan above: with 1 <= T <= total exactly
+    // one thread's pair holds the crossing; total == 0 (no token with mass,
+    // e.g. a +inf logit) gives find_bin's defaults, bin 0 and nothing above
+    auto cross = [&](u64 T) {
+        if (total == 0) {  // uniform: every thread read the same total
+            if (tid == 0) {
+                sh.r_bin = 0;
+                sh.r_above = 0;
+            }
+        } else if (excl < T && T <= incl) {
+            const bool first = excl + m0 >= T;
+            sh.r_bin = first ? 2 * tid : 2 * tid + 1;
+            sh.r_above = first ? excl : excl + m0;
+        }
         __syncthreads();
-        total = sh.r_mass;
-        __syncthreads();
-    }
+    };
     // the nucleus bin, as smp_finish will find it
     const double tc = ceil((double)a.p * (double)total);
     u64 T1 = tc < 1.0 ? 1ULL : (u64)tc;
     if (T1 > total) T1 = total;
-    find_bin(T1, sh);
+    cross(T1);
     const int b1 = min(max(sh.r_bin, 0), kDistBins - 1);
     const u64 after_b1 = sh.r_above + sh.h_mass[b1];  // nucleus mass is in [T1, after_b1]
     __syncthreads();
@@ -682,10 +711,10 @@ __global__ __launch_bounds__(kSmpNT) void smp_plan(SliceArgs a) {
         u64 T = td < 1.0 ? 1ULL : (u64)td;
         return T > nucleus ? nucleus : T;
     };
-    find_bin(draw_t(T1), sh);
+    cross(draw_t(T1));
     const int c_lo = min(max(sh.r_bin, 0), kDistBins - 1);
     __syncthreads();
-    find_bin(draw_t(after_b1), sh);
+    cross(draw_t(after_b1));
     const int c_hi = min(max(sh.r_bin, 0), kDistBins - 1);
     __syncthreads();
     if (tid == 0) a.plan[r] = SmpPlan{total, vmax, b1, c_lo, c_hi};
@@ -733,7 +762,7 @@ __global__ __launch_bounds__(kSliceNT) void smp_gather(SliceArgs a) {
 __global__ __launch_bounds__(kSmpNT) void smp_finish(SliceArgs a) {
     __shared__ SmpShared sh;
     const int r = blockIdx.x, tid = threadIdx.x;
-    const u64 seed = a.seeds ? a.seeds[r] : a.seed0;  // first, as in smp_plan
+    const u64 seed = a.seedv[r];
     const SmpPlan pl = a.plan[r];
     if (!(pl.vmax > -INFINITY)) {
         // every value -inf (or NaN): as sample_topp_rows
@@ -992,14 +1021,15 @@ void topp_launch(const float* x, int rows, int n, float p, float t, float pen,
         return at;
     };
     const size_t o_bits = take(R * a.words * 4), o_smax = take(R * S * 4),
-                 o_hm = take(R * S * kDistBins * 8), o_mh = take(R * kDistBins * 8), o_plan = take(R * sizeof(SmpPlan)),
+                 o_mh = take(R * kDistBins * 8), o_plan = take(R * sizeof(SmpPlan)),
+                 o_seed = take(R * 8),
                  o_gn = take(R * S * 4), o_gk = take(R * S * kSliceCap * 8),
                  o_gq = take(R * S * kSliceCap * 8);
     char* ws = (char*)scratch(Scratch::Sampling, off, s);
     a.bits = (unsigned*)(ws + o_bits);
     a.smax = (float*)(ws + o_smax);
-    a.hmass = (u64*)(ws + o_hm);
     a.mhist = (u64*)(ws + o_mh);
+    a.seedv = (u64*)(ws + o_seed);
     a.plan = (SmpPlan*)(ws + o_plan);
     a.gcnt = (int*)(ws + o_gn);
     a.gkey = (u64*)(ws + o_gk);
