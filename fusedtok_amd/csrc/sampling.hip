@@ -246,12 +246,15 @@ __device__ void select_prefix(const SampleRow& row, float vmax, u64 T, SmpShared
                 int sg = 0;
                 while (sh.seg_off[sg + 1] <= j) ++sg;
                 const size_t at = (size_t)sg * pre.cap + (j - sh.seg_off[sg]);
+                // the mass is loaded with the key, not after the bin test:
+                // one memory round trip per query instead of two
                 const u64 k = pre.key[at];
+                const u64 q = pre.q[at];
                 if (dist_bin(key_value(k), vmax) == bin) {
                     const int slot = atomicAdd(&sh.g_n, 1);
                     if (slot < kGather) {
                         sh.g_key[slot] = k;
-                        sh.g_q[slot] = pre.q[at];
+                        sh.g_q[slot] = q;
                     }
                 }
             }
