@@ -113,6 +113,8 @@ enum class Tune : int {
                            // fails as an allocation failure would
     PrefillPrepass,        // FT_PREFILL_PREPASS: bf16 V to fp16 in a pre-pass
                            // (0 never: in the kernel; 1 large calls; 2 always)
+    GridSync,              // FT_GRID_SYNC: 1 = never fold a per-tensor maximum
+                           // inside one launch (grid_max); the two-launch forms
     kCount
 };
 // The switch's value, or `dflt` when it is neither in the environment nor
@@ -129,12 +131,31 @@ enum class Scratch : int {
     GemmPartials = 2,
     Sampling = 3,
     PrefillV = 4,
-    kCount = 5
+    GridSync = 5,  // grid_max state (gridmax_state)
+    kCount = 6
 };
 void* scratch(Scratch which, size_t bytes, hipStream_t s);
 // Same, but memory is zero when first allocated (or re-allocated); kernels
 // that use it must leave it zero when they finish (e.g. arrival counters).
 void* scratch_zeroed(Scratch which, size_t bytes, hipStream_t s);
+
+// ---------------------------------------------------------------------------
+// Grid-wide maximum inside one launch (grid_max below). The state is one
+// 64-bit word (generation << 32 | arrivals) and one 32-bit slot per
+// workgroup, zeroed when allocated; every launch leaves the arrivals at 0.
+// Launches that use it are ordered on one stream: calls that overlap on one
+// GPU race, as with the library's other scratch.
+struct GridMax {
+    unsigned long long* word;
+    unsigned* slots;
+};
+// The state for up to `nwg` workgroups on the current device (grown outside
+// a capture only, like scratch()). runtime.hip.
+GridMax gridmax_state(int nwg, hipStream_t s);
+// True when `nwg` workgroups of `kernel` (`threads` each, no dynamic LDS)
+// can all be resident at once on the current device, and FT_GRID_SYNC does
+// not forbid the in-launch maximum. runtime.hip.
+bool grid_resident(const void* kernel, int nwg, int threads);
 
 // Per-tensor int8 quantize of x[0, n) (T = float, bf16, f16) when its max |x|
 // is already known as the max of nparts partial maxima (written by the
@@ -303,6 +324,53 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     for (int i = 1; i < NT / 64; ++i) t = fmaxf(t, red[i]);
     __syncthreads();
     return t;
+}
+
+// Maximum over every workgroup of the launch of each workgroup's `m` (>= 0,
+// the same in all NT threads of the workgroup), returned to every thread.
+// All workgroups must be resident at once (grid_resident). Values cross
+// workgroups only through device-scope atomics, which every XCD performs at
+// one coherence point, so no release fence (an L2 writeback per workgroup,
+// ~0.2 us each, serialised per XCD) is needed:
+//   1. exchange m into this workgroup's slot and wait until it is performed;
+//   2. arrive (add 1 to the word); the last arriver advances the generation
+//      and clears the arrivals with one add, the others poll the word until
+//      the generation moves (bounded: after kGridSpin polls, ~1 s, a
+//      workgroup goes on with the slots as they are, so a misuse gives wrong
+//      values and never a hang);
+//   3. every slot now holds this launch's value: read them all.
+constexpr unsigned kGridSpin = 1u << 20;
+
+template <int NT>
+__device__ __forceinline__ float grid_max(const GridMax& g, float m, float* red) {
+    const unsigned nwg = gridDim.x * gridDim.y * gridDim.z;
+    const unsigned wg = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    if (threadIdx.x == 0) {
+        const unsigned prev = __hip_atomic_exchange(g.slots + wg, __float_as_uint(m),
+                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // the exchange has returned (so it was performed) before the arrival
+        asm volatile("s_waitcnt vmcnt(0)" : : "v"(prev) : "memory");
+        const unsigned long long old = __hip_atomic_fetch_add(
+            g.word, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned gen = (unsigned)(old >> 32);
+        if ((unsigned)old + 1u == nwg) {
+            __hip_atomic_fetch_add(g.word, (1ull << 32) - nwg, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            for (unsigned i = 0; i < kGridSpin; ++i) {
+                const unsigned long long cur =
+                    __hip_atomic_load(g.word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((unsigned)(cur >> 32) != gen) break;
+                __builtin_amdgcn_s_sleep(8);
+            }
+        }
+    }
+    __syncthreads();
+    float mx = 0.0f;
+    for (unsigned i = threadIdx.x; i < nwg; i += NT)
+        mx = fmaxf(mx, __uint_as_float(__hip_atomic_load(g.slots + i, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT)));
+    return block_max<NT>(mx, red);
 }
 
 inline unsigned grid_1d(long long n, int per_block, int cap = 1 << 20) {

@@ -67,32 +67,56 @@ __device__ __forceinline__ float4 rms_add4(float4 xv, float4 rv) {
 
 constexpr int kRowChunks = 4;  // 4-element chunks per thread held in registers
 
-// One workgroup per row: sum of squares -> inv, then the row's max |y|. A row
-// of up to 4096 columns stays in registers between the two passes.
-// FK > 0: x is the output of a K-split GEMM, folded here from its partials
-// (fold width FK, kfold.hpp) and stored into x_out, as the GEMM would have.
-template <typename T, bool RES, int FK>
+// The input rows of the row passes below. FK > 0: x is the output of a
+// K-split GEMM, folded here from its partials (fold width FK, kfold.hpp);
+// FRES: plus the fold's residual (fold.res, T), rounded again, as the
+// GEMM's consumer in a decode layer adds its residual stream.
+template <typename T, int FK, bool FRES>
+struct RowIn {
+    const T* x;
+    const KFold& fold;
+    float sa;
+    // chunk c (4 elements at row offset base) as stored in T, widened to f32
+    __device__ __forceinline__ float4 load4(size_t base, int c) const {
+        if constexpr (FK > 0) {
+            const int4 a = kfold_sum4<FK>(fold, base + 4 * c);
+            float4 v = make_float4(kfold_value<T>(a.x, kfold_scale(fold, sa, 4 * c)),
+                                   kfold_value<T>(a.y, kfold_scale(fold, sa, 4 * c + 1)),
+                                   kfold_value<T>(a.z, kfold_scale(fold, sa, 4 * c + 2)),
+                                   kfold_value<T>(a.w, kfold_scale(fold, sa, 4 * c + 3)));
+            if constexpr (FRES) {
+                const float4 r = St<T>::ld4(static_cast<const T*>(fold.res) + base + 4 * c);
+                v = make_float4(kfold_add_res<T>(v.x, r.x), kfold_add_res<T>(v.y, r.y),
+                                kfold_add_res<T>(v.z, r.z), kfold_add_res<T>(v.w, r.w));
+            }
+            return v;
+        } else {
+            return St<T>::ld4(x + base + 4 * c);
+        }
+    }
+};
+
+// T(v) stored to h (the residual stream x + r of a decode layer)
+template <typename T>
+__device__ __forceinline__ void st4_rounded(T* h, float4 v) {
+    St<T>::st4(h, v);
+}
+
+// One workgroup per row: sum of squares -> inv, then the row's max |y| (the
+// first pass of rmsnorm_quant's two-launch form). A row of up to 4096
+// columns stays in registers between the two passes. FK > 0: the folded x
+// is stored into x_out, as the GEMM would have stored it. HOUT (with RES):
+// h_out receives T(x + r).
+template <typename T, bool RES, int FK, bool FRES, bool HOUT>
 __global__ __launch_bounds__(kFNT) void rmsq_rows(
     const T* __restrict__ x, const T* __restrict__ r, const float* __restrict__ w,
-    RowStat* __restrict__ stat, int cols, float eps, KFold fold, T* __restrict__ x_out) {
+    RowStat* __restrict__ stat, int cols, float eps, KFold fold, T* __restrict__ x_out,
+    T* __restrict__ h_out) {
     __shared__ float red[kFNT / 64];
     const size_t base = (size_t)blockIdx.x * cols;
     const int chunks = cols >> 2;
     constexpr bool FOLD = FK > 0;
-    float sa = 0.0f;
-    if constexpr (FOLD) sa = kfold_sa(fold);
-    // chunk c of the row as stored in T, widened to f32
-    auto load_x4 = [&](int c) -> float4 {
-        if constexpr (FOLD) {
-            const int4 a = kfold_sum4<FK>(fold, base + 4 * c);
-            return make_float4(kfold_value<T>(a.x, kfold_scale(fold, sa, 4 * c)),
-                               kfold_value<T>(a.y, kfold_scale(fold, sa, 4 * c + 1)),
-                               kfold_value<T>(a.z, kfold_scale(fold, sa, 4 * c + 2)),
-                               kfold_value<T>(a.w, kfold_scale(fold, sa, 4 * c + 3)));
-        } else {
-            return St<T>::ld4(x + base + 4 * c);
-        }
-    };
+    const RowIn<T, FK, FRES> in{x, fold, FOLD ? kfold_sa(fold) : 0.0f};
     float m = 0.0f;
     float inv;
     if (chunks <= kFNT * kRowChunks) {
@@ -102,7 +126,7 @@ __global__ __launch_bounds__(kFNT) void rmsq_rows(
 #pragma unroll
         for (int j = 0; j < kRowChunks; ++j) {
             const int c = min((int)threadIdx.x + j * kFNT, chunks - 1);
-            v[j] = load_x4(c);
+            v[j] = in.load4(base, c);
             if constexpr (RES) rv[j] = St<T>::ld4(r + base + 4 * c);
             wc[j] = *reinterpret_cast<const float4*>(w + 4 * c);
         }
@@ -114,6 +138,12 @@ __global__ __launch_bounds__(kFNT) void rmsq_rows(
         }
 #pragma unroll
         for (int j = 0; j < kRowChunks; ++j) v[j] = rms_add4<RES>(v[j], rv[j]);
+        if constexpr (HOUT) {
+#pragma unroll
+            for (int j = 0; j < kRowChunks; ++j)
+                if ((int)threadIdx.x + j * kFNT < chunks)
+                    st4_rounded(h_out + base + 4 * ((int)threadIdx.x + j * kFNT), v[j]);
+        }
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < kRowChunks; ++j) {
@@ -138,9 +168,10 @@ __global__ __launch_bounds__(kFNT) void rmsq_rows(
     } else {
         float acc = 0.0f;
         for (int c = threadIdx.x; c < chunks; c += kFNT) {
-            float4 v = load_x4(c);
+            float4 v = in.load4(base, c);
             if constexpr (FOLD) St<T>::st4(x_out + base + 4 * c, v);
             if constexpr (RES) v = rms_add4<true>(v, St<T>::ld4(r + base + 4 * c));
+            if constexpr (HOUT) st4_rounded(h_out + base + 4 * c, v);
             acc = fmaf(v.x, v.x, acc);
             acc = fmaf(v.y, v.y, acc);
             acc = fmaf(v.z, v.z, acc);
@@ -148,8 +179,11 @@ __global__ __launch_bounds__(kFNT) void rmsq_rows(
         }
         const float total = block_sum<kFNT>(acc, red);
         inv = 1.0f / sqrtf(total / (float)cols + eps);
+        // second pass: the folded rows are read back from x_out (their
+        // stored bits: the same values)
+        const T* xs = FOLD ? x_out : x;
         for (int c = threadIdx.x; c < chunks; c += kFNT) {
-            float4 v = load_x4(c);
+            float4 v = St<T>::ld4(xs + base + 4 * c);
             if constexpr (RES) v = rms_add4<true>(v, St<T>::ld4(r + base + 4 * c));
             const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c);
             m = fmaxf(m, fabsf(v.x * inv * wv.x));
@@ -160,6 +194,88 @@ __global__ __launch_bounds__(kFNT) void rmsq_rows(
     }
     m = block_max<kFNT>(m, red);
     if (threadIdx.x == 0) stat[blockIdx.x] = RowStat{m, inv};
+}
+
+// rmsnorm_quant in one launch: one workgroup per row of at most 4096
+// columns, the register row pass of rmsq_rows, then the tensor's maximum
+// through grid_max (every row's workgroup resident at once), then each
+// workgroup quantizes its row from the same registers. The arithmetic is
+// rmsq_rows' followed by rmsq_quant's, so codes and scale are the same bits
+// as the two launches. x_out (FK > 0) may be null: the folded rows are then
+// not stored.
+template <typename T, bool RES, int FK, bool FRES, bool HOUT>
+__global__ __launch_bounds__(kFNT) void rmsq_grid(
+    const T* __restrict__ x, const T* __restrict__ r, const float* __restrict__ w,
+    int cols, float eps, KFold fold, T* __restrict__ x_out, T* __restrict__ h_out,
+    signed char* __restrict__ q, float* __restrict__ scale_out, GridMax gm) {
+    __shared__ float red[kFNT / 64];
+    const size_t base = (size_t)blockIdx.x * cols;
+    const int chunks = cols >> 2;
+    constexpr bool FOLD = FK > 0;
+    const RowIn<T, FK, FRES> in{x, fold, FOLD ? kfold_sa(fold) : 0.0f};
+    float4 v[kRowChunks], rv[kRowChunks], wc[kRowChunks];
+#pragma unroll
+    for (int j = 0; j < kRowChunks; ++j) {
+        const int c = min((int)threadIdx.x + j * kFNT, chunks - 1);
+        v[j] = in.load4(base, c);
+        if constexpr (RES) rv[j] = St<T>::ld4(r + base + 4 * c);
+        wc[j] = *reinterpret_cast<const float4*>(w + 4 * c);
+    }
+    if constexpr (FOLD) {
+        if (x_out) {
+#pragma unroll
+            for (int j = 0; j < kRowChunks; ++j)
+                if ((int)threadIdx.x + j * kFNT < chunks)
+                    St<T>::st4(x_out + base + 4 * ((int)threadIdx.x + j * kFNT), v[j]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kRowChunks; ++j) v[j] = rms_add4<RES>(v[j], rv[j]);
+    if constexpr (HOUT) {
+#pragma unroll
+        for (int j = 0; j < kRowChunks; ++j)
+            if ((int)threadIdx.x + j * kFNT < chunks)
+                st4_rounded(h_out + base + 4 * ((int)threadIdx.x + j * kFNT), v[j]);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRowChunks; ++j) {
+        if ((int)threadIdx.x + j * kFNT < chunks) {
+            acc = fmaf(v[j].x, v[j].x, acc);
+            acc = fmaf(v[j].y, v[j].y, acc);
+            acc = fmaf(v[j].z, v[j].z, acc);
+            acc = fmaf(v[j].w, v[j].w, acc);
+        }
+    }
+    const float total = block_sum<kFNT>(acc, red);
+    const float inv = 1.0f / sqrtf(total / (float)cols + eps);
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRowChunks; ++j) {
+        if ((int)threadIdx.x + j * kFNT < chunks) {
+            m = fmaxf(m, fabsf(v[j].x * inv * wc[j].x));
+            m = fmaxf(m, fabsf(v[j].y * inv * wc[j].y));
+            m = fmaxf(m, fabsf(v[j].z * inv * wc[j].z));
+            m = fmaxf(m, fabsf(v[j].w * inv * wc[j].w));
+        }
+    }
+    m = block_max<kFNT>(m, red);
+    m = grid_max<kFNT>(gm, m, red);
+    const float scale = make_scale(m);
+    const float inv_s = 1.0f / scale;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+#pragma unroll
+    for (int j = 0; j < kRowChunks; ++j) {
+        const int c = (int)threadIdx.x + j * kFNT;
+        if (c < chunks) {
+            char4 o;
+            o.x = quant1(v[j].x * inv * wc[j].x, inv_s);
+            o.y = quant1(v[j].y * inv * wc[j].y, inv_s);
+            o.z = quant1(v[j].z * inv * wc[j].z, inv_s);
+            o.w = quant1(v[j].w * inv * wc[j].w, inv_s);
+            *reinterpret_cast<char4*>(q + base + 4 * c) = o;
+        }
+    }
 }
 
 // Fold of the row maxima -> scale, then the codes. Each thread's first
@@ -339,47 +455,114 @@ void rmsq_check(const T* x, const float* w, const T* r, const signed char* q,
         inval("rmsnorm_quant: operands must be aligned to 4 elements");
 }
 
-// the row pass (FOLD: folding a K-split GEMM's partials into x_out first),
-// then the fold of the row maxima and the codes
-template <typename T, bool FOLD>
-void rmsq_two_pass(const T* x, const KFold& fold, T* x_out, const float* w, const T* r,
+// What a row pass takes and writes beyond rmsnorm_quant's own operands.
+// fold.ksplit >= 2: x is a K-split GEMM's output still held as its partials
+// (plus fold.res), folded by the row pass, which stores the rows into x_out
+// (required by the two-launch form; the one-launch form skips the store
+// when x_out is null). h_out (with a residual r): T(x + r), the residual
+// stream of a decode layer.
+template <typename T>
+struct RmsqIo {
+    KFold fold;
+    T* x_out = nullptr;
+    T* h_out = nullptr;
+    bool store_x = true;  // false: the one-launch form need not store x_out
+};
+
+// Rows (workgroups) of the one-launch form. From 17 rows: below, the two
+// launches measured as fast or faster (C2 chain, M = 8 / 16, same box:
+// 15.74 / 16.35 us with two launches against 15.80 / 16.60 with one); at
+// C4's 64 rows the two forms measured the same (layer 434.6-438.3 against
+// 437.4-438.7 us): the kernel boundary a graph replay pays costs about the
+// three dependent device-scope atomic round trips of grid_max.
+constexpr int kRmsqGridMinRows = 17;
+constexpr int kRmsqGridRows = 4096;
+
+// instantiates the row kernel K<T, RES, FK, FRES, HOUT> for the run-time
+// choices and calls launch(kernel pointer) with it
+template <typename T, template <typename, bool, int, bool, bool> class K, typename L>
+void rmsq_pick(bool res, int fk, bool fres, bool hout, L&& launch) {
+    auto by_fk = [&](auto res_c, auto fres_c, auto hout_c) {
+        constexpr bool R = decltype(res_c)::value, F = decltype(fres_c)::value,
+                       H = decltype(hout_c)::value;
+        if (fk == 0) launch(K<T, R, 0, false, H>{});
+        else if (fk == 4) launch(K<T, R, 4, F, H>{});
+        else if (fk == 8) launch(K<T, R, 8, F, H>{});
+        else launch(K<T, R, 1, F, H>{});
+    };
+    using t_ = std::true_type;
+    using f_ = std::false_type;
+    if (res) {
+        if (hout) by_fk(t_{}, f_{}, t_{});
+        else by_fk(t_{}, f_{}, f_{});
+    } else {
+        if (fres) by_fk(f_{}, t_{}, f_{});
+        else by_fk(f_{}, f_{}, f_{});
+    }
+}
+
+// kernel tags: carry the template arguments to the launch lambdas
+template <typename T, bool RES, int FK, bool FRES, bool HOUT>
+struct RowsK {
+    static constexpr auto fn = rmsq_rows<T, RES, FK, FRES, HOUT>;
+};
+template <typename T, bool RES, int FK, bool FRES, bool HOUT>
+struct GridK {
+    static constexpr auto fn = rmsq_grid<T, RES, FK, FRES, HOUT>;
+};
+
+// rmsnorm_quant of x (or of the folded partials) in one launch when every
+// row's workgroup can be resident at once, else the row pass then the fold
+// of the row maxima and the codes (two launches)
+template <typename T>
+void rmsq_rows_run(const T* x, const RmsqIo<T>& io, const float* w, const T* r,
                    signed char* q, float* scale_out, int rows, int cols, float eps,
                    hipStream_t s) {
-    RowStat* stat = (RowStat*)scratch(Scratch::QuantMax, (size_t)rows * sizeof(RowStat), s);
-    const int fk = FOLD ? kfold_width(fold.ksplit) : 0;
-#define FT_ROWS(RES_, FK_)                                                                \
-    rmsq_rows<T, RES_, FK_><<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps, fold, \
-                                                            x_out)
-    if (r) {
-        if (fk == 0) FT_ROWS(true, 0);
-        else if (fk == 4) FT_ROWS(true, 4);
-        else if (fk == 8) FT_ROWS(true, 8);
-        else FT_ROWS(true, 1);
-    } else {
-        if (fk == 0) FT_ROWS(false, 0);
-        else if (fk == 4) FT_ROWS(false, 4);
-        else if (fk == 8) FT_ROWS(false, 8);
-        else FT_ROWS(false, 1);
+    const bool fold = io.fold.ksplit > 1;
+    const int fk = fold ? kfold_width(io.fold.ksplit) : 0;
+    const bool fres = fold && io.fold.res;
+    const bool hout = r && io.h_out;
+    if (fres && r) inval("rmsnorm_quant: a fold residual and a norm residual together");
+    if (cols <= 4 * kFNT * kRowChunks && rows >= kRmsqGridMinRows && rows <= kRmsqGridRows &&
+        tune(Tune::RmsqSplit, 0) == 0) {
+        const GridMax gm = gridmax_state(rows, s);
+        bool done = false;
+        rmsq_pick<T, GridK>(r != nullptr, fk, fres, hout, [&](auto k) {
+            using Kt = decltype(k);
+            if (!grid_resident((const void*)Kt::fn, rows, kFNT)) return;
+            Kt::fn<<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, cols, eps, io.fold,
+                                                   io.store_x ? io.x_out : nullptr, io.h_out,
+                                                   q, scale_out, gm);
+            launch_check("rmsnorm_quant one-launch kernel launch");
+            done = true;
+        });
+        if (done) return;
     }
-#undef FT_ROWS
+    if (fold && !io.x_out) inval("rmsnorm_quant: the folded rows need a destination");
+    RowStat* stat = (RowStat*)scratch(Scratch::QuantMax, (size_t)rows * sizeof(RowStat), s);
+    rmsq_pick<T, RowsK>(r != nullptr, fk, fres, hout, [&](auto k) {
+        decltype(k)::fn<<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, stat, cols, eps, io.fold,
+                                                        io.x_out, io.h_out);
+    });
     launch_check("rmsnorm_quant row kernel launch");
-    if constexpr (FOLD) x = x_out;
+    const T* xs = fold ? io.x_out : x;
     const long long n4 = (long long)rows * cols / 4;
     const unsigned grid = grid_1d(n4, kFNT, dev_info().cu_count * 4);
     if (r)
-        rmsq_quant<T, true><<<grid, kFNT, 0, s>>>(x, r, w, stat, q, scale_out, rows, cols);
+        rmsq_quant<T, true><<<grid, kFNT, 0, s>>>(xs, r, w, stat, q, scale_out, rows, cols);
     else
-        rmsq_quant<T, false><<<grid, kFNT, 0, s>>>(x, r, w, stat, q, scale_out, rows, cols);
+        rmsq_quant<T, false><<<grid, kFNT, 0, s>>>(xs, r, w, stat, q, scale_out, rows, cols);
     launch_check("rmsnorm_quant quantize kernel launch");
 }
 
 template <typename T>
 void rmsnorm_quant_run(const T* x, const float* w, const T* r, signed char* q,
                        float* scale_out, int rows, int cols, float eps,
-                       hipStream_t s) {
+                       hipStream_t s, T* h_out = nullptr) {
     rmsq_check(x, w, r, q, scale_out, rows, cols);
     if (rows == 0) return;
-    if (rows <= kRmsqMaxRows && cols <= kRmsqMaxCols && tune(Tune::RmsqSplit, 0) == 0) {
+    if (rows <= kRmsqMaxRows && cols <= kRmsqMaxCols && tune(Tune::RmsqSplit, 0) == 0 &&
+        !(r && h_out)) {
         if (r)
             rmsq_small<T, true><<<1, (unsigned)(rows * kFNT), 0, s>>>(x, r, w, q, scale_out,
                                                                        rows, cols, eps);
@@ -389,27 +572,36 @@ void rmsnorm_quant_run(const T* x, const float* w, const T* r, signed char* q,
         launch_check("rmsnorm_quant small kernel launch");
         return;
     }
-    rmsq_two_pass<T, false>(x, KFold{}, nullptr, w, r, q, scale_out, rows, cols, eps, s);
+    RmsqIo<T> io;
+    io.h_out = h_out;
+    rmsq_rows_run<T>(x, io, w, r, q, scale_out, rows, cols, eps, s);
 }
 
 
 // o_proj-style GEMM (a_q codes with the device scale *sa_dev, w_q [n, k],
 // per-channel w_scales) -> y [rows, n] in T, then rmsnorm_quant(y [+ r]).
-// A K-split GEMM's partials are folded by the row pass, which stores y.
+// A K-split GEMM's partials are folded by the row pass, which stores y
+// (when y_store; the one-launch form can skip it). h_out (with r): the
+// residual stream T(y + r).
 template <typename T>
 void qgemm_rmsq_run(const signed char* a_q, const float* sa_dev, const signed char* w_q,
                     const float* w_scales, T* y, const T* r, const float* w, float eps,
                     signed char* q, float* scale_out, int rows, int n, int k, int dtype,
-                    hipStream_t s) {
+                    hipStream_t s, T* h_out = nullptr, bool y_store = true) {
     if (k < 1) inval("qgemm_rmsnorm_quant: k must be >= 1");
     rmsq_check(y, w, r, q, scale_out, rows, n);
     if (rows == 0) return;
-    if (!a_q || !sa_dev || !w_q || !w_scales) inval("qgemm_rmsnorm_quant: null operand");
-    KFold fold;
-    if (qgemm_deferred(a_q, w_q, sa_dev, w_scales, y, dtype, rows, n, k, s, fold))
-        rmsq_two_pass<T, true>(nullptr, fold, y, w, r, q, scale_out, rows, n, eps, s);
-    else
-        rmsnorm_quant_run<T>(y, w, r, q, scale_out, rows, n, eps, s);
+    if (!a_q || !sa_dev || !w_q || !w_scales)
+        inval("qgemm_rmsnorm_quant: null operand");
+    RmsqIo<T> io;
+    io.h_out = h_out;
+    if (qgemm_deferred(a_q, w_q, sa_dev, w_scales, y, dtype, rows, n, k, s, io.fold)) {
+        io.x_out = y;
+        io.store_x = y_store;
+        rmsq_rows_run<T>(nullptr, io, w, r, q, scale_out, rows, n, eps, s);
+    } else {
+        rmsnorm_quant_run<T>(y, w, r, q, scale_out, rows, n, eps, s, h_out);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -543,9 +735,11 @@ void rmsnorm_quant_folded(int dtype, const KFold& fold, void* x_out, const float
 #define FT_RQF(T)                                                                         \
     do {                                                                                  \
         rmsq_check<T>((const T*)x_out, w, nullptr, q, scale_out, rows, cols);             \
+        RmsqIo<T> io;                                                                     \
+        io.fold = fold;                                                                   \
+        io.x_out = (T*)x_out;                                                             \
         if (rows > 0)                                                                     \
-            rmsq_two_pass<T, true>(nullptr, fold, (T*)x_out, w, nullptr, q, scale_out, rows, \
-                                   cols, eps, s);                                         \
+            rmsq_rows_run<T>(nullptr, io, w, nullptr, q, scale_out, rows, cols, eps, s);  \
     } while (0)
     switch (dtype) {
     case FT_DT_F32: FT_RQF(float); break;
@@ -554,6 +748,57 @@ void rmsnorm_quant_folded(int dtype, const KFold& fold, void* x_out, const float
     default: inval("rmsnorm_quant_folded: unknown dtype code");
     }
 #undef FT_RQF
+}
+
+namespace {
+
+// y = T(f32(y) + f32(h)) in place, 4 elements per thread
+template <typename T>
+__global__ __launch_bounds__(256) void residual_add_kernel(T* __restrict__ y,
+                                                          const T* __restrict__ h,
+                                                          long long n4) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const float4 a = St<T>::ld4(y + 4 * i), b = St<T>::ld4(h + 4 * i);
+    St<T>::st4(y + 4 * i, make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w));
+}
+
+}  // namespace
+
+void residual_add(int dtype, void* y, const void* h, long long n, hipStream_t s) {
+    if (n <= 0) return;
+    if (n % 4 != 0 || !y || !h) inval("residual_add: n must be a multiple of 4");
+    const unsigned grid = grid_1d(n / 4, 256, 1 << 30);
+    switch (dtype) {
+    case FT_DT_F32:
+        residual_add_kernel<float><<<grid, 256, 0, s>>>((float*)y, (const float*)h, n / 4);
+        break;
+    case FT_DT_BF16:
+        residual_add_kernel<bf16><<<grid, 256, 0, s>>>((bf16*)y, (const bf16*)h, n / 4);
+        break;
+    case FT_DT_F16:
+        residual_add_kernel<f16><<<grid, 256, 0, s>>>((f16*)y, (const f16*)h, n / 4);
+        break;
+    default: inval("residual_add: unknown dtype code");
+    }
+    launch_check("residual_add kernel launch");
+}
+
+void qgemm_rmsnorm_quant_res(int dtype, const signed char* a_q, const float* sa_dev,
+                             const signed char* w_q, const float* w_scales, void* y,
+                             const void* residual,
+                             const float* w, float eps, signed char* q, float* scale_out,
+                             void* h_out, int rows, int n, int k, hipStream_t s) {
+#define FT_QRR(T)                                                                          \
+    qgemm_rmsq_run<T>(a_q, sa_dev, w_q, w_scales, (T*)y, (const T*)residual, w, eps, q,   \
+                      scale_out, rows, n, k, dtype, s, (T*)h_out, false)
+    switch (dtype) {
+    case FT_DT_F32: FT_QRR(float); break;
+    case FT_DT_BF16: FT_QRR(bf16); break;
+    case FT_DT_F16: FT_QRR(f16); break;
+    default: inval("qgemm_rmsnorm_quant: unknown dtype code");
+    }
+#undef FT_QRR
 }
 
 namespace {

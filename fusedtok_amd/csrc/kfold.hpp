@@ -8,6 +8,9 @@
 //   s   = f32(*sa_dev * sb_vec[col])   (device activation scale, per-channel
 //                                       weight scales)
 //   y   = T(f32(acc * s))              (two f32 roundings, then one to T)
+// With a residual `res` (T [m, n], a decode layer's residual stream), the
+// folded value is T(f32(y) + f32(res[row, col])): the GEMM output as stored,
+// then the residual add of a transformer block, rounded once more.
 #pragma once
 
 #include "ft_common.hpp"
@@ -21,6 +24,7 @@ struct KFold {
     long long mn = 0;
     const float* sa_dev = nullptr;
     const float* sb_vec = nullptr;
+    const void* res = nullptr;  // optional residual added after the epilogue
 };
 
 // Runs y[m, n] = A[m, k] . B[n, k]^T (int8; device activation scale *sa_dev,
@@ -41,6 +45,10 @@ bool qgemm_deferred(const signed char* a, const signed char* b, const float* sa_
 // values: part[0 .. nparts) (library scratch, valid until the next scratch
 // user on stream s) and the result is true. Otherwise nothing is launched
 // and the result is false. qgemm.hip.
+// The K-split partials `f` (ksplit >= 2) of a GEMM folded into y [m, n]
+// (dtype FT_DT_*), plus f.res when non-null: one launch. qgemm.hip.
+void kfold_store(const KFold& f, void* y, int dtype, int m, hipStream_t s);
+
 bool qgemm_swiglu_max(const signed char* a, const signed char* b, const float* sa_dev,
                       const float* sb_vec, void* y, int y_dtype, int m, int inter, int k,
                       hipStream_t s, float*& part, int& nparts);
@@ -52,6 +60,19 @@ bool qgemm_swiglu_max(const signed char* a, const signed char* b, const float* s
 void rmsnorm_quant_folded(int dtype, const KFold& fold, void* x_out, const float* w,
                           signed char* q, float* scale_out, int rows, int cols, float eps,
                           hipStream_t s);
+
+// o_proj GEMM + rmsnorm_quant(y + residual) as ft_qgemm_rmsnorm_quant_launch,
+// plus the residual stream h_out = T(y + residual) (the two roundings of a
+// transformer block's residual add); y itself is stored only where the
+// two-launch form needs it. fused.hip.
+void qgemm_rmsnorm_quant_res(int dtype, const signed char* a_q, const float* sa_dev,
+                             const signed char* w_q, const float* w_scales, void* y,
+                             const void* residual,
+                             const float* w, float eps, signed char* q, float* scale_out,
+                             void* h_out, int rows, int n, int k, hipStream_t s);
+
+// y = T(f32(y) + f32(h)) over n elements (n % 4 == 0). fused.hip.
+void residual_add(int dtype, void* y, const void* h, long long n, hipStream_t s);
 
 __device__ __forceinline__ float kfold_sa(const KFold& f) { return *f.sa_dev; }
 
@@ -66,6 +87,12 @@ __device__ __forceinline__ float kfold_value(int acc, float s) {
     float v = (float)acc * s;
     asm("" : "+v"(v));  // rounded to f32 before the narrowing, never fused
     return (float)(T)v;
+}
+
+// the residual add of a folded value v (f32 of the stored T): T(v + r)
+template <typename T>
+__device__ __forceinline__ float kfold_add_res(float v, float r) {
+    return (float)(T)(v + r);
 }
 
 // Fold widths: a kernel instantiated with FK = 4 or 8 loads all partials

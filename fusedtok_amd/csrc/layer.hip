@@ -5,17 +5,22 @@
 //
 // Chain (T = the activation / KV storage type; every step bit-identical to
 // the unfused ops it replaces):
-//   rmsnorm_quant(x, norm1)                         -> q1, s1        1-2 launches
+//   rmsnorm_quant(x, norm1)                         -> q1, s1        1 launch
 //   QKV GEMM + RoPE + paged KV append (K-split
 //     partials folded by the RoPE kernel)           -> q_rot, pools  2
 //   paged decode over lens + 1 tokens + quantize    -> qa, sa        3
-//   o_proj GEMM + rmsnorm_quant(o + x, norm2)       -> q2, s2        3
-//   gate/up GEMM + swiglu_quant(h[:, :inter],
-//     h[:, inter:]) (SwiGLU maxima in the GEMM
-//     epilogue on the skinny kernel)                -> h, q3, s3     2-3
-//   down GEMM                                       -> y             1-2
-// The reference has no layer op: a decode layer there is these ops called
-// one by one (cuda_launch.hpp:40-59, 185-216, 324-460).
+//   o_proj GEMM + rmsnorm_quant(o + x, norm2),
+//     residual stream r = T(o + x)                  -> q2, s2, r     2
+//   gate/up GEMM + swiglu_quant(g[:, :inter],
+//     g[:, inter:]) (SwiGLU maxima in the GEMM
+//     epilogue on the skinny kernel)                -> g, q3, s3     2-3
+//   down GEMM, then y = T(down + r)                 -> y             2
+// (launch counts at config 4; the RMSNorm -> quantize steps take one launch
+// where every row's workgroup is resident at once, grid_max). y is the
+// Llama block output x + attn + mlp with the two residual adds rounded as a
+// model's T tensors round them. The reference has no layer op: a decode
+// layer there is these ops called one by one (cuda_launch.hpp:40-59,
+// 185-216, 324-460), with the residual adds left to the caller.
 #include "ft_common.hpp"
 #include "kfold.hpp"
 
@@ -31,6 +36,7 @@ struct ft_decode_layer {
     // activation buffers for max_batch rows
     signed char *q1 = nullptr, *qa = nullptr, *q2 = nullptr, *q3 = nullptr;
     void *qkv = nullptr, *qrot = nullptr, *att = nullptr, *o = nullptr, *h = nullptr;
+    void* res = nullptr;  // residual stream T(o + x)
     int* lens_next = nullptr;
     float* scales = nullptr;  // s1, sa, s2, s3
     hipGraphExec_t graph = nullptr;
@@ -95,8 +101,9 @@ struct HandIn {
 };
 
 // in: a folded input (a.x unused), or null. defer: where this layer's down
-// GEMM may leave its K-split partials for the next layer (y not written
-// when defer->ksplit > 1 on return), or null (y always written).
+// GEMM may leave its K-split partials for the next layer, with this layer's
+// residual stream as the fold's residual (y not written when
+// defer->ksplit > 1 on return), or null (y always written).
 void forward(ft_decode_layer& L, const Args& a, hipStream_t s, const HandIn* in = nullptr,
              KFold* defer = nullptr) {
     const ft_decode_layer_desc& d = L.d;
@@ -131,16 +138,23 @@ void forward(ft_decode_layer& L, const Args& a, hipStream_t s, const HandIn* in 
                                                     L.lens_next, L.att, d.dtype, L.qa, sa, B,
                                                     d.q_heads, d.kv_heads, d.page,
                                                     a.tbl_width, d.head_dim, st));
-    rc_check(ft_qgemm_rmsnorm_quant_launch(L.qa, sa, d.w_o, d.s_o, d.dtype, L.o, x, d.norm2,
-                                           d.eps, L.q2, s2, B, d.hidden, hd, st));
+    qgemm_rmsnorm_quant_res(d.dtype, L.qa, sa, d.w_o, d.s_o, L.o, x, d.norm2, d.eps, L.q2, s2,
+                            L.res, B, d.hidden, hd, s);
     rc_check(ft_qgemm_swiglu_quant_launch(L.q2, s2, d.w_gu, d.s_gu, d.dtype, L.h, L.q3, s3, B,
                                           d.inter, d.hidden, st));
-    if (defer)
-        qgemm_deferred(L.q3, d.w_down, s3, d.s_down, a.y, d.dtype, B, d.hidden, d.inter, s,
-                       *defer);
-    else
-        rc_check(ft_qgemm_launch_ex(L.q3, d.w_down, d.s_down, 0.0f, 0.0f, s3, a.y, d.dtype, B,
-                                    d.hidden, d.inter, st));
+    // down GEMM + the residual stream: folded with the K-split partials (by
+    // the next layer's first row pass in a stack), else added in place
+    KFold f;
+    if (qgemm_deferred(L.q3, d.w_down, s3, d.s_down, a.y, d.dtype, B, d.hidden, d.inter, s, f)) {
+        f.res = L.res;
+        if (defer)
+            *defer = f;
+        else
+            kfold_store(f, a.y, d.dtype, B, s);
+    } else {
+        if (defer) *defer = KFold{};
+        residual_add(d.dtype, a.y, L.res, (long long)B * d.hidden, s);
+    }
 }
 
 // ---- decode stack --------------------------------------------------------
@@ -269,9 +283,10 @@ int ft_decode_layer_create(const ft_decode_layer_desc* desc, ft_decode_layer** o
                 B * 2 * desc->inter * L->esz,    // h
                 B * sizeof(int),                 // lens_next
                 4 * sizeof(float),               // scales
+                B * desc->hidden * L->esz,       // res
             };
-            size_t off[11], total = 0;
-            for (int i = 0; i < 11; ++i) {
+            size_t off[12], total = 0;
+            for (int i = 0; i < 12; ++i) {
                 off[i] = total;
                 total += (sizes[i] + 255) & ~(size_t)255;
             }
@@ -293,6 +308,7 @@ int ft_decode_layer_create(const ft_decode_layer_desc* desc, ft_decode_layer** o
             L->h = base + off[8];
             L->lens_next = (int*)(base + off[9]);
             L->scales = (float*)(base + off[10]);
+            L->res = base + off[11];
         } catch (...) {
             delete L;
             throw;

@@ -903,9 +903,12 @@ __global__ __launch_bounds__(64 * NW) void qgemm_skinny_lds(
 // partials instead of one per partial.
 constexpr int kKsumBatch = 8;
 
+// res (optional, OUT-typed [m, n]): the stored value plus res[idx], rounded
+// again (a decode layer's residual add; kfold.hpp)
 template <int OUT>
 __global__ __launch_bounds__(256) void qgemm_ksum(const int* __restrict__ part,
-                                                  Epi e, int m, int n, int ksplit) {
+                                                  Epi e, int m, int n, int ksplit,
+                                                  const void* __restrict__ res) {
     const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
     const long long mn = (long long)m * n;
     if (idx >= mn) return;
@@ -923,6 +926,16 @@ __global__ __launch_bounds__(256) void qgemm_ksum(const int* __restrict__ part,
             v[u] = j0 + u < ksplit ? part[(size_t)(j0 + u) * mn + idx] : 0;
 #pragma unroll
         for (int u = 0; u < kKsumBatch; ++u) s += v[u];
+    }
+    if constexpr (OUT == kOutBF16 || OUT == kOutF16 || OUT == kOutF32) {
+        if (res) {
+            using T = std::conditional_t<OUT == kOutBF16, bf16,
+                                         std::conditional_t<OUT == kOutF16, f16, float>>;
+            const float v = kfold_add_res<T>(epi_stored<OUT>(s, sa * sb),
+                                             St<T>::ld(static_cast<const T*>(res) + idx));
+            St<T>::st(static_cast<T*>(e.y) + idx, v);
+            return;
+        }
     }
     epi_store_scaled<OUT>(e, n, row, col, s, sa * sb);
 }
@@ -2069,7 +2082,8 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         }
         if (ksplit > 1) {
             const long long mn = (long long)m * n;
-            qgemm_ksum<OUT><<<grid_1d(mn, 256, 1 << 30), 256, 0, s>>>(part, e, m, n, ksplit);
+            qgemm_ksum<OUT><<<grid_1d(mn, 256, 1 << 30), 256, 0, s>>>(part, e, m, n, ksplit,
+                                                                      nullptr);
             launch_check("qgemm k-split fold launch");
         }
         return;
@@ -2183,6 +2197,27 @@ bool qgemm_swiglu_max(const signed char* a, const signed char* b, const float* s
     case FT_DT_F16: return swiglu_max_launch<kOutF16>(a, b, e, m, inter, k, s, part, nparts);
     default: inval("qgemm: unknown output dtype code");
     }
+}
+
+void kfold_store(const KFold& f, void* y, int dtype, int m, hipStream_t s) {
+    if (f.ksplit < 2 || f.n < 1 || f.mn != (long long)m * f.n)
+        inval("kfold_store: partials do not match the output");
+    if (!y) inval("kfold_store: null output");
+    Epi e{y, 0.0f, f.sa_dev, 0.0f, f.sb_vec};
+    const unsigned grid = grid_1d(f.mn, 256, 1 << 30);
+    switch (dtype) {
+    case FT_DT_F32:
+        qgemm_ksum<kOutF32><<<grid, 256, 0, s>>>(f.part, e, m, f.n, f.ksplit, f.res);
+        break;
+    case FT_DT_BF16:
+        qgemm_ksum<kOutBF16><<<grid, 256, 0, s>>>(f.part, e, m, f.n, f.ksplit, f.res);
+        break;
+    case FT_DT_F16:
+        qgemm_ksum<kOutF16><<<grid, 256, 0, s>>>(f.part, e, m, f.n, f.ksplit, f.res);
+        break;
+    default: inval("kfold_store: unknown dtype code");
+    }
+    launch_check("qgemm k-split fold launch");
 }
 
 bool qgemm_deferred(const signed char* a, const signed char* b, const float* sa_dev,

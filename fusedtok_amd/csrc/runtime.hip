@@ -5,6 +5,8 @@
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <tuple>
 #include <mutex>
 #include <vector>
 
@@ -75,7 +77,7 @@ constexpr const char* kTuneNames[(int)Tune::kCount] = {
     "FT_QGEMM_BIG",          "FT_QGEMM_BAND",      "FT_RMSQ_SPLIT",
     "FT_RMSQ_GEMV_SPLIT",    "FT_PREFILL_FORCE_GENERIC", "FT_ARG_SLICES",
     "FT_SMP_SINGLE",         "FT_SMP_SLICES",      "FT_FAIL_SCRATCH",
-    "FT_PREFILL_PREPASS"};
+    "FT_PREFILL_PREPASS",    "FT_GRID_SYNC"};
 
 // value and presence per switch: the environment's (read once), then the
 // run-time override, which wins while set
@@ -168,6 +170,35 @@ void* scratch(Scratch which, size_t bytes, hipStream_t s) {
 
 void* scratch_zeroed(Scratch which, size_t bytes, hipStream_t s) {
     return scratch_impl(which, bytes, s, true);
+}
+
+GridMax gridmax_state(int nwg, hipStream_t s) {
+    // the word, then the slots from byte 256; zeroed when (re)allocated, and
+    // every launch leaves the arrivals at 0 (the generation keeps counting)
+    char* p = (char*)scratch_zeroed(Scratch::GridSync, 256 + 4 * (size_t)(nwg > 0 ? nwg : 1), s);
+    return GridMax{(unsigned long long*)p, (unsigned*)(p + 256)};
+}
+
+bool grid_resident(const void* kernel, int nwg, int threads) {
+    if (nwg < 1 || tune(Tune::GridSync, 0) == 1) return false;
+    const int dev = current_device();
+    const int cus = dev_info().cu_count;
+    static std::mutex mu;
+    static std::map<std::tuple<int, const void*, int>, int> per_cu;
+    int blocks = 0;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        const auto key = std::make_tuple(dev, kernel, threads);
+        auto it = per_cu.find(key);
+        if (it == per_cu.end()) {
+            hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, threads, 0),
+                      "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+            per_cu.emplace(key, blocks);
+        } else {
+            blocks = it->second;
+        }
+    }
+    return (long long)blocks * cus >= nwg;
 }
 
 }  // namespace ft

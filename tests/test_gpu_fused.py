@@ -132,6 +132,41 @@ def test_rmsnorm_quant_one_launch_matches_two_launch_path(dt, rows, cols, tuning
 
 
 @pytest.mark.parametrize("dt", ALL)
+@pytest.mark.parametrize("rows,cols", [(17, 4096), (20, 12), (64, 4096), (64, 4),
+                                       (257, 1028), (1000, 512), (4096, 64)])
+def test_rmsnorm_quant_grid_launch_matches_two_launches(dt, rows, cols, tuning):
+    # From 17 rows of at most 4096 columns, rmsnorm_quant is one launch: the
+    # tensor maximum is folded inside it through device-scope atomics
+    # (grid_max). FT_GRID_SYNC=1 forces the row pass + fold/quantize pair.
+    # Eight calls go back to back with no host sync, each with its largest
+    # value in another row, so a workgroup that read a stale maximum would
+    # show as a wrong scale or wrong codes.
+    rng = np.random.default_rng(rows * 17 + cols)
+    w = t(rng.uniform(0.5, 1.5, cols).astype(np.float32))
+    base = rng.standard_normal((rows, cols)).astype(np.float32)
+    xs, rs = [], []
+    for i in range(8):
+        a = base.copy()
+        a[(i * 7919) % rows, (i * 31) % cols] = 50.0 + 10 * i
+        xs.append(t(a, dt))
+        rs.append(t(rng.standard_normal((rows, cols)).astype(np.float32), dt))
+    for with_res in (False, True):
+        got = [ft.rmsnorm_quant(x, w, residual=r if with_res else None, eps=1e-5,
+                                device_scale=True) for x, r in zip(xs, rs)]
+        tuning("FT_GRID_SYNC", 1)
+        ref = [ft.rmsnorm_quant(x, w, residual=r if with_res else None, eps=1e-5,
+                                device_scale=True) for x, r in zip(xs, rs)]
+        tuning.clear("FT_GRID_SYNC")
+        for i, ((q1, s1), (q2, s2)) in enumerate(zip(got, ref)):
+            assert torch.equal(s1, s2), f"call {i}: scale"
+            assert torch.equal(q1, q2), f"call {i}: codes"
+    # and against the oracle for the last call
+    eq, es = oracle.rmsnorm_quant(as_f32(xs[-1]), w.cpu().numpy(), as_f32(rs[-1]), 1e-5)
+    np.testing.assert_array_equal(got[-1][0].cpu().numpy(), eq)
+    assert float(got[-1][1]) == es
+
+
+@pytest.mark.parametrize("dt", ALL)
 @pytest.mark.parametrize("rows,n,k,res", [(1, 11008, 4096, False), (1, 777, 1024, True),
                                           (1, 5, 48, True), (1, 300, 4112, False),
                                           (3, 300, 512, True),

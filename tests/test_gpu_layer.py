@@ -2,7 +2,10 @@
 ft_decode_layer_*):
   - its forward equals this library's unfused op chain bit for bit (output
     and KV pools), at a toy shape and at BASELINE config 4 (Llama-3-8B
-    layer, batch 64, context 8192);
+    layer, batch 64, context 8192, uniform and ragged lengths). The chain
+    is a Llama block: r = x + o_proj(attention) and y = r + mlp(norm2(r)),
+    each residual add rounded to the activation dtype as a model's tensors
+    are;
   - the captured HIP graph replays equal the eager forward, with eager work
     between replays, and a replay after the inputs are rewritten in place
     recomputes (the library's capture contract, reference
@@ -66,9 +69,11 @@ def op_chain(cfg, w, x, kp, vp, table, lens, dt):
     qa, sa = ft.quantize_int8(att.reshape(b, hq * d), device_scale=True)
     o = ft.qgemm_perchannel(qa, sa, w["w_o"], w["s_o"], out_dtype=dt)
     q2, s2 = ft.rmsnorm_quant(o, w["norm2"], residual=x, eps=EPS, device_scale=True)
+    res = (o.float() + x.float()).to(dt)  # residual stream after attention
     h = ft.qgemm_perchannel(q2, s2, w["w_gu"], w["s_gu"], out_dtype=dt)
     q3, s3 = ft.swiglu_quant(h[:, :inter], h[:, inter:], device_scale=True)
-    return ft.qgemm_perchannel(q3, s3, w["w_down"], w["s_down"], out_dtype=dt)
+    d = ft.qgemm_perchannel(q3, s3, w["w_down"], w["s_down"], out_dtype=dt)
+    return (d.float() + res.float()).to(dt)
 
 
 def make_layer(cfg, w, dt, max_batch=None):
@@ -81,10 +86,15 @@ def raw(t):
     return t.cpu().view(torch.int32 if t.dtype is torch.float32 else torch.int16).numpy()
 
 
+# config 4's batch with ragged context lengths (uniform in [512, 8192])
+C4R = dict(C4, lens=[int(v) for v in np.random.default_rng(404).integers(512, 8193, 64)])
+
+
 @pytest.mark.parametrize("name,dt", [("toy", torch.float32), ("toy", torch.bfloat16),
-                                     ("toy", torch.float16), ("c4", torch.bfloat16)])
+                                     ("toy", torch.float16), ("c4", torch.bfloat16),
+                                     ("c4r", torch.bfloat16)])
 def test_layer_forward_equals_the_op_chain(name, dt):
-    cfg = TOY if name == "toy" else C4
+    cfg = {"toy": TOY, "c4": C4, "c4r": C4R}[name]
     w, x, kp, vp, table, lens = make_case(cfg, dt, 11)
     kp_ref, vp_ref = kp.clone(), vp.clone()
     y_ref = op_chain(cfg, w, x, kp_ref, vp_ref, table, lens, dt)
@@ -151,9 +161,10 @@ def test_layer_float32_against_the_oracle_chain():
     qa, sa = oracle.quantize_int8(att.reshape(b, hq * d))
     o = oracle.qgemm_perchannel(qa, sa, h["w_o"], h["s_o"])
     q2, s2 = oracle.rmsnorm_quant(o, h["norm2"], xh, EPS)
+    res = o + xh
     gu = oracle.qgemm_perchannel(q2, s2, h["w_gu"], h["s_gu"])
     q3, s3 = oracle.swiglu_quant(gu[:, :inter], gu[:, inter:])
-    y_ref = oracle.qgemm_perchannel(q3, s3, h["w_down"], h["s_down"])
+    y_ref = oracle.qgemm_perchannel(q3, s3, h["w_down"], h["s_down"]) + res
 
     # RoPE on the device against the host's float64 trig: within an ulp or two
     np.testing.assert_allclose(kp.cpu().numpy(), kph, rtol=1e-6, atol=1e-6)
