@@ -656,46 +656,41 @@ void attn_decode_stream(
 }
 
 // ---------------------------------------------------------------------------
-// combine for attn_decode_stream: one wave per (b, q head). Row (b, kv)
+// combine for attn_decode_stream, one wave per (b, q head). Row (b, kv)
 // spans segments [s_lo, s_hi] of length S; its pieces' partials sit at
 // slots s + row. A row inside one segment was stored by the decode kernel;
 // a row of length 0 is zero-filled here (reference attention.cu:1349-1350).
 // Lanes split into 2 groups of 32 (one float4 column of D = 128 each) that
 // walk alternate pieces; the groups are summed with one xor shuffle.
+// Returns the head's stored output (as T, widened to f32), columns
+// 4 (lane & 31) .. + 3, in every lane.
 // ---------------------------------------------------------------------------
-template <typename T, bool AMAX>
-__global__ __launch_bounds__(64) void attn_combine_stream(
-    const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
-    const long long* __restrict__ pref, T* __restrict__ out, float* __restrict__ amax,
-    int batch, int hq, int hkv, int group, int nseg, int min_seg) {
+template <typename T>
+__device__ __forceinline__ float4 combine_head(const float* __restrict__ ws_ml,
+                                               const float* __restrict__ ws_acc,
+                                               const long long* __restrict__ pref,
+                                               T* __restrict__ out, int bh, int batch, int hq,
+                                               int hkv, int group, int nseg, int min_seg,
+                                               int lane) {
     constexpr int D = kMfmaDim;
-    const int b = blockIdx.x / hq;
-    const int h = blockIdx.x - b * hq;
+    const int b = bh / hq;
+    const int h = bh - b * hq;
     const int kv = h / group, gi = h - kv * group;
-    const int lane = threadIdx.x;
-    T* o = out + ((size_t)b * hq + h) * D;
+    T* o = out + (size_t)bh * D;
     const int len = (int)(pref[b + 1] - pref[b]);
+    const int d4 = lane & 31;
     if (len == 0) {
         if (lane < D / 4) St<T>::st4(o + 4 * lane, make_float4(0.f, 0.f, 0.f, 0.f));
-        if (AMAX && lane == 0) amax[blockIdx.x] = 0.0f;
-        return;
+        return make_float4(0.f, 0.f, 0.f, 0.f);
     }
     const long long S = stream_seg_len(pref[batch] * hkv, nseg, min_seg);
     const long long start = pref[b] * hkv + (long long)kv * len;
     const int s_lo = (int)(start / S), s_hi = (int)((start + len - 1) / S);
-    if (s_lo == s_hi) {
-        // stored whole by the decode kernel: the maximum from the stored
-        // values, read back here. Computed in the decode kernel's store
-        // phase instead, it slowed that kernel's main loop (batch 64,
-        // context 8192: attention + quantize 357.4 against 348.1 us here).
-        if constexpr (AMAX) {
-            float m = stored_absmax4<T>(St<T>::ld4(o + 4 * (lane & 31)));
-#pragma unroll
-            for (int o2 = 16; o2 > 0; o2 >>= 1) m = fmaxf(m, __shfl_xor(m, o2, 64));
-            if (lane == 0) amax[blockIdx.x] = m;
-        }
-        return;
-    }
+    // stored whole by the decode kernel: its stored values, read back here
+    // (a maximum computed in the decode kernel's store phase slowed that
+    // kernel's main loop: batch 64, context 8192, attention + quantize 357.4
+    // against 348.1 us here)
+    if (s_lo == s_hi) return St<T>::ld4(o + 4 * d4);
     const int row = b * hkv + kv;
     const int np = s_hi - s_lo + 1;
     auto slot = [&](int i) { return ((size_t)s_lo + i + row) * group + gi; };
@@ -706,7 +701,7 @@ __global__ __launch_bounds__(64) void attn_combine_stream(
     for (int i = lane; i < np; i += 64)
         lsum += ws_ml[slot(i) * 2 + 1] * exp2f(ws_ml[slot(i) * 2] - mx);
     lsum = wave_sum(lsum);
-    const int grp = lane >> 5, d4 = lane & 31;
+    const int grp = lane >> 5;
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll 4
     for (int i = grp; i < np; i += 2) {
@@ -719,15 +714,72 @@ __global__ __launch_bounds__(64) void attn_combine_stream(
     a.y += __shfl_xor(a.y, 32, 64);
     a.z += __shfl_xor(a.z, 32, 64);
     a.w += __shfl_xor(a.w, 32, 64);
-    if (grp != 0) return;
     const float inv = 1.0f / lsum;
     const float4 ov = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
-    St<T>::st4(o + 4 * d4, ov);
-    if constexpr (AMAX) {
-        float m = stored_absmax4<T>(ov);
+    if (grp == 0) St<T>::st4(o + 4 * d4, ov);
+    return make_float4((float)(T)ov.x, (float)(T)ov.y, (float)(T)ov.z, (float)(T)ov.w);
+}
+
+// max |v| over a head's 128 stored values (lanes 0-31 hold them all, and
+// lanes 32-63 the same again), in every lane
+__device__ __forceinline__ float head_absmax(float4 v) {
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 #pragma unroll
-        for (int o2 = 16; o2 > 0; o2 >>= 1) m = fmaxf(m, __shfl_xor(m, o2, 64));
-        if (lane == 0) amax[blockIdx.x] = m;
+    for (int o2 = 16; o2 > 0; o2 >>= 1) m = fmaxf(m, __shfl_xor(m, o2, 64));
+    return m;
+}
+
+// AMAX: the max |stored output| of each head into amax[b * hq + h], which
+// the per-tensor quantize of the output folds
+template <typename T, bool AMAX>
+__global__ __launch_bounds__(64) void attn_combine_stream(
+    const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
+    const long long* __restrict__ pref, T* __restrict__ out, float* __restrict__ amax,
+    int batch, int hq, int hkv, int group, int nseg, int min_seg) {
+    const float4 v = combine_head<T>(ws_ml, ws_acc, pref, out, blockIdx.x, batch, hq, hkv,
+                                     group, nseg, min_seg, threadIdx.x);
+    if constexpr (AMAX) {
+        const float m = head_absmax(v);
+        if (threadIdx.x == 0) amax[blockIdx.x] = m;
+    }
+}
+
+// The combine and the per-tensor int8 quantize of the output in one launch:
+// workgroups of kCqWaves waves, one (b, q head) per wave, every workgroup
+// resident at once. The heads' maxima are folded with grid_max; then each
+// wave writes its head's codes from the stored values it holds, and
+// workgroup 0 the scale: quantize_int8's codes and scale (scale = max / 127,
+// codes rint(v * (1 / scale)) clamped to +-127, quantize.cu:169-186).
+constexpr int kCqWaves = 8;
+
+template <typename T>
+__global__ __launch_bounds__(64 * kCqWaves) void attn_combine_quant(
+    const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
+    const long long* __restrict__ pref, T* __restrict__ out, signed char* __restrict__ q,
+    float* __restrict__ scale_out, int batch, int hq, int hkv, int group, int nseg,
+    int min_seg, GridMax gm) {
+    __shared__ float red[kCqWaves];
+    constexpr int D = kMfmaDim;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int bh = blockIdx.x * kCqWaves + wave;
+    const bool live = bh < batch * hq;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live)
+        v = combine_head<T>(ws_ml, ws_acc, pref, out, bh, batch, hq, hkv, group, nseg, min_seg,
+                            lane);
+    float m = block_max<64 * kCqWaves>(live ? head_absmax(v) : 0.0f, red);
+    m = grid_max<64 * kCqWaves>(gm, m, red);
+    const float scale = make_scale(m);
+    const float inv_s = 1.0f / scale;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+    if (live && lane < D / 4) {
+        char4 c;
+        c.x = quant1(v.x, inv_s);
+        c.y = quant1(v.y, inv_s);
+        c.z = quant1(v.z, inv_s);
+        c.w = quant1(v.w, inv_s);
+        *reinterpret_cast<char4*>(q + (size_t)bh * D + 4 * lane) = c;
     }
 }
 
@@ -895,11 +947,16 @@ struct Workspace {
 };
 
 template <typename T>
-bool attention_run(const T* q, const T* k, const T* v, const int* table,
+// Returns 0, or 1 when the combine kernel wrote the per-head maxima into
+// amax, or 2 when it also folded them and wrote the int8 codes of the
+// output into qcodes and the scale into *qscale (quantize_int8's; the
+// stream path with every combine workgroup resident at once).
+int attention_run(const T* q, const T* k, const T* v, const int* table,
                    const int* lens, T* out, int batch, int hq, int hkv,
                    int rows_or_page, int tbl_width, int dim, bool paged,
                    hipStream_t s, const Workspace& wsp = Workspace{},
-                   float* amax = nullptr) {
+                   float* amax = nullptr, signed char* qcodes = nullptr,
+                   float* qscale = nullptr) {
     long long span;
     if (paged) {
         span = (long long)tbl_width * rows_or_page;
@@ -915,7 +972,7 @@ bool attention_run(const T* q, const T* k, const T* v, const int* table,
         span = rows_or_page;
         attention_check(batch, hq, hkv, span, dim);
     }
-    if (batch == 0) return false;
+    if (batch == 0) return 0;
     if (!q || !out || (span > 0 && (!k || !v)) || (paged && span > 0 && !table))
         inval("attention: null operand");
     const int group = hq / hkv;
@@ -947,6 +1004,21 @@ bool attention_run(const T* q, const T* k, const T* v, const int* table,
                              pref, out, batch, hq, hkv, group, rows_or_page, tbl_width,
                              (int)span, scale_log2, min_seg);
             launch_check("attention decode kernel launch");
+            if (qcodes) {
+                const long long heads = (long long)batch * hq;
+                const long long nwg = (heads + kCqWaves - 1) / kCqWaves;
+                if (nwg <= (1 << 16)) {
+                    const GridMax gm = gridmax_state((int)nwg, s);
+                    if (grid_resident((const void*)attn_combine_quant<T>, (int)nwg,
+                                      64 * kCqWaves)) {
+                        attn_combine_quant<T><<<(unsigned)nwg, 64 * kCqWaves, 0, s>>>(
+                            ws_ml, ws_acc, pref, out, qcodes, qscale, batch, hq, hkv, group,
+                            nseg, min_seg, gm);
+                        launch_check("attention combine + quantize kernel launch");
+                        return 2;
+                    }
+                }
+            }
             if (amax)
                 attn_combine_stream<T, true><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
                     ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group, nseg, min_seg);
@@ -954,7 +1026,7 @@ bool attention_run(const T* q, const T* k, const T* v, const int* table,
                 attn_combine_stream<T, false><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
                     ws_ml, ws_acc, pref, out, nullptr, batch, hq, hkv, group, nseg, min_seg);
             launch_check("attention combine kernel launch");
-            return true;  // the combine kernel wrote amax when asked
+            return amax ? 1 : 0;
         }
     }
     const long long target = (long long)dev_info().cu_count * 16;
@@ -990,7 +1062,7 @@ bool attention_run(const T* q, const T* k, const T* v, const int* table,
     // (also the zero fill of every row when the cache holds no rows at all)
     launch_combine<T>(ws_ml, ws_acc, span > 0 ? lens : nullptr, out, batch, hq,
                       hkv, group, dim, (int)span, chunk, cmax, false, s);
-    return false;  // no per-head maxima on this path
+    return 0;  // no per-head maxima on this path
 }
 
 // ---------------------------------------------------------------------------
@@ -1067,10 +1139,12 @@ using ft::f16;
 namespace ft {
 namespace {
 // Paged decode followed by the per-tensor int8 quantize of its output. On
-// the stream kernels' path the combine kernel also writes the max |stored
+// the stream kernels' path the combine kernel also takes the max |stored
 // output| of every (sequence, q head) (split rows from its fold, whole rows
-// read back), so the quantize is one launch over those B * Hq maxima; other
-// paths quantize the output in full.
+// read back): where all its workgroups are resident at once it folds them
+// (grid_max) and writes the codes and the scale itself, else it writes them
+// out and the quantize is one launch over those B * Hq maxima; other paths
+// quantize the output in full.
 template <typename T>
 void attention_paged_quant_run(const T* q, const T* k_pool, const T* v_pool, const int* table,
                                const int* lens, T* out, signed char* codes, float* scale_out,
@@ -1081,11 +1155,12 @@ void attention_paged_quant_run(const T* q, const T* k_pool, const T* v_pool, con
     const long long rows = (long long)batch * hq;
     float* amax = rows > 0 ? (float*)scratch(Scratch::QuantMax, (size_t)rows * sizeof(float), s)
                            : nullptr;
-    const bool have_max = attention_run<T>(q, k_pool, v_pool, table, lens, out, batch, hq, hkv,
-                                           page, tbl_width, dim, true, s, Workspace{}, amax);
-    if (batch == 0) return;
+    const int have = attention_run<T>(q, k_pool, v_pool, table, lens, out, batch, hq, hkv,
+                                      page, tbl_width, dim, true, s, Workspace{}, amax, codes,
+                                      scale_out);
+    if (batch == 0 || have == 2) return;
     const long long n = rows * dim;
-    if (have_max)
+    if (have == 1)
         quantize_from_partials<T>(out, codes, amax, (int)rows, scale_out, n, s);
     else
         quantize_tensor<T>(out, codes, scale_out, n, s);

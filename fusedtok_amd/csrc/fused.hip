@@ -807,11 +807,13 @@ namespace {
 // gate rows then up rows, per-channel w_scales) -> h [rows, 2 inter] in T,
 // then swiglu_quant(h[:, :inter], h[:, inter:]). Where the GEMM runs
 // unsplit on the skinny ring kernel, its epilogue takes the SwiGLU maxima
-// (the maximum is exact in any order), and only the codes pass is left.
+// (the maximum is exact in any order): with every workgroup resident at
+// once it also folds them and writes the codes (one launch; h is then
+// stored only if store_h), else only the codes pass is left.
 template <typename T>
 void qgemm_swq_run(const signed char* a_q, const float* sa_dev, const signed char* w_gu,
                    const float* w_scales, T* h, signed char* q, float* scale_out, int rows,
-                   int inter, int k, int dtype, hipStream_t s) {
+                   int inter, int k, int dtype, hipStream_t s, bool store_h = true) {
     if (rows < 0 || inter < 1 || k < 0)
         inval("qgemm_swiglu_quant: rows and k must be >= 0, inter >= 1");
     if (rows == 0) return;
@@ -820,8 +822,10 @@ void qgemm_swq_run(const signed char* a_q, const float* sa_dev, const signed cha
     const long long ld = 2LL * inter;
     float* part = nullptr;
     int nparts = 0;
-    if (!qgemm_swiglu_max(a_q, w_gu, sa_dev, w_scales, h, dtype, rows, inter, k, s, part,
-                          nparts)) {
+    const int how = qgemm_swiglu_max(a_q, w_gu, sa_dev, w_scales, store_h ? h : nullptr, dtype,
+                                     rows, inter, k, s, part, nparts, q, scale_out);
+    if (how == 2) return;
+    if (how == 0) {
         const int rc = ft_qgemm_launch_ex(a_q, w_gu, w_scales, 0.0f, 0.0f, sa_dev, h, dtype,
                                           rows, 2 * inter, k, (uintptr_t)s);
         if (rc != FT_OK) throw Error{rc, ft_last_error()};
@@ -841,6 +845,26 @@ void qgemm_swq_run(const signed char* a_q, const float* sa_dev, const signed cha
                                                   rows, inter, ld);
     launch_check("swiglu_quant quantize kernel launch");
 }
+
+}  // namespace
+
+void qgemm_swiglu_quant_codes(int dtype, const signed char* a_q, const float* sa_dev,
+                              const signed char* w_gu, const float* w_scales, void* h,
+                              signed char* q, float* scale_out, int rows, int inter, int k,
+                              hipStream_t s) {
+#define FT_QSW(T)                                                                       \
+    qgemm_swq_run<T>(a_q, sa_dev, w_gu, w_scales, (T*)h, q, scale_out, rows, inter, k, \
+                     dtype, s, false)
+    switch (dtype) {
+    case FT_DT_F32: FT_QSW(float); break;
+    case FT_DT_BF16: FT_QSW(bf16); break;
+    case FT_DT_F16: FT_QSW(f16); break;
+    default: inval("qgemm_swiglu_quant: unknown dtype code");
+    }
+#undef FT_QSW
+}
+
+namespace {
 
 // ---------------------------------------------------------------------------
 // rope_kv_append_paged: one thread per (sequence b, head, pair j) of the

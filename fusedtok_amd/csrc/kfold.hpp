@@ -43,15 +43,19 @@ bool qgemm_deferred(const signed char* a, const signed char* b, const float* sa_
 // Where the dispatch would run it unsplit on the skinny ring kernel, that
 // kernel also takes each workgroup's max |silu(g) * u| over the stored
 // values: part[0 .. nparts) (library scratch, valid until the next scratch
-// user on stream s) and the result is true. Otherwise nothing is launched
-// and the result is false. qgemm.hip.
+// user on stream s) and the result is 1. With q (codes [m, inter]) and
+// scale_out given, and every workgroup resident at once, the kernel folds
+// the maxima itself and writes swiglu_quant's codes and scale: result 2
+// (y may then be null: not stored). Otherwise nothing is launched and the
+// result is 0. qgemm.hip.
 // The K-split partials `f` (ksplit >= 2) of a GEMM folded into y [m, n]
 // (dtype FT_DT_*), plus f.res when non-null: one launch. qgemm.hip.
 void kfold_store(const KFold& f, void* y, int dtype, int m, hipStream_t s);
 
-bool qgemm_swiglu_max(const signed char* a, const signed char* b, const float* sa_dev,
-                      const float* sb_vec, void* y, int y_dtype, int m, int inter, int k,
-                      hipStream_t s, float*& part, int& nparts);
+int qgemm_swiglu_max(const signed char* a, const signed char* b, const float* sa_dev,
+                     const float* sb_vec, void* y, int y_dtype, int m, int inter, int k,
+                     hipStream_t s, float*& part, int& nparts, signed char* q = nullptr,
+                     float* scale_out = nullptr);
 
 // rmsnorm_quant (no residual) of a K-split GEMM's output still held as its
 // partials: the row pass folds them and stores the rows into x_out (as the
@@ -70,6 +74,14 @@ void qgemm_rmsnorm_quant_res(int dtype, const signed char* a_q, const float* sa_
                              const void* residual,
                              const float* w, float eps, signed char* q, float* scale_out,
                              void* h_out, int rows, int n, int k, hipStream_t s);
+
+// ft_qgemm_swiglu_quant_launch where h [rows, 2 inter] is scratch the
+// caller does not read: the one-launch form (gate/up GEMM + SwiGLU maxima
+// folded with grid_max + codes) skips storing it. fused.hip.
+void qgemm_swiglu_quant_codes(int dtype, const signed char* a_q, const float* sa_dev,
+                              const signed char* w_gu, const float* w_scales, void* h,
+                              signed char* q, float* scale_out, int rows, int inter, int k,
+                              hipStream_t s);
 
 // y = T(f32(y) + f32(h)) over n elements (n % 4 == 0). fused.hip.
 void residual_add(int dtype, void* y, const void* h, long long n, hipStream_t s);

@@ -140,8 +140,8 @@ void forward(ft_decode_layer& L, const Args& a, hipStream_t s, const HandIn* in 
                                                     a.tbl_width, d.head_dim, st));
     qgemm_rmsnorm_quant_res(d.dtype, L.qa, sa, d.w_o, d.s_o, L.o, x, d.norm2, d.eps, L.q2, s2,
                             L.res, B, d.hidden, hd, s);
-    rc_check(ft_qgemm_swiglu_quant_launch(L.q2, s2, d.w_gu, d.s_gu, d.dtype, L.h, L.q3, s3, B,
-                                          d.inter, d.hidden, st));
+    qgemm_swiglu_quant_codes(d.dtype, L.q2, s2, d.w_gu, d.s_gu, L.h, L.q3, s3, B, d.inter,
+                             d.hidden, s);
     // down GEMM + the residual stream: folded with the K-split partials (by
     // the next layer's first row pass in a stack), else added in place
     KFold f;

@@ -734,13 +734,24 @@ __device__ __forceinline__ void sl_issue(const i8* a, const i8* b, const size_t*
 // then the up rows), inter % (8 * NW) == 0, ksplit == 1. The first NW / 2
 // waves of workgroup x take gate columns 8 NW x + 16 w .., the other NW / 2
 // the up columns inter + the same, so every gate output and its up partner
-// are in one workgroup. After y is stored, the epilogue takes the
-// workgroup's max |silu(g) * u| over the stored values into swq_part[x]:
-// the partial maxima swiglu_quant folds, without its own pass over y.
+// are in one workgroup. After y is stored (skipped when e.y is null), the
+// epilogue takes the workgroup's max |silu(g) * u| over the stored values.
+// Without `sq` it goes to swq_part[x]: the partial maxima swiglu_quant
+// folds, without its own pass over y. With `sq` (every workgroup resident
+// at once) the tensor maximum is folded here (grid_max), and each
+// workgroup writes the int8 codes of its SwiGLU outputs and workgroup 0 the
+// scale, as swiglu_quant would: the whole gate/up -> SwiGLU -> quantize step
+// in one launch.
+struct SwqGrid {
+    signed char* q = nullptr;  // [m, inter] codes, or null (partials only)
+    float* scale = nullptr;
+    GridMax gm{};
+};
 template <int MT, int NSTAGE, int NW, int OUT, bool SWQ>
 __global__ __launch_bounds__(64 * NW) void qgemm_skinny_lds(
     const i8* __restrict__ a, const i8* __restrict__ b, Epi e, int m, int n,
-    int k, int ksplit, int* __restrict__ part, int inter, float* __restrict__ swq_part) {
+    int k, int ksplit, int* __restrict__ part, int inter, float* __restrict__ swq_part,
+    SwqGrid sq) {
     constexpr int kArows = 16 * MT;
     constexpr int kStage = (kArows + 16 * NW) * kSlChunk;
     constexpr int kAIns = kArows / 4 / NW;  // A DMA instructions per wave per chunk
@@ -840,7 +851,7 @@ __global__ __launch_bounds__(64 * NW) void qgemm_skinny_lds(
             for (int i = 0; i < 4; ++i) {
                 const int row = 16 * t + 4 * g + i;
                 sv[t][i] = epi_stored<OUT>(acc[t][i], sc);
-                if (row < m) epi_store_scaled<OUT>(e, n, row, col, acc[t][i], sc);
+                if (row < m && e.y) epi_store_scaled<OUT>(e, n, row, col, acc[t][i], sc);
             }
         // the up values through LDS (the ring is free once every wave is
         // past its last chunk), then each gate lane folds its outputs
@@ -863,12 +874,29 @@ __global__ __launch_bounds__(64 * NW) void qgemm_skinny_lds(
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int row = 16 * t + 4 * g + i;
-                    if (row < m)
-                        mx = fmaxf(mx, fabsf(silu_mul(sv[t][i], xch[row * kXP + cl])));
+                    // the SwiGLU output, kept for the codes below
+                    sv[t][i] = silu_mul(sv[t][i], xch[row * kXP + cl]);
+                    if (row < m) mx = fmaxf(mx, fabsf(sv[t][i]));
                 }
         }
         mx = block_max<64 * NW>(mx, red);
-        if (threadIdx.x == 0) swq_part[blockIdx.x] = mx;
+        if (!sq.q) {
+            if (threadIdx.x == 0) swq_part[blockIdx.x] = mx;
+            return;
+        }
+        mx = grid_max<64 * NW>(sq.gm, mx, red);
+        const float scale = make_scale(mx);
+        const float inv_s = 1.0f / scale;
+        if (blockIdx.x == 0 && threadIdx.x == 0) *sq.scale = scale;
+        if (wave < kHalf) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = 16 * t + 4 * g + i;
+                    if (row < m) sq.q[(size_t)row * inter + col] = quant1(sv[t][i], inv_s);
+                }
+        }
         return;
     }
     const int col = n0 + r;
@@ -2053,7 +2081,8 @@ void qgemm_dispatch(const i8* a, const i8* b, const Epi& e, int m, int n, int k,
         if (ring) {
 #define FT_SK_LDS(MT, S, NW)                                                             \
     qgemm_skinny_lds<MT, S, NW, OUT, false><<<grid, 64 * NW, 0, s>>>(a, b, e, m, n, k, ksplit, \
-                                                                     part, 0, nullptr)
+                                                                     part, 0, nullptr,        \
+                                                                     SwqGrid{})
             if (mt <= 1) {
                 if (stages == 3) FT_SK_LDS(1, 3, 4); else FT_SK_LDS(1, 2, 4);
             } else if (mt <= 2) {
@@ -2147,54 +2176,68 @@ void qgemm_run(const i8* a, const i8* b, Epi e, int out, int m, int n, int k,
 // The skinny ring kernel with the SwiGLU maxima in its epilogue, launched
 // only where qgemm_dispatch takes qgemm_skinny_lds unsplit for the same
 // shape (same waves, stages and column tiles), so y is the same bits.
+// Returns 0 (not launched), 1 (the per-workgroup maxima are in part) or 2
+// (q given and every workgroup resident: the codes and *scale_out written).
 template <int OUT>
-bool swiglu_max_launch(const i8* a, const i8* b, const Epi& e, int m, int inter, int k,
-                       hipStream_t s, float*& part, int& nparts) {
+int swiglu_max_launch(const i8* a, const i8* b, const Epi& e, int m, int inter, int k,
+                      hipStream_t s, float*& part, int& nparts, signed char* q,
+                      float* scale_out) {
     const int n = 2 * inter;
     const bool aligned = (k % 16 == 0) && ((uintptr_t)a % 16 == 0) && ((uintptr_t)b % 16 == 0);
-    if (!aligned || tune(Tune::QgemmKernel, 0) != 0 || m <= 16 || m > 64) return false;
-    if (k % kSlChunk != 0 || tune(Tune::QgemmSkRegs, 0) != 0) return false;
-    if (tune(Tune::QgemmSkStages, 3) == 2 || tune(Tune::QgemmKsplit, 0) != 0) return false;
+    if (!aligned || tune(Tune::QgemmKernel, 0) != 0 || m <= 16 || m > 64) return 0;
+    if (k % kSlChunk != 0 || tune(Tune::QgemmSkRegs, 0) != 0) return 0;
+    if (tune(Tune::QgemmSkStages, 3) == 2 || tune(Tune::QgemmKsplit, 0) != 0) return 0;
     const int cus = dev_info().cu_count;
     const int mt = (m + 15) / 16;  // 2 or 4
     const int wide = (n + 127) / 128;
     const int nw_pick = 4 * wide >= 3 * cus ? 8 : 4;
     const int nw = tune(Tune::QgemmSkWaves, nw_pick) == 8 ? 8 : 4;
-    if (inter % (8 * nw) != 0) return false;
+    if (inter % (8 * nw) != 0) return 0;
     const int lds_bytes = (16 * (mt <= 2 ? 2 : 4) + 16 * nw) * kSlChunk * 3;
     const int slots = std::max(1, (160 << 10) / lds_bytes) * cus;
     const int col_wgs = inter / (8 * nw);
-    if (4 * col_wgs < 3 * slots) return false;  // the dispatch would split K
+    if (4 * col_wgs < 3 * slots) return 0;  // the dispatch would split K
     part = (float*)scratch(Scratch::QuantMax, (size_t)col_wgs * sizeof(float), s);
     nparts = col_wgs;
+    SwqGrid sq;
+    if (q) sq = SwqGrid{q, scale_out, gridmax_state(col_wgs, s)};
     dim3 grid(col_wgs, 1);
-#define FT_SK_SWQ(MT, NW)                                                                   \
-    qgemm_skinny_lds<MT, 3, NW, OUT, true><<<grid, 64 * NW, 0, s>>>(a, b, e, m, n, k, 1,    \
-                                                                    nullptr, inter, part)
+    int launched = 0;
+    auto go = [&](auto kernel, int threads) {
+        if (sq.q && !grid_resident((const void*)kernel, col_wgs, threads)) sq = SwqGrid{};
+        if (!sq.q && !e.y) return;  // the partials-only form needs y stored
+        kernel<<<grid, threads, 0, s>>>(a, b, e, m, n, k, 1, nullptr, inter, part, sq);
+        launch_check("qgemm swiglu-max kernel launch");
+        launched = sq.q ? 2 : 1;
+    };
     if (mt <= 2) {
-        if (nw == 8) FT_SK_SWQ(2, 8); else FT_SK_SWQ(2, 4);
+        if (nw == 8) go(qgemm_skinny_lds<2, 3, 8, OUT, true>, 512);
+        else go(qgemm_skinny_lds<2, 3, 4, OUT, true>, 256);
     } else {
-        if (nw == 8) FT_SK_SWQ(4, 8); else FT_SK_SWQ(4, 4);
+        if (nw == 8) go(qgemm_skinny_lds<4, 3, 8, OUT, true>, 512);
+        else go(qgemm_skinny_lds<4, 3, 4, OUT, true>, 256);
     }
-#undef FT_SK_SWQ
-    launch_check("qgemm swiglu-max kernel launch");
-    return true;
+    return launched;
 }
 
 }  // namespace
 
-bool qgemm_swiglu_max(const signed char* a, const signed char* b, const float* sa_dev,
-                      const float* sb_vec, void* y, int y_dtype, int m, int inter, int k,
-                      hipStream_t s, float*& part, int& nparts) {
+int qgemm_swiglu_max(const signed char* a, const signed char* b, const float* sa_dev,
+                     const float* sb_vec, void* y, int y_dtype, int m, int inter, int k,
+                     hipStream_t s, float*& part, int& nparts, signed char* q,
+                     float* scale_out) {
     if (!sa_dev || !sb_vec) inval("qgemm: a device scale and per-channel scales are required");
-    if (inter < 1 || (long long)m * 2 * inter > (1LL << 31) - 1) return false;
+    if (inter < 1 || (long long)m * 2 * inter > (1LL << 31) - 1) return 0;
     qgemm_check(m, 2 * inter, k);
-    if (m == 0 || k == 0 || !y || !a || !b) return false;
+    if (m == 0 || k == 0 || (!y && !q) || !a || !b) return 0;
     Epi e{y, 0.0f, sa_dev, 0.0f, sb_vec};
     switch (y_dtype) {
-    case FT_DT_F32: return swiglu_max_launch<kOutF32>(a, b, e, m, inter, k, s, part, nparts);
-    case FT_DT_BF16: return swiglu_max_launch<kOutBF16>(a, b, e, m, inter, k, s, part, nparts);
-    case FT_DT_F16: return swiglu_max_launch<kOutF16>(a, b, e, m, inter, k, s, part, nparts);
+    case FT_DT_F32:
+        return swiglu_max_launch<kOutF32>(a, b, e, m, inter, k, s, part, nparts, q, scale_out);
+    case FT_DT_BF16:
+        return swiglu_max_launch<kOutBF16>(a, b, e, m, inter, k, s, part, nparts, q, scale_out);
+    case FT_DT_F16:
+        return swiglu_max_launch<kOutF16>(a, b, e, m, inter, k, s, part, nparts, q, scale_out);
     default: inval("qgemm: unknown output dtype code");
     }
 }

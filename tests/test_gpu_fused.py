@@ -416,12 +416,19 @@ ATTN_Q_CASES = {
 }
 
 
+# the stream path's quantize: "grid", the combine kernel folds the heads'
+# maxima (grid_max) and writes the codes; "partials", FT_GRID_SYNC=1: it
+# writes the maxima and a second launch the codes; "generic": the generic
+# kernels, quantised in full
 @pytest.mark.parametrize("dt", ALL)
 @pytest.mark.parametrize("case", list(ATTN_Q_CASES))
-@pytest.mark.parametrize("generic", [False, True])
-def test_attention_decode_paged_quant_equals_the_two_ops(dt, case, generic, tuning):
+@pytest.mark.parametrize("path", ["grid", "partials", "generic"])
+def test_attention_decode_paged_quant_equals_the_two_ops(dt, case, path, tuning):
+    generic = path == "generic"
     if generic:
         tuning("FT_ATTN_FORCE_GENERIC", 1)
+    if path == "partials":
+        tuning("FT_GRID_SYNC", 1)
     rng = np.random.default_rng(sorted(ATTN_Q_CASES).index(case) + 7 * generic)
     b, hq, hkv, d, page, lens = ATTN_Q_CASES[case]
     if lens is None:
@@ -555,16 +562,19 @@ def test_qgemm_rmsnorm_quant_equals_the_two_ops(dt, case, tuning):
 
 
 # (m, inter, k, switches) of the gate/up GEMM + swiglu_quant. Per the GEMM
-# dispatch rules, the first five run unsplit on the skinny ring kernel with
+# dispatch rules, the first six run unsplit on the skinny ring kernel with
 # the SwiGLU maxima in its epilogue: C4's shape (8 waves, 4 row blocks) at a
-# short and at its full K, 40 rows (4 row blocks, 24 rows past M), 17 rows
-# (2 row blocks), and 4-wave workgroups (forced). The last three take the
-# GEMM + swiglu_quant fallback: a K split (inter too small to fill the
-# CUs), the decode GEMM (m <= 16), and inter not a multiple of the paired
-# column tile.
+# short and at its full K, the same with FT_GRID_SYNC=1 (the epilogue writes
+# its maxima and a second launch writes the codes, instead of folding the
+# maxima in the launch with grid_max), 40 rows (4 row blocks, 24 rows past
+# M), 17 rows (2 row blocks), and 4-wave workgroups (forced). The last three
+# take the GEMM + swiglu_quant fallback: a K split (inter too small to fill
+# the CUs), the decode GEMM (m <= 16), and inter not a multiple of the
+# paired column tile.
 SWQ_CASES = {
     "c4": (64, 14336, 512, {}),
     "c4_full_k": (64, 14336, 4096, {}),
+    "c4_partials": (64, 14336, 512, {"FT_GRID_SYNC": 1}),
     "rows40": (40, 12288, 256, {}),
     "rows17": (17, 12288, 256, {}),
     "nw4": (64, 6144, 512, {"FT_QGEMM_SK_WAVES": 4}),
