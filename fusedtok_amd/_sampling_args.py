@@ -128,7 +128,13 @@ def histories_csr(sampled_ids, ids_offsets, rows, vocab):
 # kernels were queued); where the runtime reports no mapping, one
 # non-blocking copy per call takes them up instead. A slot is refilled only
 # after the work that read it has completed (its event). A pageable copy
-# per vector made every call wait for the GPU to drain.
+# per vector made every call wait for the GPU to drain. Above IN_PLACE_MAX
+# values (long histories) the slot is uploaded too: each of a row's slices
+# reads the row's history, so in-place reads would cross PCIe once per
+# slice (64 rows x 8 slices x 8k ids is 32 MB of scattered reads).
+IN_PLACE_MAX = 4096
+
+
 class _PinnedRing:
     def __init__(self, slots=4):
         self.slots = [[None, None, 0] for _ in range(slots)]  # [buffer, event, device address]
@@ -159,9 +165,9 @@ class _PinnedRing:
         event follows the launch on the current stream."""
         slot, total, bounds = self._fill(arrays, mapper)
         base = slot[2]
-        if base:
+        if base and total <= IN_PLACE_MAX:
             launch([base + 8 * int(lo) for lo in bounds[:-1]])
-        else:  # no device mapping: one copy of the slot
+        else:  # no device mapping, or long vectors: one copy of the slot
             dev = torch.empty(total, dtype=torch.int64, device=device)
             dev.copy_(slot[0][:total], non_blocking=True)
             launch([dev.data_ptr() + 8 * int(lo) for lo in bounds[:-1]])

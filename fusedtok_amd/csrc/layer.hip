@@ -25,6 +25,7 @@
 #include "kfold.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -40,6 +41,9 @@ struct ft_decode_layer {
     int* lens_next = nullptr;
     float* scales = nullptr;  // s1, sa, s2, s3
     hipGraphExec_t graph = nullptr;
+    // stacks holding this layer (once per appearance): its buffers stay
+    // alive while any stack, or a graph a stack captured, may still use them
+    std::atomic<int> stack_refs{0};
 };
 
 namespace ft {
@@ -351,6 +355,8 @@ int ft_decode_layer_replay(ft_decode_layer* layer, uintptr_t stream) {
 int ft_decode_layer_destroy(ft_decode_layer* layer) {
     return ft::guarded([&] {
         if (!layer) return;
+        if (layer->stack_refs.load() > 0)
+            ft::inval("decode layer: still used by a decode stack (destroy the stack first)");
         if (layer->graph) (void)hipGraphExecDestroy(layer->graph);
         if (layer->arena) (void)hipFree(layer->arena);
         delete layer;
@@ -369,6 +375,7 @@ int ft_decode_stack_create(ft_decode_layer* const* layers, int n_layers,
             ft::inval("decode stack: create it with the layers' device current");
         auto* S = new ft_decode_stack();
         S->layers.assign(layers, layers + n_layers);
+        for (ft_decode_layer* L : S->layers) ++L->stack_refs;
         S->device = dev;
         S->max_batch = layers[0]->d.max_batch;
         for (int i = 1; i < n_layers; ++i)
@@ -379,6 +386,7 @@ int ft_decode_stack_create(ft_decode_layer* const* layers, int n_layers,
             hipError_t e = hipMalloc(&S->buf[0], 2 * bytes);
             if (e != hipSuccess) {
                 (void)hipGetLastError();
+                for (ft_decode_layer* L : S->layers) --L->stack_refs;
                 delete S;
                 ft::hip_fail("decode stack buffer allocation", e);
             }
@@ -430,6 +438,7 @@ int ft_decode_stack_destroy(ft_decode_stack* stack) {
         if (!stack) return;
         if (stack->graph) (void)hipGraphExecDestroy(stack->graph);
         if (stack->buf[0]) (void)hipFree(stack->buf[0]);
+        for (ft_decode_layer* L : stack->layers) --L->stack_refs;
         delete stack;
     });
 }

@@ -162,9 +162,11 @@ class DecodeLayer:
         return self._captured[1]
 
     def close(self):
-        h, self._h = getattr(self, "_h", None), None
+        h = getattr(self, "_h", None)
         if h:
+            # refused (ValueError, the layer left open) while a stack uses it
             _fusedtok.decode_layer_destroy(h)
+        self._h = None
         self._captured = None
 
     def __del__(self):
@@ -183,7 +185,8 @@ class DecodeStack:
     one. ``capture`` records the whole chain into one HIP graph.
 
     The layers (DecodeLayer objects on one device with one dtype and hidden
-    size) are kept referenced; a layer may appear more than once. Each layer
+    size) are kept referenced; a layer may appear more than once, and closing
+    a layer raises ValueError while a stack using it is open. Each layer
     has its own KV pools (``k_pools`` / ``v_pools``: sequences of tensors,
     one per layer); the block table and lens are shared.
     """
@@ -249,6 +252,8 @@ class DecodeStack:
 
     def replay(self):
         """Launch the captured chain on the current stream."""
+        if self._h is None or any(L._h is None for L in self.layers):
+            raise RuntimeError("DecodeStack: the stack or one of its layers has been closed")
         if self._captured is None:
             raise RuntimeError("DecodeStack.replay: nothing captured")
         _fusedtok.decode_stack_replay(self._h, _stream())

@@ -503,6 +503,7 @@ int ft_decode_layer_capture(ft_decode_layer* layer, const void* x, void* y, void
                             void* v_pool, const int* table, const int* lens, int batch,
                             int tbl_width, uintptr_t stream);
 int ft_decode_layer_replay(ft_decode_layer* layer, uintptr_t stream);
+/* FT_EINVAL (nothing freed) while a decode stack holds the layer. */
 int ft_decode_layer_destroy(ft_decode_layer* layer);
 
 /* Decode stack (build addition, no reference counterpart): n layers    */
@@ -514,6 +515,8 @@ int ft_decode_layer_destroy(ft_decode_layer* layer);
 /* device, dtype and hidden size; they must outlive the stack, and a    */
 /* layer may appear more than once); table and lens are shared by all   */
 /* layers, k_pools / v_pools are HOST arrays of n device pool pointers. */
+/* The stack holds a reference on each layer: ft_decode_layer_destroy    */
+/* refuses a layer until every stack using it has been destroyed.       */
 /* The stack holds two [max_batch, hidden] buffers for the activations  */
 /* between layers (max_batch = the smallest of its layers').            */
 typedef struct ft_decode_stack ft_decode_stack;

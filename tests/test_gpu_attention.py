@@ -274,11 +274,13 @@ def test_paged_no_lens_uses_full_width_and_host_table():
     assert_half_close(out.float().cpu().numpy(), ref)
 
 
-def test_paged_c3_shape_sampled_rows():
+def test_paged_c3_shape_every_row():
     """BASELINE config 3 at full size (B=32, Hq=32, Hkv=8, D=128, P=16, bf16,
     lens ~ U[512, 32768], permuted page pool) with a kv_append of one token
-    per row first; three rows (the first, the longest and the shortest) are
-    checked against the oracle over their own pages."""
+    per row first; every row is checked against the oracle over its own
+    pages (reference tests/test_attention_paged.py:62-94 check paged rows
+    against the materialised cache the same way), and every appended K/V row
+    sits at slot lens[b] bit for bit."""
     rng = np.random.default_rng(2026)
     b, hq, hkv, d, page = 32, 32, 8, 128, 16
     lens = rng.integers(512, 32769, size=b).astype(np.int32)
@@ -304,9 +306,13 @@ def test_paged_c3_shape_sampled_rows():
     out = ft.attention_decode_paged(q, kp, vp, tbl_t, lens_t + 1)
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
-    for bi in (0, int(np.argmax(lens)), int(np.argmin(lens))):
+    kn_h, vn_h = kn.cpu(), vn.cpu()
+    for bi in range(b):
         npg = (lens[bi] + 1 + page - 1) // page
         blocks = tbl[bi, :npg]
+        slot_pg, slot_in = int(tbl[bi, lens[bi] // page]), int(lens[bi] % page)
+        assert torch.equal(kp[slot_pg, :, slot_in].cpu(), kn_h[bi]), f"C3 row {bi}: k append"
+        assert torch.equal(vp[slot_pg, :, slot_in].cpu(), vn_h[bi]), f"C3 row {bi}: v append"
         kp_b = kp[torch.from_numpy(blocks).long().to(DEV)].float().cpu().numpy()
         vp_b = vp[torch.from_numpy(blocks).long().to(DEV)].float().cpu().numpy()
         sub_tbl = np.arange(npg, dtype=np.int32)[None, :]

@@ -303,10 +303,19 @@ def test_stack_argument_errors():
         stack(x, kps[:1], vps[:1], table, lens)
     with pytest.raises(RuntimeError, match="nothing captured"):
         stack.replay()
-    layers[1].close()
+    stack.capture(x, kps, vps, table, lens)
+    # the stack holds its layers: closing one is refused while the stack
+    # (and the graph it captured) may still use the layer's buffers
+    with pytest.raises(ValueError, match="still used by a decode stack"):
+        layers[1].close()
+    stack.replay()
+    torch.cuda.synchronize()
+    stack.close()
     with pytest.raises(RuntimeError, match="has been closed"):
         stack(x, kps, vps, table, lens)
-    stack.close()
+    with pytest.raises(RuntimeError, match="has been closed"):
+        stack.replay()
+    layers[1].close()
     layers[0].close()
     other.close()
 

@@ -74,6 +74,33 @@ def test_prefill_bf16_large_v_tiles_take_the_split_path(d, causal):
 
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("prepass", [0, 2])
+def test_prefill_bf16_tiny_v_tiles_take_the_split_path(d, causal, prepass, tuning):
+    # fp16 holds a bf16 value exactly only for 2^-17 <= |v| < 2^16 (or 0):
+    # below, fp16 subnormals drop significant bits. A tile holding such a
+    # value must take the bf16 split path. With every V around 1e-7 the
+    # output is of that order too, so it is checked at 1e-2 relative (the
+    # fp16 product would be off by up to ~30% there); tiles 2 and 3 alone
+    # tiny run the hand-over, at the usual bar. Pre-pass and in-kernel vote.
+    tuning("FT_PREFILL_PREPASS", prepass)
+    rng = np.random.default_rng(60 + d + 2 * causal)
+    dt = torch.bfloat16
+    q, k, v = _inputs(rng, 1, 4, 2, 300, d, dt)
+    tiny = (v.float() * 1e-7).to(dt)
+    assert 0 < tiny.float().abs().max().item() < 2.0 ** -17
+    out = ft.attention_prefill(q, k, tiny, causal=causal)
+    ref = oracle.attention_prefill(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                                   tiny.float().cpu().numpy(), causal)
+    got = out.float().cpu().numpy()
+    excess = np.abs(got - ref) - (1e-12 + 1e-2 * np.abs(ref))
+    assert excess.max() <= 0, f"max excess {excess.max()}"
+    mixed = v.clone()
+    mixed[:, :, 130:200] = tiny[:, :, 130:200]
+    _check_half(ft.attention_prefill(q, k, mixed, causal=causal), q, k, mixed, causal)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("big", [False, True])
 def test_prefill_bf16_v_prepass_equals_in_kernel_conversion(d, causal, big, tuning):
     # bf16 inputs: V converted to fp16 by a pre-pass (with a per-tile range

@@ -287,3 +287,42 @@ def test_staged_vectors_read_in_place_or_through_a_copy(monkeypatch):
         assert ft.decode_step_batched(lt, hist, 1.2, p=0.9, temperature=0.8,
                                       seeds=seeds).tolist() == first
         assert ft.sample_topp_batched(lt, 0.9, temperature=0.8, seeds=seeds).tolist() == first_s
+
+
+def test_staged_vectors_change_every_call_with_no_sync(monkeypatch):
+    # Twelve calls queued back to back with device_out=True (no host sync),
+    # alternating decode_step_batched and sample_topp_batched (whose ring
+    # slots hold different layouts), each with its own seeds, histories and
+    # (p, T): a slot read stale, or refilled before the work that read it
+    # completed, would give another call's tokens. Every call is compared
+    # with the same call through the upload path afterwards. Two of the
+    # calls carry histories long enough (> IN_PLACE_MAX ids) to be uploaded.
+    from fusedtok_amd import _sampling_args as sargs
+    lib = ft._fusedtok
+    rng = np.random.default_rng(78)
+    rows, n = 12, 50000
+    lt = t((rng.standard_normal((rows, n)) * 2).astype(np.float32))
+    calls = []
+    for i in range(12):
+        seeds = [int(x) for x in rng.integers(0, 2 ** 40, rows)]
+        top = 800 if i in (4, 9) else 60
+        hist = [rng.integers(0, n, size=int(rng.integers(0, top))).tolist() for _ in range(rows)]
+        pt = [(0.9, 0.8), (0.5, 1.1), (0.95, 0.6)][i % 3]
+        calls.append((i % 2, seeds, hist, pt))
+    assert sum(len(h) for h in calls[4][2]) > sargs.IN_PLACE_MAX
+
+    def run(call, device_out):
+        kind, seeds, hist, (p, temp) = call
+        if kind == 0:
+            return ft.decode_step_batched(lt, hist, 1.3, p=p, temperature=temp, seeds=seeds,
+                                          device_out=device_out)
+        return ft.sample_topp_batched(lt, p, temperature=temp, seeds=seeds,
+                                      device_out=device_out)
+    outs = [run(c, True) for c in calls]
+    torch.cuda.synchronize()
+    got = [o.tolist() for o in outs]
+    assert len({tuple(g) for g in got}) == len(got)  # the calls really differ
+    monkeypatch.setattr(sargs, "_RING", sargs._PinnedRing())
+    monkeypatch.setattr(lib, "host_device_address", lambda ptr: 0)
+    for i, c in enumerate(calls):
+        assert run(c, False).tolist() == got[i], f"call {i}"

@@ -5,7 +5,10 @@ outputs must be equal bit for bit (the same kernels run; only the workspace
 differs), on two calls in a row, the second with a smaller input (fewer
 rows, a different GQA group), so the static array holds the first call's
 partials when the second starts. Both are also checked against the oracle.
-A call whose partials exceed the static array is rejected before launch."""
+A call whose partials exceed the static array is rejected before launch. The
+contiguous decode's allocation-failure fallback uses the same array: a
+fallback decode and a no-allocation call in turn on one stream both give
+their own results."""
 
 import ctypes
 import os
@@ -14,6 +17,7 @@ import numpy as np
 import pytest
 import torch
 
+import fusedtok_amd as ft  # the same library instance as the ctypes handle
 import oracle
 
 pytestmark = pytest.mark.gpu
@@ -97,3 +101,42 @@ def test_noalloc_rejects_a_call_beyond_the_static_workspace(lib):
             torch.cuda.current_stream().cuda_stream)
     assert rc == FT_EINVAL
     assert b"static workspace" in lib.ft_last_error()
+
+
+def test_fallback_decode_and_noalloc_calls_share_the_static_array(lib, tuning):
+    # The contiguous decode's allocation-failure fallback (FT_FAIL_SCRATCH
+    # forces it) and the no-allocation entry point both keep their split
+    # partials in the one static array of the device. Called one after the
+    # other on one stream, with no host sync between, each must still give
+    # its own result: the second call overwrites the array only after the
+    # first call's combine has read it.
+    bf = torch.bfloat16
+    rng = np.random.default_rng(61)
+    b, hq, hkv, tt, d = 2, 16, 4, 3000, 128
+    qc = torch.from_numpy(rng.standard_normal((b, hq, d)).astype(np.float32)).to(DEV, bf)
+    kc = torch.from_numpy(rng.standard_normal((b, hkv, tt, d)).astype(np.float32)).to(DEV, bf)
+    vc = torch.from_numpy(rng.standard_normal((b, hkv, tt, d)).astype(np.float32)).to(DEV, bf)
+    lc = torch.from_numpy(np.array([3000, 1777], np.int32)).to(DEV)
+    q, kp, vp, table, ln = paged_case(62, 6, 32, 8, 128, [4000, 17, 2048, 0, 999, 3333])
+    qt, kpt, vpt = (torch.from_numpy(a).to(DEV, bf) for a in (q, kp, vp))
+    tbl_t, ln_t = torch.from_numpy(table).to(DEV), torch.from_numpy(ln).to(DEV)
+    want_c = ft.attention_decode(qc, kc, vc, lc)
+    want_p = torch.empty((6, 32, d), dtype=bf, device=DEV)
+    run(lib, "ft_attention_decode_paged_launch_bf16", qt, kpt, vpt, tbl_t, ln_t, want_p)
+    torch.cuda.synchronize()
+    tuning("FT_FAIL_SCRATCH", 1)
+    for rep in range(2):
+        got_c = ft.attention_decode(qc, kc, vc, lc)  # partials in the static array
+        got_p = torch.full((6, 32, d), float("nan"), dtype=bf, device=DEV)
+        run(lib, "ft_attention_decode_paged_launch_bf16_noalloc", qt, kpt, vpt, tbl_t, ln_t,
+            got_p)
+        got_c2 = ft.attention_decode(qc, kc, vc, lc)
+        torch.cuda.synchronize()
+        assert torch.equal(got_c, want_c), f"rep {rep}: fallback decode differs"
+        assert torch.equal(got_p, want_p), f"rep {rep}: no-allocation decode differs"
+        assert torch.equal(got_c2, want_c), f"rep {rep}: second fallback decode differs"
+    tuning.clear("FT_FAIL_SCRATCH")
+    ref = oracle.attention_decode(qc.float().cpu().numpy(), kc.float().cpu().numpy(),
+                                  vc.float().cpu().numpy(), lc.cpu().numpy())
+    err = np.abs(want_c.float().cpu().numpy() - ref) - (2e-3 + 1e-2 * np.abs(ref))
+    assert err.max() <= 0
