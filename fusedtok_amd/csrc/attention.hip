@@ -1010,7 +1010,7 @@ int attention_run(const T* q, const T* k, const T* v, const int* table,
                 if (nwg <= (1 << 16)) {
                     const GridMax gm = gridmax_state((int)nwg, s);
                     if (grid_resident((const void*)attn_combine_quant<T>, (int)nwg,
-                                      64 * kCqWaves)) {
+                                      64 * kCqWaves, GridUse::AttnOut)) {
                         attn_combine_quant<T><<<(unsigned)nwg, 64 * kCqWaves, 0, s>>>(
                             ws_ml, ws_acc, pref, out, qcodes, qscale, batch, hq, hkv, group,
                             nseg, min_seg, gm);

@@ -113,8 +113,10 @@ enum class Tune : int {
                            // fails as an allocation failure would
     PrefillPrepass,        // FT_PREFILL_PREPASS: bf16 V to fp16 in a pre-pass
                            // (0 never: in the kernel; 1 large calls; 2 always)
-    GridSync,              // FT_GRID_SYNC: 1 = never fold a per-tensor maximum
-                           // inside one launch (grid_max); the two-launch forms
+    GridSync,              // FT_GRID_SYNC: bit mask of the per-tensor maxima not
+                           // to fold inside one launch (grid_max), which then
+                           // take their two-launch forms: 1 all, 2 SwiGLU,
+                           // 4 attention output, 8 RMSNorm
     kCount
 };
 // The switch's value, or `dflt` when it is neither in the environment nor
@@ -154,8 +156,9 @@ struct GridMax {
 GridMax gridmax_state(int nwg, hipStream_t s);
 // True when `nwg` workgroups of `kernel` (`threads` each, no dynamic LDS)
 // can all be resident at once on the current device, and FT_GRID_SYNC does
-// not forbid the in-launch maximum. runtime.hip.
-bool grid_resident(const void* kernel, int nwg, int threads);
+// not turn off the in-launch maximum of this kind (GridUse). runtime.hip.
+enum class GridUse : int { SwiGLU = 2, AttnOut = 4, RmsNorm = 8 };
+bool grid_resident(const void* kernel, int nwg, int threads, GridUse use);
 
 // Per-tensor int8 quantize of x[0, n) (T = float, bf16, f16) when its max |x|
 // is already known as the max of nparts partial maxima (written by the

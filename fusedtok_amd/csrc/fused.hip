@@ -529,7 +529,7 @@ void rmsq_rows_run(const T* x, const RmsqIo<T>& io, const float* w, const T* r,
         bool done = false;
         rmsq_pick<T, GridK>(r != nullptr, fk, fres, hout, [&](auto k) {
             using Kt = decltype(k);
-            if (!grid_resident((const void*)Kt::fn, rows, kFNT)) return;
+            if (!grid_resident((const void*)Kt::fn, rows, kFNT, GridUse::RmsNorm)) return;
             Kt::fn<<<(unsigned)rows, kFNT, 0, s>>>(x, r, w, cols, eps, io.fold,
                                                    io.store_x ? io.x_out : nullptr, io.h_out,
                                                    q, scale_out, gm);

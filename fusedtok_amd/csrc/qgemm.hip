@@ -2204,7 +2204,7 @@ int swiglu_max_launch(const i8* a, const i8* b, const Epi& e, int m, int inter, 
     dim3 grid(col_wgs, 1);
     int launched = 0;
     auto go = [&](auto kernel, int threads) {
-        if (sq.q && !grid_resident((const void*)kernel, col_wgs, threads)) sq = SwqGrid{};
+        if (sq.q && !grid_resident((const void*)kernel, col_wgs, threads, GridUse::SwiGLU)) sq = SwqGrid{};
         if (!sq.q && !e.y) return;  // the partials-only form needs y stored
         kernel<<<grid, threads, 0, s>>>(a, b, e, m, n, k, 1, nullptr, inter, part, sq);
         launch_check("qgemm swiglu-max kernel launch");

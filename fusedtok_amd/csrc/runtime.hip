@@ -179,8 +179,9 @@ GridMax gridmax_state(int nwg, hipStream_t s) {
     return GridMax{(unsigned long long*)p, (unsigned*)(p + 256)};
 }
 
-bool grid_resident(const void* kernel, int nwg, int threads) {
-    if (nwg < 1 || tune(Tune::GridSync, 0) == 1) return false;
+bool grid_resident(const void* kernel, int nwg, int threads, GridUse use) {
+    const int off = tune(Tune::GridSync, 0);
+    if (nwg < 1 || (off & 1) || (off & (int)use)) return false;
     const int dev = current_device();
     const int cus = dev_info().cu_count;
     static std::mutex mu;
