@@ -7,7 +7,8 @@ context lengths uniform in [512, 32768], block table a seeded random
 permutation of a page pool four times larger than the pages in use. One
 "step" is what a decode loop does per token: kv_append_paged of one new
 token per row at position lens[b], then attention_decode_paged over
-lens[b] + 1 tokens.
+lens[b] + 1 tokens - one call of attention_decode_paged_append, whose
+decode kernel appends the fresh token itself.
 
   value     = algorithmic bytes per step / measured step time   (GB/s)
               bytes: K+V rows read (sum_b (lens_b+1) * Hkv * D * 2 * 2 B),
@@ -15,10 +16,10 @@ lens[b] + 1 tokens.
               kv_append copy (read + write of the new K/V rows). This is the
               reference's counting (benchmarks/bench.py:480,496) plus the
               table and the append.
-  roofline  = attention only (attn_decode_stream + attn_combine_stream,
-              timed together with HIP events recorded on the stream they
-              are launched on): attention bytes / attention time, against
-              8 TB/s.
+  roofline  = the step's kernels (attn_decode_stream in its appending form
+              + attn_combine_stream, timed together with HIP events
+              recorded on the stream they are launched on): step bytes /
+              their time, against 8 TB/s.
   secondary = BASELINE config 5a: W8A8 GEMM M=4096 K=8192 N=28672, int8
               uniform in [-127, 127], per-channel scales, bf16 output;
               TOPS = 2*M*N*K / t (reference benchmarks/bench.py:451), against
@@ -158,10 +159,10 @@ def make_c3(torch, np, dev):
 
 
 def c3_step(ft, w):
-    ft.kv_append_paged(w["kp"], w["vp"], w["table_t"], w["kn"], w["vn"],
-                       w["lens_t"])
-    ft.attention_decode_paged(w["q"], w["kp"], w["vp"], w["table_t"],
-                              w["lens1_t"])
+    # kv_append_paged(..., lens) + attention_decode_paged(..., lens + 1) in
+    # one call: the decode kernel appends the fresh token itself
+    ft.attention_decode_paged_append(w["q"], w["kp"], w["vp"], w["table_t"], w["kn"],
+                                     w["vn"], w["lens_t"])
 
 
 def bench_c3(torch, np, ft, dev, steps, warmup):
@@ -175,11 +176,8 @@ def bench_c3(torch, np, ft, dev, steps, warmup):
           for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
-        ft.kv_append_paged(w["kp"], w["vp"], w["table_t"], w["kn"], w["vn"],
-                           w["lens_t"])
         ev[i][0].record(stream)
-        ft.attention_decode_paged(w["q"], w["kp"], w["vp"], w["table_t"],
-                                  w["lens1_t"])
+        c3_step(ft, w)
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -862,8 +860,8 @@ def main():
     step_bytes = w["attn_bytes"] + w["append_bytes"]
     ms_step = wall / args.steps * 1e3
     value = step_bytes / (wall / args.steps) / 1e9
-    attn_gbs = w["attn_bytes"] / (attn_ms * 1e-3) / 1e9
-    log(f"config 3: {ms_step:.4f} ms/step, {value:.1f} GB/s; attention "
+    attn_gbs = step_bytes / (attn_ms * 1e-3) / 1e9
+    log(f"config 3: {ms_step:.4f} ms/step, {value:.1f} GB/s; attention + append "
         f"{attn_ms * 1e3:.1f} us, {attn_gbs:.1f} GB/s")
     if args.only == "decode":
         return
@@ -939,8 +937,9 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) K/V/q, lens ~ U[512,32768], permuted page pool)",
         "config": {"workload": "BASELINE config 3: kv_append_paged + "
-                               "attention_decode_paged, bf16, B=32 Hq=32 Hkv=8 "
-                               "D=128 P=16",
+                               "attention_decode_paged (one call: "
+                               "attention_decode_paged_append), bf16, B=32 Hq=32 "
+                               "Hkv=8 D=128 P=16",
                    "seed": C3["seed"], "tokens": w["tokens"],
                    "pool_pages": w["pool_pages"], "used_pages": w["used_pages"],
                    "bytes_per_step": step_bytes, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
@@ -948,9 +947,10 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic_for("attention_c3"),
-                     "kernel": "attention_decode_paged = attn_decode_stream + attn_combine_stream",
+                     "kernel": "attention_decode_paged_append = attn_decode_stream "
+                               "(appending form) + attn_combine_stream",
                      "avg_us": round(attn_ms * 1e3, 2),
-                     "bytes_per_launch": w["attn_bytes"],
+                     "bytes_per_launch": step_bytes,
                      "copy_gbs": round(copy_gbs, 1) if copy_gbs else None,
                      "frac_of_copy": round(attn_gbs / copy_gbs, 4) if copy_gbs else None},
         "cpu_baseline": cpu,

@@ -86,6 +86,7 @@ __all__ = [
     "attention_decode",
     "attention_decode_paged",
     "attention_decode_paged_quant",
+    "attention_decode_paged_append",
     "attention_prefill",
     "kv_append",
     "kv_append_paged",
@@ -442,6 +443,46 @@ def kv_append_paged(k_pool, v_pool, block_table, k_new, v_new, lens, *,
         c.ptr("k_new"), c.ptr("v_new"), c.ptr("block_table"), c.ptr("lens"),
         c.ptr("k_pool"), c.ptr("v_pool"), c.B, c.Hkv, c.D, c.P, c.S, _stream())
     return None
+
+
+_DECODE_APPEND = _Contract(
+    _Arr("q", "B Hq D"),
+    _Arr("k_pool", "Nb Hkv P D", same_dtype="q", inplace=True,
+         mismatch="pools must match q's dim and each other"),
+    _Arr("v_pool", "=k_pool", same_dtype="q", inplace=True,
+         mismatch="pools must match q's dim and each other"),
+    _Arr("k_new", "B Hkv D", same_dtype="q", mismatch=_NEW_KV_MISMATCH,
+         rank_msg="k_new/v_new must be [B, Hkv, D]"),
+    _Arr("v_new", "=k_new", same_dtype="q", mismatch=_NEW_KV_MISMATCH),
+    _table(),
+    _Idx("lens", "B", lambda c: c.S * c.P, open_bound=True, what=_LENS_WHAT),
+    rank_msg="q must be [B, Hq, D]; pools [Nb, Hkv, P, D]",
+    rules=(_HEADS, _GQA, _PAGED_GROUP), host_rules=(_DIM_HOST,))
+
+
+def attention_decode_paged_append(q, k_pool, v_pool, block_table, k_new, v_new, lens):
+    """One decode step over a paged cache: ``kv_append_paged(k_pool, v_pool,
+    block_table, k_new, v_new, lens)`` then ``attention_decode_paged(q,
+    k_pool, v_pool, block_table, lens + 1)``, in one call (lens is not
+    modified). GPU tensors only. For bf16 / fp16 with D = 128 the decode
+    kernel takes the fresh token itself (merged into the row's online
+    softmax in float32: the output equals the two ops' within the attention
+    tolerance, the pools bit for bit) and writes it into the pools, one
+    launch fewer; other shapes run the two ops. Build addition: the
+    reference runs the two ops (``attention.cu:1924-1966``, then
+    ``attention.cu:1785-1900``)."""
+    c = _DECODE_APPEND.bind(q=q, k_pool=k_pool, v_pool=v_pool, k_new=k_new, v_new=v_new,
+                            block_table=block_table, lens=lens)
+    if not c.on_gpu:
+        raise TypeError("attention_decode_paged_append takes GPU tensors (fused ops have no "
+                        "host path)")
+    out = torch.empty((c.B, c.Hq, c.D), dtype=c.q.dtype, device=c.device)
+    if c.B:
+        _fusedtok.attention_decode_paged_append_launch(
+            c.ptr("q"), c.ptr("k_pool"), c.ptr("v_pool"), c.ptr("block_table"),
+            c.ptr("k_new"), c.ptr("v_new"), c.ptr("lens"), out.data_ptr(),
+            _CODE[c.q.dtype], c.B, c.Hq, c.Hkv, c.P, c.S, c.D, _stream())
+    return out
 
 
 _APPEND = _Contract(

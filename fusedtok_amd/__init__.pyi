@@ -29,6 +29,7 @@ __all__ = [
     "attention_decode",
     "attention_decode_paged",
     "attention_decode_paged_quant",
+    "attention_decode_paged_append",
     "attention_prefill",
     "kv_append",
     "kv_append_paged",
@@ -71,6 +72,10 @@ def attention_decode_paged_quant(q: torch.Tensor, k_pool: torch.Tensor, v_pool: 
                                  lens: Optional[torch.Tensor] = ..., *,
                                  device_scale: bool = ...
                                  ) -> Tuple[torch.Tensor, torch.Tensor, Scale]: ...
+def attention_decode_paged_append(q: torch.Tensor, k_pool: torch.Tensor,
+                                  v_pool: torch.Tensor, block_table: torch.Tensor,
+                                  k_new: torch.Tensor, v_new: torch.Tensor,
+                                  lens: torch.Tensor) -> torch.Tensor: ...
 def attention_prefill(q: Array, k: Array, v: Array, causal: bool = ..., *,
                       cuda: bool = ...) -> Array: ...
 def kv_append(k_cache: Array, v_cache: Array, k_new: Array, v_new: Array,

@@ -24,6 +24,7 @@
 //   attn_chunk_generic any storage type, D % 4 == 0 <= 512, any G: VALU
 //     + attn_combine   dot products, chunk scores staged in LDS; the grid
 //                      covers the cache capacity in fixed chunks.
+#include <climits>
 #include "ft_common.hpp"
 
 #include <algorithm>
@@ -359,7 +360,37 @@ __device__ __forceinline__ long long stream_seg_len(long long total, int nseg, i
     return s < min_seg ? (long long)min_seg : s;
 }
 
-template <typename T, int MODE>
+// The fresh token of the appending decode: ap.k_new / ap.v_new [batch, hkv,
+// D], written at position lens[b] of row (b, kv) in the pools ap.k_pool /
+// ap.v_pool (the K / V the decode kernel reads, as writable pointers) when
+// 0 <= lens[b] < span, and attended with the row's lens[b] cached tokens.
+template <typename T>
+struct AppendArgs {
+    const T* k_new = nullptr;
+    const T* v_new = nullptr;
+    T* k_pool = nullptr;
+    T* v_pool = nullptr;
+};
+
+// Element offset of row (b, kv)'s cache position t in a pool.
+template <int MODE>
+__device__ __forceinline__ size_t kv_row_offset(const int* table, int b, int kv, int t, int hkv,
+                                                int rows_or_page, int page_shift,
+                                                int tbl_width) {
+    constexpr int D = kMfmaDim;
+    if constexpr (MODE == kRowsContig) {
+        return ((size_t)(b * hkv + kv) * rows_or_page + t) * D;
+    } else {
+        const int pg = MODE == kRowsPagedPow2 ? (t >> page_shift) : (t / rows_or_page);
+        const int in_pg = MODE == kRowsPagedPow2 ? (t & (rows_or_page - 1)) : (t % rows_or_page);
+        const int ent = table[(size_t)b * tbl_width + pg];
+        return (((size_t)ent * hkv + kv) * rows_or_page + in_pg) * D;
+    }
+}
+
+// NEW (the appending decode): every piece, whole rows included, leaves its
+// partial for attn_combine_append, which folds the fresh token in.
+template <typename T, int MODE, bool NEW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_decode_stream(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
@@ -421,7 +452,6 @@ void attn_decode_stream(
         const bool whole = (t0 == 0 && n == len);
         const int row = b * hkv + kv;
         const int* trow = PAGED ? table + (size_t)b * tbl_width : nullptr;
-
         // B operand of the score MFMAs: Q[head r][32j + 8g .. +7]
         V8 qb[4];
         {
@@ -638,7 +668,7 @@ void attn_decode_stream(
                 const float4 a = *reinterpret_cast<const float4*>(&s_acc[w][hh][4 * d4]);
                 o.x += wt * a.x; o.y += wt * a.y; o.z += wt * a.z; o.w += wt * a.w;
             }
-            if (whole) {
+            if (whole && !NEW) {
                 const float inv = 1.0f / lsum;
                 St<T>::st4(orow + (size_t)hh * D + 4 * d4,
                            make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv));
@@ -671,7 +701,7 @@ __device__ __forceinline__ float4 combine_head(const float* __restrict__ ws_ml,
                                                const long long* __restrict__ pref,
                                                T* __restrict__ out, int bh, int batch, int hq,
                                                int hkv, int group, int nseg, int min_seg,
-                                               int lane) {
+                                               int lane, bool skip_empty = false) {
     constexpr int D = kMfmaDim;
     const int b = bh / hq;
     const int h = bh - b * hq;
@@ -679,8 +709,9 @@ __device__ __forceinline__ float4 combine_head(const float* __restrict__ ws_ml,
     T* o = out + (size_t)bh * D;
     const int len = (int)(pref[b + 1] - pref[b]);
     const int d4 = lane & 31;
-    if (len == 0) {
-        if (lane < D / 4) St<T>::st4(o + 4 * lane, make_float4(0.f, 0.f, 0.f, 0.f));
+    if (len == 0) {  // (skip_empty: written by the decode kernel)
+        if (!skip_empty && lane < D / 4)
+            St<T>::st4(o + 4 * lane, make_float4(0.f, 0.f, 0.f, 0.f));
         return make_float4(0.f, 0.f, 0.f, 0.f);
     }
     const long long S = stream_seg_len(pref[batch] * hkv, nseg, min_seg);
@@ -730,18 +761,105 @@ __device__ __forceinline__ float head_absmax(float4 v) {
 }
 
 // AMAX: the max |stored output| of each head into amax[b * hq + h], which
-// the per-tensor quantize of the output folds
+// the per-tensor quantize of the output folds. skip_empty: rows of length 0
+// were written by the decode kernel (its append form).
 template <typename T, bool AMAX>
 __global__ __launch_bounds__(64) void attn_combine_stream(
     const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
     const long long* __restrict__ pref, T* __restrict__ out, float* __restrict__ amax,
-    int batch, int hq, int hkv, int group, int nseg, int min_seg) {
+    int batch, int hq, int hkv, int group, int nseg, int min_seg, int skip_empty) {
     const float4 v = combine_head<T>(ws_ml, ws_acc, pref, out, blockIdx.x, batch, hq, hkv,
-                                     group, nseg, min_seg, threadIdx.x);
+                                     group, nseg, min_seg, threadIdx.x, skip_empty != 0);
     if constexpr (AMAX) {
         const float m = head_absmax(v);
         if (threadIdx.x == 0) amax[blockIdx.x] = m;
     }
+}
+
+// Combine of the appending decode (attention_append_run), one wave per
+// (b, q head). Every piece of row (b, kv) was left as a partial (whole rows
+// too); the fresh token - score q . k_new, value v_new - is folded in with
+// them by the log-sum-exp rule, in float32, and the wave of the group's
+// first q head writes k_new / v_new to position lens[b] of the pools (the
+// decode kernel has finished reading them). A row with no cached token gets
+// v_new alone (softmax weight 1: exactly v_new), or zeros when lens[b] has
+// no room in the row or is negative (kv_append_paged then writes nothing).
+template <typename T, int MODE>
+__global__ __launch_bounds__(64) void attn_combine_append(
+    const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
+    const long long* __restrict__ pref, const int* __restrict__ lens, const T* __restrict__ q,
+    AppendArgs<T> ap, const int* __restrict__ table, T* __restrict__ out, int batch, int hq,
+    int hkv, int group, int nseg, int min_seg, int span, int rows_or_page, int page_shift,
+    int tbl_width, float scale_log2) {
+    constexpr int D = kMfmaDim;
+    const int bh = blockIdx.x, lane = threadIdx.x;
+    const int b = bh / hq, h = bh - b * hq;
+    const int kv = h / group, gi = h - kv * group;
+    const int d4 = lane & 31;
+    T* o = out + (size_t)bh * D;
+    const int len = (int)(pref[b + 1] - pref[b]);
+    const int raw = lens[b];
+    const bool fresh = raw >= 0 && raw < span;  // then raw == len
+    // the fresh token: lane d4 takes dims 4 d4 .. + 3 (lanes 32-63 again)
+    float sv = -INFINITY;
+    float4 vn = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (fresh) {
+        const size_t nrow = ((size_t)b * hkv + kv) * D + 4 * d4;
+        const float4 qq = St<T>::ld4(q + (size_t)bh * D + 4 * d4);
+        const float4 kk = St<T>::ld4(ap.k_new + nrow);
+        vn = St<T>::ld4(ap.v_new + nrow);
+        float dot = qq.x * kk.x;
+        dot = fmaf(qq.y, kk.y, dot);
+        dot = fmaf(qq.z, kk.z, dot);
+        dot = fmaf(qq.w, kk.w, dot);
+#pragma unroll
+        for (int o2 = 16; o2 > 0; o2 >>= 1) dot += __shfl_xor(dot, o2, 64);
+        sv = dot * scale_log2;
+        if (gi == 0 && lane < 32) {
+            const size_t dst = kv_row_offset<MODE>(table, b, kv, raw, hkv, rows_or_page,
+                                                   page_shift, tbl_width) + 4 * d4;
+            St<T>::st4(ap.k_pool + dst, kk);
+            St<T>::st4(ap.v_pool + dst, vn);
+        }
+    }
+    int s_lo = 0, np = 0;
+    if (len > 0) {
+        const long long S = stream_seg_len(pref[batch] * hkv, nseg, min_seg);
+        const long long start = pref[b] * hkv + (long long)kv * len;
+        s_lo = (int)(start / S);
+        np = (int)((start + len - 1) / S) - s_lo + 1;
+    }
+    const int row = b * hkv + kv;
+    auto slot = [&](int i) { return ((size_t)s_lo + i + row) * group + gi; };
+    float mx = sv;
+    for (int i = lane; i < np; i += 64) mx = fmaxf(mx, ws_ml[slot(i) * 2]);
+    mx = wave_max(mx);
+    if (mx == -INFINITY) {  // no token at all
+        if (lane < D / 4) St<T>::st4(o + 4 * lane, make_float4(0.f, 0.f, 0.f, 0.f));
+        return;
+    }
+    float lsum = 0.0f;
+    for (int i = lane; i < np; i += 64)
+        lsum += ws_ml[slot(i) * 2 + 1] * exp2f(ws_ml[slot(i) * 2] - mx);
+    lsum = wave_sum(lsum);
+    const float pn = fresh ? exp2f(sv - mx) : 0.0f;
+    lsum += pn;
+    const int grp = lane >> 5;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+    for (int i = grp; i < np; i += 2) {
+        const size_t sl = slot(i);
+        const float wt = exp2f(ws_ml[sl * 2] - mx);
+        const float4 x = *reinterpret_cast<const float4*>(ws_acc + sl * D + 4 * d4);
+        a.x += wt * x.x; a.y += wt * x.y; a.z += wt * x.z; a.w += wt * x.w;
+    }
+    a.x += __shfl_xor(a.x, 32, 64);
+    a.y += __shfl_xor(a.y, 32, 64);
+    a.z += __shfl_xor(a.z, 32, 64);
+    a.w += __shfl_xor(a.w, 32, 64);
+    a.x += pn * vn.x; a.y += pn * vn.y; a.z += pn * vn.z; a.w += pn * vn.w;
+    const float inv = 1.0f / lsum;
+    if (grp == 0) St<T>::st4(o + 4 * d4, make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv));
 }
 
 // The combine and the per-tensor int8 quantize of the output in one launch:
@@ -895,24 +1013,28 @@ bool mfma_eligible(const T* q, const T* k, const T* v, int group, int dim) {
 
 // attn_decode_stream in the row mode of the layout (paged with a power-of-2
 // page, paged with any page, contiguous).
+// fresh: the appending decode's form (NEW).
 template <typename T>
 void launch_stream(bool paged, int page_shift, int nseg, hipStream_t s, const T* q,
                    const T* k, const T* v, const int* table, const int* lens, float* ws_ml,
                    float* ws_acc, long long* pref, T* out, int batch, int hq, int hkv,
                    int group, int rows_or_page, int tbl_width, int span, float scale_log2,
-                   int min_seg) {
-    if (paged && page_shift >= 0)
-        attn_decode_stream<T, kRowsPagedPow2><<<(unsigned)nseg, 256, 0, s>>>(
-            q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
-            rows_or_page, page_shift, tbl_width, span, scale_log2, min_seg);
-    else if (paged)
-        attn_decode_stream<T, kRowsPagedDiv><<<(unsigned)nseg, 256, 0, s>>>(
-            q, k, v, table, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
-            rows_or_page, -1, tbl_width, span, scale_log2, min_seg);
-    else
-        attn_decode_stream<T, kRowsContig><<<(unsigned)nseg, 256, 0, s>>>(
-            q, k, v, nullptr, lens, ws_ml, ws_acc, pref, out, batch, hq, hkv, group,
-            rows_or_page, -1, 0, span, scale_log2, min_seg);
+                   int min_seg, bool fresh) {
+    auto go = [&](auto kernel, const int* tbl, int shift, int width) {
+        kernel<<<(unsigned)nseg, 256, 0, s>>>(q, k, v, tbl, lens, ws_ml, ws_acc, pref, out,
+                                              batch, hq, hkv, group, rows_or_page, shift,
+                                              width, span, scale_log2, min_seg);
+    };
+    if (paged && page_shift >= 0) {
+        if (fresh) go(attn_decode_stream<T, kRowsPagedPow2, true>, table, page_shift, tbl_width);
+        else go(attn_decode_stream<T, kRowsPagedPow2, false>, table, page_shift, tbl_width);
+    } else if (paged) {
+        if (fresh) go(attn_decode_stream<T, kRowsPagedDiv, true>, table, -1, tbl_width);
+        else go(attn_decode_stream<T, kRowsPagedDiv, false>, table, -1, tbl_width);
+    } else {
+        if (fresh) inval("attention: the append form is paged only");
+        go(attn_decode_stream<T, kRowsContig, false>, nullptr, -1, 0);
+    }
 }
 
 // Device workspace of one decode call (split partials and the length
@@ -956,7 +1078,7 @@ int attention_run(const T* q, const T* k, const T* v, const int* table,
                    int rows_or_page, int tbl_width, int dim, bool paged,
                    hipStream_t s, const Workspace& wsp = Workspace{},
                    float* amax = nullptr, signed char* qcodes = nullptr,
-                   float* qscale = nullptr) {
+                   float* qscale = nullptr, const AppendArgs<T>& ap = AppendArgs<T>{}) {
     long long span;
     if (paged) {
         span = (long long)tbl_width * rows_or_page;
@@ -1000,10 +1122,26 @@ int attention_run(const T* q, const T* k, const T* v, const int* table,
             float* ws_ml = (float*)ws;
             float* ws_acc = ws_ml + ml_floats;
             long long* pref = (long long*)(ws_acc + acc_floats);
+            if (ap.k_new && (amax || qcodes))
+                inval("attention: the append form keeps no per-head maxima");
             launch_stream<T>(paged, page_shift, nseg, s, q, k, v, table, lens, ws_ml, ws_acc,
                              pref, out, batch, hq, hkv, group, rows_or_page, tbl_width,
-                             (int)span, scale_log2, min_seg);
+                             (int)span, scale_log2, min_seg, ap.k_new != nullptr);
             launch_check("attention decode kernel launch");
+            if (ap.k_new) {
+                const unsigned grid = (unsigned)((long long)batch * hq);
+                if (page_shift >= 0)
+                    attn_combine_append<T, kRowsPagedPow2><<<grid, 64, 0, s>>>(
+                        ws_ml, ws_acc, pref, lens, q, ap, table, out, batch, hq, hkv, group,
+                        nseg, min_seg, (int)span, rows_or_page, page_shift, tbl_width,
+                        scale_log2);
+                else
+                    attn_combine_append<T, kRowsPagedDiv><<<grid, 64, 0, s>>>(
+                        ws_ml, ws_acc, pref, lens, q, ap, table, out, batch, hq, hkv, group,
+                        nseg, min_seg, (int)span, rows_or_page, -1, tbl_width, scale_log2);
+                launch_check("attention combine + append kernel launch");
+                return 0;
+            }
             if (qcodes) {
                 const long long heads = (long long)batch * hq;
                 const long long nwg = (heads + kCqWaves - 1) / kCqWaves;
@@ -1021,14 +1159,15 @@ int attention_run(const T* q, const T* k, const T* v, const int* table,
             }
             if (amax)
                 attn_combine_stream<T, true><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
-                    ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group, nseg, min_seg);
+                    ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group, nseg, min_seg, 0);
             else
                 attn_combine_stream<T, false><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
-                    ws_ml, ws_acc, pref, out, nullptr, batch, hq, hkv, group, nseg, min_seg);
+                    ws_ml, ws_acc, pref, out, nullptr, batch, hq, hkv, group, nseg, min_seg, 0);
             launch_check("attention combine kernel launch");
             return amax ? 1 : 0;
         }
     }
+    if (ap.k_new) inval("attention: the append form runs on the stream kernel only");
     const long long target = (long long)dev_info().cu_count * 16;
     int chunk = choose_chunk(batch, hkv, span, 64, kGenMaxChunk, target);
     const int forced = tune(Tune::AttnChunk, 0);
@@ -1128,6 +1267,52 @@ void kv_append_run(const T* k_new, const T* v_new, const int* table,
     kv_append_kernel<T><<<(unsigned)(batch * per_row), 256, 0, s>>>(
         k_new, v_new, lens, rm, (int)cap, per_row, k_dst, v_dst);
     launch_check("kv append kernel launch");
+}
+
+__global__ __launch_bounds__(256) void lens_plus1_kernel(const int* __restrict__ lens,
+                                                         int* __restrict__ out, int batch) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < batch) out[i] = lens[i] == INT_MAX ? INT_MAX : lens[i] + 1;
+}
+
+// kv_append_paged(k_pool, v_pool, table, k_new, v_new, lens) followed by
+// attention_decode_paged(q, k_pool, v_pool, table, lens + 1), in one call.
+// On the stream path (bf16 / fp16, D = 128) the decode kernel does the
+// append itself: the row's last piece takes the fresh token from k_new /
+// v_new (a merge into its online softmax in float32) and writes it to the
+// pools, and rows with no cached token are written by workgroup 0 - one
+// launch fewer. Elsewhere: the two ops, lens + 1 through library scratch.
+template <typename T>
+void attention_append_run(const T* q, T* k_pool, T* v_pool, const int* table, const T* k_new,
+                          const T* v_new, const int* lens, T* out, int batch, int hq, int hkv,
+                          int page, int tbl_width, int dim, hipStream_t s) {
+    if (batch < 0) inval("batch must be >= 0");
+    if (batch == 0) return;
+    if (!lens || !k_new || !v_new) inval("attention append: null operand");
+    const long long span = (long long)tbl_width * page;
+    const int group = hkv > 0 ? hq / hkv : 0;
+    const bool fast = !std::is_same<T, float>::value && hkv > 0 && hq % hkv == 0 &&
+                      mfma_eligible(q, k_pool, v_pool, group, dim) &&
+                      (uintptr_t)k_new % 16 == 0 && (uintptr_t)v_new % 16 == 0 &&
+                      batch <= kStreamScanRows && tune(Tune::AttnForceGeneric, 0) == 0 &&
+                      span > 0 && page >= 1 && tbl_width >= 0;
+    if (fast) {
+        AppendArgs<T> ap;
+        ap.k_new = k_new;
+        ap.v_new = v_new;
+        ap.k_pool = k_pool;
+        ap.v_pool = v_pool;
+        attention_run<T>(q, k_pool, v_pool, table, lens, out, batch, hq, hkv, page, tbl_width,
+                         dim, true, s, Workspace{}, nullptr, nullptr, nullptr, ap);
+        return;
+    }
+    kv_append_run<T>(k_new, v_new, table, lens, k_pool, v_pool, batch, hkv, dim, page,
+                     tbl_width, true, s);
+    int* lens1 = (int*)scratch(Scratch::AttnLens, (size_t)batch * sizeof(int), s);
+    lens_plus1_kernel<<<(unsigned)((batch + 255) / 256), 256, 0, s>>>(lens, lens1, batch);
+    launch_check("lens + 1 kernel launch");
+    attention_run<T>(q, k_pool, v_pool, table, lens1, out, batch, hq, hkv, page, tbl_width, dim,
+                     true, s);
 }
 
 }  // namespace
@@ -1239,6 +1424,39 @@ int ft_attention_decode_paged_quant_launch(const void* q, const void* k_pool,
             break;
         default:
             ft::inval("attention quantize: unknown dtype code");
+        }
+    });
+}
+
+int ft_attention_decode_paged_append_launch(const void* q, void* k_pool, void* v_pool,
+                                            const int* table, const void* k_new,
+                                            const void* v_new, const int* lens, void* out,
+                                            int dtype, int batch, int q_heads, int kv_heads,
+                                            int page, int tbl_width, int dim,
+                                            uintptr_t stream) {
+    return ft::guarded([&] {
+        hipStream_t s = ft::as_stream(stream);
+        switch (dtype) {
+        case FT_DT_F32:
+            ft::attention_append_run<float>((const float*)q, (float*)k_pool, (float*)v_pool,
+                                            table, (const float*)k_new, (const float*)v_new,
+                                            lens, (float*)out, batch, q_heads, kv_heads, page,
+                                            tbl_width, dim, s);
+            break;
+        case FT_DT_BF16:
+            ft::attention_append_run<bf16>((const bf16*)q, (bf16*)k_pool, (bf16*)v_pool, table,
+                                           (const bf16*)k_new, (const bf16*)v_new, lens,
+                                           (bf16*)out, batch, q_heads, kv_heads, page,
+                                           tbl_width, dim, s);
+            break;
+        case FT_DT_F16:
+            ft::attention_append_run<f16>((const f16*)q, (f16*)k_pool, (f16*)v_pool, table,
+                                          (const f16*)k_new, (const f16*)v_new, lens,
+                                          (f16*)out, batch, q_heads, kv_heads, page, tbl_width,
+                                          dim, s);
+            break;
+        default:
+            ft::inval("attention append: unknown dtype code");
         }
     });
 }

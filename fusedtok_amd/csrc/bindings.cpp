@@ -136,6 +136,20 @@ PYBIND11_MODULE(_fusedtok, m) {
           py::arg("scale"), py::arg("batch"), py::arg("q_heads"), py::arg("kv_heads"),
           py::arg("page"), py::arg("tbl_width"), py::arg("dim"), py::arg("stream") = 0);
 
+    m.def("attention_decode_paged_append_launch",
+          [](uintptr_t q, uintptr_t kp, uintptr_t vp, uintptr_t table, uintptr_t kn,
+             uintptr_t vn, uintptr_t lens, uintptr_t out, int dtype, int batch, int hq,
+             int hkv, int page, int tbl_width, int dim, uintptr_t stream) {
+              check(ft_attention_decode_paged_append_launch(
+                  P<const void>(q), P<void>(kp), P<void>(vp), P<const int>(table),
+                  P<const void>(kn), P<const void>(vn), P<const int>(lens), P<void>(out),
+                  dtype, batch, hq, hkv, page, tbl_width, dim, stream));
+          },
+          py::arg("q"), py::arg("k_pool"), py::arg("v_pool"), py::arg("table"),
+          py::arg("k_new"), py::arg("v_new"), py::arg("lens"), py::arg("out"),
+          py::arg("dtype"), py::arg("batch"), py::arg("q_heads"), py::arg("kv_heads"),
+          py::arg("page"), py::arg("tbl_width"), py::arg("dim"), py::arg("stream") = 0);
+
     // ---- kv append --------------------------------------------------------
 #define FT_KVP(NAME, FN, T)                                                    \
     m.def(NAME,                                                                \

@@ -134,7 +134,8 @@ enum class Scratch : int {
     Sampling = 3,
     PrefillV = 4,
     GridSync = 5,  // grid_max state (gridmax_state)
-    kCount = 6
+    AttnLens = 6,  // lens + 1 of the two-op form of the appending decode
+    kCount = 7
 };
 void* scratch(Scratch which, size_t bytes, hipStream_t s);
 // Same, but memory is zero when first allocated (or re-allocated); kernels

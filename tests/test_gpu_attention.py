@@ -251,6 +251,61 @@ def test_stream_lds_staging_matches_oracle_and_repeats(dt):
                                                     rounded(ovp, dt), otbl, oln), "page 5")
 
 
+@pytest.mark.parametrize("dt", [torch.float32] + HALF)
+@pytest.mark.parametrize("group,page", [(1, 16), (4, 16), (8, 5), (16, 16)])
+@pytest.mark.parametrize("min_seg", [32, 512])
+def test_paged_append_decode_equals_the_two_ops(dt, group, page, min_seg, tuning):
+    # attention_decode_paged_append == kv_append_paged, then
+    # attention_decode_paged(lens + 1): the pools bit for bit; the output
+    # within the attention tolerance (the fresh token is merged in float32
+    # by the stream kernel; f32 storage runs the two ops: bit for bit),
+    # also against the oracle on the appended pools. Rows: empty (the fresh
+    # token alone), one token, page - 1, page, full (no room: nothing
+    # appended), one short of full, negative (nothing appended, zeros),
+    # longer ones; small segments split the rows into many pieces. Three
+    # steps in a row, lens + 1 each time.
+    tuning("FT_ATTN_MIN_SEG", min_seg)
+    rng = np.random.default_rng(group * 100 + page + min_seg + (0 if dt is torch.float32 else
+                                                                7 if dt is torch.float16 else 11))
+    hkv, d = 2, 128
+    hq = hkv * group
+    lens0 = [0, 1, page - 1, page, 0, 0, -1, 37, 300, 1027]
+    width = (1027 + 3 + page - 1) // page + 1
+    cap = width * page
+    lens0[4], lens0[5] = cap, cap - 1
+    b = len(lens0)
+    q, kp, vp, tbl, _ = paged_case(rng, b, hq, hkv, d, [cap] * b, page=page)
+    kp1, vp1 = t(kp, dt), t(vp, dt)
+    kp2, vp2 = kp1.clone(), vp1.clone()
+    qt, tblt = t(q, dt), t(tbl)
+    lens = np.array(lens0, np.int32)
+    for step in range(3):
+        kn = t(rng.standard_normal((b, hkv, d)).astype(np.float32), dt)
+        vn = t(rng.standard_normal((b, hkv, d)).astype(np.float32), dt)
+        lt = t(lens)
+        out1 = ft.attention_decode_paged_append(qt, kp1, vp1, tblt, kn, vn, lt)
+        ft.kv_append_paged(kp2, vp2, tblt, kn, vn, lt)
+        out2 = ft.attention_decode_paged(qt, kp2, vp2, tblt, t(lens + 1))
+        torch.cuda.synchronize()
+        assert torch.equal(kp1, kp2) and torch.equal(vp1, vp2), f"step {step}: pools differ"
+        assert torch.equal(t(lens), lt), "lens modified"
+        if dt is torch.float32:
+            assert torch.equal(out1, out2), f"step {step}"
+        else:
+            got = out1.float().cpu().numpy()
+            assert_half_close(got, out2.float().cpu().numpy(), f"step {step} vs two ops")
+            ref = oracle.attention_decode_paged(rounded(q, dt), kp1.float().cpu().numpy(),
+                                                vp1.float().cpu().numpy(), tbl,
+                                                np.clip(lens + 1, 0, cap).astype(np.int32))
+            assert_half_close(got, ref, f"step {step} vs oracle")
+            # the empty row: the fresh token's V exactly; the negative one: zeros
+            if step == 0:
+                assert torch.equal(out1[0].view(hkv, group, d),
+                                   vn[0].unsqueeze(1).expand(hkv, group, d))
+                assert (out1[6].float() == 0).all()
+        lens = lens + 1
+
+
 def test_paged_equals_contiguous_materialisation():
     rng = np.random.default_rng(41)
     q, kp, vp, tbl, ln = paged_case(rng, 3, 8, 2, 64, [37, 16, 48])
