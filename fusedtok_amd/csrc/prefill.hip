@@ -98,28 +98,35 @@ __device__ __forceinline__ int pack2(float a, float b) {
 
 // two bf16 (one dword) -> two fp16, exact for v = 0 and 2^-17 <= |v| < 2^16:
 // fp16 keeps a bf16 value's 8 significant bits down to 2^-14 as a normal
-// number and down to 2^-17 as a subnormal (step 2^-24); smaller values lose
-// bits or flush to zero
+// number and down to 2^-17 as a subnormal (step 2^-24); smaller values are
+// rounded to that 2^-24 grid (an error of at most 2^-25)
 __device__ __forceinline__ unsigned bf2_to_h2(unsigned w) {
     return (unsigned)pack2<f16>(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
 }
 
-// |bf16| bit patterns of the fp16-exact range: every value with bits b in
-// {0} or [kF16Lo, kF16Hi) converts exactly (inf and NaN are above kF16Hi)
-constexpr unsigned kF16Lo = 0x3700u;  // 2^-17
-constexpr unsigned kF16Hi = 0x4780u;  // 2^16
+// |bf16| bit patterns. A tile takes the fp16 PV product when its largest
+// |v| (its scale) lies in [kF16Scale, kF16Hi): every value from 2^-17 up
+// then converts exactly, and a smaller one is off by at most 2^-25 = 2^-17
+// of the scale (bf16's own step is 2^-8 of a value), an absolute error of
+// at most 2^-25 in the output, whose weights sum to 1. A tile whose values
+// are all small (a scaled-down V) takes the bf16 split product, exact in
+// V, so its outputs keep their relative precision. Inf and NaN are above
+// kF16Hi.
+constexpr unsigned kF16Scale = 0x3B80u;  // 2^-8
+constexpr unsigned kF16Hi = 0x4780u;     // 2^16
 
-// running maximum of the |v| bit patterns and minimum of (bits - 1) of two
-// bf16 lanes (per 16-bit lane, so a zero wraps to 0xffff and never counts
-// as small)
+// running maximum of the |v| bit patterns of two bf16 lanes
 typedef unsigned short us2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ void f16_range_acc(unsigned w, us2_t& mx, us2_t& mn) {
-    const us2_t b = __builtin_bit_cast(us2_t, w & 0x7fff7fffu);
-    mx = __builtin_elementwise_max(mx, b);
-    mn = __builtin_elementwise_min(mn, b - us2_t{1, 1});
+__device__ __forceinline__ void f16_range_acc(unsigned w, us2_t& mx) {
+    mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2_t, w & 0x7fff7fffu));
 }
-__device__ __forceinline__ bool f16_range_bad(us2_t mx, us2_t mn) {
-    return mx[0] >= kF16Hi || mx[1] >= kF16Hi || mn[0] < kF16Lo - 1 || mn[1] < kF16Lo - 1;
+// the workgroup's vote (every thread calls it): whether the tile whose
+// pieces the threads' mx cover takes the fp16 product
+__device__ __forceinline__ bool f16_tile_ok(us2_t mx) {
+    const unsigned m = mx[0] > mx[1] ? mx[0] : mx[1];
+    const int too_big = __syncthreads_or(m >= kF16Hi ? 1 : 0);
+    const int has_scale = __syncthreads_or(m >= kF16Scale ? 1 : 0);
+    return !too_big && has_scale;
 }
 
 // maximum over lanes l, l ^ 16, l ^ 32, l ^ 48 without LDS: with both
@@ -136,9 +143,9 @@ __device__ __forceinline__ float max4_rows(float x) {
 }
 
 // V of bf16 inputs converted to fp16 once per call (one workgroup per
-// 64-key tile of a (b, kv head) slab), with a flag per tile: 1 when every
-// v of the tile is 0 or 2^-17 <= |v| < 2^16 (the conversion is then exact
-// and the tile takes the fp16 PV product). The attention kernel then stages those tiles
+// 64-key tile of a (b, kv head) slab), with a flag per tile: 1 when the
+// tile's largest |v| is in [2^-8, 2^16) (f16_tile_ok: the tile then takes
+// the fp16 PV product). The attention kernel then stages those tiles
 // as they are, instead of converting and voting in every one of the
 // workgroups that read the tile (Hq / Hkv heads x S / 128 query tiles).
 __global__ __launch_bounds__(256) void prefill_v_to_f16(const bf16* __restrict__ v,
@@ -150,19 +157,18 @@ __global__ __launch_bounds__(256) void prefill_v_to_f16(const bf16* __restrict__
     const size_t base = ((size_t)slab * seq + (size_t)kt * kPKV) * dim;
     const int rows = min(kPKV, seq - kt * kPKV);
     const int nchunk = rows * dim / 8;  // 16-byte chunks
-    us2_t mx = {0, 0}, mn = {0xffff, 0xffff};
+    us2_t mx = {0, 0};
     for (int c = threadIdx.x; c < nchunk; c += 256) {
         i32x4_t x = *reinterpret_cast<const i32x4_t*>(v + base + 8 * (size_t)c);
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            f16_range_acc((unsigned)x[w], mx, mn);
+            f16_range_acc((unsigned)x[w], mx);
             x[w] = (int)bf2_to_h2((unsigned)x[w]);
         }
         *reinterpret_cast<i32x4_t*>(v16 + base + 8 * (size_t)c) = x;
     }
-    const bool bad = f16_range_bad(mx, mn);
-    const int any_bad = __syncthreads_or(bad ? 1 : 0);
-    if (threadIdx.x == 0) ok[blockIdx.x] = any_bad ? 0 : 1;
+    const bool fits = f16_tile_ok(mx);
+    if (threadIdx.x == 0) ok[blockIdx.x] = fits ? 1 : 0;
 }
 
 // PRE (bf16 inputs): v16 / v_ok hold prefill_v_to_f16's output; the fp16 PV
@@ -179,8 +185,8 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
     using C = PCfg<D>;
     typedef _Float16 h8 __attribute__((ext_vector_type(8)));
     // bf16 inputs: P and V go through an fp16 PV product (P rounded to 11
-    // significant bits) on every tile whose V values are all 0 or in
-    // [2^-17, 2^16) in magnitude, bf16 hi + lo P otherwise
+    // significant bits) on every tile whose largest |v| is in [2^-8, 2^16)
+    // (f16_tile_ok), bf16 hi + lo P otherwise
     constexpr bool kF16PV = std::is_same<T, bf16>::value;
     __shared__ __attribute__((aligned(16))) char smem[2 * C::kStage];
 
@@ -266,17 +272,15 @@ void attn_prefill_mfma(const T* __restrict__ q, const T* __restrict__ k,
     const int wrow0 = q0 + 32 * wave;  // first query row of this wave
     const float lazy_raw = kLazy / scale_log2;
 
-    // whether the V tile in vreg fits fp16 exactly (a workgroup vote; every
-    // thread must call it): the largest |v| bit pattern of the thread's
-    // pieces (inf and NaN counting as too large) and the smallest nonzero one
+    // whether the V tile in vreg takes the fp16 product (f16_tile_ok, a
+    // workgroup vote: every thread must call it)
     auto v_fits_f16 = [&]() {
-        us2_t mx = {0, 0}, mn = {0xffff, 0xffff};
+        us2_t mx = {0, 0};
 #pragma unroll
         for (int j = 0; j < C::kKChunks; ++j)
 #pragma unroll
-            for (int w = 0; w < 4; ++w) f16_range_acc((unsigned)vreg[j][w], mx, mn);
-        const bool bad = f16_range_bad(mx, mn);
-        return __syncthreads_or(bad ? 1 : 0) == 0;
+            for (int w = 0; w < 4; ++w) f16_range_acc((unsigned)vreg[j][w], mx);
+        return f16_tile_ok(mx);
     };
 
     bool f16_first;

@@ -77,11 +77,13 @@ def test_prefill_bf16_large_v_tiles_take_the_split_path(d, causal):
 @pytest.mark.parametrize("prepass", [0, 2])
 def test_prefill_bf16_tiny_v_tiles_take_the_split_path(d, causal, prepass, tuning):
     # fp16 holds a bf16 value exactly only for 2^-17 <= |v| < 2^16 (or 0):
-    # below, fp16 subnormals drop significant bits. A tile holding such a
-    # value must take the bf16 split path. With every V around 1e-7 the
-    # output is of that order too, so it is checked at 1e-2 relative (the
-    # fp16 product would be off by up to ~30% there); tiles 2 and 3 alone
-    # tiny run the hand-over, at the usual bar. Pre-pass and in-kernel vote.
+    # below, fp16 subnormals drop significant bits. A tile whose values are
+    # all small (largest |v| < 2^-8) takes the bf16 split path. With every V
+    # around 1e-7 the output is of that order too, so it is checked at 1e-2
+    # relative (the fp16 product would be off by up to ~30% there). Keys
+    # 130-199 tiny (tiles 2 and 3 keep larger values: the fp16 product,
+    # tiny values off by at most 2^-25) and tile 2 wholly tiny (the
+    # hand-over) at the usual bar. Pre-pass and in-kernel vote.
     tuning("FT_PREFILL_PREPASS", prepass)
     rng = np.random.default_rng(60 + d + 2 * causal)
     dt = torch.bfloat16
@@ -97,6 +99,9 @@ def test_prefill_bf16_tiny_v_tiles_take_the_split_path(d, causal, prepass, tunin
     mixed = v.clone()
     mixed[:, :, 130:200] = tiny[:, :, 130:200]
     _check_half(ft.attention_prefill(q, k, mixed, causal=causal), q, k, mixed, causal)
+    whole = v.clone()
+    whole[:, :, 128:192] = tiny[:, :, 128:192]
+    _check_half(ft.attention_prefill(q, k, whole, causal=causal), q, k, whole, causal)
 
 
 @pytest.mark.parametrize("d", [64, 128])
