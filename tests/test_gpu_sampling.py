@@ -305,7 +305,7 @@ def test_staged_vectors_change_every_call_with_no_sync(monkeypatch):
     calls = []
     for i in range(12):
         seeds = [int(x) for x in rng.integers(0, 2 ** 40, rows)]
-        top = 800 if i in (4, 9) else 60
+        top = 2000 if i in (4, 9) else 60
         hist = [rng.integers(0, n, size=int(rng.integers(0, top))).tolist() for _ in range(rows)]
         pt = [(0.9, 0.8), (0.5, 1.1), (0.95, 0.6)][i % 3]
         calls.append((i % 2, seeds, hist, pt))
