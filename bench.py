@@ -8,7 +8,7 @@ permutation of a page pool four times larger than the pages in use. One
 "step" is what a decode loop does per token: kv_append_paged of one new
 token per row at position lens[b], then attention_decode_paged over
 lens[b] + 1 tokens - one call of attention_decode_paged_append, whose
-decode kernel appends the fresh token itself.
+combine kernel folds the fresh token in and appends it to the pools.
 
   value     = algorithmic bytes per step / measured step time   (GB/s)
               bytes: K+V rows read (sum_b (lens_b+1) * Hkv * D * 2 * 2 B),
@@ -160,7 +160,7 @@ def make_c3(torch, np, dev):
 
 def c3_step(ft, w):
     # kv_append_paged(..., lens) + attention_decode_paged(..., lens + 1) in
-    # one call: the decode kernel appends the fresh token itself
+    # one call: the combine kernel folds the fresh token in and appends it
     ft.attention_decode_paged_append(w["q"], w["kp"], w["vp"], w["table_t"], w["kn"],
                                      w["vn"], w["lens_t"])
 

@@ -465,10 +465,10 @@ def attention_decode_paged_append(q, k_pool, v_pool, block_table, k_new, v_new, 
     block_table, k_new, v_new, lens)`` then ``attention_decode_paged(q,
     k_pool, v_pool, block_table, lens + 1)``, in one call (lens is not
     modified). GPU tensors only. For bf16 / fp16 with D = 128 the decode
-    kernel takes the fresh token itself (merged into the row's online
-    softmax in float32: the output equals the two ops' within the attention
-    tolerance, the pools bit for bit) and writes it into the pools, one
-    launch fewer; other shapes run the two ops. Build addition: the
+    kernel attends the cached tokens and its combine kernel folds the fresh token into each row's log-sum-exp merge
+    (in float32: the output equals the two ops' within the attention
+    tolerance) and writes it into the pools (bit for bit), one launch
+    fewer; other shapes run the two ops. Build addition: the
     reference runs the two ops (``attention.cu:1924-1966``, then
     ``attention.cu:1785-1900``)."""
     c = _DECODE_APPEND.bind(q=q, k_pool=k_pool, v_pool=v_pool, k_new=k_new, v_new=v_new,

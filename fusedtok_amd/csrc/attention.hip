@@ -1277,10 +1277,10 @@ __global__ __launch_bounds__(256) void lens_plus1_kernel(const int* __restrict__
 
 // kv_append_paged(k_pool, v_pool, table, k_new, v_new, lens) followed by
 // attention_decode_paged(q, k_pool, v_pool, table, lens + 1), in one call.
-// On the stream path (bf16 / fp16, D = 128) the decode kernel does the
-// append itself: the row's last piece takes the fresh token from k_new /
-// v_new (a merge into its online softmax in float32) and writes it to the
-// pools, and rows with no cached token are written by workgroup 0 - one
+// On the stream path (bf16 / fp16, D = 128) the decode
+// kernel attends the lens[b] cached tokens (every piece leaves a partial)
+// and attn_combine_append folds the fresh token from k_new / v_new into
+// each row's log-sum-exp merge (float32) and writes it to the pools - one
 // launch fewer. Elsewhere: the two ops, lens + 1 through library scratch.
 template <typename T>
 void attention_append_run(const T* q, T* k_pool, T* v_pool, const int* table, const T* k_new,

@@ -142,23 +142,6 @@ int ft_attention_decode_paged_launch_fp16(const void* q, const void* k_pool,
 /* bytes: 1.6 MB for batch 32 with 32 / 8 heads on 256 CUs; batch 512   */
 /* at 32 / 8 heads still fits. Every call on one GPU shares that GPU's  */
 /* array, which keeps the last call's contents: calls that overlap on   */
-/* Build addition (decode step): ft_kv_append_paged_launch(k_new, v_new,
- * table, lens, k_pool, v_pool, ...) followed by
- * ft_attention_decode_paged_launch(q, k_pool, v_pool, table, lens + 1,
- * out, ...) in one call (reference: the two ops, attention.cu:1924-1966
- * then 1785-1900; lens is not modified). dtype FT_DT_F32 / BF16 / F16 for
- * q, the pools, k_new / v_new [batch, kv_heads, dim] and out. For bf16 /
- * fp16 with dim 128 the decode kernel takes the fresh token itself (merged
- * into the row's online softmax in float32, so out equals the two ops'
- * within the attention tolerance, not bit for bit; the pools are equal bit
- * for bit) and writes it into the pools: one launch fewer. Other shapes
- * run the two ops. */
-int ft_attention_decode_paged_append_launch(const void* q, void* k_pool, void* v_pool,
-                                            const int* table, const void* k_new,
-                                            const void* v_new, const int* lens, void* out,
-                                            int dtype, int batch, int q_heads, int kv_heads,
-                                            int page, int tbl_width, int dim,
-                                            uintptr_t stream);
 /* one GPU (unordered streams) race and must be serialised.             */
 #define FT_NOALLOC_WORKSPACE_BYTES (16u << 20)
 int ft_attention_decode_paged_launch_bf16_noalloc(const void* q, const void* k_pool,
@@ -168,6 +151,25 @@ int ft_attention_decode_paged_launch_bf16_noalloc(const void* q, const void* k_p
                                                   int kv_heads, int page,
                                                   int tbl_width, int dim,
                                                   uintptr_t stream);
+
+/* Build addition (decode step): ft_kv_append_paged_launch(k_new, v_new,
+ * table, lens, k_pool, v_pool, ...) followed by
+ * ft_attention_decode_paged_launch(q, k_pool, v_pool, table, lens + 1,
+ * out, ...) in one call (reference: the two ops, attention.cu:1924-1966
+ * then 1785-1900; lens is not modified). dtype FT_DT_F32 / BF16 / F16 for
+ * q, the pools, k_new / v_new [batch, kv_heads, dim] and out. For bf16 /
+ * fp16 with dim 128 the decode kernel attends the lens[b] cached
+ * tokens, and its combine kernel folds the fresh token's
+ * score and value into each row's log-sum-exp merge (in float32, so out
+ * equals the two ops' within the attention tolerance, not bit for bit)
+ * and writes the fresh K / V rows into the pools (equal bit for bit): one
+ * launch fewer. Other shapes run the two ops. */
+int ft_attention_decode_paged_append_launch(const void* q, void* k_pool, void* v_pool,
+                                            const int* table, const void* k_new,
+                                            const void* v_new, const int* lens, void* out,
+                                            int dtype, int batch, int q_heads, int kv_heads,
+                                            int page, int tbl_width, int dim,
+                                            uintptr_t stream);
 
 /* ------------------------------------------------------------------ */
 /* KV append: one fresh token per sequence written at position lens[b] */
