@@ -319,19 +319,44 @@ constexpr int kStreamScanRows = 2048;        // sequences per launch (LDS prefix
 // 20.0 us at 512, 21.3 us at 256.
 constexpr int kStreamMinSeg = 512;
 
+// Rows of equal length, each at least this long, take one segment per CU
+// instead of two when the host launched the default two per CU (the
+// launch's second half then returns at once). Measured on one box, two
+// rounds each, one against two per CU: config 4's layer (64 rows of 8193
+// tokens) 431.8-432.2 against 438.8-439.8 us, config 5b (8 x 8 rows of
+// 131072) 646.1-646.5 against 659.9 us; config 3's ragged rows keep two
+// per CU (0.390 against 0.401-0.403 ms per step with one).
+constexpr int kStreamUniformLong = 4096;
+
 // Row addressing modes of attn_decode_stream.
 enum RowMode { kRowsContig = 0, kRowsPagedPow2 = 1, kRowsPagedDiv = 2 };
 
 // Exclusive prefix of the clamped lengths into s_pref[0..batch] (wave 0;
-// each lane takes a contiguous run of rows, then a wave scan of the runs).
+// each lane takes a contiguous run of rows, then a wave scan of the runs),
+// and their minimum and maximum into s_mm[0], s_mm[1].
 __device__ __forceinline__ void scan_lengths(const int* __restrict__ lens,
                                              int batch, int span, int lane,
-                                             long long* s_pref) {
+                                             long long* s_pref, int* s_mm) {
     const int per = (batch + 63) / 64;
     const int r0 = lane * per;
     long long local = 0;
+    int lmin = INT_MAX, lmax = 0;
     for (int i = 0; i < per; ++i)
-        if (r0 + i < batch) local += clamp_len(lens, r0 + i, span);
+        if (r0 + i < batch) {
+            const int l = clamp_len(lens, r0 + i, span);
+            local += l;
+            lmin = min(lmin, l);
+            lmax = max(lmax, l);
+        }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        lmin = min(lmin, __shfl_xor(lmin, o, 64));
+        lmax = max(lmax, __shfl_xor(lmax, o, 64));
+    }
+    if (lane == 0) {
+        s_mm[0] = lmin;
+        s_mm[1] = lmax;
+    }
     long long incl = local;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -398,7 +423,7 @@ void attn_decode_stream(
     float* __restrict__ ws_ml, float* __restrict__ ws_acc,
     long long* __restrict__ pref_out, T* __restrict__ out, int batch, int hq, int hkv,
     int group, int rows_or_page, int page_shift, int tbl_width, int span, float scale_log2,
-    int min_seg) {
+    int min_seg, int halve) {
     using M = Mfma<T>;
     using V8 = typename M::v8;
     constexpr int D = kMfmaDim;
@@ -406,6 +431,7 @@ void attn_decode_stream(
     __shared__ float s_acc[4][16][kMfmaAccPitch];
     __shared__ float s_m[4][16], s_l[4][16];
     __shared__ long long s_pref[kStreamScanRows + 1];
+    __shared__ int s_mm[2];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -413,12 +439,17 @@ void attn_decode_stream(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15, g = lane >> 4;
 
-    if (wave == 0) scan_lengths(lens, batch, span, lane, s_pref);
+    if (wave == 0) scan_lengths(lens, batch, span, lane, s_pref, s_mm);
     __syncthreads();
-    if (blockIdx.x == 0)  // the combine kernel's copy of the prefix
+    // segments: the grid, or half of it for long rows of equal length
+    int nseg = (int)gridDim.x;
+    if (halve && s_mm[0] == s_mm[1] && s_mm[0] >= kStreamUniformLong) nseg = (nseg + 1) >> 1;
+    nseg = __builtin_amdgcn_readfirstlane(nseg);
+    if (blockIdx.x == 0) {  // the combine kernel's copy of the prefix and the count
         for (int i = tid; i <= batch; i += 256) pref_out[i] = s_pref[i];
+        if (tid == 0) pref_out[batch + 1] = nseg;
+    }
     const long long total = uniform64(s_pref[batch]) * hkv;
-    const int nseg = gridDim.x;
     const long long S = stream_seg_len(total, nseg, min_seg);
     const long long seg_lo = (long long)blockIdx.x * S;
     if (seg_lo >= total) return;
@@ -700,8 +731,8 @@ __device__ __forceinline__ float4 combine_head(const float* __restrict__ ws_ml,
                                                const float* __restrict__ ws_acc,
                                                const long long* __restrict__ pref,
                                                T* __restrict__ out, int bh, int batch, int hq,
-                                               int hkv, int group, int nseg, int min_seg,
-                                               int lane, bool skip_empty = false) {
+                                               int hkv, int group, int min_seg, int lane,
+                                               bool skip_empty = false) {
     constexpr int D = kMfmaDim;
     const int b = bh / hq;
     const int h = bh - b * hq;
@@ -714,7 +745,8 @@ __device__ __forceinline__ float4 combine_head(const float* __restrict__ ws_ml,
             St<T>::st4(o + 4 * lane, make_float4(0.f, 0.f, 0.f, 0.f));
         return make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    const long long S = stream_seg_len(pref[batch] * hkv, nseg, min_seg);
+    // the decode kernel's segment count, after the prefix
+    const long long S = stream_seg_len(pref[batch] * hkv, (int)pref[batch + 1], min_seg);
     const long long start = pref[b] * hkv + (long long)kv * len;
     const int s_lo = (int)(start / S), s_hi = (int)((start + len - 1) / S);
     // stored whole by the decode kernel: its stored values, read back here
@@ -767,9 +799,9 @@ template <typename T, bool AMAX>
 __global__ __launch_bounds__(64) void attn_combine_stream(
     const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
     const long long* __restrict__ pref, T* __restrict__ out, float* __restrict__ amax,
-    int batch, int hq, int hkv, int group, int nseg, int min_seg, int skip_empty) {
+    int batch, int hq, int hkv, int group, int min_seg, int skip_empty) {
     const float4 v = combine_head<T>(ws_ml, ws_acc, pref, out, blockIdx.x, batch, hq, hkv,
-                                     group, nseg, min_seg, threadIdx.x, skip_empty != 0);
+                                     group, min_seg, threadIdx.x, skip_empty != 0);
     if constexpr (AMAX) {
         const float m = head_absmax(v);
         if (threadIdx.x == 0) amax[blockIdx.x] = m;
@@ -789,7 +821,7 @@ __global__ __launch_bounds__(64) void attn_combine_append(
     const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
     const long long* __restrict__ pref, const int* __restrict__ lens, const T* __restrict__ q,
     AppendArgs<T> ap, const int* __restrict__ table, T* __restrict__ out, int batch, int hq,
-    int hkv, int group, int nseg, int min_seg, int span, int rows_or_page, int page_shift,
+    int hkv, int group, int min_seg, int span, int rows_or_page, int page_shift,
     int tbl_width, float scale_log2) {
     constexpr int D = kMfmaDim;
     const int bh = blockIdx.x, lane = threadIdx.x;
@@ -824,7 +856,7 @@ __global__ __launch_bounds__(64) void attn_combine_append(
     }
     int s_lo = 0, np = 0;
     if (len > 0) {
-        const long long S = stream_seg_len(pref[batch] * hkv, nseg, min_seg);
+        const long long S = stream_seg_len(pref[batch] * hkv, (int)pref[batch + 1], min_seg);
         const long long start = pref[b] * hkv + (long long)kv * len;
         s_lo = (int)(start / S);
         np = (int)((start + len - 1) / S) - s_lo + 1;
@@ -874,8 +906,8 @@ template <typename T>
 __global__ __launch_bounds__(64 * kCqWaves) void attn_combine_quant(
     const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
     const long long* __restrict__ pref, T* __restrict__ out, signed char* __restrict__ q,
-    float* __restrict__ scale_out, int batch, int hq, int hkv, int group, int nseg,
-    int min_seg, GridMax gm) {
+    float* __restrict__ scale_out, int batch, int hq, int hkv, int group, int min_seg,
+    GridMax gm) {
     __shared__ float red[kCqWaves];
     constexpr int D = kMfmaDim;
     const int lane = threadIdx.x & 63;
@@ -884,8 +916,7 @@ __global__ __launch_bounds__(64 * kCqWaves) void attn_combine_quant(
     const bool live = bh < batch * hq;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live)
-        v = combine_head<T>(ws_ml, ws_acc, pref, out, bh, batch, hq, hkv, group, nseg, min_seg,
-                            lane);
+        v = combine_head<T>(ws_ml, ws_acc, pref, out, bh, batch, hq, hkv, group, min_seg, lane);
     float m = block_max<64 * kCqWaves>(live ? head_absmax(v) : 0.0f, red);
     m = grid_max<64 * kCqWaves>(gm, m, red);
     const float scale = make_scale(m);
@@ -1019,11 +1050,11 @@ void launch_stream(bool paged, int page_shift, int nseg, hipStream_t s, const T*
                    const T* k, const T* v, const int* table, const int* lens, float* ws_ml,
                    float* ws_acc, long long* pref, T* out, int batch, int hq, int hkv,
                    int group, int rows_or_page, int tbl_width, int span, float scale_log2,
-                   int min_seg, bool fresh) {
+                   int min_seg, bool fresh, bool halve) {
     auto go = [&](auto kernel, const int* tbl, int shift, int width) {
         kernel<<<(unsigned)nseg, 256, 0, s>>>(q, k, v, tbl, lens, ws_ml, ws_acc, pref, out,
                                               batch, hq, hkv, group, rows_or_page, shift,
-                                              width, span, scale_log2, min_seg);
+                                              width, span, scale_log2, min_seg, halve ? 1 : 0);
     };
     if (paged && page_shift >= 0) {
         if (fresh) go(attn_decode_stream<T, kRowsPagedPow2, true>, table, page_shift, tbl_width);
@@ -1110,15 +1141,19 @@ int attention_run(const T* q, const T* k, const T* v, const int* table,
     if constexpr (!std::is_same<T, float>::value) {
         if (fast && span > 0) {
             // stream split: G equal token segments, G = 2 workgroups per CU
-            // (the kernel's register budget allows exactly two per CU)
-            int nseg = tune(Tune::AttnSegs, 2 * dev_info().cu_count);
+            // (the kernel's register budget allows exactly two per CU); the
+            // kernel takes one per CU for long rows of equal length unless
+            // FT_ATTN_SEGS sets the count
+            const int forced = tune(Tune::AttnSegs, 0);
+            int nseg = forced > 0 ? forced : 2 * dev_info().cu_count;
             nseg = std::max(1, std::min(nseg, 1 << 20));
+            const bool halve = forced <= 0;
             const int min_seg = std::max(32, tune(Tune::AttnMinSeg, kStreamMinSeg));
             const size_t nslots = ((size_t)nseg + (size_t)batch * hkv) * group;
             const size_t ml_floats = (nslots * 2 + 63) & ~(size_t)63;
             const size_t acc_floats = nslots * dim;
             char* ws = (char*)wsp.get(
-                (ml_floats + acc_floats) * sizeof(float) + (batch + 1) * sizeof(long long), s);
+                (ml_floats + acc_floats) * sizeof(float) + (batch + 2) * sizeof(long long), s);
             float* ws_ml = (float*)ws;
             float* ws_acc = ws_ml + ml_floats;
             long long* pref = (long long*)(ws_acc + acc_floats);
@@ -1126,19 +1161,18 @@ int attention_run(const T* q, const T* k, const T* v, const int* table,
                 inval("attention: the append form keeps no per-head maxima");
             launch_stream<T>(paged, page_shift, nseg, s, q, k, v, table, lens, ws_ml, ws_acc,
                              pref, out, batch, hq, hkv, group, rows_or_page, tbl_width,
-                             (int)span, scale_log2, min_seg, ap.k_new != nullptr);
+                             (int)span, scale_log2, min_seg, ap.k_new != nullptr, halve);
             launch_check("attention decode kernel launch");
             if (ap.k_new) {
                 const unsigned grid = (unsigned)((long long)batch * hq);
                 if (page_shift >= 0)
                     attn_combine_append<T, kRowsPagedPow2><<<grid, 64, 0, s>>>(
                         ws_ml, ws_acc, pref, lens, q, ap, table, out, batch, hq, hkv, group,
-                        nseg, min_seg, (int)span, rows_or_page, page_shift, tbl_width,
-                        scale_log2);
+                        min_seg, (int)span, rows_or_page, page_shift, tbl_width, scale_log2);
                 else
                     attn_combine_append<T, kRowsPagedDiv><<<grid, 64, 0, s>>>(
                         ws_ml, ws_acc, pref, lens, q, ap, table, out, batch, hq, hkv, group,
-                        nseg, min_seg, (int)span, rows_or_page, -1, tbl_width, scale_log2);
+                        min_seg, (int)span, rows_or_page, -1, tbl_width, scale_log2);
                 launch_check("attention combine + append kernel launch");
                 return 0;
             }
@@ -1151,7 +1185,7 @@ int attention_run(const T* q, const T* k, const T* v, const int* table,
                                       64 * kCqWaves, GridUse::AttnOut)) {
                         attn_combine_quant<T><<<(unsigned)nwg, 64 * kCqWaves, 0, s>>>(
                             ws_ml, ws_acc, pref, out, qcodes, qscale, batch, hq, hkv, group,
-                            nseg, min_seg, gm);
+                            min_seg, gm);
                         launch_check("attention combine + quantize kernel launch");
                         return 2;
                     }
@@ -1159,10 +1193,10 @@ int attention_run(const T* q, const T* k, const T* v, const int* table,
             }
             if (amax)
                 attn_combine_stream<T, true><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
-                    ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group, nseg, min_seg, 0);
+                    ws_ml, ws_acc, pref, out, amax, batch, hq, hkv, group, min_seg, 0);
             else
                 attn_combine_stream<T, false><<<(unsigned)((long long)batch * hq), 64, 0, s>>>(
-                    ws_ml, ws_acc, pref, out, nullptr, batch, hq, hkv, group, nseg, min_seg, 0);
+                    ws_ml, ws_acc, pref, out, nullptr, batch, hq, hkv, group, min_seg, 0);
             launch_check("attention combine kernel launch");
             return amax ? 1 : 0;
         }

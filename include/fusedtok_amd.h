@@ -138,7 +138,7 @@ int ft_attention_decode_paged_launch_fp16(const void* q, const void* k_pool,
 /* buffer, and no hipMalloc, hipFree or other allocating routine is     */
 /* called. A call whose partials do not fit returns FT_EINVAL before    */
 /* anything is launched. With D = 128 and G = q_heads / kv_heads <= 16  */
-/* the need is (2 * CUs + batch * kv_heads) * G * 520 + 8 * (batch + 1) */
+/* the need is (2 * CUs + batch * kv_heads) * G * 520 + 8 * (batch + 2) */
 /* bytes: 1.6 MB for batch 32 with 32 / 8 heads on 256 CUs; batch 512   */
 /* at 32 / 8 heads still fits. Every call on one GPU shares that GPU's  */
 /* array, which keeps the last call's contents: calls that overlap on   */

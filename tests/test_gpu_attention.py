@@ -306,6 +306,47 @@ def test_paged_append_decode_equals_the_two_ops(dt, group, page, min_seg, tuning
         lens = lens + 1
 
 
+@pytest.mark.parametrize("dt", HALF)
+def test_long_equal_rows_take_one_segment_per_cu(dt, tuning):
+    # Rows of equal length >= 4096 run on one segment per CU instead of the
+    # default two (the decode kernel halves its own grid and tells the
+    # combine kernels the count); shorter or ragged rows keep two. The
+    # default call must equal the call with FT_ATTN_SEGS forced to the count
+    # the kernel picks, bit for bit, in every combine form (plain, with the
+    # quantize fold, the appending step), and the oracle.
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    rng = np.random.default_rng(4242)
+    cases = [([5000] * 4, cus), ([4095] * 4, 2 * cus), ([5000, 4999, 5000, 5000], 2 * cus),
+             ([9000] * 2, cus)]
+    for lens, picked in cases:
+        q, kp, vp, tbl, ln = paged_case(rng, len(lens), 32, 8, 128, lens)
+        qd, kd, vd, td, lt = t(q, dt), t(kp, dt), t(vp, dt), t(tbl), t(ln)
+        kn = t(rng.standard_normal((len(lens), 8, 128)).astype(np.float32), dt)
+        vn = t(rng.standard_normal((len(lens), 8, 128)).astype(np.float32), dt)
+        cap = tbl.shape[1] * 16
+        ln_app = t(np.minimum(ln, cap - 1).astype(np.int32))
+
+        def run():
+            out = ft.attention_decode_paged(qd, kd, vd, td, lt)
+            qout, codes, scale = ft.attention_decode_paged_quant(qd, kd, vd, td, lt,
+                                                                  device_scale=True)
+            ka, va = kd.clone(), vd.clone()
+            app = ft.attention_decode_paged_append(qd, ka, va, td, kn, vn, ln_app)
+            torch.cuda.synchronize()
+            return out, qout, codes, scale, app, ka, va
+
+        got = run()
+        tuning("FT_ATTN_SEGS", picked)
+        ref = run()
+        tuning.clear("FT_ATTN_SEGS")
+        for i, (a, b) in enumerate(zip(got, ref)):
+            assert torch.equal(a, b), f"lens {lens[:2]}..: output {i} differs from {picked} segments"
+        assert_half_close(got[0].float().cpu().numpy(),
+                          oracle.attention_decode_paged(rounded(q, dt), rounded(kp, dt),
+                                                        rounded(vp, dt), tbl, ln),
+                          f"lens {lens[:2]}..")
+
+
 def test_paged_equals_contiguous_materialisation():
     rng = np.random.default_rng(41)
     q, kp, vp, tbl, ln = paged_case(rng, 3, 8, 2, 64, [37, 16, 48])
