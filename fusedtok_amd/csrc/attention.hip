@@ -900,7 +900,10 @@ __global__ __launch_bounds__(64) void attn_combine_append(
 // wave writes its head's codes from the stored values it holds, and
 // workgroup 0 the scale: quantize_int8's codes and scale (scale = max / 127,
 // codes rint(v * (1 / scale)) clamped to +-127, quantize.cu:169-186).
-constexpr int kCqWaves = 8;
+// 16 waves per workgroup: config 4's 2048 heads take 128 workgroups, so
+// 128 arrivals meet in grid_max (layer 432.5-432.9 us against 433.6-433.7
+// with 8 waves and 437.0-437.2 with 4, same box).
+constexpr int kCqWaves = 16;
 
 template <typename T>
 __global__ __launch_bounds__(64 * kCqWaves) void attn_combine_quant(
