@@ -465,6 +465,56 @@ def test_paged_graph_capture_replay():
         assert torch.equal(replayed, eager), f"replay {it} differs from eager"
 
 
+def test_graph_replay_follows_the_lengths_segment_choice():
+    # The segment count for equal long rows is chosen on the device from the
+    # lengths, so one captured graph must follow lens that change between
+    # replays: equal (one segment per CU), ragged (two), equal again. Every
+    # replay equals an eager call on the same lens, bit for bit, for the
+    # plain and the quantizing decode.
+    rng = np.random.default_rng(91)
+    dt = torch.bfloat16
+    q, kp, vp, tbl, _ = paged_case(rng, 4, 32, 8, 128, [5000] * 4)
+    qt, kpt, vpt, tblt = t(q, dt), t(kp, dt), t(vp, dt), t(tbl)
+    lnt = t(np.full(4, 5000, np.int32))
+    out = torch.empty_like(qt)
+    qout = torch.empty_like(qt)
+    codes = torch.empty(qt.shape, dtype=torch.int8, device=DEV)
+    scale = torch.empty(1, dtype=torch.float32, device=DEV)
+
+    def step():
+        s_ = torch.cuda.current_stream().cuda_stream
+        ft._fusedtok.attention_decode_paged_launch_bf16(
+            qt.data_ptr(), kpt.data_ptr(), vpt.data_ptr(), tblt.data_ptr(), lnt.data_ptr(),
+            out.data_ptr(), 4, 32, 8, 16, tbl.shape[1], 128, s_)
+        ft._fusedtok.attention_decode_paged_quant_launch(
+            qt.data_ptr(), kpt.data_ptr(), vpt.data_ptr(), tblt.data_ptr(), lnt.data_ptr(),
+            qout.data_ptr(), 1, codes.data_ptr(), scale.data_ptr(), 4, 32, 8, 16,
+            tbl.shape[1], 128, s_)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for it, lens in enumerate([[5000] * 4, [5000, 4100, 5000, 1], [4096] * 4, [5000] * 4]):
+        lnt.copy_(torch.tensor(lens, dtype=torch.int32))
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        got = (out.clone(), qout.clone(), codes.clone(), scale.clone())
+        e_out = ft.attention_decode_paged(qt, kpt, vpt, tblt, lnt)
+        e_q, e_codes, e_scale = ft.attention_decode_paged_quant(qt, kpt, vpt, tblt, lnt,
+                                                               device_scale=True)
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], e_out), f"replay {it} ({lens}): output"
+        assert torch.equal(got[1], e_q) and torch.equal(got[2], e_codes), f"replay {it}: codes"
+        assert torch.equal(got[3], e_scale.reshape(1)), f"replay {it}: scale"
+
+
 def test_paged_staged_host_inputs():
     rng = np.random.default_rng(43)
     q, kp, vp, tbl, ln = paged_case(rng, 2, 2, 2, 128, [1, 16])
