@@ -948,7 +948,7 @@ def main():
                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic_for("attention_c3"),
                      "kernel": "attention_decode_paged_append = attn_decode_stream "
-                               "(appending form) + attn_combine_stream",
+                               "(appending form) + attn_combine_append",
                      "avg_us": round(attn_ms * 1e3, 2),
                      "bytes_per_launch": step_bytes,
                      "copy_gbs": round(copy_gbs, 1) if copy_gbs else None,
