@@ -466,6 +466,46 @@ def test_paged_graph_capture_replay():
         assert torch.equal(replayed, eager), f"replay {it} differs from eager"
 
 
+@pytest.mark.parametrize("layout", ["page5", "contiguous"])
+def test_long_equal_rows_other_layouts(layout, tuning):
+    # the segment choice in the other two row modes: paged with a page size
+    # that is not a power of two, and the contiguous cache (without lens:
+    # every row holds the cache's capacity). 8 x 8 rows of ~4200 tokens
+    # exceed 512 segments of the 512-token minimum, so the two counts cut
+    # the rows differently.
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    tuning("FT_ATTN_SEGS", 0)
+    rng = np.random.default_rng(515)
+    dt = torch.float16
+    for lens, picked in [([4200] * 8, cus), ([4200, 4100] * 4, 2 * cus)]:
+        if layout == "page5":
+            q, kp, vp, tbl, ln = paged_case(rng, len(lens), 32, 8, 128, lens, page=5)
+            args = (t(q, dt), t(kp, dt), t(vp, dt), t(tbl), t(ln))
+            call = ft.attention_decode_paged
+            ref_fn = lambda: oracle.attention_decode_paged(rounded(q, dt), rounded(kp, dt),
+                                                           rounded(vp, dt), tbl, ln)
+        else:
+            q, k, v, _ = make_case(rng, len(lens), 32, 8, max(lens), 128, False)
+            ln = np.asarray(lens, np.int32)
+            use_lens = len(set(lens)) > 1  # equal rows: no lens, the capacity is the length
+            args = (t(q, dt), t(k, dt), t(v, dt)) + ((t(ln),) if use_lens else ())
+            call = ft.attention_decode
+            ref_fn = lambda: oracle.attention_decode(rounded(q, dt), rounded(k, dt),
+                                                     rounded(v, dt), ln if use_lens else None)
+        got = call(*args)
+        tuning("FT_ATTN_SEGS", picked)
+        ref = call(*args)
+        tuning("FT_ATTN_SEGS", 3 * cus - picked)  # the count not picked
+        other = call(*args)
+        tuning("FT_ATTN_SEGS", 0)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"{layout} lens {lens}: differs from {picked} segments"
+        # the rows are cut differently under the other count: the float32
+        # merges of 4 and 8 pieces round differently
+        assert not torch.equal(got, other), f"{layout} lens {lens}: the count made no difference"
+        assert_half_close(got.float().cpu().numpy(), ref_fn(), f"{layout} lens {lens}")
+
+
 def test_graph_replay_follows_the_lengths_segment_choice():
     # The segment count for equal long rows is chosen on the device from the
     # lengths, so one captured graph must follow lens that change between
